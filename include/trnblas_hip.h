@@ -1,0 +1,203 @@
+/*
+ * trnblas_hip.h — C ABI of the MI355X (gfx950) Level-3 op library.
+ *
+ * One function per kernel family. Every pointer argument is a device pointer
+ * unless stated otherwise; every function is asynchronous on `stream` (a
+ * hipStream_t passed as void*; NULL = the null stream), allocates nothing and
+ * returns 0 on success or a negative TRNBLAS_E_* code. The message of the
+ * last failure on the calling thread is returned by trnblas_hip_last_error().
+ * Outputs are caller-allocated; inputs are never written. Functions are
+ * reentrant and keep no mutable global state.
+ *
+ * The reference (trnsci/trnblas 0.13.0) has no native code: its device path is
+ * the NKI kernels behind the `torch.ops.trnblas.*` custom ops registered in
+ * trnblas/nki/_native.py:49-259 and called from trnblas/nki/dispatch.py
+ * (`_call_kernel` :2168-2184, `_launch` :2187-2194). Each entry point below
+ * names the reference interface it replaces.
+ */
+#ifndef TRNBLAS_HIP_H
+#define TRNBLAS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types */
+#define TRNBLAS_F32 0
+#define TRNBLAS_BF16 1
+#define TRNBLAS_F16 2
+
+/* error codes */
+#define TRNBLAS_OK 0
+#define TRNBLAS_E_ARG (-1)       /* invalid argument (shape, stride, dtype, flag) */
+#define TRNBLAS_E_LAUNCH (-2)    /* a kernel launch failed (hipGetLastError) */
+#define TRNBLAS_E_NONFINITE (-3) /* reserved: non-finite data where the op cannot represent it */
+#define TRNBLAS_E_WORKSPACE (-4) /* workspace too small */
+
+/* Version of this ABI (bumped on any signature change). */
+int trnblas_hip_abi_version(void);
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* trnblas_hip_last_error(void);
+
+/*
+ * GEMM, strided-batched:  D[b] = alpha * op(A[b]) * op(B[b]) + beta * C[b]
+ *
+ * Replaces the GEMM kernel family behind torch.ops.trnblas.gemm_{64,128}_128_
+ * {128,256,512}, gemm_ragged, gemm_lnc and gemm_lnc_tn
+ * (trnblas/nki/_native.py:49-74; kernels trnblas/nki/dispatch.py:3324-3760),
+ * plus the `_scale_add` epilogue of trnblas/level3.py:42-66, which is fused
+ * here, and the per-slice launch loop of `nki_batched_gemm`
+ * (dispatch.py:1384-1427), which is one launch here (grid over the batch).
+ *
+ * dtype: TRNBLAS_F32 (fp32 MFMA) or TRNBLAS_BF16 / TRNBLAS_F16 (16-bit MFMA,
+ * fp32 accumulate). A, B, C, D all have that element type.
+ * op(A) is M x K: A is row-major M x K (lda >= K) when transA == 0, row-major
+ * K x M (lda >= M) when transA != 0; likewise op(B) is K x N. C and D are
+ * row-major M x N with leading dimensions ldc, ldd. C may be NULL when
+ * beta == 0 (then C is not read, as in BLAS). Any M, N, K >= 0 (ragged edges
+ * are handled in the kernel; K == 0 gives D = beta * C). Batch strides are in
+ * elements; a stride of 0 broadcasts that operand over the batch. D must not
+ * overlap A, B or C.
+ */
+int trnblas_hip_gemm(int dtype, int transA, int transB, int64_t M, int64_t N, int64_t K,
+                     double alpha, const void* A, int64_t lda, int64_t strideA,
+                     const void* B, int64_t ldb, int64_t strideB, double beta,
+                     const void* C, int64_t ldc, int64_t strideC, void* D, int64_t ldd,
+                     int64_t strideD, int64_t batch, void* stream);
+
+/*
+ * SYRK:  D = alpha * op(A) * op(A)^T + beta * sym_uplo(C), returned full.
+ *
+ * Replaces torch.ops.trnblas.syrk (trnblas/nki/_native.py:124-132; kernel
+ * dispatch.py:4493-4544) together with the host symmetrisation
+ * `_symmetrize` (dispatch.py:3167-3199) and the triangle rule
+ * `_sym_from_triangle` of trnblas/level3.py:298-302. Only the lower triangle
+ * of op(A) op(A)^T is computed (n(n+1)k flops); each value is written to
+ * both D[i][j] and D[j][i], so D is exactly symmetric.
+ * op(A) is N x K: A row-major N x K (trans == 0) or K x N (trans != 0).
+ * uplo: 0 = the lower triangle of C is referenced, 1 = the upper. C may be
+ * NULL when beta == 0. dtype as in trnblas_hip_gemm.
+ */
+int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64_t K, double alpha,
+                     const void* A, int64_t lda, double beta, const void* C, int64_t ldc,
+                     void* D, int64_t ldd, void* stream);
+
+/*
+ * DF-MP2 pair energies, fused (T never leaves the chip).
+ *
+ * For each pair p = (i, j):
+ *   e_p = sum_{a,b < nvir} T_ab (2 T_ab - T_ba) / (eps_i[i] + eps_j[j] - eps_vir[a] - eps_vir[b]),
+ *   T = X_i X_j^T,  X_i = Bi + i*ldi_occ,  X_j = Bj + j*ldj_occ,
+ * each X an nvir x naux fp32 matrix with rows ld_vir elements apart (naux
+ * contiguous).
+ *
+ * Pair set: when pair_i == NULL, every unordered pair i <= j of
+ * [0, nocc) with weight 1 (i == j) or 2 (i != j) — the symmetric walk of the
+ * reference (e_ij = e_ji); this needs Bi == Bj, eps_i == eps_j, ldi_occ ==
+ * ldj_occ. Otherwise the npairs pairs (pair_i[p], pair_j[p]) (device int32
+ * arrays) with weights pair_w[p] (device double array, NULL = all 1).
+ *
+ * out_pairs (device double[npairs], may be NULL) receives the unweighted e_p;
+ * out_total (device double[1], may be NULL) receives sum_p w_p e_p. Both are
+ * deterministic (fixed reduction order). workspace must hold
+ * trnblas_hip_pair_energy_workspace(nvir, npairs) bytes (npairs =
+ * nocc (nocc + 1) / 2 in the implicit mode).
+ *
+ * Replaces torch.ops.trnblas.pair_energy_sym and the per-row launch loop of
+ * `_nki_pair_energy_sym_impl` (trnblas/nki/_native.py:221-239,
+ * dispatch.py:2768-2795, kernel :4899-5001), and is the engine of the
+ * batched_pair / j_batched / fused_gemm_energy op surface
+ * (_native.py:168-218).
+ */
+size_t trnblas_hip_pair_energy_workspace(int64_t nvir, int64_t npairs);
+int trnblas_hip_pair_energy(int64_t nvir, int64_t naux, const float* Bi, int64_t ldi_occ,
+                            const float* Bj, int64_t ldj_occ, int64_t ld_vir,
+                            const float* eps_i, const float* eps_j, const float* eps_vir,
+                            int64_t nocc, int64_t npairs, const int32_t* pair_i,
+                            const int32_t* pair_j, const double* pair_w, double* out_pairs,
+                            double* out_total, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/*
+ * MP2 energy of a precomputed amplitude block (no GEMM), HBM-bound.
+ *
+ * T[i][j][a][b] = T_flat[(i*nvir + a) * ldt + j*nvir + b] for i < ic,
+ * j < nocc. out_pairs (device double[ic*nocc], row-major (i, j)) receives
+ *   sum_ab T_ijab (2 T_ijab - T_ijba) / (eo_chunk[i] + eo_full[j] - ev[a] - ev[b]).
+ * Replaces torch.ops.trnblas.mp2_energy (trnblas/nki/_native.py:135-158,
+ * kernel dispatch.py:4356-4491).
+ */
+int trnblas_hip_mp2_energy(int64_t ic, int64_t nocc, int64_t nvir, const float* T_flat,
+                           int64_t ldt, const float* eps_occ_chunk, const float* eps_occ_full,
+                           const float* eps_vir, double* out_pairs, void* stream);
+
+/*
+ * Ozaki split of a finite fp64 matrix into `slices` int8 digits (per row or
+ * per column), as trnblas/ozaki.py:123-219 `split` (digit_0 = rint(x 2^(6-e)),
+ * digit_s = rint(2^7 * remainder), |digit| <= 64, e = frexp exponent of the
+ * row / column maximum), with native fp64 arithmetic. Replaces
+ * torch.ops.trnblas.ozaki_emax / ozaki_emax_col / ozaki_split /
+ * ozaki_split_col (trnblas/nki/_native.py:77-121; kernels
+ * dispatch.py:3994-4354), which derive the same digits from raw bits
+ * because Trainium has no fp64.
+ *
+ * X: R x C fp64, element (r, c) at X[r*ldx + c].
+ * per_row != 0: one exponent per row (the A operand); digits are written as
+ *   digits[s*ld_slice + r*ld_digit + c] (K = C contiguous).
+ * per_row == 0: one exponent per column (the B operand); digits are written
+ *   transposed, digits[s*ld_slice + c*ld_digit + r] (K = R contiguous).
+ * The digit buffer must be zero beyond the matrix (the caller pads to the
+ * kernel's tile; entries beyond R x C are not written). exps (device int32,
+ * R or C entries) receives e. scratch: device int32[2] (scale-mode flag and
+ * non-finite flag). Returns TRNBLAS_OK; a non-finite X is reported through
+ * scratch[1] != 0 (checked by the caller after synchronising), the digits
+ * are then undefined.
+ */
+int trnblas_hip_ozaki_split(int per_row, int64_t R, int64_t C, const double* X, int64_t ldx,
+                            int slices, int8_t* digits, int64_t ld_digit, int64_t ld_slice,
+                            int32_t* exps, int32_t* scratch, void* stream);
+
+/*
+ * Ozaki slice GEMM with fused recombination:
+ *   C[m][n] = sum over K blocks of (hi + lo) * 2^(eA[m] + eB[n] + off),
+ * where (hi, lo) is the fp32 TwoSum chain of trnblas/ozaki.py:358-415
+ * (`schedule`, `_two_sum32`, `reference_from_digits`) over exact int32
+ * group sums of int8 digit products (int8 MFMA). With mode 0 the result
+ * equals `ozaki.reference_gemm` bit for bit (same groups, same TwoSum order,
+ * same combine, ozaki.py:418-455). Mode 1 (fast) accumulates each diagonal
+ * of slice pairs exactly in int32 and recombines in fp64 (error within the
+ * same bound, not bitwise).
+ *
+ * dA: digits (slices, >= M, Kp) with dA[s*lda_slice + m*lda + k];
+ * dB: digits (slices, >= N, Kp) with dB[s*ldb_slice + n*ldb + k]; both K
+ * contiguous, zero beyond M / N / K. Kp is K padded to 128. kb: K block
+ * (a multiple of 128 dividing into Kp blocks, `ozaki.plan`), blocks summed
+ * in fp64 in order. C element (m, n) at C[m*ldc_m + n*ldc_n] (ldc_m, ldc_n
+ * let the caller write C^T for the narrow-N swap of `ozaki.run`).
+ * Replaces torch.ops.trnblas.ozaki_gemm (trnblas/nki/_native.py:77-85;
+ * kernel dispatch.py:3887-3918) and the host `combine`.
+ */
+int trnblas_hip_ozaki_gemm(int mode, int slices, int64_t M, int64_t N, int64_t Kp,
+                           int64_t kb, const int8_t* dA, int64_t lda, int64_t lda_slice,
+                           const int8_t* dB, int64_t ldb, int64_t ldb_slice, const int32_t* eA,
+                           const int32_t* eB, double* C, int64_t ldc_m, int64_t ldc_n,
+                           void* stream);
+
+/*
+ * Raw (hi, lo) output of the Ozaki slice GEMM, mode 0, for one K block:
+ * hilo[0][m][n] = hi, hilo[1][m][n] = lo (fp32, row-major M x N each,
+ * leading dimension ldh). The `torch.ops.trnblas.ozaki_gemm` surface
+ * (trnblas/nki/_native.py:77-85: (k, Kp, Mp) x (k, Kp, N) -> (2, Mp, N)).
+ */
+int trnblas_hip_ozaki_hilo(int slices, int64_t M, int64_t N, int64_t Kp, const int8_t* dA,
+                           int64_t lda, int64_t lda_slice, const int8_t* dB, int64_t ldb,
+                           int64_t ldb_slice, float* hilo, int64_t ldh, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TRNBLAS_HIP_H */

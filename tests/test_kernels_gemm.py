@@ -1,0 +1,98 @@
+"""GPU parity of the HIP GEMM / SYRK kernels against an fp64 torch reference
+(the componentwise gate of trnblas's north star: |C - C_ref| <= 1e-6 (|A||B|)ij
+for fp32), through the C ABI (trnblas_amd.hip.kernels)."""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref(A, B, alpha, beta, C):
+    R = alpha * (A.double() @ B.double())
+    if C is not None and beta != 0:
+        R = R + beta * C.double()
+    return R
+
+
+def _cw_err(D, A, B, alpha, beta, C):
+    den = abs(alpha) * (A.double().abs() @ B.double().abs())
+    if C is not None and beta != 0:
+        den = den + abs(beta) * C.double().abs()
+    den = torch.where(den > 0, den, torch.ones_like(den))
+    return ((D.double() - _ref(A, B, alpha, beta, C)).abs() / den).max().item()
+
+
+@pytest.mark.parametrize(
+    "M,N,K",
+    [(128, 128, 16), (256, 384, 512), (1, 1, 1), (37, 53, 71), (130, 257, 1000), (64, 200, 3)],
+)
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_gemm_fp32_layouts(dev, M, N, K, ta, tb):
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(M * 7 + N * 3 + K)
+    A0 = torch.randn((K, M) if ta else (M, K), generator=g)
+    B0 = torch.randn((N, K) if tb else (K, N), generator=g)
+    C = torch.randn(M, N, generator=g)
+    A = (A0.mT if ta else A0).to(dev)
+    B = (B0.mT if tb else B0).to(dev)
+    D = kernels.gemm(A, B, 1.0, 0.5, C.to(dev))
+    torch.cuda.synchronize()
+    err = _cw_err(D.cpu(), A.cpu(), B.cpu(), 1.0, 0.5, C)
+    assert err <= 1e-6, err
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2e-2), (torch.float16, 3e-3)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_gemm_16bit(dev, dtype, tol, ta, tb):
+    from trnblas_amd.hip import kernels
+
+    M, N, K = 200, 136, 300
+    g = torch.Generator().manual_seed(1)
+    A0 = torch.randn((K, M) if ta else (M, K), generator=g).to(dtype)
+    B0 = torch.randn((N, K) if tb else (K, N), generator=g).to(dtype)
+    A = (A0.mT if ta else A0).to(dev)
+    B = (B0.mT if tb else B0).to(dev)
+    D = kernels.gemm(A, B, 2.0)
+    torch.cuda.synchronize()
+    assert D.dtype == dtype
+    ref = 2.0 * (A.cpu().double() @ B.cpu().double())
+    den = 2.0 * (A.cpu().double().abs() @ B.cpu().double().abs())
+    assert ((D.cpu().double() - ref).abs() / den).max().item() <= tol
+
+
+def test_gemm_batched_broadcast(dev):
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(2)
+    A = torch.randn(5, 70, 90, generator=g)
+    B = torch.randn(1, 90, 33, generator=g)
+    C = torch.randn(70, 33, generator=g)
+    D = kernels.gemm(A.to(dev), B.to(dev), 1.5, -0.25, C.to(dev))
+    torch.cuda.synchronize()
+    ref = 1.5 * (A.double() @ B.double()) - 0.25 * C.double()
+    assert (D.cpu().double() - ref).abs().max().item() < 1e-3
+
+
+@pytest.mark.parametrize("n,k", [(256, 128), (300, 77), (1, 5), (129, 1000)])
+@pytest.mark.parametrize("trans", [False, True])
+@pytest.mark.parametrize("uplo", ["lower", "upper"])
+def test_syrk_triangle(dev, n, k, trans, uplo):
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(n + k)
+    A = torch.randn((k, n) if trans else (n, k), generator=g)
+    X = torch.randn(n, n, generator=g)
+    D = kernels.syrk(A.to(dev), 1.0, 0.5, X.to(dev), trans=trans, uplo=uplo)
+    torch.cuda.synchronize()
+    D = D.cpu()
+    assert torch.equal(D, D.T)
+    opA = A.T if trans else A
+    Cs = torch.tril(X) + torch.tril(X, -1).T if uplo == "lower" else torch.triu(X) + torch.triu(X, 1).T
+    ref = opA.double() @ opA.double().T + 0.5 * Cs.double()
+    den = opA.double().abs() @ opA.double().abs().T + 0.5 * Cs.double().abs()
+    # SYRK diagonals are sums of k positive terms: fp32 accumulation error
+    # grows like sqrt(k) u there (probabilistic bound, u = 2^-24).
+    tol = max(1e-6, 2 * k**0.5 * 2.0**-24)
+    assert ((D.double() - ref).abs() / den).max().item() <= tol

@@ -1,0 +1,62 @@
+// Shared helpers of the gfx950 op library: error reporting, MFMA vector types,
+// XCD-aware block remapping.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/trnblas_hip.h"
+
+namespace trnblas {
+
+// Thread-local last-error message (trnblas_hip_last_error).
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define TRNBLAS_CHECK_ARG(cond, ...)           \
+  do {                                         \
+    if (!(cond)) {                             \
+      ::trnblas::set_error(__VA_ARGS__);       \
+      return TRNBLAS_E_ARG;                    \
+    }                                          \
+  } while (0)
+
+// After a launch: map hipGetLastError to TRNBLAS_E_LAUNCH.
+int check_launch(const char* what);
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// MI355X: 256 CUs in 8 XCDs. Workgroups are handed to the XCDs round-robin
+// (workgroup b runs on XCD b % 8), and each XCD has its own L2. This maps the
+// launch order to a tile order in which each XCD works on one contiguous
+// range of tiles, so tiles that share operand panels share an L2.
+constexpr int kNumXcd = 8;
+
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+  const int q = nblocks / kNumXcd, r = nblocks % kNumXcd;
+  const int x = bid % kNumXcd, i = bid / kNumXcd;
+  return x * q + (x < r ? x : r) + i;
+}
+
+// Grouped tile order: `group` consecutive tile rows are walked column by
+// column, so a band of A panels stays hot while B panels stream.
+__device__ __forceinline__ void grouped_tile(int t, int ntm, int ntn, int group, int& tm,
+                                             int& tn) {
+  const int per_group = group * ntn;
+  const int g = t / per_group;
+  const int first = g * group;
+  const int gs = (ntm - first) < group ? (ntm - first) : group;
+  const int r = t - g * per_group;
+  tm = first + r % gs;
+  tn = r / gs;
+}
+
+}  // namespace trnblas

@@ -1,0 +1,462 @@
+// Level-3 GEMM and SYRK for gfx950 on MFMA: fp32 (v_mfma_f32_32x32x2_f32) and
+// bf16 / fp16 (v_mfma_f32_32x32x16_{bf16,f16}, fp32 accumulate).
+//
+// Semantics follow trnblas/level3.py:69-134 (`gemm`, `batched_gemm`:
+// D = alpha op(A) op(B) + beta C into a fresh output, C never written) and
+// :243-302 (`syrk`: full symmetric result from the `uplo` triangle of C).
+// The kernels are written for CDNA4, not translated from the reference's NKI
+// tiling (trnblas/nki/dispatch.py:3324-3760, :4493-4544):
+//  * a 256-thread workgroup (4 wave64s) owns a 128x128 tile of D; each wave a
+//    64x64 sub-tile as 2x2 MFMA 32x32 blocks with the accumulators in
+//    AGPR/VGPRs;
+//  * operand panels are staged in LDS, double buffered: the global loads of
+//    k-tile t+1 are in flight while the MFMAs of k-tile t run, one barrier
+//    per k-tile;
+//  * an operand whose K dimension is contiguous in HBM is kept K-contiguous
+//    in LDS (rows padded by 16 bytes, so each 16-byte fragment read is
+//    bank-conflict free); one whose M / N dimension is contiguous (a
+//    transposed operand: transA / transB, the C1 `Aᵀ B`) is kept that way and
+//    read a column at a time — no transposed copy is ever made in HBM;
+//  * the K order inside an 8-wide (fp32) / 16-wide (16-bit) chunk is permuted
+//    the same way for both operands (lane half h takes k = h*EV .. h*EV+EV-1),
+//    so a fragment is one 16-byte LDS read;
+//  * ragged M / N / K edges are zero-filled at load and masked at store;
+//  * the alpha / beta epilogue is fused into the store;
+//  * SYRK launches only the lower-triangle tiles (n(n+1)/2 of them for n
+//    tiles) and writes each value to D[i][j] and D[j][i];
+//  * the tile walk is XCD-aware: each of the 8 XCDs (own L2) walks a
+//    contiguous range of tiles in grouped order.
+#include "common.hpp"
+
+namespace trnblas {
+
+struct GemmArgs {
+  int M, N, K;
+  float alpha, beta;
+  const void* A;
+  int64_t lda, sA;
+  const void* B;
+  int64_t ldb, sB;
+  const void* C;
+  int64_t ldc, sC;
+  void* D;
+  int64_t ldd, sD;
+  int batch;
+  int tiles_m, tiles_n;
+  int uplo;  // SYRK: 0 = lower triangle of C referenced, 1 = upper
+};
+
+template <typename T>
+struct Zero {
+  __device__ static T v() { return T(0.0f); }
+};
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T x) {
+  return (float)x;
+}
+
+// Buffer-resource loads: an offset at or beyond num_records reads zero with
+// no memory access, so ragged edges are masked by a select on the offset
+// (no branches around loads).
+constexpr uint32_t kOob = 0x80000000u;  // offsets >= this read as zero
+constexpr uint32_t kRecords = 0x7ffffff0u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)kRecords,
+                                           0x00020000);
+}
+
+// One 16-byte group of EV consecutive elements at byte offset `off` from the
+// resource base. VEC: all EV elements are valid or none is (`ok`); otherwise
+// `nvalid` (0..EV) leading elements are valid.
+template <typename T, bool VEC>
+__device__ __forceinline__ i32x4 load_group(__amdgpu_buffer_rsrc_t rs, uint32_t off, bool ok,
+                                            int nvalid) {
+  constexpr int EV = 16 / sizeof(T);
+  if (VEC) return __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? off : kOob, 0, 0);
+  union {
+    i32x4 v;
+    T e[EV];
+    unsigned short h[EV];
+    int w[EV];
+  } u;
+#pragma unroll
+  for (int e = 0; e < EV; ++e) {
+    const uint32_t o = (ok && e < nvalid) ? off + e * (uint32_t)sizeof(T) : kOob;
+    if (sizeof(T) == 4)
+      u.w[e] = __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, 0);
+    else
+      u.h[e] = __builtin_amdgcn_raw_buffer_load_b16(rs, o, 0, 0);
+  }
+  return u.v;
+}
+
+// acc += a * b over one fragment: 4 fp32 MFMAs (one per element) or one
+// 16-bit MFMA.
+__device__ __forceinline__ void mma_frag(f32x16& acc, const i32x4& a, const i32x4& b, float*) {
+  const f32x4 av = __builtin_bit_cast(f32x4, a);
+  const f32x4 bv = __builtin_bit_cast(f32x4, b);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[0], bv[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[1], bv[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[2], bv[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[3], bv[3], acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma_frag(f32x16& acc, const i32x4& a, const i32x4& b, __bf16*) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma_frag(f32x16& acc, const i32x4& a, const i32x4& b,
+                                         _Float16*) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                               __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
+}
+
+// Fragment of 32 rows (row index `row` for this lane) at k offset `kk`:
+// from a K-contiguous LDS panel (one 16-byte read) or an M/N-contiguous one
+// (EV column reads).
+template <typename T, bool KC, int ROWS, int BK>
+__device__ __forceinline__ i32x4 read_frag(const T* buf, int row, int kk) {
+  constexpr int EV = 16 / sizeof(T);
+  if (KC) {
+    return *reinterpret_cast<const i32x4*>(buf + row * (BK + EV) + kk);
+  } else {
+    union {
+      i32x4 v;
+      T e[EV];
+    } u;
+#pragma unroll
+    for (int e = 0; e < EV; ++e) u.e[e] = buf[(kk + e) * (ROWS + EV) + row];
+    return u.v;
+  }
+}
+
+// Lower-triangle tile t -> (tm, tn), tm >= tn, row-major over the triangle.
+__device__ __forceinline__ void tri_tile(int t, int& tm, int& tn) {
+  int r = (int)((sqrtf(8.0f * (float)t + 1.0f) - 1.0f) * 0.5f);
+  while (r * (r + 1) / 2 > t) --r;
+  while ((r + 1) * (r + 2) / 2 <= t) ++r;
+  tm = r;
+  tn = t - r * (r + 1) / 2;
+}
+
+template <typename T, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, bool VEC,
+          bool SYRK>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1) void gemm_kernel(GemmArgs g) {
+  constexpr int EV = 16 / sizeof(T);
+  constexpr int NT = (BM / WM) * (BN / WN) * 64;
+  constexpr int WAVES_N = BN / WN;
+  constexpr int FM = WM / 32, FN = WN / 32;
+  constexpr int CH = 2 * EV;  // k per fragment read
+  static_assert(BK % CH == 0, "BK must be a multiple of the fragment k");
+  // LDS panels: [row][k] (K-contiguous) or [k][row], rows padded by EV.
+  constexpr int A_LC = AKC ? BK : BM, A_LR = AKC ? BM : BK;
+  constexpr int B_LC = BKC ? BK : BN, B_LR = BKC ? BN : BK;
+  constexpr int A_SZ = A_LR * (A_LC + EV), B_SZ = B_LR * (B_LC + EV);
+  constexpr int A_NV = A_LR * A_LC / EV / NT, B_NV = B_LR * B_LC / EV / NT;
+  static_assert(A_NV * EV * NT == A_LR * A_LC && B_NV * EV * NT == B_LR * B_LC, "tile split");
+  __shared__ __attribute__((aligned(16))) T lds[2 * (A_SZ + B_SZ)];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
+
+  int tm, tn;
+  if (SYRK) {
+    tri_tile(blockIdx.x, tm, tn);
+  } else {
+    const int t = xcd_remap(blockIdx.x, gridDim.x);
+    grouped_tile(t, g.tiles_m, g.tiles_n, 8, tm, tn);
+  }
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int M = g.M, N = g.N, K = g.K;
+  const int nk = (K + BK - 1) / BK;
+
+  for (int bat = blockIdx.y; bat < g.batch; bat += gridDim.y) {
+    const T* A = static_cast<const T*>(g.A) + bat * g.sA;
+    const T* B = static_cast<const T*>(g.B) + bat * g.sB;
+
+    // Per-thread offsets inside a k-tile are loop invariant; the tile corner
+    // moves with k0 (scalar base of the buffer resource).
+    i32x4 ra[A_NV], rb[B_NV];
+    auto load_tiles = [&](int k0) {
+      const __amdgpu_buffer_rsrc_t rsa =
+          make_rsrc(AKC ? A + (int64_t)m0 * g.lda + k0 : A + (int64_t)k0 * g.lda + m0);
+      const __amdgpu_buffer_rsrc_t rsb =
+          make_rsrc(BKC ? B + (int64_t)n0 * g.ldb + k0 : B + (int64_t)k0 * g.ldb + n0);
+#pragma unroll
+      for (int i = 0; i < A_NV; ++i) {
+        const int idx = tid + i * NT, r = idx / (A_LC / EV), c = (idx % (A_LC / EV)) * EV;
+        const uint32_t off = (uint32_t)((r * g.lda + c) * (int64_t)sizeof(T));
+        // AKC: rows are m, columns k. Otherwise rows are k, columns m.
+        const int rl = AKC ? M - m0 : K - k0, cl = AKC ? K - k0 : M - m0;
+        ra[i] = load_group<T, VEC>(rsa, off, r < rl && c < cl, cl - c);
+      }
+#pragma unroll
+      for (int i = 0; i < B_NV; ++i) {
+        const int idx = tid + i * NT, r = idx / (B_LC / EV), c = (idx % (B_LC / EV)) * EV;
+        const uint32_t off = (uint32_t)((r * g.ldb + c) * (int64_t)sizeof(T));
+        // BKC: rows are n, columns k. Otherwise rows are k, columns n.
+        const int rl = BKC ? N - n0 : K - k0, cl = BKC ? K - k0 : N - n0;
+        rb[i] = load_group<T, VEC>(rsb, off, r < rl && c < cl, cl - c);
+      }
+    };
+    auto store_tiles = [&](int buf) {
+      T* la = lds + buf * (A_SZ + B_SZ);
+      T* lb = la + A_SZ;
+#pragma unroll
+      for (int i = 0; i < A_NV; ++i) {
+        const int idx = tid + i * NT, r = idx / (A_LC / EV), c = (idx % (A_LC / EV)) * EV;
+        *reinterpret_cast<i32x4*>(la + r * (A_LC + EV) + c) = ra[i];
+      }
+#pragma unroll
+      for (int i = 0; i < B_NV; ++i) {
+        const int idx = tid + i * NT, r = idx / (B_LC / EV), c = (idx % (B_LC / EV)) * EV;
+        *reinterpret_cast<i32x4*>(lb + r * (B_LC + EV) + c) = rb[i];
+      }
+    };
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    if (nk > 0) {
+      load_tiles(0);
+      store_tiles(0);
+      __syncthreads();
+    }
+    for (int kt = 0; kt < nk; ++kt) {
+      const bool more = kt + 1 < nk;
+      if (more) load_tiles((kt + 1) * BK);
+      const T* la = lds + (kt & 1) * (A_SZ + B_SZ);
+      const T* lb = la + A_SZ;
+#pragma unroll
+      for (int c = 0; c < BK / CH; ++c) {
+        const int kk = c * CH + (lane >> 5) * EV;
+        i32x4 fa[FM], fb[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          fa[i] = read_frag<T, AKC, BM, BK>(la, wm0 + i * 32 + (lane & 31), kk);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          fb[j] = read_frag<T, BKC, BN, BK>(lb, wn0 + j * 32 + (lane & 31), kk);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) mma_frag(acc[i][j], fa[i], fb[j], (T*)nullptr);
+      }
+      if (more) store_tiles((kt + 1) & 1);
+      __syncthreads();
+    }
+
+    // Epilogue: D = alpha * acc + beta * C (C not read when beta == 0). Lane
+    // (l) of an MFMA 32x32 block holds column l % 32 and rows
+    // 8 (r / 4) + 4 (l / 32) + r % 4 of its 16 registers r.
+    const T* C = static_cast<const T*>(g.C) + (g.C ? bat * g.sC : 0);
+    T* D = static_cast<T*>(g.D) + bat * g.sD;
+    const bool add = g.beta != 0.0f;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int mb = m0 + wm0 + i * 32 + (lane >> 5) * 4;
+        const int n = n0 + wn0 + j * 32 + (lane & 31);
+        T* dcol = D + n;
+        const T* ccol = C + n;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = mb + (r >> 2) * 8 + (r & 3);
+          if (SYRK) {
+            if (m < M && n <= m) {
+              float v = g.alpha * acc[i][j][r];
+              if (add) {
+                const int64_t ci = g.uplo ? (int64_t)n * g.ldc + m : (int64_t)m * g.ldc + n;
+                v += g.beta * to_f32(C[ci]);
+              }
+              const T o = (T)v;
+              dcol[(int64_t)m * g.ldd] = o;
+              D[(int64_t)n * g.ldd + m] = o;
+            }
+          } else if (m < M && n < N) {
+            float v = g.alpha * acc[i][j][r];
+            if (add) v += g.beta * to_f32(ccol[(int64_t)m * g.ldc]);
+            dcol[(int64_t)m * g.ldd] = (T)v;
+          }
+        }
+      }
+  }
+}
+
+template <typename T>
+struct Cfg {
+  static constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
+  static constexpr int BK = sizeof(T) == 4 ? 16 : 32;
+  static constexpr int NT = (BM / WM) * (BN / WN) * 64;
+};
+
+template <typename T, bool AKC, bool BKC, bool VEC, bool SYRK>
+static int launch_t(const GemmArgs& g, int ntiles, hipStream_t s) {
+  using C = Cfg<T>;
+  dim3 grid(ntiles, g.batch < 65535 ? g.batch : 65535);
+  hipLaunchKernelGGL((gemm_kernel<T, C::BM, C::BN, C::BK, C::WM, C::WN, AKC, BKC, VEC, SYRK>),
+                     grid, dim3(C::NT), 0, s, g);
+  return check_launch(SYRK ? "trnblas_hip_syrk" : "trnblas_hip_gemm");
+}
+
+template <typename T, bool SYRK>
+static int launch_dtype(const GemmArgs& g, bool akc, bool bkc, bool vec, int ntiles,
+                        hipStream_t s) {
+#define TRNBLAS_L(a, b, v)                                 \
+  if (akc == a && bkc == b && vec == v)                    \
+    return launch_t<T, a, b, v, SYRK>(g, ntiles, s);
+  TRNBLAS_L(true, true, true)
+  TRNBLAS_L(true, true, false)
+  TRNBLAS_L(false, false, true)
+  TRNBLAS_L(false, false, false)
+  if (!SYRK) {
+    TRNBLAS_L(true, false, true)
+    TRNBLAS_L(true, false, false)
+    TRNBLAS_L(false, true, true)
+    TRNBLAS_L(false, true, false)
+  }
+#undef TRNBLAS_L
+  set_error("gemm: unsupported layout combination");
+  return TRNBLAS_E_ARG;
+}
+
+static int elem_size(int dtype) { return dtype == TRNBLAS_F32 ? 4 : 2; }
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <bool SYRK>
+static int dispatch(int dtype, const GemmArgs& g, bool akc, bool bkc, int ntiles,
+                    hipStream_t s) {
+  const int ev = 16 / elem_size(dtype);
+  // Buffer offsets inside one k-tile panel are 32-bit: the panel (tile rows
+  // times the leading dimension) must stay below 2 GiB.
+  const int64_t es = elem_size(dtype), bk = es == 4 ? 16 : 32;
+  const int64_t span_a = (akc ? 128 : bk) * g.lda * es, span_b = (bkc ? 128 : bk) * g.ldb * es;
+  if (span_a >= (int64_t)kRecords - 64 || span_b >= (int64_t)kRecords - 64) {
+    set_error("gemm: leading dimension too large for 32-bit panel offsets (lda %lld, ldb %lld)",
+              (long long)g.lda, (long long)g.ldb);
+    return TRNBLAS_E_ARG;
+  }
+  // VEC: 16-byte aligned groups that are wholly inside or outside the matrix
+  // (the contiguous extent of each operand is a multiple of EV).
+  const int a_ext = akc ? g.K : g.M, b_ext = bkc ? g.K : g.N;
+  const bool vec = aligned16(g.A) && aligned16(g.B) && g.lda % ev == 0 && g.ldb % ev == 0 &&
+                   g.sA % ev == 0 && g.sB % ev == 0 && a_ext % ev == 0 && b_ext % ev == 0;
+  switch (dtype) {
+    case TRNBLAS_F32:
+      return launch_dtype<float, SYRK>(g, akc, bkc, vec, ntiles, s);
+    case TRNBLAS_BF16:
+      return launch_dtype<__bf16, SYRK>(g, akc, bkc, vec, ntiles, s);
+    case TRNBLAS_F16:
+      return launch_dtype<_Float16, SYRK>(g, akc, bkc, vec, ntiles, s);
+  }
+  set_error("unsupported dtype %d", dtype);
+  return TRNBLAS_E_ARG;
+}
+
+}  // namespace trnblas
+
+using namespace trnblas;
+
+extern "C" int trnblas_hip_gemm(int dtype, int transA, int transB, int64_t M, int64_t N,
+                                int64_t K, double alpha, const void* A, int64_t lda,
+                                int64_t strideA, const void* B, int64_t ldb, int64_t strideB,
+                                double beta, const void* C, int64_t ldc, int64_t strideC,
+                                void* D, int64_t ldd, int64_t strideD, int64_t batch,
+                                void* stream) {
+  clear_error();
+  TRNBLAS_CHECK_ARG(dtype == TRNBLAS_F32 || dtype == TRNBLAS_BF16 || dtype == TRNBLAS_F16,
+                    "gemm: dtype %d not supported", dtype);
+  TRNBLAS_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "gemm: negative size");
+  TRNBLAS_CHECK_ARG(M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31),
+                    "gemm: dimension >= 2^31");
+  if (M == 0 || N == 0 || batch == 0) return TRNBLAS_OK;
+  TRNBLAS_CHECK_ARG(D != nullptr, "gemm: D is NULL");
+  TRNBLAS_CHECK_ARG(ldd >= N, "gemm: ldd %lld < N %lld", (long long)ldd, (long long)N);
+  if (K > 0) {
+    TRNBLAS_CHECK_ARG(A != nullptr && B != nullptr, "gemm: A or B is NULL");
+    TRNBLAS_CHECK_ARG(lda >= (transA ? M : K), "gemm: lda too small");
+    TRNBLAS_CHECK_ARG(ldb >= (transB ? K : N), "gemm: ldb too small");
+  }
+  if (beta != 0.0) {
+    TRNBLAS_CHECK_ARG(C != nullptr, "gemm: beta != 0 needs C");
+    TRNBLAS_CHECK_ARG(ldc >= N, "gemm: ldc too small");
+  }
+  GemmArgs g;
+  g.M = (int)M;
+  g.N = (int)N;
+  g.K = (int)K;
+  g.alpha = (float)alpha;
+  g.beta = (float)beta;
+  g.A = A;
+  g.lda = lda;
+  g.sA = strideA;
+  g.B = B;
+  g.ldb = ldb;
+  g.sB = strideB;
+  g.C = beta != 0.0 ? C : nullptr;
+  g.ldc = ldc;
+  g.sC = strideC;
+  g.D = D;
+  g.ldd = ldd;
+  g.sD = strideD;
+  g.batch = (int)batch;
+  g.uplo = 0;
+  const int bm = 128, bn = 128;
+  g.tiles_m = (int)((M + bm - 1) / bm);
+  g.tiles_n = (int)((N + bn - 1) / bn);
+  const int64_t ntiles = (int64_t)g.tiles_m * g.tiles_n;
+  TRNBLAS_CHECK_ARG(ntiles < (1ll << 31), "gemm: too many tiles");
+  // A is K-contiguous unless transposed; B is K-contiguous only when transposed.
+  return dispatch<false>(dtype, g, !transA, transB != 0, (int)ntiles, (hipStream_t)stream);
+}
+
+extern "C" int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64_t K,
+                                double alpha, const void* A, int64_t lda, double beta,
+                                const void* C, int64_t ldc, void* D, int64_t ldd, void* stream) {
+  clear_error();
+  TRNBLAS_CHECK_ARG(dtype == TRNBLAS_F32 || dtype == TRNBLAS_BF16 || dtype == TRNBLAS_F16,
+                    "syrk: dtype %d not supported", dtype);
+  TRNBLAS_CHECK_ARG(N >= 0 && K >= 0, "syrk: negative size");
+  TRNBLAS_CHECK_ARG(N < (1ll << 31) && K < (1ll << 31), "syrk: dimension >= 2^31");
+  if (N == 0) return TRNBLAS_OK;
+  TRNBLAS_CHECK_ARG(D != nullptr && ldd >= N, "syrk: bad D / ldd");
+  if (K > 0) {
+    TRNBLAS_CHECK_ARG(A != nullptr, "syrk: A is NULL");
+    TRNBLAS_CHECK_ARG(lda >= (trans ? N : K), "syrk: lda too small");
+  }
+  if (beta != 0.0) TRNBLAS_CHECK_ARG(C != nullptr && ldc >= N, "syrk: bad C / ldc");
+  GemmArgs g;
+  g.M = (int)N;
+  g.N = (int)N;
+  g.K = (int)K;
+  g.alpha = (float)alpha;
+  g.beta = (float)beta;
+  g.A = A;
+  g.lda = lda;
+  g.sA = 0;
+  g.B = A;  // B(k, n) = op(A)[n][k]
+  g.ldb = lda;
+  g.sB = 0;
+  g.C = beta != 0.0 ? C : nullptr;
+  g.ldc = ldc;
+  g.sC = 0;
+  g.D = D;
+  g.ldd = ldd;
+  g.sD = 0;
+  g.batch = 1;
+  g.uplo = uplo ? 1 : 0;
+  const int t = (int)((N + 127) / 128);
+  g.tiles_m = g.tiles_n = t;
+  const int64_t ntri = (int64_t)t * (t + 1) / 2;
+  // trans == 0: op(A) = A (N x K, K-contiguous) and B(k, n) = A[n][k] (K-contiguous).
+  // trans != 0: op(A) = A^T with A K x N (N-contiguous), B(k, n) = A[k][n].
+  return dispatch<true>(dtype, g, !trans, !trans, (int)ntri, (hipStream_t)stream);
+}

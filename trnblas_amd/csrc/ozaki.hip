@@ -1,0 +1,622 @@
+// Ozaki fp64-class GEMM on gfx950: native-fp64 digit split + int8 MFMA slice
+// products with exact int32 groups + fp32 TwoSum + fused fp64 recombination.
+//
+// Arithmetic contract (trnblas/ozaki.py): digits as `split` (:123-219), the
+// group cut and order of `schedule` / `diag_groups` (:337-365), the TwoSum of
+// `_two_sum32` (:378-386) as folded by `reference_from_digits` (:389-415), and
+// `combine` (:418-455). Mode 0 reproduces `reference_gemm` bit for bit.
+//
+// Design for CDNA4 (not a translation of the NKI kernels,
+// trnblas/nki/dispatch.py:3768-4354, which emulate fp64 with bit fields and
+// run bf16 matmuls on the Tensor Engine):
+//  * the split is plain fp64 (rint chain), one pass per operand, writing
+//    int8 digits K-contiguous for both operands (B is transposed on the fly
+//    through LDS), so both MFMA operands are 16-byte K-contiguous loads;
+//  * slice products run on v_mfma_i32_32x32x32_i8 with int32 accumulation:
+//    a group of at most 4096 terms of |d| <= 64 digits sums to at most 2^24,
+//    exact in int32 and in fp32;
+//  * a 256-thread workgroup owns a 128x128 output tile; per lane it keeps the
+//    int32 group accumulators and the fp32 (hi, lo) pairs of its 64 outputs
+//    in registers for the whole schedule; the operand tiles are staged in
+//    LDS, double buffered, and the k-step pipeline runs straight across
+//    group and slice-pair boundaries;
+//  * the fp64 recombination (hi + lo) 2^(eA + eB + off) is fused into the
+//    store (no (hi, lo) round trip through HBM), including the fp64 sum of K
+//    blocks for very long K (`plan`'s K blocking).
+#include "common.hpp"
+
+namespace trnblas {
+
+constexpr int kSliceBits = 7;
+constexpr int kTileK = 128;     // K tile of the schedule
+constexpr int kGroupTiles = 32;  // 4096 terms
+constexpr int kNonFinite = (int)0x80000000;
+
+// ---------------------------------------------------------------------------
+// split
+
+// frexp exponent of |x| (x finite, >= 0): x < 2^e, 0 -> 0.
+__device__ __forceinline__ int frexp_exp(double x) {
+  int e = 0;
+  (void)frexp(x, &e);
+  return x == 0.0 ? 0 : e;
+}
+
+// Exponent of the largest |x| of each row (per_row) or column; non-finite
+// rows / columns get kNonFinite.
+__global__ __launch_bounds__(256) void oz_emax_row_kernel(const double* X, int64_t ldx, int R,
+                                                          int C, int32_t* exps) {
+  __shared__ double smax[4];
+  __shared__ int sbad[4];
+  const int r = blockIdx.x;
+  const double* row = X + (int64_t)r * ldx;
+  double m = 0.0;
+  int bad = 0;
+  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    const double v = fabs(row[c]);
+    bad |= !isfinite(v);
+    m = v > m ? v : m;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const double o = __shfl_xor(m, off, 64);
+    m = o > m ? o : m;
+    bad |= __shfl_xor(bad, off, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    smax[threadIdx.x >> 6] = m;
+    sbad[threadIdx.x >> 6] = bad;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double mm = 0.0;
+    int bb = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
+      mm = smax[w] > mm ? smax[w] : mm;
+      bb |= sbad[w];
+    }
+    exps[r] = bb ? kNonFinite : frexp_exp(mm);
+  }
+}
+
+// Column maxima: a 64-column strip per workgroup, 4 row lanes per column.
+__global__ __launch_bounds__(256) void oz_emax_col_kernel(const double* X, int64_t ldx, int R,
+                                                          int C, int32_t* exps) {
+  __shared__ double smax[4][64];
+  __shared__ int sbad[4][64];
+  const int cx = threadIdx.x & 63, ry = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + cx;
+  double m = 0.0;
+  int bad = 0;
+  if (c < C) {
+    for (int r = ry; r < R; r += 4) {
+      const double v = fabs(X[(int64_t)r * ldx + c]);
+      bad |= !isfinite(v);
+      m = v > m ? v : m;
+    }
+  }
+  smax[ry][cx] = m;
+  sbad[ry][cx] = bad;
+  __syncthreads();
+  if (ry == 0 && c < C) {
+    for (int k = 1; k < 4; ++k) {
+      m = smax[k][cx] > m ? smax[k][cx] : m;
+      bad |= sbad[k][cx];
+    }
+    exps[c] = bad ? kNonFinite : frexp_exp(m);
+  }
+}
+
+// flags[0] = 1 when some shift 6 - e is not a normal exponent (the global
+// two-factor scaling of ozaki.py:185-188); flags[1] = 1 on non-finite input.
+__global__ __launch_bounds__(1024) void oz_flags_kernel(const int32_t* exps, int n,
+                                                        int32_t* flags) {
+  __shared__ int s2[16], sn[16];
+  int two = 0, nf = 0;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int e = exps[i];
+    if (e == kNonFinite) {
+      nf = 1;
+    } else {
+      const int sh = (kSliceBits - 1) - e;
+      two |= (sh > 1023 || sh < -1022);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    two |= __shfl_xor(two, off, 64);
+    nf |= __shfl_xor(nf, off, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    s2[threadIdx.x >> 6] = two;
+    sn[threadIdx.x >> 6] = nf;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int a = 0, b = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
+      a |= s2[w];
+      b |= sn[w];
+    }
+    flags[0] = a;
+    flags[1] = b;
+  }
+}
+
+__device__ __forceinline__ double pow2(int n) {  // n a normal exponent
+  return __longlong_as_double((long long)(n + 1023) << 52);
+}
+
+__device__ __forceinline__ int floor_div2(int v) { return v >= 0 ? v / 2 : -((1 - v) / 2); }
+
+// The k digits of x for exponent e (ozaki.py:191-217), as int8 into d[].
+template <int KMAX>
+__device__ __forceinline__ void digits_of(double x, int e, int k, bool two, int8_t* d) {
+  const int sh = (kSliceBits - 1) - e;
+  double rem;
+  if (two) {
+    const int h = floor_div2(sh);
+    rem = x * pow2(h);
+    rem = rem * pow2(sh - h);
+  } else {
+    rem = x * pow2(sh);
+  }
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) {
+    if (s < k) {
+      if (s) rem = rem * 128.0;
+      const double q = rint(rem);
+      if (s + 1 < k) rem = rem - q;
+      d[s] = (int8_t)(int)q;
+    }
+  }
+}
+
+// Row split: X (R, C) row-major, one exponent per row, digits
+// out[s*ld_slice + r*ld_digit + c]. Each thread: 16 consecutive columns.
+__global__ __launch_bounds__(256) void oz_digits_row_kernel(const double* X, int64_t ldx, int R,
+                                                            int C, int k, const int32_t* exps,
+                                                            const int32_t* flags, int8_t* out,
+                                                            int64_t ld_digit, int64_t ld_slice) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int cg = (C + 15) / 16;
+  const int64_t r = gid / cg;
+  if (r >= R) return;
+  const int c0 = (int)(gid - r * cg) * 16;
+  const int e = exps[r];
+  if (e == kNonFinite) return;
+  const bool two = flags[0] != 0;
+  union {
+    int8_t b[16];
+    i32x4 v;
+  } u[12];
+  const double* src = X + r * ldx;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = c0 + i;
+    int8_t d[12];
+    const double x = c < C ? src[c] : 0.0;
+    digits_of<12>(x, e, k, two, d);
+#pragma unroll
+    for (int s = 0; s < 12; ++s) u[s].b[i] = s < k ? d[s] : 0;
+  }
+  const bool full = c0 + 16 <= C && (((uintptr_t)out + r * ld_digit + c0) & 15) == 0 &&
+                    (ld_slice & 15) == 0;
+  for (int s = 0; s < k; ++s) {
+    int8_t* dst = out + (int64_t)s * ld_slice + r * ld_digit + c0;
+    if (full) {
+      *reinterpret_cast<i32x4*>(dst) = u[s].v;
+    } else {
+      for (int i = 0; i < 16 && c0 + i < C; ++i) dst[i] = u[s].b[i];
+    }
+  }
+}
+
+// Column split, written transposed: X (R, C) row-major, one exponent per
+// column c, digits out[s*ld_slice + c*ld_digit + r] (R contiguous). 64 x 64
+// tiles through LDS: reads are coalesced along c, writes along r.
+__global__ __launch_bounds__(256) void oz_digits_col_kernel(const double* X, int64_t ldx, int R,
+                                                            int C, int k, const int32_t* exps,
+                                                            const int32_t* flags, int8_t* out,
+                                                            int64_t ld_digit, int64_t ld_slice) {
+  __shared__ __attribute__((aligned(16))) int8_t tile[12][64][64 + 16];
+  const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  const int cx = threadIdx.x & 63, ry = threadIdx.x >> 6;  // ry: 16-row group
+  const int c = c0 + cx;
+  const bool two = flags[0] != 0;
+  const int e = c < C ? exps[c] : 0;
+  const bool bad = e == kNonFinite;
+  union {
+    int8_t b[16];
+    i32x4 v;
+  } u[12];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = r0 + ry * 16 + i;
+    int8_t d[12];
+    const double x = (c < C && r < R && !bad) ? X[(int64_t)r * ldx + c] : 0.0;
+    digits_of<12>(x, bad ? 0 : e, k, two, d);
+#pragma unroll
+    for (int s = 0; s < 12; ++s) u[s].b[i] = s < k ? d[s] : 0;
+  }
+  for (int s = 0; s < k; ++s) *reinterpret_cast<i32x4*>(&tile[s][cx][ry * 16]) = u[s].v;
+  __syncthreads();
+  // write: thread -> (column cc = t / 4, 16-row chunk t % 4) per slice
+  const int cc = threadIdx.x >> 2, rq = (threadIdx.x & 3) * 16;
+  const int col = c0 + cc;
+  if (col >= C || (col < C && exps[col] == kNonFinite)) return;
+  for (int s = 0; s < k; ++s) {
+    int8_t* dst = out + (int64_t)s * ld_slice + (int64_t)col * ld_digit + r0 + rq;
+    const i32x4 v = *reinterpret_cast<const i32x4*>(&tile[s][cc][rq]);
+    const bool full = r0 + rq + 16 <= R && (((uintptr_t)dst) & 15) == 0;
+    if (full) {
+      *reinterpret_cast<i32x4*>(dst) = v;
+    } else {
+      union {
+        i32x4 v;
+        int8_t b[16];
+      } w;
+      w.v = v;
+      for (int i = 0; i < 16 && r0 + rq + i < R; ++i) dst[i] = w.b[i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// slice GEMM
+
+struct OzArgs {
+  int k;         // slices
+  int M, N;
+  int Kp, kb;    // padded K, K block (multiples of 128)
+  const int8_t* A;
+  int64_t lda, lda_s;
+  const int8_t* B;
+  int64_t ldb, ldb_s;
+  const int32_t* eA;
+  const int32_t* eB;
+  double* C;      // combine target (mode 0 / 1), or
+  float* hilo;    // raw (hi, lo) planes (hilo output)
+  int64_t ldc_m, ldc_n, ldh;
+  int tiles_m, tiles_n;
+};
+
+__device__ __forceinline__ void two_sum32(float& hi, float& lo, float p) {
+#pragma clang fp contract(off)
+  const float s = hi + p;
+  const float bb = s - hi;
+  const float t = s - bb;
+  const float e = (hi - t) + (p - bb);
+  hi = s;
+  lo = lo + e;
+}
+
+constexpr uint32_t kOzOob = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t oz_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7ffffff0,
+                                           0x00020000);
+}
+
+// (d, s, kstep) walk of the schedule: diagonals d = k-1 .. 0, pairs
+// s = 0 .. d (t = d - s), k-steps of BK bytes over the K block.
+struct OzStep {
+  int d, s, ks;
+};
+
+template <int BM, int BN, int BK, int OUT>  // OUT: 0 combine into C, 1 raw hilo
+__global__ __launch_bounds__(256) void oz_gemm_kernel(OzArgs g) {
+  constexpr int NT = 256;
+  constexpr int WM = BM / 2, WN = BN / 2;  // 2 x 2 waves
+  constexpr int FM = WM / 32, FN = WN / 32;
+  constexpr int LD = BK + 16;  // padded LDS row (bytes)
+  constexpr int A_SZ = BM * LD, B_SZ = BN * LD;
+  constexpr int NVA = BM * BK / 16 / NT, NVB = BN * BK / 16 / NT;
+  static_assert(NVA * 16 * NT == BM * BK && NVB * 16 * NT == BN * BK, "tile split");
+  constexpr int SUB = kTileK / BK;  // k-steps per 128-K tile
+  __shared__ __attribute__((aligned(16))) int8_t lds[2 * (A_SZ + B_SZ)];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  int tm, tn;
+  grouped_tile(t, g.tiles_m, g.tiles_n, 8, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int k = g.k;
+  const int nkb = g.Kp / g.kb;
+  const int kt = g.kb / kTileK;  // 128-tiles per slice in a K block
+  const int steps_per_pair = kt * SUB;
+  const int npairs = k * (k + 1) / 2;
+  const int total = npairs * steps_per_pair;
+  const int per = kt >= kGroupTiles ? 1 : kGroupTiles / kt;
+
+  i32x4 ra[NVA], rb[NVB];
+  int kbase = 0;
+  auto load = [&](const OzStep& st) {
+    const int tt = st.d - st.s;
+    const int64_t koff = kbase + (int64_t)st.ks * BK;
+    const __amdgpu_buffer_rsrc_t rsa = oz_rsrc(g.A + st.s * g.lda_s + (int64_t)m0 * g.lda + koff);
+    const __amdgpu_buffer_rsrc_t rsb = oz_rsrc(g.B + tt * g.ldb_s + (int64_t)n0 * g.ldb + koff);
+#pragma unroll
+    for (int i = 0; i < NVA; ++i) {
+      const int idx = tid + i * NT, r = idx / (BK / 16), c = (idx % (BK / 16)) * 16;
+      const uint32_t off = (uint32_t)(r * g.lda + c);
+      ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rsa, m0 + r < g.M ? off : kOzOob, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NVB; ++i) {
+      const int idx = tid + i * NT, r = idx / (BK / 16), c = (idx % (BK / 16)) * 16;
+      const uint32_t off = (uint32_t)(r * g.ldb + c);
+      rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rsb, n0 + r < g.N ? off : kOzOob, 0, 0);
+    }
+  };
+  auto store = [&](int buf) {
+    int8_t* la = lds + buf * (A_SZ + B_SZ);
+    int8_t* lb = la + A_SZ;
+#pragma unroll
+    for (int i = 0; i < NVA; ++i) {
+      const int idx = tid + i * NT, r = idx / (BK / 16), c = (idx % (BK / 16)) * 16;
+      *reinterpret_cast<i32x4*>(la + r * LD + c) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NVB; ++i) {
+      const int idx = tid + i * NT, r = idx / (BK / 16), c = (idx % (BK / 16)) * 16;
+      *reinterpret_cast<i32x4*>(lb + r * LD + c) = rb[i];
+    }
+  };
+  auto advance = [&](OzStep st) {
+    if (++st.ks == steps_per_pair) {
+      st.ks = 0;
+      if (++st.s > st.d) {
+        st.s = 0;
+        --st.d;
+      }
+    }
+    return st;
+  };
+  // True when the step just computed closes a group (ozaki.py:337-355).
+  auto group_end = [&](const OzStep& st) {
+    if (st.ks % SUB != SUB - 1) return false;
+    const int tile = st.ks / SUB;
+    if (kt >= kGroupTiles) return (tile + 1) % kGroupTiles == 0 || tile + 1 == kt;
+    return tile + 1 == kt && ((st.s + 1) % per == 0 || st.s == st.d);
+  };
+
+  for (int kbi = 0; kbi < nkb; ++kbi) {
+    kbase = kbi * g.kb;
+    i32x16 acc[FM][FN];
+    float hi[FM][FN][16], lo[FM][FN][16];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          acc[i][j][r] = 0;
+          hi[i][j][r] = 0.0f;
+          lo[i][j][r] = 0.0f;
+        }
+    OzStep cur{k - 1, 0, 0};
+    load(cur);
+    store(0);
+    __syncthreads();
+    for (int n = 0; n < total; ++n) {
+      const bool more = n + 1 < total;
+      const OzStep nxt = advance(cur);
+      if (more) load(nxt);
+      const int8_t* la = lds + (n & 1) * (A_SZ + B_SZ);
+      const int8_t* lb = la + A_SZ;
+#pragma unroll
+      for (int c = 0; c < BK / 32; ++c) {
+        const int kk = c * 32 + (lane >> 5) * 16;
+        i32x4 fa[FM], fb[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          fa[i] = *reinterpret_cast<const i32x4*>(la + (wm0 + i * 32 + (lane & 31)) * LD + kk);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          fb[j] = *reinterpret_cast<const i32x4*>(lb + (wn0 + j * 32 + (lane & 31)) * LD + kk);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      }
+      if (group_end(cur)) {
+        const float scale = __int_as_float((127 + kSliceBits * (k - 1 - cur.d)) << 23);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const float pv = (float)acc[i][j][r] * scale;  // exact: |G| <= 2^24
+              two_sum32(hi[i][j][r], lo[i][j][r], pv);
+              acc[i][j][r] = 0;
+            }
+      }
+      if (more) store((n + 1) & 1);
+      __syncthreads();
+      cur = nxt;
+    }
+
+    // Epilogue (lane l of a 32x32 block: column l % 32, rows
+    // 8 (r/4) + 4 (l/32) + r % 4).
+    const int off = -2 * (kSliceBits - 1) - kSliceBits * (k - 1);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn0 + j * 32 + (lane & 31);
+        const int eb = n < g.N ? (OUT == 0 ? g.eB[n] : 0) : 0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm0 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+          if (m >= g.M || n >= g.N) continue;
+          if (OUT == 1) {
+            g.hilo[(int64_t)m * g.ldh + n] = hi[i][j][r];
+            g.hilo[(int64_t)g.M * g.ldh + (int64_t)m * g.ldh + n] = lo[i][j][r];
+            continue;
+          }
+          const int ea = g.eA[m] + off;
+          const double v = (double)hi[i][j][r] + (double)lo[i][j][r];
+          double c;
+          if (ea < 900 && ea > -900 && eb < 900 && eb > -900)
+            c = (v * pow2(ea)) * pow2(eb);
+          else
+            c = ldexp(v, ea + eb);
+          double* dst = g.C + (int64_t)m * g.ldc_m + (int64_t)n * g.ldc_n;
+          *dst = kbi == 0 ? c : *dst + c;
+        }
+      }
+  }
+}
+
+constexpr int kOzBM = 128, kOzBN = 128, kOzBK = 64;
+
+static int oz_launch(OzArgs& g, int out, hipStream_t s) {
+  g.tiles_m = (g.M + kOzBM - 1) / kOzBM;
+  g.tiles_n = (g.N + kOzBN - 1) / kOzBN;
+  const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
+  TRNBLAS_CHECK_ARG(nt < (1ll << 31), "ozaki: too many tiles");
+  if (out == 0)
+    hipLaunchKernelGGL((oz_gemm_kernel<kOzBM, kOzBN, kOzBK, 0>), dim3((unsigned)nt), dim3(256),
+                       0, s, g);
+  else
+    hipLaunchKernelGGL((oz_gemm_kernel<kOzBM, kOzBN, kOzBK, 1>), dim3((unsigned)nt), dim3(256),
+                       0, s, g);
+  return check_launch("ozaki_gemm");
+}
+
+static int oz_check_operands(int slices, int64_t M, int64_t N, int64_t Kp, int64_t kb,
+                             const int8_t* dA, int64_t lda, int64_t lda_slice, const int8_t* dB,
+                             int64_t ldb, int64_t ldb_slice) {
+  TRNBLAS_CHECK_ARG(slices >= 1 && slices <= 12, "ozaki: slices %d not in [1, 12]", slices);
+  TRNBLAS_CHECK_ARG(M >= 0 && N >= 0 && Kp >= 0 && M < (1 << 30) && N < (1 << 30),
+                    "ozaki: bad size");
+  TRNBLAS_CHECK_ARG(Kp % kTileK == 0, "ozaki: Kp %lld not a multiple of 128", (long long)Kp);
+  TRNBLAS_CHECK_ARG(kb > 0 && kb % kTileK == 0 && Kp % kb == 0,
+                    "ozaki: K block %lld must be a multiple of 128 dividing Kp", (long long)kb);
+  TRNBLAS_CHECK_ARG(dA && dB, "ozaki: NULL digits");
+  TRNBLAS_CHECK_ARG(lda >= Kp && ldb >= Kp && lda % 16 == 0 && ldb % 16 == 0 &&
+                        lda_slice % 16 == 0 && ldb_slice % 16 == 0,
+                    "ozaki: digit leading dimensions must be >= Kp and multiples of 16");
+  TRNBLAS_CHECK_ARG(((uintptr_t)dA & 15) == 0 && ((uintptr_t)dB & 15) == 0,
+                    "ozaki: digit buffers must be 16-byte aligned");
+  TRNBLAS_CHECK_ARG((int64_t)kOzBM * lda < 0x7fffff00ll && (int64_t)kOzBN * ldb < 0x7fffff00ll,
+                    "ozaki: leading dimension too large for 32-bit tile offsets");
+  return TRNBLAS_OK;
+}
+
+}  // namespace trnblas
+
+using namespace trnblas;
+
+extern "C" int trnblas_hip_ozaki_split(int per_row, int64_t R, int64_t C, const double* X,
+                                       int64_t ldx, int slices, int8_t* digits,
+                                       int64_t ld_digit, int64_t ld_slice, int32_t* exps,
+                                       int32_t* scratch, void* stream) {
+  clear_error();
+  hipStream_t s = (hipStream_t)stream;
+  TRNBLAS_CHECK_ARG(slices >= 1 && slices <= 12, "ozaki_split: slices %d not in [1, 12]",
+                    slices);
+  TRNBLAS_CHECK_ARG(R >= 0 && C >= 0 && R < (1 << 30) && C < (1 << 30), "ozaki_split: bad size");
+  TRNBLAS_CHECK_ARG(scratch && exps, "ozaki_split: NULL exps / scratch");
+  const int n = per_row ? (int)R : (int)C;
+  if (R == 0 || C == 0) {
+    // zero exponents, no digits (the caller zero-fills the digit buffer)
+    hipLaunchKernelGGL(oz_flags_kernel, dim3(1), dim3(1024), 0, s, (const int32_t*)exps, 0,
+                       scratch);
+    if (n > 0 && hipMemsetAsync(exps, 0, n * sizeof(int32_t), s) != hipSuccess)
+      return check_launch("ozaki_split");
+    return check_launch("ozaki_split");
+  }
+  TRNBLAS_CHECK_ARG(X && digits && ldx >= C, "ozaki_split: bad X / digits");
+  if (per_row) {
+    TRNBLAS_CHECK_ARG(ld_digit >= C && ld_slice >= R * ld_digit, "ozaki_split: bad digit layout");
+    hipLaunchKernelGGL(oz_emax_row_kernel, dim3((unsigned)R), dim3(256), 0, s, X, ldx, (int)R,
+                       (int)C, exps);
+  } else {
+    TRNBLAS_CHECK_ARG(ld_digit >= R && ld_slice >= C * ld_digit, "ozaki_split: bad digit layout");
+    hipLaunchKernelGGL(oz_emax_col_kernel, dim3((unsigned)((C + 63) / 64)), dim3(256), 0, s, X,
+                       ldx, (int)R, (int)C, exps);
+  }
+  int rc = check_launch("ozaki_split(emax)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(oz_flags_kernel, dim3(1), dim3(1024), 0, s, (const int32_t*)exps, n,
+                     scratch);
+  rc = check_launch("ozaki_split(flags)");
+  if (rc) return rc;
+  if (per_row) {
+    const int64_t threads = R * ((C + 15) / 16);
+    hipLaunchKernelGGL(oz_digits_row_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256),
+                       0, s, X, ldx, (int)R, (int)C, slices, (const int32_t*)exps,
+                       (const int32_t*)scratch, digits, ld_digit, ld_slice);
+  } else {
+    hipLaunchKernelGGL(oz_digits_col_kernel,
+                       dim3((unsigned)((C + 63) / 64), (unsigned)((R + 63) / 64)), dim3(256), 0,
+                       s, X, ldx, (int)R, (int)C, slices, (const int32_t*)exps,
+                       (const int32_t*)scratch, digits, ld_digit, ld_slice);
+  }
+  return check_launch("ozaki_split(digits)");
+}
+
+extern "C" int trnblas_hip_ozaki_gemm(int mode, int slices, int64_t M, int64_t N, int64_t Kp,
+                                      int64_t kb, const int8_t* dA, int64_t lda,
+                                      int64_t lda_slice, const int8_t* dB, int64_t ldb,
+                                      int64_t ldb_slice, const int32_t* eA, const int32_t* eB,
+                                      double* C, int64_t ldc_m, int64_t ldc_n, void* stream) {
+  clear_error();
+  TRNBLAS_CHECK_ARG(mode == 0, "ozaki_gemm: mode %d not supported", mode);
+  if (M == 0 || N == 0) return TRNBLAS_OK;
+  int rc = oz_check_operands(slices, M, N, Kp, kb, dA, lda, lda_slice, dB, ldb, ldb_slice);
+  if (rc) return rc;
+  TRNBLAS_CHECK_ARG(Kp > 0, "ozaki_gemm: K == 0 (the caller returns zeros)");
+  TRNBLAS_CHECK_ARG(C && eA && eB, "ozaki_gemm: NULL C / exponents");
+  OzArgs g{};
+  g.k = slices;
+  g.M = (int)M;
+  g.N = (int)N;
+  g.Kp = (int)Kp;
+  g.kb = (int)kb;
+  g.A = dA;
+  g.lda = lda;
+  g.lda_s = lda_slice;
+  g.B = dB;
+  g.ldb = ldb;
+  g.ldb_s = ldb_slice;
+  g.eA = eA;
+  g.eB = eB;
+  g.C = C;
+  g.ldc_m = ldc_m;
+  g.ldc_n = ldc_n;
+  return oz_launch(g, 0, (hipStream_t)stream);
+}
+
+extern "C" int trnblas_hip_ozaki_hilo(int slices, int64_t M, int64_t N, int64_t Kp,
+                                      const int8_t* dA, int64_t lda, int64_t lda_slice,
+                                      const int8_t* dB, int64_t ldb, int64_t ldb_slice,
+                                      float* hilo, int64_t ldh, void* stream) {
+  clear_error();
+  if (M == 0 || N == 0) return TRNBLAS_OK;
+  int rc = oz_check_operands(slices, M, N, Kp, Kp > 0 ? Kp : kTileK, dA, lda, lda_slice, dB,
+                             ldb, ldb_slice);
+  if (rc) return rc;
+  TRNBLAS_CHECK_ARG(Kp > 0, "ozaki_hilo: K == 0");
+  TRNBLAS_CHECK_ARG(hilo && ldh >= N, "ozaki_hilo: bad output");
+  OzArgs g{};
+  g.k = slices;
+  g.M = (int)M;
+  g.N = (int)N;
+  g.Kp = (int)Kp;
+  g.kb = (int)Kp;
+  g.A = dA;
+  g.lda = lda;
+  g.lda_s = lda_slice;
+  g.B = dB;
+  g.ldb = ldb;
+  g.ldb_s = ldb_slice;
+  g.hilo = hilo;
+  g.ldh = ldh;
+  return oz_launch(g, 1, (hipStream_t)stream);
+}

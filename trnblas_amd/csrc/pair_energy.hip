@@ -1,0 +1,463 @@
+// Fused DF-MP2 pair energy on gfx950 fp32 MFMA.
+//
+//   e_ij = sum_{a,b} T_ab (2 T_ab - T_ba) / (e_i + e_j - v_a - v_b),  T = B_i B_j^T
+//
+// The reference evaluates this per occupied row with one NKI launch per row,
+// materialising T in SBUF and transposing blocks of it on the Tensor Engine
+// (trnblas/nki/dispatch.py:4899-5001, driven by :2768-2795; the CPU oracle is
+// :2514-2533). Here one launch covers every pair, and T never leaves the
+// registers:
+//
+//  * work item = (pair (i, j), virtual tile pair (A, B) with A <= B), S x S
+//    tiles (S = 96: nvir 672 = 7 tiles). For A < B the workgroup computes
+//    X = B_i[A] B_j[B]^T and X' = B_j[A] B_i[B]^T, i.e. T[A,B] and T[B,A]^T in
+//    the same register layout, and adds
+//        sum_{a in A, b in B} 2 (X^2 + X'^2 - X X') / D_ab,
+//    which is the (a, b) and (b, a) terms of both tiles (D is symmetric in
+//    a, b). For A == B it computes X = T[A,A] only, takes X' = X^T through
+//    LDS, and adds sum X (2 X - X') / D. So each T entry is computed once.
+//  * pairs: every i <= j with weight 1 (i == j) or 2 (e_ij = e_ji), or an
+//    explicit pair list (the per-row / per-window op surface).
+//  * the denominator and the energy terms are evaluated in fp64 from the fp32
+//    T; each workgroup writes one fp64 partial; a second kernel sums the
+//    partials of each pair, then the weighted pair energies, in a fixed order
+//    (deterministic, no atomics).
+//  * operand panels (four 96 x 16 fp32 panels per k-step) are staged in LDS,
+//    double buffered, K-contiguous with 16-byte row padding (conflict-free
+//    fragment reads); loads are branch-free buffer loads with zero fill.
+//  * items of one pair are consecutive on one XCD (shared L2 for its B_i,
+//    B_j panels).
+#include "common.hpp"
+
+namespace trnblas {
+
+constexpr uint32_t kPeOob = 0x80000000u;
+
+struct PairArgs {
+  int nvir, naux;
+  const float* Bi;
+  int64_t ldi_occ;
+  const float* Bj;
+  int64_t ldj_occ;
+  int64_t ld_vir;
+  const float* eps_i;
+  const float* eps_j;
+  const float* eps_vir;
+  int nocc;  // implicit mode when pair_i == nullptr
+  int npairs;
+  const int32_t* pair_i;
+  const int32_t* pair_j;
+  const double* pair_w;
+  int nb, nq;  // virtual tiles, tile pairs (A <= B) per pair
+  double* partial;  // [npairs * nq]
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t pe_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7ffffff0,
+                                           0x00020000);
+}
+
+// Pair index p -> (i, j), i <= j, row-major over the upper triangle of nocc.
+__device__ __forceinline__ void tri_pair(int p, int nocc, int& i, int& j) {
+  // rows before i: f(i) = i * nocc - i (i - 1) / 2
+  const double n = nocc + 0.5;
+  int r = (int)(n - sqrt(n * n - 2.0 * (double)p));
+  if (r < 0) r = 0;
+  if (r > nocc - 1) r = nocc - 1;
+  while (r > 0 && (int64_t)r * nocc - (int64_t)r * (r - 1) / 2 > p) --r;
+  while (r + 1 < nocc && (int64_t)(r + 1) * nocc - (int64_t)(r + 1) * r / 2 <= p) ++r;
+  i = r;
+  j = i + (p - (r * nocc - r * (r - 1) / 2));
+}
+
+// Tile-pair index q -> (A, B), A <= B, row-major over the upper triangle of nb.
+__device__ __forceinline__ void tri_tiles(int q, int nb, int& A, int& B) {
+  int a = 0, rem = q;
+  while (rem >= nb - a) {
+    rem -= nb - a;
+    ++a;
+  }
+  A = a;
+  B = a + rem;
+}
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int S, int BK, bool VEC>
+__global__ __launch_bounds__(S / 32 * 64, 2) void pair_energy_kernel(PairArgs g) {
+  constexpr int NW = S / 32;  // waves; wave w owns rows 32w..32w+31 of the tile
+  constexpr int NT = NW * 64;
+  constexpr int NJ = S / 32;  // column blocks per wave
+  constexpr int LD = BK + 4;  // padded LDS row (floats)
+  constexpr int PANEL = S * LD;
+  constexpr int NV = S * BK / 4 / NT;  // float4 groups per thread per panel
+  static_assert(NV * 4 * NT == S * BK, "panel split");
+  constexpr int STAGE = 4 * PANEL;
+  constexpr int XT_LD = S + 1;
+  static_assert(2 * STAGE >= S * XT_LD, "transpose buffer fits in the stage buffers");
+  __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
+  __shared__ double red[NW];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int item = xcd_remap(blockIdx.x, gridDim.x);
+  const int p = item / g.nq, q = item - p * g.nq;
+  int i, j;
+  if (g.pair_i) {
+    i = g.pair_i[p];
+    j = g.pair_j[p];
+  } else {
+    tri_pair(p, g.nocc, i, j);
+  }
+  int TA, TB;
+  tri_tiles(q, g.nb, TA, TB);
+  const bool diag = TA == TB;
+  const int a0 = TA * S, b0 = TB * S;
+  const int nvir = g.nvir, naux = g.naux;
+  const float* Xi = g.Bi + (int64_t)i * g.ldi_occ;
+  const float* Xj = g.Bj + (int64_t)j * g.ldj_occ;
+
+  // panels: 0 = B_i[A], 1 = B_j[A], 2 = B_j[B], 3 = B_i[B]
+  const float* pbase[4] = {Xi + (int64_t)a0 * g.ld_vir, Xj + (int64_t)a0 * g.ld_vir,
+                           Xj + (int64_t)b0 * g.ld_vir, Xi + (int64_t)b0 * g.ld_vir};
+  const int prow[4] = {nvir - a0, nvir - a0, nvir - b0, nvir - b0};
+  const int npanel = diag ? 2 : 4;
+
+  i32x4 st[4][NV];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int pn = 0; pn < 4; ++pn) {
+      if (pn >= npanel) break;
+      const __amdgpu_buffer_rsrc_t rs = pe_rsrc(pbase[pn] + k0);
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const int idx = tid + v * NT, r = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
+        const bool ok = r < prow[pn] && c < naux - k0;
+        const uint32_t off = (uint32_t)((r * g.ld_vir + c) * 4);
+        if (VEC) {
+          st[pn][v] = __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? off : kPeOob, 0, 0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            st[pn][v][e] = __builtin_amdgcn_raw_buffer_load_b32(
+                rs, (ok && c + e < naux - k0) ? off + 4 * e : kPeOob, 0, 0);
+        }
+      }
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int pn = 0; pn < 4; ++pn) {
+      if (pn >= npanel) break;
+      float* dst = lds + buf * STAGE + pn * PANEL;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const int idx = tid + v * NT, r = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
+        *reinterpret_cast<i32x4*>(dst + r * LD + c) = st[pn][v];
+      }
+    }
+  };
+
+  f32x16 X[NJ], Xp[NJ];
+#pragma unroll
+  for (int jb = 0; jb < NJ; ++jb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) X[jb][r] = Xp[jb][r] = 0.0f;
+
+  const int nk = (naux + BK - 1) / BK;
+  if (nk > 0) {
+    load(0);
+    store(0);
+    __syncthreads();
+  }
+  const int arow = 32 * w + (lane & 31);
+  for (int kt = 0; kt < nk; ++kt) {
+    const bool more = kt + 1 < nk;
+    if (more) load((kt + 1) * BK);
+    const float* buf = lds + (kt & 1) * STAGE;
+#pragma unroll
+    for (int c = 0; c < BK / 8; ++c) {
+      const int kk = c * 8 + (lane >> 5) * 4;
+      const f32x4 fai = *reinterpret_cast<const f32x4*>(buf + 0 * PANEL + arow * LD + kk);
+      f32x4 fbj[NJ];
+#pragma unroll
+      for (int jb = 0; jb < NJ; ++jb)
+        fbj[jb] = *reinterpret_cast<const f32x4*>(buf + (diag ? 1 : 2) * PANEL +
+                                                  (32 * jb + (lane & 31)) * LD + kk);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int jb = 0; jb < NJ; ++jb)
+          X[jb] = __builtin_amdgcn_mfma_f32_32x32x2f32(fai[e], fbj[jb][e], X[jb], 0, 0, 0);
+      if (!diag) {
+        const f32x4 faj = *reinterpret_cast<const f32x4*>(buf + 1 * PANEL + arow * LD + kk);
+        f32x4 fbi[NJ];
+#pragma unroll
+        for (int jb = 0; jb < NJ; ++jb)
+          fbi[jb] = *reinterpret_cast<const f32x4*>(buf + 3 * PANEL +
+                                                    (32 * jb + (lane & 31)) * LD + kk);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int jb = 0; jb < NJ; ++jb)
+            Xp[jb] = __builtin_amdgcn_mfma_f32_32x32x2f32(faj[e], fbi[jb][e], Xp[jb], 0, 0, 0);
+      }
+    }
+    if (more) store((kt + 1) & 1);
+    __syncthreads();
+  }
+
+  // Lane l of a 32x32 block holds column l % 32 and rows 8 (r/4) + 4 (l/32) + r % 4.
+  if (diag) {
+    // X' = X^T through LDS (the stage buffers are free after the last barrier).
+    float* xt = lds;
+#pragma unroll
+    for (int jb = 0; jb < NJ; ++jb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int a = 32 * w + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        const int b = 32 * jb + (lane & 31);
+        xt[a * XT_LD + b] = X[jb][r];
+      }
+    __syncthreads();
+#pragma unroll
+    for (int jb = 0; jb < NJ; ++jb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int a = 32 * w + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        const int b = 32 * jb + (lane & 31);
+        Xp[jb][r] = xt[b * XT_LD + a];
+      }
+  }
+
+  const double eo = (double)g.eps_i[i] + (double)g.eps_j[j];
+  double sum = 0.0;
+#pragma unroll
+  for (int jb = 0; jb < NJ; ++jb) {
+    const int b = b0 + 32 * jb + (lane & 31);
+    const double eb = b < nvir ? (double)g.eps_vir[b] : 0.0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int a = a0 + 32 * w + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      if (a < nvir && b < nvir) {
+        const double x = X[jb][r], xp = Xp[jb][r];
+        const double d = eo - (double)g.eps_vir[a] - eb;
+        const double num = diag ? x * (2.0 * x - xp) : 2.0 * (x * x + xp * xp - x * xp);
+        sum += num / d;
+      }
+    }
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) red[w] = sum;
+  __syncthreads();
+  if (tid == 0) {
+    double t = 0.0;
+#pragma unroll
+    for (int k = 0; k < NW; ++k) t += red[k];
+    g.partial[item] = t;
+  }
+}
+
+// Per-pair sums of the partials (fixed order), then the weighted total.
+__global__ __launch_bounds__(256) void pair_sum_kernel(const double* partial, int npairs,
+                                                       int nq, double* e_pair) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= npairs) return;
+  const double* src = partial + (int64_t)p * nq;
+  double s = 0.0;
+  for (int q = 0; q < nq; ++q) s += src[q];
+  e_pair[p] = s;
+}
+
+__global__ __launch_bounds__(1024) void pair_total_kernel(const double* e_pair, int npairs,
+                                                          int nocc, const int32_t* pair_i,
+                                                          const int32_t* pair_j,
+                                                          const double* pair_w, double* total) {
+  __shared__ double red[16];
+  const int tid = threadIdx.x;
+  double s = 0.0;
+  for (int p = tid; p < npairs; p += blockDim.x) {
+    double w;
+    if (pair_i) {
+      w = pair_w ? pair_w[p] : 1.0;
+    } else {
+      int i, j;
+      tri_pair(p, nocc, i, j);
+      w = i == j ? 1.0 : 2.0;
+    }
+    s += w * e_pair[p];
+  }
+  s = wave_sum(s);
+  if ((tid & 63) == 0) red[tid >> 6] = s;
+  __syncthreads();
+  if (tid == 0) {
+    double t = 0.0;
+    for (int k = 0; k < (int)(blockDim.x >> 6); ++k) t += red[k];
+    *total = t;
+  }
+}
+
+// MP2 energy of a precomputed amplitude block (the `mp2_energy` surface,
+// trnblas/nki/dispatch.py:4356-4491): one workgroup per (i, j) pair walks the
+// 32 x 32 tile pairs (A <= B) of T_ij, reading T[A,B] and T[B,A] once each
+// through LDS (transposed read of the second), so every amplitude is read
+// once from HBM. fp64 terms, fixed-order reduction.
+__global__ __launch_bounds__(256) void mp2_energy_kernel(int ic, int nocc, int nvir,
+                                                         const float* T, int64_t ldt,
+                                                         const float* eo_chunk,
+                                                         const float* eo_full,
+                                                         const float* ev, double* out) {
+  __shared__ float x[32][33], y[32][33];
+  __shared__ double red[4];
+  const int pair = blockIdx.x;
+  const int i = pair / nocc, j = pair - i * nocc;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 8 rows of 32
+  const double eo = (double)eo_chunk[i] + (double)eo_full[j];
+  const float* Tij = T + (int64_t)i * nvir * ldt + (int64_t)j * nvir;
+  const int nb = (nvir + 31) / 32;
+  double sum = 0.0;
+  for (int A = 0; A < nb; ++A)
+    for (int B = A; B < nb; ++B) {
+      __syncthreads();
+      for (int r = ty; r < 32; r += 8) {
+        const int a = A * 32 + r, b = B * 32 + tx;
+        x[r][tx] = (a < nvir && b < nvir) ? Tij[(int64_t)a * ldt + b] : 0.0f;
+        const int a2 = B * 32 + r, b2 = A * 32 + tx;
+        y[r][tx] = (a2 < nvir && b2 < nvir) ? Tij[(int64_t)a2 * ldt + b2] : 0.0f;
+      }
+      __syncthreads();
+      for (int r = ty; r < 32; r += 8) {
+        const int a = A * 32 + r, b = B * 32 + tx;
+        if (a < nvir && b < nvir) {
+          const double tab = x[r][tx], tba = y[tx][r];
+          const double d = eo - (double)ev[a] - (double)ev[b];
+          sum += (A == B ? tab * (2.0 * tab - tba) : 2.0 * (tab * tab + tba * tba - tab * tba)) / d;
+        }
+      }
+    }
+  sum = wave_sum(sum);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sum;
+  __syncthreads();
+  if (threadIdx.x == 0) out[pair] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+constexpr int kPeS = 96, kPeBK = 16;
+
+static int64_t pe_nq(int64_t nvir) {
+  const int64_t nb = (nvir + kPeS - 1) / kPeS;
+  return nb * (nb + 1) / 2;
+}
+
+}  // namespace trnblas
+
+using namespace trnblas;
+
+extern "C" size_t trnblas_hip_pair_energy_workspace(int64_t nvir, int64_t npairs) {
+  if (nvir <= 0 || npairs <= 0) return 0;
+  return (size_t)(npairs * pe_nq(nvir) + npairs) * sizeof(double);
+}
+
+extern "C" int trnblas_hip_pair_energy(int64_t nvir, int64_t naux, const float* Bi,
+                                       int64_t ldi_occ, const float* Bj, int64_t ldj_occ,
+                                       int64_t ld_vir, const float* eps_i, const float* eps_j,
+                                       const float* eps_vir, int64_t nocc, int64_t npairs,
+                                       const int32_t* pair_i, const int32_t* pair_j,
+                                       const double* pair_w, double* out_pairs,
+                                       double* out_total, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  clear_error();
+  hipStream_t s = (hipStream_t)stream;
+  TRNBLAS_CHECK_ARG(nvir >= 0 && naux >= 0 && nocc >= 0 && npairs >= 0,
+                    "pair_energy: negative size");
+  TRNBLAS_CHECK_ARG(nvir < (1 << 30) && naux < (1 << 30), "pair_energy: size too large");
+  if (pair_i == nullptr) {
+    TRNBLAS_CHECK_ARG(Bi == Bj && eps_i == eps_j && ldi_occ == ldj_occ,
+                      "pair_energy: the implicit i <= j walk needs Bi == Bj, eps_i == eps_j");
+    npairs = nocc * (nocc + 1) / 2;
+  } else {
+    TRNBLAS_CHECK_ARG(pair_j != nullptr, "pair_energy: pair_j is NULL");
+  }
+  if (npairs == 0 || nvir == 0) {
+    // Empty sums: zero energies.
+    if (out_total && hipMemsetAsync(out_total, 0, sizeof(double), s) != hipSuccess)
+      return check_launch("pair_energy");
+    if (out_pairs && npairs > 0 &&
+        hipMemsetAsync(out_pairs, 0, npairs * sizeof(double), s) != hipSuccess)
+      return check_launch("pair_energy");
+    return TRNBLAS_OK;
+  }
+  TRNBLAS_CHECK_ARG(Bi && Bj && eps_i && eps_j && eps_vir, "pair_energy: NULL operand");
+  TRNBLAS_CHECK_ARG(ld_vir >= naux, "pair_energy: ld_vir < naux");
+  TRNBLAS_CHECK_ARG((int64_t)kPeS * ld_vir * 4 < 0x7fffff00ll,
+                    "pair_energy: ld_vir too large for 32-bit panel offsets");
+  const int64_t nq = pe_nq(nvir);
+  const int64_t items = npairs * nq;
+  TRNBLAS_CHECK_ARG(items < (1ll << 31), "pair_energy: too many work items");
+  const size_t need = trnblas_hip_pair_energy_workspace(nvir, npairs);
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_error("pair_energy: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    return TRNBLAS_E_WORKSPACE;
+  }
+  PairArgs g;
+  g.nvir = (int)nvir;
+  g.naux = (int)naux;
+  g.Bi = Bi;
+  g.ldi_occ = ldi_occ;
+  g.Bj = Bj;
+  g.ldj_occ = ldj_occ;
+  g.ld_vir = ld_vir;
+  g.eps_i = eps_i;
+  g.eps_j = eps_j;
+  g.eps_vir = eps_vir;
+  g.nocc = (int)nocc;
+  g.npairs = (int)npairs;
+  g.pair_i = pair_i;
+  g.pair_j = pair_j;
+  g.pair_w = pair_w;
+  g.nb = (int)((nvir + kPeS - 1) / kPeS);
+  g.nq = (int)nq;
+  g.partial = static_cast<double*>(workspace);
+  double* e_pair = out_pairs ? out_pairs : g.partial + items;
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const bool vec = al16(Bi) && al16(Bj) && naux % 4 == 0 && ld_vir % 4 == 0 &&
+                   ldi_occ % 4 == 0 && ldj_occ % 4 == 0;
+  constexpr int NT = kPeS / 32 * 64;
+  if (vec)
+    hipLaunchKernelGGL((pair_energy_kernel<kPeS, kPeBK, true>), dim3((unsigned)items), dim3(NT),
+                       0, s, g);
+  else
+    hipLaunchKernelGGL((pair_energy_kernel<kPeS, kPeBK, false>), dim3((unsigned)items),
+                       dim3(NT), 0, s, g);
+  int rc = check_launch("pair_energy");
+  if (rc) return rc;
+  hipLaunchKernelGGL(pair_sum_kernel, dim3((unsigned)((npairs + 255) / 256)), dim3(256), 0, s,
+                     (const double*)g.partial, (int)npairs, (int)nq, e_pair);
+  rc = check_launch("pair_energy(sum)");
+  if (rc) return rc;
+  if (out_total) {
+    hipLaunchKernelGGL(pair_total_kernel, dim3(1), dim3(1024), 0, s, (const double*)e_pair,
+                       (int)npairs, (int)nocc, pair_i, pair_j, pair_w, out_total);
+    rc = check_launch("pair_energy(total)");
+  }
+  return rc;
+}
+
+extern "C" int trnblas_hip_mp2_energy(int64_t ic, int64_t nocc, int64_t nvir, const float* T_flat,
+                                      int64_t ldt, const float* eps_occ_chunk,
+                                      const float* eps_occ_full, const float* eps_vir,
+                                      double* out_pairs, void* stream) {
+  clear_error();
+  TRNBLAS_CHECK_ARG(ic >= 0 && nocc >= 0 && nvir >= 0, "mp2_energy: negative size");
+  if (ic == 0 || nocc == 0) return TRNBLAS_OK;
+  TRNBLAS_CHECK_ARG(ic * nocc < (1ll << 31) && nvir < (1 << 30), "mp2_energy: size too large");
+  TRNBLAS_CHECK_ARG(out_pairs && eps_occ_chunk && eps_occ_full, "mp2_energy: NULL operand");
+  if (nvir > 0)
+    TRNBLAS_CHECK_ARG(T_flat && eps_vir && ldt >= nocc * nvir, "mp2_energy: bad T_flat / ldt");
+  hipLaunchKernelGGL(mp2_energy_kernel, dim3((unsigned)(ic * nocc)), dim3(256), 0,
+                     (hipStream_t)stream, (int)ic, (int)nocc, (int)nvir, T_flat, ldt,
+                     eps_occ_chunk, eps_occ_full, eps_vir, out_pairs);
+  return check_launch("mp2_energy");
+}

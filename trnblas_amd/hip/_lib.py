@@ -1,0 +1,159 @@
+"""ctypes binding of `libtrnblas_hip.so` (the C ABI in include/trnblas_hip.h).
+
+The library is loaded lazily on first use, after torch (whose bundled HIP
+runtime then also serves the library: both resolve `libamdhip64.so.7`, so
+streams and device pointers are shared). There is no fallback: a missing or
+unloadable library raises `HipLibraryError`, and callers that asked for the
+HIP path see that error.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (loads torch's HIP runtime before the library)
+
+_PKG = Path(__file__).resolve().parent.parent
+LIB_PATH = Path(os.environ.get("TRNBLAS_HIP_LIB", _PKG / "lib" / "libtrnblas_hip.so"))
+
+ABI_VERSION = 1
+
+F32, BF16, F16 = 0, 1, 2
+DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+E_ARG, E_LAUNCH, E_NONFINITE, E_WORKSPACE = -1, -2, -3, -4
+
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_dbl = ctypes.c_double
+_c_ptr = ctypes.c_void_p
+_c_size = ctypes.c_size_t
+
+# name -> (restype, argtypes); the exported surface of include/trnblas_hip.h
+SIGNATURES = {
+    "trnblas_hip_abi_version": (_c_int, []),
+    "trnblas_hip_last_error": (ctypes.c_char_p, []),
+    "trnblas_hip_gemm": (
+        _c_int,
+        [_c_int, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_dbl]
+        + [_c_ptr, _c_i64, _c_i64] * 2
+        + [_c_dbl, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr],
+    ),
+    "trnblas_hip_syrk": (
+        _c_int,
+        [_c_int, _c_int, _c_int, _c_i64, _c_i64, _c_dbl, _c_ptr, _c_i64, _c_dbl, _c_ptr]
+        + [_c_i64, _c_ptr, _c_i64, _c_ptr],
+    ),
+    "trnblas_hip_pair_energy_workspace": (_c_size, [_c_i64, _c_i64]),
+    "trnblas_hip_pair_energy": (
+        _c_int,
+        [_c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr],
+    ),
+    "trnblas_hip_mp2_energy": (
+        _c_int,
+        [_c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr],
+    ),
+    "trnblas_hip_ozaki_split": (
+        _c_int,
+        [_c_int, _c_i64, _c_i64, _c_ptr, _c_i64, _c_int, _c_ptr, _c_i64, _c_i64, _c_ptr]
+        + [_c_ptr, _c_ptr],
+    ),
+    "trnblas_hip_ozaki_gemm": (
+        _c_int,
+        [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr]
+        + [_c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr],
+    ),
+    "trnblas_hip_ozaki_hilo": (
+        _c_int,
+        [_c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64]
+        + [_c_ptr, _c_i64, _c_ptr],
+    ),
+}
+
+
+class HipLibraryError(RuntimeError):
+    """The HIP op library is missing, stale, or cannot be loaded."""
+
+
+class HipKernelError(RuntimeError):
+    """A C-ABI call returned an error code."""
+
+    def __init__(self, fn: str, code: int, message: str):
+        super().__init__(f"{fn} failed ({code}): {message}")
+        self.fn, self.code, self.message = fn, code, message
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load(path: Path | str | None = None) -> ctypes.CDLL:
+    """The loaded library (cached). Raises HipLibraryError if it cannot be loaded."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = Path(path) if path is not None else LIB_PATH
+        if not p.exists():
+            raise HipLibraryError(
+                f"{p} not found: build it with `python -m trnblas_amd.build` "
+                "(or __graft_entry__.build())"
+            )
+        try:
+            lib = ctypes.CDLL(str(p))
+        except OSError as exc:
+            raise HipLibraryError(f"cannot load {p}: {exc}") from exc
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name, None)
+            if fn is None:
+                continue  # reported by missing_symbols(); calling it raises
+            fn.restype = res
+            fn.argtypes = args
+        v = lib.trnblas_hip_abi_version()
+        if v != ABI_VERSION:
+            raise HipLibraryError(f"{p}: ABI version {v}, expected {ABI_VERSION} (rebuild)")
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def missing_symbols(lib: ctypes.CDLL | None = None) -> list[str]:
+    """Entry points of include/trnblas_hip.h the loaded library lacks."""
+    lib = lib or load()
+    return [n for n in SIGNATURES if getattr(lib, n, None) is None]
+
+
+def available() -> bool:
+    try:
+        load()
+        return True
+    except HipLibraryError:
+        return False
+
+
+def call(name: str, *args) -> int:
+    """Call C-ABI function `name`; raise HipKernelError on a negative return."""
+    lib = load()
+    fn = getattr(lib, name, None)
+    if fn is None:
+        raise HipLibraryError(f"{LIB_PATH} does not export {name} (rebuild)")
+    rc = fn(*args)
+    if rc < 0:
+        msg = lib.trnblas_hip_last_error()
+        raise HipKernelError(name, rc, msg.decode() if msg else "")
+    return rc
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    """hipStream_t of torch's current stream on `device`, as an int."""
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,316 @@
+"""Tensor-level wrappers of the C ABI: each takes device tensors, allocates
+the output with torch on the operands' device, and launches on torch's
+current stream. No routing and no fallback here (see `dispatch.py`): a call
+with host tensors, or without the library, raises.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import call, ptr, stream_of
+
+
+def _require_device(*ts: torch.Tensor) -> torch.device:
+    dev = ts[0].device
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError(f"HIP kernel operands must be on the GPU, got {t.device}")
+        if t.device != dev:
+            raise ValueError(f"operands on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _mat_layout(X: torch.Tensor):
+    """(tensor, trans, ld) describing a 2-D view X without a copy when it is
+    row-major (trans=False) or a transposed row-major view (trans=True);
+    otherwise a contiguous copy."""
+    s0, s1 = X.stride()
+    r, c = X.shape
+    if s1 == 1 and (s0 >= max(c, 1) or r <= 1):
+        return X, False, max(s0, c, 1)
+    if s0 == 1 and (s1 >= max(r, 1) or c <= 1):
+        return X, True, max(s1, r, 1)
+    X = X.contiguous()
+    return X, False, max(c, 1)
+
+
+def _batched_layout(X: torch.Tensor):
+    """(tensor, trans, ld, batch_stride) for a 3-D (batch, r, c) view whose
+    matrices are row-major or transposed row-major with one batch stride
+    (0 = broadcast); else a contiguous copy."""
+    b, r, c = X.shape
+    sb, s0, s1 = X.stride()
+    if b == 1:
+        sb = 0
+    if s1 == 1 and (s0 >= max(c, 1) or r <= 1):
+        return X, False, max(s0, c, 1), sb
+    if s0 == 1 and (s1 >= max(r, 1) or c <= 1):
+        return X, True, max(s1, r, 1), sb
+    X = X.contiguous()
+    return X, False, max(c, 1), r * c
+
+
+def gemm(
+    A: torch.Tensor,
+    B: torch.Tensor,
+    alpha: float = 1.0,
+    beta: float = 0.0,
+    C: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """alpha * A @ B + beta * C for device A (M, K), B (K, N) (or batched
+    (b, M, K), (b, K, N) with equal or broadcast batch), one launch. Transposed
+    views are read in place. Returns a fresh (M, N) / (b, M, N) tensor in
+    A's dtype; C (same shape, or broadcast over the batch) is never written."""
+    dev = _require_device(A, B, *(() if C is None else (C,)))
+    if A.dtype != B.dtype or (C is not None and C.dtype != A.dtype):
+        raise TypeError(f"gemm: mixed dtypes {A.dtype}, {B.dtype}")
+    code = _lib.DTYPE_CODES.get(A.dtype)
+    if code is None:
+        raise TypeError(f"gemm: dtype {A.dtype} not supported by the HIP kernel")
+    if A.dim() == 2 and B.dim() == 2:
+        M, K = A.shape
+        K2, N = B.shape
+        if K != K2:
+            raise ValueError(f"gemm: inner dimensions differ: {tuple(A.shape)} @ {tuple(B.shape)}")
+        a, ta, lda = _mat_layout(A)
+        b, tb, ldb = _mat_layout(B)
+        D = torch.empty((M, N), dtype=A.dtype, device=dev)
+        c, ldc = None, N
+        if beta != 0.0 and C is not None:
+            c = C.expand(M, N)
+            if c.stride(1) != 1 or c.stride(0) < N:
+                c = c.contiguous()
+            ldc = c.stride(0)
+        call(
+            "trnblas_hip_gemm", code, int(ta), int(tb), M, N, K, float(alpha),
+            ptr(a), lda, 0, ptr(b), ldb, 0, float(beta) if c is not None else 0.0,
+            ptr(c), ldc, 0, ptr(D), N, 0, 1, stream_of(dev),
+        )  # fmt: skip
+        return D
+    if A.dim() != 3 or B.dim() != 3:
+        raise ValueError("gemm: operands must both be 2-D or both 3-D")
+    bA, M, K = A.shape
+    bB, K2, N = B.shape
+    if K != K2:
+        raise ValueError(f"gemm: inner dimensions differ: {tuple(A.shape)} @ {tuple(B.shape)}")
+    nb = max(bA, bB)
+    if bA not in (1, nb) or bB not in (1, nb):
+        raise ValueError(f"gemm: batch sizes {bA} and {bB} do not broadcast")
+    a, ta, lda, sa = _batched_layout(A)
+    b, tb, ldb, sb = _batched_layout(B)
+    D = torch.empty((nb, M, N), dtype=A.dtype, device=dev)
+    c, ldc, sc = None, N, 0
+    if beta != 0.0 and C is not None:
+        c = C.expand(nb, M, N)
+        if c.stride(2) != 1 or c.stride(1) < N:
+            c = c.contiguous()
+        ldc, sc = c.stride(1), (0 if nb == 1 else c.stride(0))
+    call(
+        "trnblas_hip_gemm", code, int(ta), int(tb), M, N, K, float(alpha),
+        ptr(a), lda, sa, ptr(b), ldb, sb, float(beta) if c is not None else 0.0,
+        ptr(c), ldc, sc, ptr(D), N, M * N, nb, stream_of(dev),
+    )  # fmt: skip
+    return D
+
+
+def syrk(
+    A: torch.Tensor,
+    alpha: float = 1.0,
+    beta: float = 0.0,
+    C: torch.Tensor | None = None,
+    trans: bool = False,
+    uplo: str = "lower",
+) -> torch.Tensor:
+    """alpha * op(A) op(A)^T + beta * sym_uplo(C), full symmetric (n, n),
+    computing only the lower triangle of the product. op(A) = A (n, k), or
+    A^T for trans (A (k, n))."""
+    dev = _require_device(A, *(() if C is None else (C,)))
+    code = _lib.DTYPE_CODES.get(A.dtype)
+    if code is None:
+        raise TypeError(f"syrk: dtype {A.dtype} not supported by the HIP kernel")
+    a, t, lda = _mat_layout(A)
+    t = t != bool(trans)  # a transposed view flips the layout flag
+    n = A.shape[1] if trans else A.shape[0]
+    k = A.shape[0] if trans else A.shape[1]
+    D = torch.empty((n, n), dtype=A.dtype, device=dev)
+    c, ldc = None, n
+    if beta != 0.0 and C is not None:
+        if C.dtype != A.dtype:
+            raise TypeError("syrk: C dtype differs from A")
+        c = C if (C.stride(1) == 1 and C.stride(0) >= n) else C.contiguous()
+        ldc = c.stride(0)
+    call(
+        "trnblas_hip_syrk", code, 1 if uplo == "upper" else 0, int(t), n, k, float(alpha),
+        ptr(a), lda, float(beta) if c is not None else 0.0, ptr(c), ldc, ptr(D), n,
+        stream_of(dev),
+    )  # fmt: skip
+    return D
+
+
+# ── DF-MP2 pair energy ───────────────────────────────────────────────────────
+
+
+def _pe_operand(X: torch.Tensor) -> torch.Tensor:
+    """fp32 (n, nvir, naux) with the aux index contiguous (a view if it is)."""
+    if X.dtype != torch.float32:
+        raise TypeError(f"pair energy kernel takes float32 amplitudes, got {X.dtype}")
+    if X.stride(-1) != 1 or (X.shape[1] > 1 and X.stride(1) < X.shape[2]):
+        X = X.contiguous()
+    return X
+
+
+def pair_energy_sym(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tensor):
+    """E = sum_{i,j} e_ij over all ordered pairs, evaluated as the i <= j walk
+    (weights 1 / 2) in one launch. B (nocc, nvir, naux) fp32 on the GPU.
+    Returns a 0-d float64 device tensor."""
+    dev = _require_device(B, eps_occ, eps_vir)
+    B = _pe_operand(B)
+    nocc, nvir, naux = B.shape
+    eo = eps_occ.to(torch.float32).contiguous()
+    ev = eps_vir.to(torch.float32).contiguous()
+    total = torch.empty((), dtype=torch.float64, device=dev)
+    npairs = nocc * (nocc + 1) // 2
+    ws = _lib.load().trnblas_hip_pair_energy_workspace(nvir, npairs)
+    work = torch.empty(max(ws, 8), dtype=torch.uint8, device=dev)
+    ld_occ = B.stride(0) if nocc > 1 else nvir * naux
+    call(
+        "trnblas_hip_pair_energy", nvir, naux, ptr(B), ld_occ, ptr(B), ld_occ,
+        B.stride(1) if nvir > 1 else naux, ptr(eo), ptr(eo), ptr(ev), nocc, npairs,
+        None, None, None, None, ptr(total), ptr(work), work.numel(), stream_of(dev),
+    )  # fmt: skip
+    return total
+
+
+def pair_energies(
+    Bi: torch.Tensor,
+    Bj: torch.Tensor,
+    eps_i: torch.Tensor,
+    eps_j: torch.Tensor,
+    eps_vir: torch.Tensor,
+    pair_i: torch.Tensor,
+    pair_j: torch.Tensor,
+) -> torch.Tensor:
+    """Unweighted e_p for the pairs (pair_i[p], pair_j[p]), with T = Bi[i]
+    Bj[j]^T. Bi (ni, nvir, naux), Bj (nj, nvir, naux) fp32; returns float64
+    (npairs,) on the device."""
+    dev = _require_device(Bi, Bj, eps_i, eps_j, eps_vir)
+    Bi, Bj = _pe_operand(Bi), _pe_operand(Bj)
+    if Bi.shape[1:] != Bj.shape[1:]:
+        raise ValueError(f"pair operands differ: {tuple(Bi.shape)} vs {tuple(Bj.shape)}")
+    if Bi.stride(1) != Bj.stride(1):
+        Bi, Bj = Bi.contiguous(), Bj.contiguous()
+    _, nvir, naux = Bi.shape
+    pi = pair_i.to(device=dev, dtype=torch.int32).contiguous()
+    pj = pair_j.to(device=dev, dtype=torch.int32).contiguous()
+    npairs = pi.numel()
+    out = torch.empty(npairs, dtype=torch.float64, device=dev)
+    if npairs == 0:
+        return out
+    ws = _lib.load().trnblas_hip_pair_energy_workspace(nvir, npairs)
+    work = torch.empty(max(ws, 8), dtype=torch.uint8, device=dev)
+    ei = eps_i.to(torch.float32).contiguous()
+    ej = eps_j.to(torch.float32).contiguous()
+    ev = eps_vir.to(torch.float32).contiguous()
+    ld_vir = Bi.stride(1) if nvir > 1 else naux
+    call(
+        "trnblas_hip_pair_energy", nvir, naux, ptr(Bi), Bi.stride(0), ptr(Bj), Bj.stride(0),
+        ld_vir, ptr(ei), ptr(ej), ptr(ev), 0, npairs, ptr(pi), ptr(pj), None, ptr(out),
+        None, ptr(work), work.numel(), stream_of(dev),
+    )  # fmt: skip
+    return out
+
+
+def mp2_energy_pairs(T_flat, eps_occ_chunk, eps_occ_full, eps_vir) -> torch.Tensor:
+    """Per-pair MP2 energies (ic * nocc,) float64 of a precomputed T_flat
+    (ic * nvir, nocc * nvir) fp32 (row stride >= nocc * nvir)."""
+    dev = _require_device(T_flat, eps_occ_chunk, eps_occ_full, eps_vir)
+    if T_flat.dtype != torch.float32:
+        raise TypeError("mp2_energy kernel takes float32 T_flat")
+    if T_flat.stride(1) != 1:
+        T_flat = T_flat.contiguous()
+    ic, nocc, nvir = eps_occ_chunk.numel(), eps_occ_full.numel(), eps_vir.numel()
+    out = torch.empty(ic * nocc, dtype=torch.float64, device=dev)
+    f32 = torch.float32
+    eoc = eps_occ_chunk.to(f32).contiguous()
+    eof = eps_occ_full.to(f32).contiguous()
+    ev = eps_vir.to(f32).contiguous()
+    call(
+        "trnblas_hip_mp2_energy", ic, nocc, nvir, ptr(T_flat), T_flat.stride(0) if ic else 1,
+        ptr(eoc), ptr(eof), ptr(ev), ptr(out), stream_of(dev),
+    )  # fmt: skip
+    return out
+
+
+# ── Ozaki ────────────────────────────────────────────────────────────────────
+
+OZ_TILE = 128  # K padding of the digit stacks (ozaki.TILE_K)
+OZ_ROW_PAD = 128  # row padding of the digit stacks (tile of the slice GEMM)
+
+
+def _round_up(n: int, m: int) -> int:
+    return -(-n // m) * m
+
+
+def ozaki_split(X: torch.Tensor, slices: int, per: str):
+    """Digits and exponents of a device fp64 matrix X (R, C).
+
+    per="row": digits (k, Rp, Cp) int8 with digit[s, r, c] (K = C contiguous);
+    per="col": digits (k, Cp, Rp) int8 with digit[s, c, r] (K = R contiguous,
+    the column split written transposed). Exponents int32 (R,) / (C,).
+    Returns (digits, exps, nonfinite) where `nonfinite` is a 0-d int32 device
+    flag (the digits are undefined when it is set)."""
+    dev = _require_device(X)
+    if X.dtype != torch.float64:
+        raise TypeError("ozaki_split takes float64")
+    if X.stride(-1) != 1:
+        X = X.contiguous()
+    R, C = X.shape
+    per_row = per == "row"
+    rows, cols = (R, C) if per_row else (C, R)
+    rp, cp = _round_up(max(rows, 1), OZ_ROW_PAD), _round_up(max(cols, 1), OZ_TILE)
+    digits = torch.zeros((slices, rp, cp), dtype=torch.int8, device=dev)
+    exps = torch.empty(rows, dtype=torch.int32, device=dev)
+    scratch = torch.zeros(2, dtype=torch.int32, device=dev)
+    call(
+        "trnblas_hip_ozaki_split", int(per_row), R, C, ptr(X), X.stride(0) if R else 1,
+        slices, ptr(digits), cp, rp * cp, ptr(exps), ptr(scratch), stream_of(dev),
+    )  # fmt: skip
+    return digits, exps, scratch[1]
+
+
+def ozaki_gemm(dA, eA, dB, eB, M: int, N: int, slices: int, kb: int | None = None,
+               out: torch.Tensor | None = None, transpose_out: bool = False) -> torch.Tensor:
+    """fp64 C (M, N) from digit stacks dA (k, >=M, Kp), dB (k, >=N, Kp)
+    (K-contiguous) and their exponents, by the bit-exact schedule. With
+    transpose_out, writes C^T into `out` (N, M) instead."""
+    dev = _require_device(dA, dB, eA, eB)
+    k, _, Kp = dA.shape
+    kb = Kp if kb is None else kb
+    if out is None:
+        out = torch.empty((N, M) if transpose_out else (M, N), dtype=torch.float64, device=dev)
+    if transpose_out:
+        ldc_m, ldc_n = out.stride(1), out.stride(0)
+    else:
+        ldc_m, ldc_n = out.stride(0), out.stride(1)
+    call(
+        "trnblas_hip_ozaki_gemm", 0, slices, M, N, Kp, kb, ptr(dA), dA.stride(1),
+        dA.stride(0), ptr(dB), dB.stride(1), dB.stride(0), ptr(eA), ptr(eB), ptr(out),
+        ldc_m, ldc_n, stream_of(dev),
+    )  # fmt: skip
+    return out
+
+
+def ozaki_hilo(dA, dB, M: int, N: int, slices: int) -> torch.Tensor:
+    """Raw (2, M, N) fp32 (hi, lo) of the slice GEMM (one K block)."""
+    dev = _require_device(dA, dB)
+    Kp = dA.shape[2]
+    hilo = torch.empty((2, M, N), dtype=torch.float32, device=dev)
+    call(
+        "trnblas_hip_ozaki_hilo", slices, M, N, Kp, ptr(dA), dA.stride(1), dA.stride(0),
+        ptr(dB), dB.stride(1), dB.stride(0), ptr(hilo), N, stream_of(dev),
+    )  # fmt: skip
+    return hilo
