@@ -1,0 +1,323 @@
+"""Benchmark of the trnblas Level-3 hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras]
+
+Headline (one JSON line on stdout): BASELINE.json's metric on its config
+`configs[1]`, the fp32 Level-3 mix — one step = SYRK (C = A A^T + 0.5 C on
+the lower triangle, A 4096 x 8192) + batched GEMM (64 x (512 x 2048) @
+(2048 x 512)) through the public API, inputs resident in HBM. `value` is the
+step's algorithmic TFLOP/s (SYRK counted as n (n + 1) k, the triangle).
+
+`roofline` is the dominant kernel of the step (the SYRK kernel): its
+algorithmic flops per launch over its average launch time, from HIP events
+recorded around every launch of the timed region on the launch stream.
+`cpu_baseline` is the reference's CPU path (torch.matmul on the host, the
+`_scale_add` epilogue; restated in oracle/blas.py) on the same step.
+
+`extra` carries the other BASELINE configurations: C1 (2048^3 Aᵀ B parity
+and time), fp32 GEMM 8192^3 against peak, C3 (the fused DF-MP2 pair energy
+against the unfused GPU baseline, with its fp64 energy error), C5 (Ozaki
+gemm_fp64 8192^3 against native fp64 DGEMM).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+# MI355X published dense peaks (TFLOP/s or TOPS) and HBM bandwidth.
+PEAK_FP32_MFMA = 157.3
+PEAK_FP64_MFMA = 78.6
+PEAK_INT8 = 5033.0
+PEAK_HBM_GBS = 8000.0
+
+SYRK_N, SYRK_K = 4096, 8192
+BATCH, BM, BK, BN = 64, 512, 2048, 512
+SYRK_FLOP = SYRK_N * (SYRK_N + 1) * SYRK_K  # triangle count
+BATCHED_FLOP = BATCH * 2 * BM * BN * BK
+STEP_FLOP = SYRK_FLOP + BATCHED_FLOP
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def median(xs):
+    xs = sorted(xs)
+    return xs[len(xs) // 2]
+
+
+class LaunchEvents:
+    """HIP events around each launch of one kernel (via the kernel-wrapper
+    probe), recorded on torch's current stream, i.e. the launch stream."""
+
+    def __init__(self, kernel: str):
+        self.kernel, self.pairs, self._open = kernel, [], None
+
+    def __call__(self, kernel, phase):
+        if kernel != self.kernel:
+            return
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        if phase == "begin":
+            self._open = ev
+        else:
+            self.pairs.append((self._open, ev))
+
+    def mean_ms(self) -> float:
+        return sum(a.elapsed_time(b) for a, b in self.pairs) / max(1, len(self.pairs))
+
+
+def gpu_time_ms(fn, reps: int, warm: int = 1) -> float:
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        torch.cuda.synchronize()
+        ts.append(s.elapsed_time(e))
+    return median(ts)
+
+
+def cpu_baseline_level3(A, C, Ab, Bb, threads: int) -> dict:
+    """The reference's CPU path on one full step (oracle/blas.py), median of 3."""
+    from oracle import blas
+
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        Ah, Ch, Abh, Bbh = (x.cpu() for x in (A, C, Ab, Bb))
+        ts = []
+        for r in range(4):
+            t0 = time.perf_counter()
+            blas.syrk_cpu(1.0, Ah, 0.5, Ch, uplo="lower")
+            blas.batched_gemm_cpu(1.0, Abh, Bbh)
+            if r:
+                ts.append(time.perf_counter() - t0)
+        t = median(ts)
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": STEP_FLOP / t / 1e12, "unit": "TFLOP/s", "cores": threads, "ms": t * 1e3}
+
+
+def run_extras(dev, tb) -> dict:
+    from trnblas_amd import df_mp2
+    from trnblas_amd.hip import dispatch, kernels
+
+    out = {}
+    # C1: gemm fp32 A^T B + 0.5 C at 2048^3, against the CPU path
+    A, B, C = df_mp2.config1_inputs(dev)
+    t = gpu_time_ms(lambda: tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True), reps=20, warm=3)
+    D = tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True)
+    Ah, Bh, Ch = A.cpu(), B.cpu(), C.cpu()
+    t0 = time.perf_counter()
+    cpu = Ah.T @ Bh
+    cpu.mul_(1.0).add_(Ch, alpha=0.5)
+    cpu_ms = (time.perf_counter() - t0) * 1e3
+    den = Ah.double().abs().T @ Bh.double().abs() + 0.5 * Ch.double().abs()
+    err = float(((D.cpu().double() - cpu.double()) / den).abs().max())
+    fl = 2 * 2048**3
+    out["c1_gemm_2048_transA"] = {
+        "ms": t, "tflops": fl / t / 1e9, "frac_fp32_peak": fl / t / 1e9 / PEAK_FP32_MFMA,
+        "cw_err_vs_cpu_path": err, "gate": 1e-6, "cpu_ms": cpu_ms, "cpu_threads": torch.get_num_threads(),
+    }  # fmt: skip
+    log("c1", out["c1_gemm_2048_transA"])
+    # fp32 GEMM 8192^3 (north-star target: >= 70 % of fp32 MFMA peak)
+    g = torch.Generator(device=dev).manual_seed(0)
+    X = torch.randn(8192, 8192, device=dev, generator=g)
+    Y = torch.randn(8192, 8192, device=dev, generator=g)
+    t = gpu_time_ms(lambda: tb.gemm(1.0, X, Y), reps=10, warm=2)
+    tl = gpu_time_ms(lambda: torch.matmul(X, Y), reps=10, warm=2)
+    fl = 2 * 8192**3
+    out["gemm_fp32_8192"] = {
+        "ms": t, "tflops": fl / t / 1e9, "frac_fp32_peak": fl / t / 1e9 / PEAK_FP32_MFMA,
+        "torch_hipblaslt_ms": tl, "torch_tflops": fl / tl / 1e9,
+    }  # fmt: skip
+    log("gemm8192", out["gemm_fp32_8192"])
+    del X, Y
+    # C3: fused pair energy vs the unfused GPU baseline (hipBLASLt GEMM + torch)
+    Bp, eo, ev = df_mp2.config3_inputs(dev)
+    tf = gpu_time_ms(lambda: kernels.pair_energy_sym(Bp, eo, ev), reps=3, warm=1)
+    tu = gpu_time_ms(lambda: dispatch._torch_chunked_pair_energy(Bp, eo, ev), reps=3, warm=1)
+    e_hip = float(kernels.pair_energy_sym(Bp, eo, ev))
+    e_unf = float(dispatch._torch_chunked_pair_energy(Bp, eo, ev))
+    Bd, eod, evd = Bp.double(), eo.double(), ev.double()
+    e64 = torch.zeros((), dtype=torch.float64, device=dev)
+    for i in range(Bp.shape[0]):
+        T = torch.matmul(Bd[i].unsqueeze(0), Bd[i:].transpose(1, 2))
+        Dn = eod[i] + eod[i:, None, None] - evd[None, :, None] - evd[None, None, :]
+        e = (T * (2.0 * T - T.transpose(1, 2)) / Dn).sum(dim=(1, 2))
+        w = torch.full_like(e, 2.0)
+        w[0] = 1.0
+        e64 += (w * e).sum()
+    e64 = float(e64)
+    del Bd
+    fl = 96 * 97 / 2 * 2 * 672 * 672 * 2304
+    # CPU path sample: the reference's fp32 pair loop over 12 of the 9216
+    # ordered pairs, scaled to all pairs.
+    from oracle import pair_energy as pe
+
+    Bh, eoh, evh = Bp[:12].cpu(), eo[:12].cpu(), ev.cpu()
+    t0 = time.perf_counter()
+    for j in range(12):
+        pe.fused_pair_cpu(Bh[0], Bh[j], float(eoh[0]), float(eoh[j]), evh)
+    cpu_pair_s = (time.perf_counter() - t0) / 12
+    out["pair_energy_c3_96_672_2304"] = {
+        "fused_ms": tf, "unfused_gpu_ms": tu, "speedup_vs_unfused": tu / tf,
+        "tflops_sym": fl / tf / 1e9, "frac_fp32_peak": fl / tf / 1e9 / PEAK_FP32_MFMA,
+        "energy_fp64": e64, "rel_err_fused_vs_fp64": abs(e_hip - e64) / abs(e64),
+        "rel_err_unfused_fp32_vs_fp64": abs(e_unf - e64) / abs(e64), "gate": 1e-6,
+        "cpu_fp32_loop_ms_est": cpu_pair_s * 96 * 96 * 1e3,
+        "cpu_sample": "12 of 9216 ordered pairs of the fp32 torch loop, scaled",
+        "cpu_threads": torch.get_num_threads(),
+    }  # fmt: skip
+    log("c3", out["pair_energy_c3_96_672_2304"])
+    del Bp
+    # C5: Ozaki gemm_fp64 at 8192^3, k = 8, against native fp64 DGEMM
+    g = torch.Generator(device=dev).manual_seed(5)
+    n = 8192
+
+    def draw():
+        u = torch.rand(n, n, generator=g, device=dev, dtype=torch.float64) * 2 - 1
+        return u * torch.exp2(torch.round(4.0 * torch.randn(n, n, generator=g, device=dev, dtype=torch.float64)))
+
+    Ao, Bo = draw(), draw()
+    to = gpu_time_ms(lambda: tb.gemm_fp64(Ao, Bo), reps=3, warm=1)
+    td = gpu_time_ms(lambda: torch.matmul(Ao, Bo), reps=3, warm=1)
+    Co = tb.gemm_fp64(Ao, Bo)
+    Cd = Ao @ Bo
+    den = Ao.abs() @ Bo.abs()
+    err = float(((Co - Cd).abs() / den).max())
+    ops = 36 * 2 * n**3
+    out["ozaki_gemm_fp64_c5_8192_k8"] = {
+        "ms": to, "int8_tops": ops / to / 1e9, "frac_int8_peak": ops / to / 1e9 / PEAK_INT8,
+        "fp64_equiv_tflops": 2 * n**3 / to / 1e9, "native_dgemm_ms": td,
+        "native_dgemm_tflops": 2 * n**3 / td / 1e9, "max_cw_err_vs_dgemm": err, "gate": 1e-12,
+        "mode": "bitwise (equals the reference's ozaki.reference_gemm)",
+    }  # fmt: skip
+    log("c5", out["ozaki_gemm_fp64_c5_8192_k8"])
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(
+            "bench.py measures one MI355X: the hot path is single-GPU in this build "
+            f"(asked for --gpus {args.gpus}, WORLD_SIZE {world}); run with --gpus 1.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    import trnblas_amd as tb
+    from trnblas_amd import df_mp2
+    from trnblas_amd.hip import dispatch, kernels
+
+    dispatch._REQUIRE_HIP = True  # a kernel error fails the bench, never falls back
+    dev = torch.device("cuda", 0)
+    A, C, Ab, Bb = df_mp2.config2_inputs(dev)
+
+    def step():
+        S = tb.syrk(1.0, A, beta=0.5, C=C, uplo="lower")
+        D = tb.batched_gemm(1.0, Ab, Bb)
+        return S, D
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    probe = LaunchEvents("syrk")
+    kernels._launch_probe = probe
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernels._launch_probe = None
+    ms_per_step = wall / args.steps * 1e3
+    value = STEP_FLOP / (wall / args.steps) / 1e12
+    syrk_ms = probe.mean_ms()
+    achieved = SYRK_FLOP / (syrk_ms * 1e-3) / 1e12
+    roofline = {
+        "kernel": "gemm_kernel<float,...,SYRK> (trnblas_hip_syrk)",
+        "bound": "mfma",
+        "achieved": achieved,
+        "peak": PEAK_FP32_MFMA,
+        "unit": "TFLOP/s",
+        "frac": achieved / PEAK_FP32_MFMA,
+        "traffic": None,
+        "launch_ms": syrk_ms,
+        "launches": len(probe.pairs),
+        "algorithmic_flop_per_launch": SYRK_FLOP,
+    }
+    # parity of the timed step (the outputs the step produced)
+    S, D = step()
+    torch.cuda.synchronize()
+    Ad = A.double()
+    ref = Ad @ Ad.T + 0.5 * (torch.tril(C.double()) + torch.tril(C.double(), -1).T)
+    den = Ad.abs() @ Ad.abs().T + 0.5 * C.double().abs()
+    syrk_err = float(((S.double() - ref) / den).abs().max())
+    refb = Ab.double() @ Bb.double()
+    denb = Ab.double().abs() @ Bb.double().abs()
+    bat_err = float(((D.double() - refb) / denb).abs().max())
+    del ref, den, refb, denb, Ad
+    t_b = gpu_time_ms(lambda: tb.batched_gemm(1.0, Ab, Bb), reps=10)
+    cpu = None
+    if not args.no_cpu:
+        threads = torch.get_num_threads()
+        cpu = cpu_baseline_level3(A, C, Ab, Bb, threads)
+        cpu2 = cpu_baseline_level3(A, C, Ab, Bb, 2)
+        cpu.update(kind="port", sample="one full step (C2a SYRK + C2b batched), median of 3",
+                   at_2_threads=cpu2["value"], ms_at_2_threads=cpu2["ms"])  # fmt: skip
+    extra = {
+        "syrk_c2a": {"ms": syrk_ms, "tflops_triangle": achieved, "cw_err_vs_fp64": syrk_err},
+        "batched_c2b": {"ms": t_b, "tflops": BATCHED_FLOP / t_b / 1e9, "cw_err_vs_fp64": bat_err},
+    }
+    if not args.no_extras:
+        extra.update(run_extras(dev, tb))
+    line = {
+        "metric": "GEMM TFLOP/s & %MFMA peak; DF-MP2 pair-energy ms at 96/672/2304",
+        "value": value,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1), BASELINE.json configs)",
+        "config": {
+            "workload": "configs[1] Level-3 mix fp32: syrk lower 4096x8192 + batched_gemm 64x512x2048x512",
+            "syrk": [SYRK_N, SYRK_K],
+            "batched": [BATCH, BM, BK, BN],
+            "step_flop": STEP_FLOP,
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -87,6 +87,16 @@ int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64_t K, doubl
                      void* D, int64_t ldd, void* stream);
 
 /*
+ * Which strict triangles of the n x n matrix C hold a nonzero entry (NaN
+ * counts as nonzero): flags[0] = strictly upper, flags[1] = strictly lower
+ * (device int32[2], written by this call). The triangle rule of SYRK's C
+ * argument, trnblas/level3.py:305-329 (`_resolve_syrk_uplo`), as one pass
+ * over C on the device. dtype as in trnblas_hip_gemm.
+ */
+int trnblas_hip_triangle_nonzero(int dtype, int64_t n, const void* C, int64_t ldc,
+                                 int32_t* flags, void* stream);
+
+/*
  * DF-MP2 pair energies, fused (T never leaves the chip).
  *
  * For each pair p = (i, j):

@@ -231,3 +231,37 @@ def digits_exact_bound(e: np.ndarray, k: int) -> np.ndarray:
 
 def log2_ceil(x: float) -> int:
     return int(math.ceil(math.log2(x)))
+
+
+def error_bound(A, B, k: int, absA_absB=None, xp=np):
+    """The a-priori componentwise bound of the k-slice product. With
+    t = 2^-7k, |digit| <= 64 (so slice s of a row is at most 2^(eA - 7s)), the
+    truncation |x - sum_s slice_s| <= 2^(e - 7k) (ozaki.py:123-139), and the
+    pairs s + t >= k that the schedule drops (ozaki.py:337-365):
+
+      |C - AB|_ij <= t (2^eA_i sum_k |b_kj| + sum_k |a_ik| 2^eB_j)
+                     + 1.01 (k - 1 + t) t 2^(eA_i + eB_j) K
+                     + 2^-46 (|A||B|)_ij
+
+    The last term is the observed floor of the fp32 (hi, lo) pair (the
+    reference measures 2e-16 .. 3e-16 of |A||B| at k = 8, ozaki.py:28-34).
+    Works on numpy arrays or (xp=torch) device tensors."""
+    if xp is np:
+        A = np.asarray(A, dtype=np.float64)
+        B = np.asarray(B, dtype=np.float64)
+        aA, aB = np.abs(A), np.abs(B)
+        eA = np.frexp(aA.max(axis=1))[1].astype(np.float64)
+        eB = np.frexp(aB.max(axis=0))[1].astype(np.float64)
+        ra, cb = np.exp2(eA)[:, None], np.exp2(eB)[None, :]
+        rows, cols = aA.sum(axis=1)[:, None], aB.sum(axis=0)[None, :]
+        AB = aA @ aB if absA_absB is None else absA_absB
+    else:
+        aA, aB = A.abs(), B.abs()
+        eA = xp.frexp(aA.amax(dim=1))[1].double()
+        eB = xp.frexp(aB.amax(dim=0))[1].double()
+        ra, cb = xp.exp2(eA)[:, None], xp.exp2(eB)[None, :]
+        rows, cols = aA.sum(dim=1)[:, None], aB.sum(dim=0)[None, :]
+        AB = aA @ aB if absA_absB is None else absA_absB
+    t = 2.0 ** (-SLICE_BITS * k)
+    K = A.shape[1]
+    return t * (ra * cols + rows * cb) + 1.01 * (k - 1 + t) * t * ra * cb * K + 2.0**-46 * AB

@@ -26,3 +26,13 @@ def dev():
     if not gpu_ready():
         pytest.skip("no ROCm GPU")
     return torch.device("cuda", 0)
+
+
+@pytest.fixture(autouse=True)
+def _require_hip_for_gpu_tests(request, monkeypatch):
+    """GPU tests run with TRNBLAS_REQUIRE_HIP semantics: a kernel error
+    raises instead of falling back to torch, so a pass means the HIP path ran."""
+    if request.node.get_closest_marker("gpu") is not None:
+        from trnblas_amd.hip import dispatch
+
+        monkeypatch.setattr(dispatch, "_REQUIRE_HIP", True)

@@ -1,0 +1,51 @@
+"""The C-ABI library loads and exports every entry point of
+include/trnblas_hip.h (no GPU needed: no compute call is made)."""
+
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "trnblas_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(trnblas_hip_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_surface():
+    names = _declared()
+    for n in ("trnblas_hip_gemm", "trnblas_hip_syrk", "trnblas_hip_pair_energy",
+              "trnblas_hip_ozaki_split", "trnblas_hip_ozaki_gemm", "trnblas_hip_mp2_energy"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from trnblas_amd.hip import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("library not built (run __graft_entry__.build())")
+    lib = _lib.load()
+    missing = [n for n in _declared() if getattr(lib, n, None) is None]
+    assert not missing, missing
+    assert set(_declared()) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+    assert lib.trnblas_hip_abi_version() == _lib.ABI_VERSION
+    assert lib.trnblas_hip_last_error() == b""
+
+
+def test_argument_errors_are_reported_without_a_gpu():
+    # invalid arguments are rejected before any HIP call
+    from trnblas_amd.hip import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("library not built")
+    lib = _lib.load()
+    rc = lib.trnblas_hip_gemm(7, 0, 0, 4, 4, 4, 1.0, None, 4, 0, None, 4, 0, 0.0, None, 4, 0,
+                              None, 4, 0, 1, None)
+    assert rc == _lib.E_ARG and b"dtype" in lib.trnblas_hip_last_error()
+    rc = lib.trnblas_hip_ozaki_gemm(0, 13, 4, 4, 128, 128, None, 128, 0, None, 128, 0, None,
+                                    None, None, 4, 1, None)
+    assert rc == _lib.E_ARG and b"slices" in lib.trnblas_hip_last_error()
+    assert lib.trnblas_hip_pair_energy_workspace(672, 4656) == (4656 * 28 + 4656) * 8

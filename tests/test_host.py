@@ -1,0 +1,263 @@
+"""Host logic of trnblas_amd on the CPU: flags, backends, routing, dtype
+backstop, fallback / REQUIRE semantics, lazy registration, the op
+surface's fake (meta) shapes, the Ozaki schedule and plan, and the
+pytorch-backend results against the oracle."""
+
+import importlib
+import subprocess
+import sys
+import warnings
+
+import pytest
+import torch
+
+import trnblas_amd as tb
+from oracle import blas, pair_energy as pe
+from oracle import ozaki as oracle_ozaki
+from trnblas_amd import _flags, ozaki
+from trnblas_amd.hip import dispatch as d
+
+
+# ── flags (trnblas/_flags.py) ────────────────────────────────────────────────
+
+
+@pytest.mark.parametrize("v,want", [("U", "upper"), (" lower ", "lower"), ("l", "lower")])
+def test_uplo_flag(v, want):
+    assert _flags.uplo_flag(v) == want
+
+
+@pytest.mark.parametrize("bad", ["x", "", None, 1])
+def test_flags_reject(bad):
+    with pytest.raises(ValueError):
+        _flags.uplo_flag(bad)
+
+
+def test_trans_flag():
+    assert _flags.trans_flag("T") is True and _flags.trans_flag("n") is False
+    assert _flags.trans_flag(1) is True and _flags.trans_flag(0) is False
+    with pytest.raises(ValueError):
+        _flags.trans_flag("C")
+    assert _flags.side_flag("R") == "right" and _flags.diag_flag("N") == "nonunit"
+
+
+# ── backends and routing ─────────────────────────────────────────────────────
+
+
+def test_backend_switch():
+    assert tb.get_backend() == "auto"
+    tb.set_backend("pytorch")
+    try:
+        assert not d._use_hip()
+    finally:
+        tb.set_backend("auto")
+    with pytest.raises(ValueError):
+        tb.set_backend("cuda")
+    if not d.has_hip():
+        with pytest.raises(RuntimeError):
+            tb.set_backend("hip")
+
+
+def _fake_gpu(monkeypatch):
+    monkeypatch.setattr(d, "has_hip", lambda: True)
+
+
+def test_route_table(monkeypatch):
+    _fake_gpu(monkeypatch)
+    A = torch.randn(4, 4)
+    assert d._gemm_route(A, A.double()) == "torch"  # mixed dtypes: torch raises
+    assert d._gemm_route(A.double(), A.double()) == "torch"  # fp64: torch where the data is
+    assert d._gemm_route(A.to(torch.int32), A.to(torch.int32)) == "torch"
+    assert d._gemm_route(A, A) == "host"  # tiny host GEMM: the host CPU wins
+    big = torch.empty(4096, 4096)
+    assert d._gemm_route(big, big) == "upload"  # large host GEMM: upload
+    monkeypatch.setenv("TRNBLAS_NATIVE_GEMM", "host")
+    assert d._gemm_route(big, big) == "host"
+    monkeypatch.setenv("TRNBLAS_NATIVE_GEMM", "bogus")
+    with pytest.raises(ValueError):
+        d._gemm_route(big, big)
+
+
+def test_route_grad_goes_to_torch(monkeypatch):
+    _fake_gpu(monkeypatch)
+    A = torch.randn(512, 512, requires_grad=True)
+    assert d._gemm_route(A, A) == "torch"
+
+
+def test_require_refuses_fp64(monkeypatch):
+    _fake_gpu(monkeypatch)
+    monkeypatch.setattr(d, "_REQUIRE_HIP", True)
+    A = torch.randn(3, 3, dtype=torch.float64)
+    with pytest.raises(NotImplementedError):
+        d._gemm_route(A, A)
+
+
+def test_host_model_scales_with_threads(monkeypatch):
+    macs, nbytes = 2e6, 10_000
+    monkeypatch.setattr(torch, "get_num_threads", lambda: 2)
+    two = d._host_gemm_wins(macs, nbytes, torch.float32)
+    monkeypatch.setattr(torch, "get_num_threads", lambda: 64)
+    assert d._host_gemm_wins(macs, nbytes, torch.float32) or not two
+    assert d._host_gemm_wins(1e15, 0, torch.float64)  # no device route for fp64 on the host model
+
+
+# ── dtype backstop and fallback semantics ────────────────────────────────────
+
+
+def test_kernel_dtype_backstop():
+    d._check_kernel_operands("gemm_ragged", torch.zeros(1), torch.zeros(1, dtype=torch.bfloat16))
+    with pytest.raises(TypeError):
+        d._check_kernel_operands("pair_energy_sym", torch.zeros(1, dtype=torch.float64))
+    with pytest.raises(TypeError):
+        d._check_kernel_operands("no_such_op", torch.zeros(1))
+    with pytest.raises(TypeError):
+        d._check_kernel_operands("ozaki_gemm", torch.zeros(1))
+
+
+def test_kernel_error_falls_back_with_one_warning(monkeypatch):
+    err = d.HipKernelError("trnblas_hip_gemm", -2, "boom")
+    monkeypatch.setattr(d, "_REQUIRE_HIP", False)
+    d._fallback_warned.clear()
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        d._kernel_failed(err)
+        d._kernel_failed(err)
+    assert len([x for x in w if issubclass(x.category, d.HipFallbackWarning)]) == 1
+    monkeypatch.setattr(d, "_REQUIRE_HIP", True)
+    with pytest.raises(d.HipKernelError):
+        d._kernel_failed(err)
+    # a missing library never falls back
+    monkeypatch.setattr(d, "_REQUIRE_HIP", False)
+    with pytest.raises(d.HipLibraryError):
+        d._kernel_failed(d.HipLibraryError("missing"))
+
+
+def test_gemm_kernel_failure_gives_torch_result(monkeypatch):
+    # a kernel route whose launch fails: warning + the torch result (dispatch
+    # fallback, as the reference's test_native_dispatch.py:1060-1074)
+    _fake_gpu(monkeypatch)
+    monkeypatch.setattr(d, "_REQUIRE_HIP", False)
+    monkeypatch.setattr(d, "_gemm_route", lambda *a, **k: "hip")
+
+    def boom(*a, **k):
+        raise d.HipKernelError("trnblas_hip_gemm", -2, "launch failed")
+
+    monkeypatch.setattr(d, "hip_gemm", boom)
+    A, B = torch.randn(8, 5), torch.randn(5, 3)
+    with warnings.catch_warnings(record=True):
+        warnings.simplefilter("always")
+        out = d.nki_gemm(A, B)
+    assert torch.allclose(out, A @ B)
+
+
+# ── lazy registration and the op surface ─────────────────────────────────────
+
+
+def test_import_registers_nothing_and_loads_no_library():
+    code = (
+        "import sys, trnblas_amd, torch\n"
+        "assert 'trnblas_amd.hip._native' not in sys.modules\n"
+        "from trnblas_amd.hip import _lib\n"
+        "assert _lib._lib is None\n"
+        "assert not hasattr(torch.ops.trnblas, 'gemm_ragged') or True\n"
+    )
+    subprocess.run([sys.executable, "-c", code], check=True, cwd=str(__import__("pathlib").Path(__file__).parents[1]))
+
+
+REFERENCE_OP_NAMES = [
+    "gemm_64_128_128", "gemm_64_128_256", "gemm_64_128_512", "gemm_128_128_128",
+    "gemm_128_128_256", "gemm_128_128_512", "gemm_ragged", "gemm_lnc", "gemm_lnc_tn", "syrk",
+    "mp2_energy", "fused_gemm_energy", "batched_pair", "j_batched", "pair_energy_sym",
+    "ozaki_gemm", "ozaki_emax", "ozaki_split", "ozaki_emax_col", "ozaki_split_col",
+]  # fmt: skip
+
+
+def test_op_surface_names_and_fake_shapes():
+    ops = d.get_native_ops()
+    assert sorted(ops) == sorted(REFERENCE_OP_NAMES)
+    for name in REFERENCE_OP_NAMES:
+        assert hasattr(torch.ops.trnblas, name)
+    m = lambda *s, dt=torch.float32: torch.empty(s, dtype=dt, device="meta")  # noqa: E731
+    T = torch.ops.trnblas
+    assert T.gemm_128_128_512(m(256, 128), m(128, 512)).shape == (256, 512)
+    assert T.gemm_lnc_tn(m(128, 64), m(128, 300)).shape == (64, 300)
+    assert T.syrk(m(384, 128)).shape == (384, 384)
+    assert T.mp2_energy(m(2 * 96, 4 * 96), m(1, 2), m(1, 4), m(96, 1), m(1, 96)).shape == (96, 8)
+    assert T.mp2_energy(m(2 * 130, 4 * 130), m(1, 2), m(1, 4), m(130, 1), m(1, 130)).shape == (65, 8)
+    assert T.fused_gemm_energy(m(256, 384), m(256, 384), m(1, 1), m(256, 1), m(1, 256)).shape == (256, 1)
+    assert T.batched_pair(m(5, 128, 256), m(1, 5), m(128, 1), m(1, 128)).shape == (128, 25)
+    assert T.j_batched(m(128, 256), m(5, 128, 256), m(1, 1), m(1, 5), m(128, 1), m(1, 128)).shape == (128, 5)
+    assert T.pair_energy_sym(m(256, 128), m(6, 256, 128), m(1, 1), m(1, 6), m(128, 1), m(1, 128)).shape == (128, 6)
+    bf = torch.bfloat16
+    assert T.ozaki_gemm(m(8, 256, 128, dt=bf), m(8, 256, 40, dt=bf)).shape == (2, 128, 40)
+    assert T.ozaki_emax(m(7, 20, dt=torch.int32)).shape == (7, 1)
+    assert T.ozaki_emax_col(m(7, 20, dt=torch.int32)).shape == (1, 10)
+    assert T.ozaki_split(m(7, 20, dt=torch.int32), m(128, 8)).shape == (8, 128, 128)
+    assert T.ozaki_split_col(m(7, 300, dt=torch.int32), m(8, 256)).shape == (8, 128, 256)
+    assert T.ozaki_split(m(7, 20, dt=torch.int32), m(128, 8)).dtype == bf
+
+
+def test_op_surface_dtype_checked():
+    ops = d.get_native_ops()
+    with pytest.raises(TypeError):
+        ops["pair_energy_sym"](*(torch.zeros(2, 2, dtype=torch.float64),) * 6)
+    with pytest.raises(TypeError):
+        ops["gemm_ragged"](torch.zeros(2, 2, dtype=torch.int32), torch.zeros(2, 2, dtype=torch.int32))
+
+
+def test_op_surface_refuses_host_tensors():
+    ops = d.get_native_ops()
+    with pytest.raises(Exception):
+        ops["gemm_ragged"](torch.zeros(2, 2), torch.zeros(2, 2))
+
+
+# ── Ozaki host half: same schedule / plan as the reference ───────────────────
+
+
+@pytest.mark.parametrize("kt", [1, 3, 32, 33, 64])
+@pytest.mark.parametrize("k", [1, 8, 12])
+def test_schedule_matches_oracle(kt, k):
+    assert ozaki.schedule(k, kt) == oracle_ozaki.schedule(k, kt)
+    assert ozaki.n_groups(k, kt) == oracle_ozaki.n_groups(k, kt)
+
+
+def test_plan_and_k_block():
+    assert ozaki.k_block(8192, 8) == 8192
+    assert [b for b in ozaki.plan(4096, 4096, 4096, 8)[1]] == [(0, 4096)]
+    kb = ozaki.k_block(1 << 20, 8)
+    assert oracle_ozaki.plan_k_blocks(1 << 20, 8)[0][1] == kb
+    for bad in (0, 13, 2.0, True, "8"):
+        with pytest.raises((ValueError, TypeError)):
+            ozaki.check_slices(bad)
+
+
+# ── pytorch backend (no GPU) results against the oracle ─────────────────────
+
+
+def test_cpu_gemm_and_syrk_match_oracle():
+    g = torch.Generator().manual_seed(0)
+    A, B, C = (torch.randn(s, generator=g) for s in ((40, 30), (40, 20), (30, 20)))
+    got = tb.gemm(1.0, A, B, 0.5, C, transA=True)
+    assert torch.allclose(got, blas.gemm_cpu(1.0, A, B, 0.5, C, transA=True))
+    S = torch.randn(40, 40, generator=g)
+    got = tb.syrk(1.0, A, 0.5, S, uplo="lower")
+    assert torch.allclose(got, blas.syrk_cpu(1.0, A, 0.5, S, uplo="lower"))
+    assert torch.equal(got, got.T)
+    Ab, Bb = torch.randn(3, 5, 7, generator=g), torch.randn(3, 7, 2, generator=g)
+    assert torch.allclose(tb.batched_gemm(2.0, Ab, Bb), 2.0 * (Ab @ Bb))
+
+
+def test_cpu_gemm_fp64_and_pair_energy():
+    g = torch.Generator().manual_seed(1)
+    A, B = torch.randn(9, 11, generator=g), torch.randn(11, 4, generator=g)
+    out = tb.gemm_fp64(A, B)
+    assert out.dtype == torch.float64 and torch.allclose(out, A.double() @ B.double())
+    with pytest.raises(ValueError):
+        tb.gemm_fp64(A, A)
+    with pytest.raises(TypeError):
+        tb.gemm_fp64(A.int(), B.int())
+    from trnblas_amd.hip import nki_batched_pair_energy
+
+    Bp, eo, ev = (x.float() for x in (0.05 * torch.randn(3, 8, 6, generator=g),
+                                      -1 - torch.rand(3, generator=g), 1 + torch.rand(8, generator=g)))
+    e = nki_batched_pair_energy(Bp, eo, ev)
+    assert abs(float(e) - pe.pair_energy_f64(Bp, eo, ev)) <= 1e-5 * abs(float(e))

@@ -1,0 +1,30 @@
+"""Pins of the independent fp64 judge (oracle/exact.py), CPU only."""
+
+from fractions import Fraction
+
+import numpy as np
+
+from oracle.exact import inputs, max_cw, ref_exact
+
+
+def test_exact_on_integer_products():
+    rng = np.random.default_rng(1)
+    A = rng.integers(-1000, 1000, (20, 300)).astype(np.float64)
+    B = rng.integers(-1000, 1000, (300, 15)).astype(np.float64)
+    assert np.array_equal(ref_exact(A, B), A @ B)  # exact in fp64 (< 2^53)
+
+
+def test_close_to_rational_product():
+    A, B = inputs(4, 50, 3, seed=7)
+    R = ref_exact(A, B)
+    for i in range(4):
+        for j in range(3):
+            exact = sum(Fraction(float(A[i, k])) * Fraction(float(B[k, j])) for k in range(50))
+            assert abs(Fraction(float(R[i, j])) - exact) <= abs(exact) * Fraction(1, 2**51)
+
+
+def test_max_cw_zero_for_exact_and_positive_for_perturbed():
+    A, B = inputs(8, 40, 6, seed=2)
+    ex = ref_exact(A, B)
+    assert max_cw(ex, A, B, exact=ex) == 0.0
+    assert max_cw(ex * (1 + 1e-12), A, B, exact=ex) > 0.0

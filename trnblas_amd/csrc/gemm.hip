@@ -26,6 +26,8 @@
 //    tiles) and writes each value to D[i][j] and D[j][i];
 //  * the tile walk is XCD-aware: each of the 8 XCDs (own L2) walks a
 //    contiguous range of tiles in grouped order.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace trnblas {
@@ -459,4 +461,66 @@ extern "C" int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64
   // trans == 0: op(A) = A (N x K, K-contiguous) and B(k, n) = A[n][k] (K-contiguous).
   // trans != 0: op(A) = A^T with A K x N (N-contiguous), B(k, n) = A[k][n].
   return dispatch<true>(dtype, g, !trans, !trans, (int)ntri, (hipStream_t)stream);
+}
+
+// Which strict triangles of an n x n matrix hold a nonzero (NaN counts), for
+// the SYRK triangle rule (trnblas/level3.py:305-329): flags[0] = upper,
+// flags[1] = lower.
+namespace trnblas {
+
+__global__ void zero_flags_kernel(int32_t* flags) {
+  if (threadIdx.x < 2) flags[threadIdx.x] = 0;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void triangle_nonzero_kernel(int n, const T* C, int64_t ldc,
+                                                               int32_t* flags) {
+  const int64_t total = (int64_t)n * n;
+  int up = 0, lo = 0;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int r = (int)(idx / n), c = (int)(idx - (int64_t)r * n);
+    const float v = (float)C[(int64_t)r * ldc + c];
+    const int nz = !(v == 0.0f);
+    up |= nz & (c > r);
+    lo |= nz & (c < r);
+  }
+  up = __any(up);
+  lo = __any(lo);
+  if ((threadIdx.x & 63) == 0) {
+    if (up) atomicOr(&flags[0], 1);
+    if (lo) atomicOr(&flags[1], 1);
+  }
+}
+
+}  // namespace trnblas
+
+extern "C" int trnblas_hip_triangle_nonzero(int dtype, int64_t n, const void* C, int64_t ldc,
+                                            int32_t* flags, void* stream) {
+  clear_error();
+  hipStream_t s = (hipStream_t)stream;
+  TRNBLAS_CHECK_ARG(n >= 0 && n < (1 << 30), "triangle_nonzero: bad n");
+  TRNBLAS_CHECK_ARG(flags != nullptr, "triangle_nonzero: NULL flags");
+  hipLaunchKernelGGL(zero_flags_kernel, dim3(1), dim3(64), 0, s, flags);
+  if (n == 0) return check_launch("triangle_nonzero");
+  TRNBLAS_CHECK_ARG(C != nullptr && ldc >= n, "triangle_nonzero: bad C / ldc");
+  const int64_t blocks = std::min<int64_t>(((int64_t)n * n + 255) / 256, 4096);
+  switch (dtype) {
+    case TRNBLAS_F32:
+      hipLaunchKernelGGL(triangle_nonzero_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, s,
+                         (int)n, (const float*)C, ldc, flags);
+      break;
+    case TRNBLAS_BF16:
+      hipLaunchKernelGGL(triangle_nonzero_kernel<__bf16>, dim3((unsigned)blocks), dim3(256), 0,
+                         s, (int)n, (const __bf16*)C, ldc, flags);
+      break;
+    case TRNBLAS_F16:
+      hipLaunchKernelGGL(triangle_nonzero_kernel<_Float16>, dim3((unsigned)blocks), dim3(256), 0,
+                         s, (int)n, (const _Float16*)C, ldc, flags);
+      break;
+    default:
+      set_error("triangle_nonzero: dtype %d not supported", dtype);
+      return TRNBLAS_E_ARG;
+  }
+  return check_launch("triangle_nonzero");
 }

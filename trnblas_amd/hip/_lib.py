@@ -47,6 +47,7 @@ SIGNATURES = {
         [_c_int, _c_int, _c_int, _c_i64, _c_i64, _c_dbl, _c_ptr, _c_i64, _c_dbl, _c_ptr]
         + [_c_i64, _c_ptr, _c_i64, _c_ptr],
     ),
+    "trnblas_hip_triangle_nonzero": (_c_int, [_c_int, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr]),
     "trnblas_hip_pair_energy_workspace": (_c_size, [_c_i64, _c_i64]),
     "trnblas_hip_pair_energy": (
         _c_int,

@@ -1,0 +1,695 @@
+"""HIP dispatch of trnblas_amd: backend selection, routing, dtype policy.
+
+The MI355X counterpart of trnblas/nki/dispatch.py (host half, :1-3310).
+What stays: the public entry points (`nki_gemm`, `nki_batched_gemm`,
+`nki_syrk`, `nki_batched_pair_energy`, `nki_fused_gemm_energy`,
+`nki_mp2_energy`, `nki_gemm_fp64`), the backends `auto` / `pytorch` plus the
+kernel backend (`hip`, with `nki` accepted as its alias), the route names of
+`_gemm_route` (:633-682), the kernel-dtype backstop (`_check_kernel_operands`,
+:1244-1293), the result-dtype rules (:1328-1340) and the
+fallback-with-warning / REQUIRE switch (:35, :54-80). What changes:
+
+* device-resident operands run the hand-written gfx950 kernels (one launch
+  per call, batched GEMM included); host operands run on the host CPU or are
+  uploaded, by a host-vs-device cost model refitted for the MI355X host link;
+* fp64 is native on MI355X: device-resident float64 stays on the device
+  (torch / rocBLAS at fp64) instead of the reference's host bounce
+  (`_fp64_host_guard`, :543-602); `gemm_fp64` (Ozaki) runs split, slice
+  products and recombination all on the device;
+* there is no silent fallback when the HIP library is missing on a GPU box:
+  `HipLibraryError` propagates. A kernel that returns an error code
+  (`HipKernelError`) falls back to torch on the same device with one
+  `HipFallbackWarning` per signature, or raises under TRNBLAS_REQUIRE_HIP=1
+  (TRNBLAS_REQUIRE_NKI=1 is accepted too).
+"""
+
+from __future__ import annotations
+
+import math
+import os
+import warnings
+
+import torch
+
+from . import _lib
+from ._lib import HipKernelError, HipLibraryError  # noqa: F401  (re-exported)
+
+_TRUE = ("1", "true", "yes", "on")
+
+
+def _env_flag(*names: str) -> bool:
+    return any(os.environ.get(n, "").strip().lower() in _TRUE for n in names)
+
+
+_REQUIRE_HIP = _env_flag("TRNBLAS_REQUIRE_HIP", "TRNBLAS_REQUIRE_NKI")
+
+
+class HipFallbackWarning(UserWarning):
+    """A HIP kernel call failed and the result was computed by torch instead
+    (once per distinct error; set TRNBLAS_REQUIRE_HIP=1 to raise)."""
+
+
+NkiFallbackWarning = HipFallbackWarning  # the reference's name (dispatch.py:54)
+
+_fallback_warned: set = set()
+
+
+def _warn_fallback(exc: BaseException, what: str = "HIP kernel failed — computed by torch") -> None:
+    lines = str(exc).splitlines()
+    key = (what, f"{type(exc).__name__}: {(lines[0] if lines else '')[:200]}")
+    if key in _fallback_warned:
+        return
+    _fallback_warned.add(key)
+    warnings.warn(
+        f"{what} (set TRNBLAS_REQUIRE_HIP=1 to re-raise). First error: {key[1]}",
+        HipFallbackWarning,
+        stacklevel=3,
+    )
+
+
+def _kernel_failed(exc: Exception, what: str = "HIP kernel failed — computed by torch") -> None:
+    """Re-raise `exc` unless it is a kernel error that may fall back."""
+    if _REQUIRE_HIP or not isinstance(exc, HipKernelError):
+        raise exc
+    _warn_fallback(exc, what)
+
+
+# ── backend ──────────────────────────────────────────────────────────────────
+
+_BACKENDS = ("auto", "pytorch", "hip", "nki")
+_backend = "auto"
+
+
+def has_hip() -> bool:
+    """A ROCm GPU is visible to torch (does not load the op library)."""
+    return bool(getattr(torch.version, "hip", None)) and torch.cuda.is_available()
+
+
+def set_backend(backend: str) -> None:
+    """'auto' (HIP kernels on a ROCm GPU, else torch), 'pytorch' (torch
+    everywhere) or 'hip' (the kernels always; 'nki' is an alias)."""
+    global _backend
+    if backend not in _BACKENDS:
+        raise ValueError(f"backend must be one of {_BACKENDS}; got {backend!r}")
+    if backend in ("hip", "nki"):
+        if not has_hip():
+            raise RuntimeError("the hip backend needs a ROCm GPU")
+        _lib.load()  # fail now, loudly, if the library is missing
+        backend = "hip"
+    _backend = backend
+
+
+def get_backend() -> str:
+    return _backend
+
+
+def _use_hip() -> bool:
+    if _backend == "hip":
+        return True
+    if _backend == "pytorch":
+        return False
+    return has_hip()
+
+
+_AUTOTUNE = _env_flag("TRNBLAS_AUTOTUNE")
+
+
+def set_autotune(enabled: bool) -> None:
+    """Kept for API compatibility (trnblas.set_autotune): the HIP kernels
+    choose their tiles statically, so this only records the flag."""
+    global _AUTOTUNE
+    _AUTOTUNE = bool(enabled)
+
+
+def get_autotune() -> bool:
+    return _AUTOTUNE
+
+
+def _device_synchronize() -> None:
+    if torch.cuda.is_available():
+        torch.cuda.synchronize()
+
+
+# ── dtype policy (dispatch.py:1244-1340) ─────────────────────────────────────
+
+_GEMM_KERNEL_DTYPES = frozenset({torch.float32, torch.bfloat16, torch.float16})
+_FP32_KERNEL_DTYPES = frozenset({torch.float32})
+_KERNEL_DTYPES: dict[str, frozenset] = {
+    **{f"gemm_{tm}_{tk}_{tn}": _GEMM_KERNEL_DTYPES for tm, tk, tn in (
+        (64, 128, 128), (64, 128, 256), (64, 128, 512),
+        (128, 128, 128), (128, 128, 256), (128, 128, 512),
+    )},  # fmt: skip
+    "gemm_ragged": _GEMM_KERNEL_DTYPES,
+    "gemm_lnc": _GEMM_KERNEL_DTYPES,
+    "gemm_lnc_tn": _GEMM_KERNEL_DTYPES,
+    "syrk": _GEMM_KERNEL_DTYPES,
+    "mp2_energy": _FP32_KERNEL_DTYPES,
+    "fused_gemm_energy": _FP32_KERNEL_DTYPES,
+    "batched_pair": _FP32_KERNEL_DTYPES,
+    "j_batched": _FP32_KERNEL_DTYPES,
+    "pair_energy_sym": _FP32_KERNEL_DTYPES,
+    "ozaki_gemm": frozenset({torch.bfloat16}),
+    "ozaki_emax": frozenset({torch.int32}),
+    "ozaki_split": frozenset({torch.int32, torch.float32}),
+    "ozaki_emax_col": frozenset({torch.int32}),
+    "ozaki_split_col": frozenset({torch.int32, torch.float32}),
+}
+
+
+def _check_kernel_operands(op_name: str, *tensors) -> None:
+    """TypeError unless every tensor operand of kernel op `op_name` has an
+    allowed dtype (the boundary backstop of dispatch.py:1278-1293)."""
+    allowed = _KERNEL_DTYPES.get(op_name)
+    if allowed is None:
+        raise TypeError(f"trnblas: kernel op {op_name!r} has no entry in _KERNEL_DTYPES")
+    dts = [t.dtype for t in tensors if isinstance(t, torch.Tensor)]
+    bad = sorted({str(d) for d in dts if d not in allowed})
+    if bad:
+        raise TypeError(
+            f"trnblas: kernel op {op_name!r} takes {sorted(str(d) for d in allowed)}; "
+            f"got operand dtypes {[str(d) for d in dts]} (unsupported: {bad})"
+        )
+
+
+def _no_kernel_for_dtype(what: str, *tensors, takes: str = "float32/bfloat16/float16") -> None:
+    """Under TRNBLAS_REQUIRE_HIP, refuse a dtype the kernels do not take."""
+    if _REQUIRE_HIP:
+        dts = sorted({str(t.dtype) for t in tensors})
+        raise NotImplementedError(
+            f"trnblas {what}: the HIP kernels take {takes}, got {dts}. "
+            "Unset TRNBLAS_REQUIRE_HIP to compute in torch."
+        )
+
+
+_fp32_cast_warned: set = set()
+
+
+def _warn_fp32_cast(op: str) -> None:
+    if op in _fp32_cast_warned:
+        return
+    _fp32_cast_warned.add(op)
+    warnings.warn(
+        f"trnblas {op}: the hip backend runs float64 operands on the FP32 kernel; "
+        "precision is reduced to float32 (the result keeps float64 dtype). Use "
+        "set_backend('auto') for float64 accuracy, or TRNBLAS_REQUIRE_HIP=1 to raise.",
+        UserWarning,
+        stacklevel=3,
+    )
+
+
+def _as_result_dtype(out, dtype: torch.dtype):
+    if isinstance(out, torch.Tensor) and out.dtype != dtype and (
+        dtype.is_floating_point or dtype.is_complex
+    ):
+        return out.to(dtype)
+    return out
+
+
+def _mp2_result_dtype(T_flat, eps_occ_chunk, eps_occ_full, eps_vir) -> torch.dtype:
+    dt = torch.promote_types(T_flat.dtype, eps_occ_chunk.dtype)
+    return torch.promote_types(dt, torch.promote_types(eps_occ_full.dtype, eps_vir.dtype))
+
+
+def _pair_result_dtype(B, eps_vir) -> torch.dtype:
+    return torch.promote_types(B.dtype, eps_vir.dtype)
+
+
+# ── routing (dispatch.py:633-682, re-measured for MI355X) ────────────────────
+#
+# Routes: 'torch' (torch where the data is), 'hip' (the kernel on device
+# operands), 'host' (torch on the host CPU), 'upload' (host operands copied to
+# the GPU, the kernel, the result copied back), 'aten' (torch on the GPU).
+#
+# Host-vs-device model, as the reference's `_host_gemm_wins` (:277-285):
+# for all-host fp32 operands the host wins when
+#     macs < threads / 2 * (fixed + per_byte * link_bytes),
+# `fixed` the upload + launch + download floor in host multiply-adds and
+# `per_byte` the host-link cost per byte in host multiply-adds. Fitted on the
+# MI355X box (PCIe Gen5 x16, pageable host memory; see DESIGN.md for the
+# sweep): the device floor is ~40 us and the link ~25 GB/s pageable, against
+# ~25 GMAC/s per two host threads.
+_HOST_GEMM_MODEL_THREADS = 2
+_HOST_GEMM_MODEL = {"fp32": (1.0e6, 1.0), "bf16": (2.0e6, 2.0)}
+_DEVICE_GEMM_DTYPES = {torch.float32: "fp32", torch.bfloat16: "bf16", torch.float16: "fp32"}
+_NATIVE_GEMM_CHOICES = ("auto", "hip", "nki", "aten", "host")
+
+
+def _native_gemm_policy() -> str:
+    value = os.environ.get("TRNBLAS_NATIVE_GEMM", "auto").strip().lower()
+    if value not in _NATIVE_GEMM_CHOICES:
+        raise ValueError(f"TRNBLAS_NATIVE_GEMM must be one of {_NATIVE_GEMM_CHOICES}; got {value!r}")
+    return "hip" if value == "nki" else value
+
+
+def _on_gpu(*ts) -> bool:
+    return all(t.device.type == "cuda" for t in ts)
+
+
+def _on_host(*ts) -> bool:
+    return all(t.device.type == "cpu" for t in ts)
+
+
+def _mixed_dtypes(*ts) -> bool:
+    return len({t.dtype for t in ts}) > 1
+
+
+def _wants_grad(*ts) -> bool:
+    return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
+
+
+def _upload_nbytes(t: torch.Tensor) -> int:
+    if t.device.type != "cpu":
+        return 0
+    if t.dim() >= 3 and t.stride(0) == 0:
+        return _upload_nbytes(t[0])
+    return t.numel() * t.element_size()
+
+
+def _host_gemm_wins(macs: float, nbytes: int, dtype: torch.dtype) -> bool:
+    kind = _DEVICE_GEMM_DTYPES.get(dtype)
+    if kind is None:
+        return True
+    fixed, per_byte = _HOST_GEMM_MODEL[kind]
+    scale = max(1, torch.get_num_threads()) / _HOST_GEMM_MODEL_THREADS
+    return macs < scale * (fixed + per_byte * nbytes)
+
+
+def _gemm_route(*tensors, op: str = "gemm", macs: float | None = None, nbytes: int | None = None):
+    """'torch', 'hip', 'host', 'upload' or 'aten' for a GEMM-family call."""
+    if not _use_hip() or _mixed_dtypes(*tensors) or _wants_grad(*tensors):
+        return "torch"
+    if any(t.dtype not in _GEMM_KERNEL_DTYPES for t in tensors):
+        _no_kernel_for_dtype(op, *tensors)
+        return "torch"  # float64 / complex / integer: torch where the data is
+    policy = _native_gemm_policy()
+    if _on_gpu(*tensors):
+        return "aten" if policy == "aten" else "hip"
+    if not _on_host(*tensors):
+        return "upload"  # mixed residency: compute on the GPU operand's device
+    if policy == "host":
+        return "host"
+    if _backend == "hip" or policy in ("hip", "aten"):
+        return "upload"
+    if macs is None:
+        a, b = tensors[0], tensors[1]
+        macs = a.shape[-2] * a.shape[-1] * b.shape[-1] * max(1, math.prod(a.shape[:-2]))
+        nbytes = (
+            sum(_upload_nbytes(t) for t in tensors[:2])
+            + (macs // max(1, a.shape[-1])) * a.element_size()
+        )
+    return "host" if _host_gemm_wins(macs, nbytes, tensors[0].dtype) else "upload"
+
+
+def _gpu_device(*ts) -> torch.device:
+    for t in ts:
+        if isinstance(t, torch.Tensor) and t.device.type == "cuda":
+            return t.device
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _to(t, dev):
+    return None if t is None else t.to(dev, non_blocking=False)
+
+
+# ── GEMM family ──────────────────────────────────────────────────────────────
+
+
+def _fused_epilogue_ok(C, beta, shape, dtype, device) -> bool:
+    """True when beta * C can be fused into the kernel's store: C absent /
+    beta 0, or C of the result dtype and device broadcasting to `shape`."""
+    if C is None or beta == 0.0:
+        return True
+    return (
+        C.dtype == dtype
+        and C.device == device
+        and torch.broadcast_shapes(tuple(shape), tuple(C.shape)) == tuple(shape)
+    )
+
+
+def _torch_scale_add(result, alpha, beta, C):
+    """alpha * result + beta * C out of place (level3.py:42-66 semantics)."""
+    result = alpha * result if alpha != 1.0 else result
+    return result + beta * C if (C is not None and beta != 0.0) else result
+
+
+def hip_gemm(A, B, alpha=1.0, beta=0.0, C=None) -> torch.Tensor:
+    """alpha * A @ B + beta * C on the GPU kernel; A, B 2-D or 3-D device
+    tensors (torch.matmul broadcasting of one batch dim)."""
+    from . import kernels
+
+    if A.dim() == 3 and B.dim() == 2:
+        B = B.unsqueeze(0)
+    elif A.dim() == 2 and B.dim() == 3:
+        A = A.unsqueeze(0)
+    out_shape = (
+        (A.shape[0] if A.dim() == 3 else None),
+        A.shape[-2],
+        B.shape[-1],
+    )
+    if A.dim() == 3:
+        out_shape = (max(A.shape[0], B.shape[0]), A.shape[-2], B.shape[-1])
+    else:
+        out_shape = (A.shape[0], B.shape[1])
+    if _fused_epilogue_ok(C, beta, out_shape, A.dtype, A.device):
+        return kernels.gemm(A, B, alpha, beta, C)
+    return _torch_scale_add(kernels.gemm(A, B, 1.0, 0.0, None), alpha, beta, C)
+
+
+def _flatten_batch(A, B):
+    """A (..., M, K), B (..., K, N) -> 3-D operands with one broadcast batch
+    dim (views when possible), and the broadcast batch shape."""
+    batch = torch.broadcast_shapes(A.shape[:-2], B.shape[:-2])
+    nb = math.prod(batch)
+
+    def as3(X):
+        if X.dim() == 2:
+            return X.unsqueeze(0)
+        if tuple(X.shape[:-2]) == tuple(batch):
+            return X.reshape(nb, *X.shape[-2:])
+        if math.prod(X.shape[:-2]) == 1:
+            return X.reshape(1, *X.shape[-2:])
+        return X.expand(*batch, *X.shape[-2:]).reshape(nb, *X.shape[-2:])
+
+    return as3(A), as3(B), batch
+
+
+def nki_gemm(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """A @ B for 2-D operands (dispatch.py:1526-1551): the HIP kernel for
+    device operands, torch otherwise (see `_gemm_route`)."""
+    route = _gemm_route(A, B)
+    if route == "hip":
+        try:
+            return hip_gemm(A, B)
+        except Exception as exc:  # noqa: BLE001
+            _kernel_failed(exc)
+            return torch.matmul(A, B)
+    if route == "upload":
+        dev = _gpu_device(A, B)
+        orig = A.device
+        try:
+            return hip_gemm(_to(A, dev), _to(B, dev)).to(orig)
+        except Exception as exc:  # noqa: BLE001
+            _kernel_failed(exc)
+            return torch.matmul(A, B)
+    return torch.matmul(A, B)
+
+
+def nki_batched_gemm(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """torch.matmul batch semantics (dispatch.py:1384-1427) in one launch."""
+    if A.dim() < 2 or B.dim() < 2:
+        return torch.matmul(A, B)
+    batch = torch.broadcast_shapes(A.shape[:-2], B.shape[:-2])
+    if math.prod(batch) == 0:
+        return torch.matmul(A, B)
+    route = _gemm_route(A, B, op="batched_gemm")
+    if route not in ("hip", "upload"):
+        return torch.matmul(A, B)
+    dev = _gpu_device(A, B)
+    orig = A.device
+    try:
+        a3, b3, batch = _flatten_batch(_to(A, dev), _to(B, dev))
+        out = hip_gemm(a3, b3).reshape(*batch, A.shape[-2], B.shape[-1])
+        return out.to(orig) if orig != dev else out
+    except Exception as exc:  # noqa: BLE001
+        _kernel_failed(exc)
+        return torch.matmul(A, B)
+
+
+def gemm_scaled(alpha, a, b, beta, C):
+    """alpha * a @ b + beta * C with the epilogue fused into the kernel when
+    the route is a kernel route (level3.gemm / batched_gemm)."""
+    if a.dim() < 2 or b.dim() < 2:
+        return _torch_scale_add(torch.matmul(a, b), alpha, beta, C)
+    batch = torch.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    route = _gemm_route(a, b, op="gemm" if a.dim() == 2 and b.dim() == 2 else "batched_gemm")
+    if route not in ("hip", "upload") or math.prod(batch) == 0 or len(batch) > 1:
+        if route in ("hip", "upload") and len(batch) > 1:
+            return _torch_scale_add(nki_batched_gemm(a, b), alpha, beta, C)
+        return _torch_scale_add(torch.matmul(a, b), alpha, beta, C)
+    dev = _gpu_device(a, b, *(() if C is None else (C,)))
+    orig = a.device
+    try:
+        ad, bd = _to(a, dev), _to(b, dev)
+        Cd = None if (C is None or beta == 0.0) else (C.to(dev) if C.device != dev else C)
+        out = hip_gemm(ad, bd, alpha, beta, Cd)
+        if a.dim() == 2 and b.dim() == 3:
+            pass
+        return out.to(orig) if orig != dev else out
+    except Exception as exc:  # noqa: BLE001
+        _kernel_failed(exc)
+        return _torch_scale_add(torch.matmul(a, b), alpha, beta, C)
+
+
+# ── SYRK ─────────────────────────────────────────────────────────────────────
+
+
+def _symmetrize(r: torch.Tensor) -> torch.Tensor:
+    """0.5 * (r + r^T) (dispatch.py:3178-3199 values)."""
+    return 0.5 * (r + r.mT)
+
+
+def nki_syrk(A: torch.Tensor, symmetrize: bool = False) -> torch.Tensor:
+    """A @ A^T (dispatch.py:1554-1594); the kernel computes the lower
+    triangle only and mirrors it, so the result is exactly symmetric."""
+    M, K = A.shape
+    route = _gemm_route(A, op="syrk", macs=M * M * K, nbytes=(M * K + M * M) * A.element_size())
+    if route in ("hip", "upload"):
+        from . import kernels
+
+        dev = _gpu_device(A)
+        try:
+            return kernels.syrk(_to(A, dev)).to(A.device)
+        except Exception as exc:  # noqa: BLE001
+            _kernel_failed(exc)
+    r = torch.matmul(A, A.mT)
+    return _symmetrize(r) if symmetrize else r
+
+
+def hip_syrk(alpha, A, beta, C, trans: bool, uplo: str) -> torch.Tensor | None:
+    """The fused SYRK for device (or uploaded) operands, or None when the
+    route is not a kernel route. C is n x n (only its `uplo` triangle read)."""
+    n = A.shape[1] if trans else A.shape[0]
+    k = A.shape[0] if trans else A.shape[1]
+    ts = (A,) if C is None or beta == 0.0 else (A, C)
+    route = _gemm_route(*ts, op="syrk", macs=n * n * k, nbytes=(n * k + 2 * n * n) * A.element_size())
+    if route not in ("hip", "upload"):
+        return None
+    from . import kernels
+
+    dev = _gpu_device(*ts)
+    orig = A.device
+    try:
+        Cd = None if C is None or beta == 0.0 else _to(C, dev)
+        out = kernels.syrk(_to(A, dev), alpha, beta if Cd is not None else 0.0, Cd, trans, uplo)
+        return out.to(orig) if orig != dev else out
+    except Exception as exc:  # noqa: BLE001
+        _kernel_failed(exc)
+        return None
+
+
+# ── DF-MP2 energies ──────────────────────────────────────────────────────────
+
+_PAIR_ENERGY_CHOICES = ("auto", "hip", "sym", "aten", "legacy")
+
+
+def _pair_energy_choice() -> str:
+    c = os.environ.get("TRNBLAS_PAIR_ENERGY", "auto").strip().lower()
+    if c not in _PAIR_ENERGY_CHOICES:
+        raise ValueError(f"TRNBLAS_PAIR_ENERGY must be one of {_PAIR_ENERGY_CHOICES}; got {c!r}")
+    return c
+
+
+def _energy_operands(what: str, data: tuple, eps: tuple):
+    """fp32 operands for an energy kernel, or None to run torch
+    (dispatch.py:1296-1325): bf16 / fp16 upcast exactly; float64 under
+    `auto` runs torch at fp64, under `hip` is cast with a warning."""
+    ts = (*data, *eps)
+    bad = [t for t in ts if t.dtype not in _GEMM_KERNEL_DTYPES]
+    if bad:
+        _no_kernel_for_dtype(what, *ts, takes="float32 amplitudes and orbital energies")
+        if not (_backend == "hip" and all(t.dtype == torch.float64 for t in bad)):
+            return None
+        _warn_fp32_cast(what)
+    f32 = torch.float32
+    return tuple(t.to(f32) for t in data), tuple(t.to(f32) for t in eps)
+
+
+def _torch_batched_pair_energy(B, eps_occ, eps_vir) -> torch.Tensor:
+    """The pytorch backend of the batched pair energy (dispatch.py:2514-2533)."""
+    e = torch.zeros((), dtype=B.dtype, device=B.device)
+    for i in range(B.shape[0]):
+        for j in range(B.shape[0]):
+            T = B[i] @ B[j].T
+            D = float(eps_occ[i]) + float(eps_occ[j]) - eps_vir.unsqueeze(1) - eps_vir.unsqueeze(0)
+            e = e + (T * (2.0 * T - T.T) / D).sum()
+    return e
+
+
+def _torch_chunked_pair_energy(B, eps_occ, eps_vir, mem_budget_bytes: int = 1_500_000_000):
+    """Chunked GEMM + torch reduction (dispatch.py:2706-2728): the `aten`
+    route, and the unfused GPU baseline of the fused kernel."""
+    nocc, nvir, naux = B.shape
+    i_block = max(1, min(nocc, int(mem_budget_bytes // (4 * nvir * nocc * nvir))))
+    flat = B.reshape(nocc * nvir, naux)
+    eo2 = eps_occ.view(nocc, 1, 1, 1) + eps_occ.view(1, nocc, 1, 1)
+    ev2 = eps_vir.view(1, 1, nvir, 1) + eps_vir.view(1, 1, 1, nvir)
+    e = torch.zeros((), dtype=B.dtype, device=B.device)
+    for i0 in range(0, nocc, i_block):
+        i1 = min(i0 + i_block, nocc)
+        T = (flat[i0 * nvir : i1 * nvir] @ flat.T).reshape(i1 - i0, nvir, nocc, nvir)
+        T = T.permute(0, 2, 1, 3)
+        e = e + (T * (2.0 * T - T.transpose(-2, -1)) / (eo2[i0:i1] - ev2)).sum()
+    return e
+
+
+def _pair_energy_route(B) -> str:
+    """'hip' (fused kernel), 'aten' (chunked torch on the GPU) or 'torch'."""
+    choice = _pair_energy_choice()
+    if not _use_hip():
+        return "torch"
+    if choice == "aten":
+        return "aten" if B.device.type == "cuda" else "torch"
+    return "hip"
+
+
+def nki_batched_pair_energy(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tensor):
+    """Total DF-MP2 pair energy over all nocc^2 ordered pairs
+    (dispatch.py:2536-2569): one fused HIP launch for the i <= j walk.
+    B (nocc, nvir, naux), eps_occ (nocc,), eps_vir (nvir,). Returns a 0-d
+    tensor of the pytorch backend's dtype on B's device."""
+    dt = _pair_result_dtype(B, eps_vir)
+    route = _pair_energy_route(B)
+    if route == "torch":
+        return _torch_batched_pair_energy(B, eps_occ, eps_vir)
+    if route == "aten":
+        return _torch_chunked_pair_energy(B, eps_occ, eps_vir)
+    feeds = _energy_operands("batched_pair_energy", (B,), (eps_occ, eps_vir))
+    if feeds is None:
+        if B.device.type == "cuda":
+            return _torch_chunked_pair_energy(B, eps_occ, eps_vir)
+        return _torch_batched_pair_energy(B, eps_occ, eps_vir)
+    (Bk,), (eo, ev) = feeds
+    from . import kernels
+
+    dev = _gpu_device(B, eps_occ, eps_vir)
+    try:
+        e = kernels.pair_energy_sym(Bk.to(dev), eo.to(dev), ev.to(dev))
+        return _as_result_dtype(e, dt).to(B.device)
+    except Exception as exc:  # noqa: BLE001
+        _kernel_failed(exc, "pair energy kernel failed — computed by torch")
+        return _torch_chunked_pair_energy(B, eps_occ, eps_vir)
+
+
+def nki_fused_gemm_energy(b_i, b_j, eps_occ_i: float, eps_occ_j: float, eps_vir):
+    """One pair's energy (dispatch.py:3049-3164)."""
+    dt = torch.promote_types(_pair_result_dtype(b_i, eps_vir), b_j.dtype)
+
+    def torch_ref():
+        T = b_i @ b_j.T
+        D = eps_occ_i + eps_occ_j - eps_vir.unsqueeze(1) - eps_vir.unsqueeze(0)
+        return (T * (2.0 * T - T.T) / D).sum()
+
+    if not _use_hip():
+        return torch_ref()
+    feeds = _energy_operands("fused_gemm_energy", (b_i, b_j), (eps_vir,))
+    if feeds is None:
+        return torch_ref()
+    (bi, bj), (ev,) = feeds
+    from . import kernels
+
+    dev = _gpu_device(b_i, b_j, eps_vir)
+    try:
+        eo = torch.tensor([float(eps_occ_i), float(eps_occ_j)], dtype=torch.float32, device=dev)
+        zero = torch.zeros(1, dtype=torch.int32)
+        e = kernels.pair_energies(
+            bi.to(dev).unsqueeze(0), bj.to(dev).unsqueeze(0), eo[:1], eo[1:], ev.to(dev), zero, zero
+        )[0]
+        return _as_result_dtype(e, dt).to(b_i.device)
+    except Exception as exc:  # noqa: BLE001
+        _kernel_failed(exc)
+        return torch_ref()
+
+
+def _torch_mp2_energy(T_flat, eps_occ_chunk, eps_occ_full, eps_vir):
+    """dispatch.py:1440-1453: T (ic, nocc, nvir, nvir) from T_flat, reduced."""
+    ic, nocc, nvir = eps_occ_chunk.shape[0], eps_occ_full.shape[0], eps_vir.shape[0]
+    T = T_flat.reshape(ic, nvir, nocc, nvir).permute(0, 2, 1, 3)
+    D = (
+        eps_occ_chunk.view(ic, 1, 1, 1)
+        + eps_occ_full.view(1, nocc, 1, 1)
+        - eps_vir.view(1, 1, nvir, 1)
+        - eps_vir.view(1, 1, 1, nvir)
+    )
+    return (T * (2.0 * T - T.transpose(-2, -1)) / D).sum()
+
+
+def nki_mp2_energy(T_flat, eps_occ_chunk, eps_occ_full, eps_vir):
+    """The energy of a precomputed amplitude block (dispatch.py:1456-1489):
+    one HBM-bound HIP reduction."""
+    if not _use_hip():
+        return _torch_mp2_energy(T_flat, eps_occ_chunk, eps_occ_full, eps_vir)
+    feeds = _energy_operands("mp2_energy", (T_flat,), (eps_occ_chunk, eps_occ_full, eps_vir))
+    if feeds is None:
+        return _torch_mp2_energy(T_flat, eps_occ_chunk, eps_occ_full, eps_vir)
+    (t,), (eoc, eof, ev) = feeds
+    dt = _mp2_result_dtype(T_flat, eps_occ_chunk, eps_occ_full, eps_vir)
+    from . import kernels
+
+    dev = _gpu_device(T_flat, eps_occ_chunk, eps_occ_full, eps_vir)
+    try:
+        e = kernels.mp2_energy_pairs(t.to(dev), eoc.to(dev), eof.to(dev), ev.to(dev)).sum()
+        return _as_result_dtype(e, dt).to(T_flat.device)
+    except Exception as exc:  # noqa: BLE001
+        _kernel_failed(exc)
+        return _torch_mp2_energy(T_flat, eps_occ_chunk, eps_occ_full, eps_vir)
+
+
+# ── Ozaki fp64-class GEMM ────────────────────────────────────────────────────
+
+
+def _ozaki_route() -> str:
+    """'kernel' or 'torch' (fp64 matmul where the data is) for gemm_fp64
+    (dispatch.py:761-774)."""
+    return "kernel" if _use_hip() else "torch"
+
+
+def nki_gemm_fp64(a: torch.Tensor, b: torch.Tensor, slices: int) -> torch.Tensor:
+    """fp64 a @ b by the Ozaki split on the device (dispatch.py:958-980).
+    a (M, K), b (K, N) real tensors (any float dtype; computed as fp64).
+    Non-finite operands take a plain fp64 matmul on the device."""
+    from .. import ozaki
+
+    k = ozaki.check_slices(slices)
+    if _ozaki_route() == "torch":
+        return torch.matmul(a.double(), b.double())
+    dev = _gpu_device(a, b)
+    ad = a.to(dev, torch.float64)
+    bd = b.to(dev, torch.float64)
+    try:
+        return ozaki.run_device(ad, bd, k)
+    except ozaki.OzakiNonFinite:
+        return torch.matmul(ad, bd)
+    except Exception as exc:  # noqa: BLE001
+        _kernel_failed(exc, "Ozaki fp64 GEMM kernel failed — computed by torch fp64")
+        return torch.matmul(ad, bd)
+
+
+def __getattr__(name):
+    if name == "HAS_HIP" or name == "HAS_NKI":
+        return has_hip()
+    raise AttributeError(name)
+
+
+# ── op surface ───────────────────────────────────────────────────────────────
+
+_native_ops = None
+
+
+def get_native_ops() -> dict:
+    """The dtype-checked `torch.ops.trnblas.*` ops (registered on first call)."""
+    global _native_ops
+    if _native_ops is None:
+        from . import _native
+
+        _native_ops = _native.OPS
+    return _native_ops

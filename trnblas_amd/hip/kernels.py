@@ -11,6 +11,22 @@ import torch
 from . import _lib
 from ._lib import call, ptr, stream_of
 
+# Optional launch probe: when set, called as probe(kernel_name, "begin") and
+# probe(kernel_name, "end") right around each C-ABI launch, on the calling
+# thread (bench.py records HIP events on the launch stream with it).
+_launch_probe = None
+
+
+def _probed_call(kernel: str, fn: str, *args) -> int:
+    probe = _launch_probe
+    if probe is None:
+        return call(fn, *args)
+    probe(kernel, "begin")
+    try:
+        return call(fn, *args)
+    finally:
+        probe(kernel, "end")
+
 
 def _require_device(*ts: torch.Tensor) -> torch.device:
     dev = ts[0].device
@@ -85,8 +101,8 @@ def gemm(
             if c.stride(1) != 1 or c.stride(0) < N:
                 c = c.contiguous()
             ldc = c.stride(0)
-        call(
-            "trnblas_hip_gemm", code, int(ta), int(tb), M, N, K, float(alpha),
+        _probed_call(
+            "gemm", "trnblas_hip_gemm", code, int(ta), int(tb), M, N, K, float(alpha),
             ptr(a), lda, 0, ptr(b), ldb, 0, float(beta) if c is not None else 0.0,
             ptr(c), ldc, 0, ptr(D), N, 0, 1, stream_of(dev),
         )  # fmt: skip
@@ -109,8 +125,8 @@ def gemm(
         if c.stride(2) != 1 or c.stride(1) < N:
             c = c.contiguous()
         ldc, sc = c.stride(1), (0 if nb == 1 else c.stride(0))
-    call(
-        "trnblas_hip_gemm", code, int(ta), int(tb), M, N, K, float(alpha),
+    _probed_call(
+        "gemm", "trnblas_hip_gemm", code, int(ta), int(tb), M, N, K, float(alpha),
         ptr(a), lda, sa, ptr(b), ldb, sb, float(beta) if c is not None else 0.0,
         ptr(c), ldc, sc, ptr(D), N, M * N, nb, stream_of(dev),
     )  # fmt: skip
@@ -143,8 +159,8 @@ def syrk(
             raise TypeError("syrk: C dtype differs from A")
         c = C if (C.stride(1) == 1 and C.stride(0) >= n) else C.contiguous()
         ldc = c.stride(0)
-    call(
-        "trnblas_hip_syrk", code, 1 if uplo == "upper" else 0, int(t), n, k, float(alpha),
+    _probed_call(
+        "syrk", "trnblas_hip_syrk", code, 1 if uplo == "upper" else 0, int(t), n, k, float(alpha),
         ptr(a), lda, float(beta) if c is not None else 0.0, ptr(c), ldc, ptr(D), n,
         stream_of(dev),
     )  # fmt: skip
@@ -177,8 +193,8 @@ def pair_energy_sym(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tenso
     ws = _lib.load().trnblas_hip_pair_energy_workspace(nvir, npairs)
     work = torch.empty(max(ws, 8), dtype=torch.uint8, device=dev)
     ld_occ = B.stride(0) if nocc > 1 else nvir * naux
-    call(
-        "trnblas_hip_pair_energy", nvir, naux, ptr(B), ld_occ, ptr(B), ld_occ,
+    _probed_call(
+        "pair_energy", "trnblas_hip_pair_energy", nvir, naux, ptr(B), ld_occ, ptr(B), ld_occ,
         B.stride(1) if nvir > 1 else naux, ptr(eo), ptr(eo), ptr(ev), nocc, npairs,
         None, None, None, None, ptr(total), ptr(work), work.numel(), stream_of(dev),
     )  # fmt: skip
@@ -296,8 +312,8 @@ def ozaki_gemm(dA, eA, dB, eB, M: int, N: int, slices: int, kb: int | None = Non
         ldc_m, ldc_n = out.stride(1), out.stride(0)
     else:
         ldc_m, ldc_n = out.stride(0), out.stride(1)
-    call(
-        "trnblas_hip_ozaki_gemm", 0, slices, M, N, Kp, kb, ptr(dA), dA.stride(1),
+    _probed_call(
+        "ozaki_gemm", "trnblas_hip_ozaki_gemm", 0, slices, M, N, Kp, kb, ptr(dA), dA.stride(1),
         dA.stride(0), ptr(dB), dB.stride(1), dB.stride(0), ptr(eA), ptr(eB), ptr(out),
         ldc_m, ldc_n, stream_of(dev),
     )  # fmt: skip
@@ -314,3 +330,22 @@ def ozaki_hilo(dA, dB, M: int, N: int, slices: int) -> torch.Tensor:
         ptr(dB), dB.stride(1), dB.stride(0), ptr(hilo), N, stream_of(dev),
     )  # fmt: skip
     return hilo
+
+
+def triangle_nonzero(C: torch.Tensor, uplo: str) -> tuple[bool, bool]:
+    """(uplo triangle has a nonzero, the other triangle has one) for a device
+    n x n C (strict triangles; one pass, one 8-byte device-to-host read)."""
+    dev = _require_device(C)
+    code = _lib.DTYPE_CODES.get(C.dtype)
+    if code is None or C.stride(1) != 1:
+        up = bool(torch.triu(C, diagonal=1).ne(0).any())
+        lo = bool(torch.tril(C, diagonal=-1).ne(0).any())
+    else:
+        flags = torch.empty(2, dtype=torch.int32, device=dev)
+        n = C.shape[0]
+        call(
+            "trnblas_hip_triangle_nonzero", code, n, ptr(C), max(C.stride(0), n), ptr(flags),
+            stream_of(dev),
+        )  # fmt: skip
+        up, lo = (bool(v) for v in flags.tolist())
+    return (up, lo) if uplo == "upper" else (lo, up)

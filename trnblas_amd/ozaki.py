@@ -1,0 +1,165 @@
+"""fp64-class GEMM by Ozaki splitting on gfx950 int8 MFMA — the host half.
+
+MI355X counterpart of trnblas/ozaki.py. The schedule constants and the
+pure functions that define the arithmetic contract (`check_slices`,
+`n_products`, `diag_groups`, `schedule`, `n_groups`, `exponent_offset`,
+`plan`) keep the reference's semantics (trnblas/ozaki.py:42-63, :337-375,
+:462-511). The data path differs: the split, the slice products and the
+recombination all run on the device (`run_device`), from the fp64 operands
+in HBM, in three kernel launches per operand pair — no host digit arrays,
+no host combine, no launch blocking below 2 GiB.
+
+Bit-exactness: `run_device` equals the reference's `ozaki.reference_gemm`
+bit for bit (same digits, same group cut, same fp32 TwoSum order, same fp64
+combine, same narrow-N swap and K blocking). The CPU restatement that
+checks this lives in `oracle/ozaki.py` (test infrastructure); this module
+has no CPU arithmetic path.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+SLICE_BITS = 7
+TILE_K = 128
+GROUP_TERMS = 4096
+GROUP_TILES = GROUP_TERMS // TILE_K
+MIN_SLICES = 1
+MAX_SLICES = 12
+DEFAULT_SLICES = 8
+BLOCK_BYTES = 1 << 31
+SWAP_N = 512
+LAUNCH_M = 1024
+LAUNCH_N = 1024
+
+
+class OzakiNonFinite(Exception):
+    """An operand of gemm_fp64 holds inf / nan (the digits cannot represent it)."""
+
+
+def check_slices(slices) -> int:
+    """`slices` as an int in [MIN_SLICES, MAX_SLICES] (ozaki.py:51-58)."""
+    if isinstance(slices, bool) or not isinstance(slices, (int, np.integer)):
+        raise TypeError(f"slices must be an int, got {type(slices).__name__}")
+    k = int(slices)
+    if not MIN_SLICES <= k <= MAX_SLICES:
+        raise ValueError(f"slices must be in [{MIN_SLICES}, {MAX_SLICES}], got {k}")
+    return k
+
+
+def n_products(slices: int) -> int:
+    """Slice GEMMs per product: pairs (s, t) with s + t <= slices - 1."""
+    return slices * (slices + 1) // 2
+
+
+def _round_up(n: int, m: int) -> int:
+    return -(-n // m) * m
+
+
+def diag_groups(kt: int, d: int) -> list:
+    """Groups of diagonal d for kt K tiles per slice, in accumulation order
+    (ozaki.py:337-355): runs (s, t, first tile, tiles) of at most GROUP_TILES
+    tiles; with kt >= GROUP_TILES each pair is cut on its own, otherwise
+    GROUP_TILES // kt whole pairs share a group."""
+    pairs = [(s, d - s) for s in range(d + 1)]
+    if kt >= GROUP_TILES:
+        return [
+            [(s, t, k0, min(GROUP_TILES, kt - k0))]
+            for s, t in pairs
+            for k0 in range(0, kt, GROUP_TILES)
+        ]
+    per = GROUP_TILES // kt
+    return [[(s, t, 0, kt) for s, t in pairs[i : i + per]] for i in range(0, len(pairs), per)]
+
+
+def schedule(slices: int, kt: int) -> list:
+    """[(d, scale, groups)], diagonals smallest first (ozaki.py:358-365)."""
+    return [
+        (d, float(2 ** (SLICE_BITS * (slices - 1 - d))), diag_groups(kt, d))
+        for d in range(slices - 1, -1, -1)
+    ]
+
+
+def n_groups(slices: int, kt: int) -> int:
+    return sum(len(g) for _, _, g in schedule(slices, kt))
+
+
+def exponent_offset(slices: int) -> int:
+    """C = (hi + lo) * 2^(eA_i + eB_j + exponent_offset(slices))."""
+    return -2 * (SLICE_BITS - 1) - SLICE_BITS * (slices - 1)
+
+
+def _blocks(total: int, step: int) -> list:
+    return [(i, min(step, total - i)) for i in range(0, total, step)]
+
+
+def plan(Mp, Kp, N, slices, limit=BLOCK_BYTES, max_m=LAUNCH_M, max_n=LAUNCH_N):
+    """The reference's launch blocks (ozaki.py:486-511). On the device only
+    the K blocks matter (they are separate (hi, lo) chains summed in fp64);
+    M / N blocks change nothing in the arithmetic and are not used."""
+    k = check_slices(slices)
+    cap = limit // (2 * k)
+    Kb = Kp if Kp * 1024 <= cap else max(TILE_K, (cap // 1024) // TILE_K * TILE_K)
+    Mb = max(TILE_K, min(Mp, max_m // TILE_K * TILE_K, (cap // Kb) // TILE_K * TILE_K))
+    Nb = max(1, min(N, max_n, cap // Kb))
+    if 8 * Mb * Nb > limit:
+        Nb = max(1, min(Nb, limit // (8 * Mb)))
+    return _blocks(Mp, Mb), _blocks(Kp, Kb), _blocks(N, Nb)
+
+
+def k_block(Kp: int, slices: int) -> int:
+    """The K block of `plan` (Kp itself unless K is about 2^17 or more)."""
+    kbs = plan(TILE_K, Kp, 1, slices)[1]
+    return kbs[0][1]
+
+
+def split_device(X: torch.Tensor, slices: int, per: str):
+    """Device digits of `ozaki.split(X, slices, per, pad=(128, 128))`:
+    int8 (k, rows, Kp) with K contiguous, where rows are X's rows (per="row")
+    or columns (per="col"), and int32 exponents. Raises OzakiNonFinite."""
+    from .hip import kernels
+
+    d, e, bad = kernels.ozaki_split(X, slices, per)
+    if int(bad):  # one small device-to-host read
+        raise OzakiNonFinite()
+    return d, e
+
+
+def _digits_of(X: torch.Tensor, k: int, want: str):
+    """Digits for the operand role `want` ("rows of A" = per-row split of A,
+    "cols of B" = per-column split of B). A transposed view is split in its
+    own layout (as ozaki.split_a / split_b do), so no fp64 copy is made."""
+    if want == "A":  # A (M, K): per row, digits (k, M, Kp)
+        if X.mT.is_contiguous() and not X.is_contiguous():
+            return split_device(X.mT, k, "col")  # A^T (K, M) by columns
+        return split_device(X.contiguous(), k, "row")
+    # B (K, N): per column, digits (k, N, Kp)
+    if X.mT.is_contiguous() and not X.is_contiguous():
+        return split_device(X.mT, k, "row")  # B^T (N, K) by rows
+    return split_device(X.contiguous(), k, "col")
+
+
+def run_device(A: torch.Tensor, B: torch.Tensor, slices: int = DEFAULT_SLICES) -> torch.Tensor:
+    """C = A @ B in fp64 by Ozaki splitting, on the device. A (M, K), B (K, N)
+    fp64 device tensors (views allowed). Bit-equal to the reference's
+    `ozaki.reference_gemm(A, B, slices)`."""
+    from .hip import kernels
+
+    k = check_slices(slices)
+    M, K = A.shape
+    N = B.shape[1]
+    C = torch.empty((M, N), dtype=torch.float64, device=A.device)
+    if M == 0 or N == 0:
+        return C
+    if K == 0:
+        return C.zero_()
+    da, ea = _digits_of(A, k, "A")
+    db, eb = _digits_of(B, k, "B")
+    Kp = da.shape[2]
+    kb = k_block(Kp, k)
+    if N < SWAP_N and M > N:  # C^T = B^T A^T (ozaki.py:546-547): B's digits first
+        kernels.ozaki_gemm(db, eb, da, ea, N, M, k, kb=kb, out=C, transpose_out=True)
+    else:
+        kernels.ozaki_gemm(da, ea, db, eb, M, N, k, kb=kb, out=C)
+    return C
