@@ -67,7 +67,17 @@ int trnblas_hip_gemm(int dtype, int transA, int transB, int64_t M, int64_t N, in
                      double alpha, const void* A, int64_t lda, int64_t strideA,
                      const void* B, int64_t ldb, int64_t strideB, double beta,
                      const void* C, int64_t ldc, int64_t strideC, void* D, int64_t ldd,
-                     int64_t strideD, int64_t batch, void* stream);
+                     int64_t strideD, int64_t batch, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/*
+ * Workspace that lets trnblas_hip_gemm / trnblas_hip_syrk balance a launch
+ * whose tiles do not fill the GPU evenly (stream-K: the k-iterations of all
+ * tiles are split evenly over the resident workgroups; split tiles are summed
+ * by a second, deterministic kernel). Bytes for the current device; with a
+ * NULL or smaller workspace the calls run one tile per workgroup.
+ */
+size_t trnblas_hip_gemm_workspace(void);
 
 /*
  * SYRK:  D = alpha * op(A) * op(A)^T + beta * sym_uplo(C), returned full.
@@ -80,11 +90,12 @@ int trnblas_hip_gemm(int dtype, int transA, int transB, int64_t M, int64_t N, in
  * both D[i][j] and D[j][i], so D is exactly symmetric.
  * op(A) is N x K: A row-major N x K (trans == 0) or K x N (trans != 0).
  * uplo: 0 = the lower triangle of C is referenced, 1 = the upper. C may be
- * NULL when beta == 0. dtype as in trnblas_hip_gemm.
+ * NULL when beta == 0. dtype and workspace as in trnblas_hip_gemm.
  */
 int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64_t K, double alpha,
                      const void* A, int64_t lda, double beta, const void* C, int64_t ldc,
-                     void* D, int64_t ldd, void* stream);
+                     void* D, int64_t ldd, void* workspace, size_t workspace_bytes,
+                     void* stream);
 
 /*
  * Which strict triangles of the n x n matrix C hold a nonzero entry (NaN

@@ -96,3 +96,44 @@ def test_syrk_triangle(dev, n, k, trans, uplo):
     # grows like sqrt(k) u there (probabilistic bound, u = 2^-24).
     tol = max(1e-6, 2 * k**0.5 * 2.0**-24)
     assert ((D.double() - ref).abs() / den).max().item() <= tol
+
+
+@pytest.mark.parametrize(
+    "M,N,K,ta,tb",
+    [(1024, 1024, 4096, False, False), (300, 200, 5000, True, False), (2048, 2048, 2048, True, False),
+     (130, 70, 20000, False, True)],
+)
+def test_gemm_stream_k_splits(dev, M, N, K, ta, tb):
+    # shapes whose tiles underfill the GPU: the k-iterations are split over
+    # many workgroups and summed by the fixup kernel (several-way splits)
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(M + K)
+    A0 = torch.randn((K, M) if ta else (M, K), generator=g)
+    B0 = torch.randn((N, K) if tb else (K, N), generator=g)
+    C = torch.randn(M, N, generator=g)
+    A = (A0.mT if ta else A0).to(dev)
+    B = (B0.mT if tb else B0).to(dev)
+    D1 = kernels.gemm(A, B, 1.0, 0.5, C.to(dev))
+    D2 = kernels.gemm(A, B, 1.0, 0.5, C.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(D1, D2)  # deterministic
+    err = _cw_err(D1.cpu(), A.cpu(), B.cpu(), 1.0, 0.5, C)
+    assert err <= 1e-6, err
+
+
+@pytest.mark.parametrize("n,k,uplo", [(4096, 1024, "lower"), (640, 9000, "upper")])
+def test_syrk_stream_k(dev, n, k, uplo):
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(n)
+    A = torch.randn(n, k, generator=g)
+    X = torch.randn(n, n, generator=g)
+    D = kernels.syrk(A.to(dev), 1.0, 0.5, X.to(dev), uplo=uplo).cpu()
+    assert torch.equal(D, D.T)
+    Cs = torch.tril(X) + torch.tril(X, -1).T if uplo == "lower" else torch.triu(X) + torch.triu(X, 1).T
+    Ad = A.double()
+    ref = Ad @ Ad.T + 0.5 * Cs.double()
+    den = Ad.abs() @ Ad.abs().T + 0.5 * Cs.double().abs()
+    tol = max(1e-6, 2 * k**0.5 * 2.0**-24)
+    assert ((D.double() - ref).abs() / den).max().item() <= tol

@@ -44,8 +44,13 @@ struct GemmArgs {
   void* D;
   int64_t ldd, sD;
   int batch;
-  int tiles_m, tiles_n;
-  int uplo;  // SYRK: 0 = lower triangle of C referenced, 1 = upper
+  int tiles_m, tiles_n;  // tile grid of one batch entry
+  int ntiles;            // tiles of the launch (all batch entries, or the SYRK triangle)
+  int nk;                // k-tiles per tile
+  int uplo;              // SYRK: 0 = lower triangle of C referenced, 1 = upper
+  int sk_groups;         // stream-K workgroups (0 = data-parallel)
+  int dp_tiles;          // under stream-K: leading tiles computed whole
+  float* ws;             // stream-K partial tiles [sk_groups][2][BM * BN]
 };
 
 template <typename T>
@@ -142,6 +147,53 @@ __device__ __forceinline__ void tri_tile(int t, int& tm, int& tn) {
   tn = t - r * (r + 1) / 2;
 }
 
+// D = alpha acc + beta C for one output element (C not read when beta == 0);
+// SYRK: m >= n only, written to both triangles, C read from the uplo side.
+template <typename T, bool SYRK>
+__device__ __forceinline__ void store_out(const GemmArgs& g, const T* C, T* D, int m, int n,
+                                          float acc) {
+  if (SYRK) {
+    if (m < g.M && n <= m) {
+      float v = g.alpha * acc;
+      if (g.beta != 0.0f) {
+        const int64_t ci = g.uplo ? (int64_t)n * g.ldc + m : (int64_t)m * g.ldc + n;
+        v += g.beta * to_f32(C[ci]);
+      }
+      const T o = (T)v;
+      D[(int64_t)m * g.ldd + n] = o;
+      D[(int64_t)n * g.ldd + m] = o;
+    }
+  } else if (m < g.M && n < g.N) {
+    float v = g.alpha * acc;
+    if (g.beta != 0.0f) v += g.beta * to_f32(C[(int64_t)m * g.ldc + n]);
+    D[(int64_t)m * g.ldd + n] = (T)v;
+  }
+}
+
+// Tile t -> (batch, tile row, tile column).
+template <bool SYRK>
+__device__ __forceinline__ void decode_tile(const GemmArgs& g, int t, int& bat, int& tm, int& tn) {
+  if (SYRK) {
+    bat = 0;
+    tri_tile(t, tm, tn);
+  } else {
+    const int per = g.tiles_m * g.tiles_n;
+    bat = t / per;
+    grouped_tile(t - bat * per, g.tiles_m, g.tiles_n, 8, tm, tn);
+  }
+}
+
+// Stream-K: workgroup w owns k-iterations [sk_start(w), sk_start(w + 1)) of
+// the tiles x nk iteration space.
+__device__ __forceinline__ int64_t sk_start(int w, int64_t total, int groups) {
+  return (int64_t)w * total / groups;
+}
+
+// Each workgroup computes whole tiles (data-parallel: one tile per
+// workgroup) or, under stream-K, a contiguous range of the k-iterations of
+// all tiles: whole tiles it covers get the epilogue directly, the partial
+// tiles at either end of its range are written to its two workspace slots
+// and summed by gemm_fixup_kernel.
 template <typename T, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, bool VEC,
           bool SYRK>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1) void gemm_kernel(GemmArgs g) {
@@ -161,19 +213,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
-
-  int tm, tn;
-  if (SYRK) {
-    tri_tile(blockIdx.x, tm, tn);
-  } else {
-    const int t = xcd_remap(blockIdx.x, gridDim.x);
-    grouped_tile(t, g.tiles_m, g.tiles_n, 8, tm, tn);
-  }
-  const int m0 = tm * BM, n0 = tn * BN;
   const int M = g.M, N = g.N, K = g.K;
-  const int nk = (K + BK - 1) / BK;
+  const int nk = g.nk;
 
-  for (int bat = blockIdx.y; bat < g.batch; bat += gridDim.y) {
+  // One segment: k-iterations [kb0, kb1) of tile t; slot < 0 = whole tile.
+  auto segment = [&](int t, int kb0, int kb1, int slot, int w) {
+    int bat, tm, tn;
+    decode_tile<SYRK>(g, t, bat, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
     const T* A = static_cast<const T*>(g.A) + bat * g.sA;
     const T* B = static_cast<const T*>(g.B) + bat * g.sB;
 
@@ -225,15 +272,16 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    if (nk > 0) {
-      load_tiles(0);
+    if (kb1 > kb0) {
+      load_tiles(kb0 * BK);
       store_tiles(0);
       __syncthreads();
     }
-    for (int kt = 0; kt < nk; ++kt) {
-      const bool more = kt + 1 < nk;
+    for (int kt = kb0; kt < kb1; ++kt) {
+      const int cur = (kt - kb0) & 1;
+      const bool more = kt + 1 < kb1;
       if (more) load_tiles((kt + 1) * BK);
-      const T* la = lds + (kt & 1) * (A_SZ + B_SZ);
+      const T* la = lds + cur * (A_SZ + B_SZ);
       const T* lb = la + A_SZ;
 #pragma unroll
       for (int c = 0; c < BK / CH; ++c) {
@@ -250,46 +298,104 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1)
 #pragma unroll
           for (int j = 0; j < FN; ++j) mma_frag(acc[i][j], fa[i], fb[j], (T*)nullptr);
       }
-      if (more) store_tiles((kt + 1) & 1);
+      if (more) store_tiles(cur ^ 1);
       __syncthreads();
     }
 
-    // Epilogue: D = alpha * acc + beta * C (C not read when beta == 0). Lane
-    // (l) of an MFMA 32x32 block holds column l % 32 and rows
+    // Lane l of an MFMA 32x32 block holds column l % 32 and rows
     // 8 (r / 4) + 4 (l / 32) + r % 4 of its 16 registers r.
-    const T* C = static_cast<const T*>(g.C) + (g.C ? bat * g.sC : 0);
-    T* D = static_cast<T*>(g.D) + bat * g.sD;
-    const bool add = g.beta != 0.0f;
+    if (slot < 0) {
+      const T* C = static_cast<const T*>(g.C) + (g.C ? bat * g.sC : 0);
+      T* D = static_cast<T*>(g.D) + bat * g.sD;
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int mb = m0 + wm0 + i * 32 + (lane >> 5) * 4;
-        const int n = n0 + wn0 + j * 32 + (lane & 31);
-        T* dcol = D + n;
-        const T* ccol = C + n;
+        for (int j = 0; j < FN; ++j) {
+          const int mb = m0 + wm0 + i * 32 + (lane >> 5) * 4;
+          const int n = n0 + wn0 + j * 32 + (lane & 31);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = mb + (r >> 2) * 8 + (r & 3);
-          if (SYRK) {
-            if (m < M && n <= m) {
-              float v = g.alpha * acc[i][j][r];
-              if (add) {
-                const int64_t ci = g.uplo ? (int64_t)n * g.ldc + m : (int64_t)m * g.ldc + n;
-                v += g.beta * to_f32(C[ci]);
-              }
-              const T o = (T)v;
-              dcol[(int64_t)m * g.ldd] = o;
-              D[(int64_t)n * g.ldd + m] = o;
-            }
-          } else if (m < M && n < N) {
-            float v = g.alpha * acc[i][j][r];
-            if (add) v += g.beta * to_f32(ccol[(int64_t)m * g.ldc]);
-            dcol[(int64_t)m * g.ldd] = (T)v;
-          }
+          for (int r = 0; r < 16; ++r)
+            store_out<T, SYRK>(g, C, D, mb + (r >> 2) * 8 + (r & 3), n, acc[i][j][r]);
         }
-      }
+    } else {
+      float* P = g.ws + ((int64_t)w * 2 + slot) * (BM * BN);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int mb = wm0 + i * 32 + (lane >> 5) * 4;
+          const int n = wn0 + j * 32 + (lane & 31);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) P[(mb + (r >> 2) * 8 + (r & 3)) * BN + n] = acc[i][j][r];
+        }
+    }
+  };
+
+  if (g.sk_groups == 0) {
+    segment(xcd_remap(blockIdx.x, gridDim.x), 0, nk, -1, 0);
+    return;
   }
+  // Hybrid schedule: the first dp_tiles tiles whole (G per round), then the
+  // k-iterations of the remaining tiles split evenly over the G workgroups.
+  const int G = g.sk_groups;
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  for (int t = w; t < g.dp_tiles; t += G) segment(t, 0, nk, -1, w);
+  const int64_t total = (int64_t)(g.ntiles - g.dp_tiles) * nk;
+  const int64_t x0 = sk_start(w, total, G), x1 = sk_start(w + 1, total, G);
+  for (int64_t x = x0; x < x1;) {
+    const int tt = (int)(x / nk);
+    const int kb0 = (int)(x - (int64_t)tt * nk);
+    const int kb1 = (int)((int64_t)kb0 + (x1 - x) < nk ? kb0 + (x1 - x) : nk);
+    const bool whole = kb0 == 0 && kb1 == nk;
+    segment(g.dp_tiles + tt, kb0, kb1, whole ? -1 : (x == x0 ? 0 : 1), w);
+    x += kb1 - kb0;
+  }
+}
+
+// Sums the stream-K partials of each split tile in workgroup order
+// (deterministic) and applies the epilogue. Grid: (split tiles, BM / 8):
+// each workgroup finishes 8 rows of one tile, one float4 of partials per
+// thread and contributor (all contributors' loads in flight at once).
+template <typename T, int BM, int BN, bool SYRK>
+__global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs g) {
+  constexpr int MAXC = 64;  // contributors per tile (>= 4 k-iterations each)
+  constexpr int ROWS = 8;
+  static_assert(ROWS * BN / 4 == 256, "one float4 per thread");
+  __shared__ int64_t src[MAXC];
+  __shared__ int ncontrib;
+  const int t = g.dp_tiles + blockIdx.x;
+  const int nk = g.nk, G = g.sk_groups;
+  const int64_t total = (int64_t)(g.ntiles - g.dp_tiles) * nk;
+  const int64_t lo = (int64_t)blockIdx.x * nk, hi = lo + nk;
+  if (threadIdx.x == 0) {
+    int w0 = (int)(lo * G / total);
+    while (w0 + 1 < G && sk_start(w0 + 1, total, G) <= lo) ++w0;
+    while (w0 > 0 && sk_start(w0, total, G) > lo) --w0;
+    int n = 0;
+    if (!(sk_start(w0, total, G) <= lo && sk_start(w0 + 1, total, G) >= hi)) {
+      for (int w = w0; w < G && n < MAXC; ++w) {
+        const int64_t st = sk_start(w, total, G);
+        if (st >= hi) break;
+        src[n++] = ((int64_t)w * 2 + (st >= lo ? 0 : 1)) * (BM * BN);
+      }
+    }
+    ncontrib = n;
+  }
+  __syncthreads();
+  const int nc = ncontrib;
+  if (nc == 0) return;  // whole tile, already written
+  int bat, tm, tn;
+  decode_tile<SYRK>(g, t, bat, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const T* C = static_cast<const T*>(g.C) + (g.C ? bat * g.sC : 0);
+  T* D = static_cast<T*>(g.D) + bat * g.sD;
+  const int r = blockIdx.y * ROWS + threadIdx.x / (BN / 4);
+  const int c = (threadIdx.x % (BN / 4)) * 4;
+  const int e = r * BN + c;
+  f32x4 v = *reinterpret_cast<const f32x4*>(g.ws + src[0] + e);
+  for (int q = 1; q < nc; ++q) v += *reinterpret_cast<const f32x4*>(g.ws + src[q] + e);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) store_out<T, SYRK>(g, C, D, m0 + r, n0 + c + u, v[u]);
 }
 
 template <typename T>
@@ -299,21 +405,66 @@ struct Cfg {
   static constexpr int NT = (BM / WM) * (BN / WN) * 64;
 };
 
+constexpr int kTileM = 128, kTileN = 128;
+constexpr size_t kSkSlotBytes = (size_t)kTileM * kTileN * sizeof(float);
+
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        v <= 0)
+      v = 256;
+    cus[dev] = v;
+  }
+  return cus[dev];
+}
+
+// Stream-K groups for this launch, or 0 for data-parallel: stream-K when the
+// last round of one-tile workgroups would leave more than 10 % of the
+// resident slots idle and the workspace holds two partial tiles per group.
+static int choose_sk(GemmArgs& g, int occupancy, size_t ws_bytes) {
+  g.dp_tiles = 0;
+  if (g.ws == nullptr || g.nk < 8) return 0;
+  const int64_t slots = (int64_t)device_cus() * (occupancy > 0 ? occupancy : 1);
+  const int64_t rounds = (g.ntiles + slots - 1) / slots;
+  const double eff = (double)g.ntiles / (double)(rounds * slots);
+  // Tiles that give every CU at most one workgroup are already balanced.
+  if (eff >= 0.9 || rounds > 8 || g.ntiles <= device_cus()) return 0;
+  int64_t groups = slots;
+  const int64_t dp = (g.ntiles / groups) * groups;  // whole rounds
+  const int64_t tail = (int64_t)(g.ntiles - dp) * g.nk;
+  if (tail / groups < 4) groups = tail / 4;  // at least 4 k-iterations each
+  if (groups < 1 || (size_t)groups * 2 * kSkSlotBytes > ws_bytes) return 0;
+  if (dp > 0 && groups != slots) return 0;  // keep one workgroup per slot
+  g.dp_tiles = (int)dp;
+  return (int)groups;
+}
+
 template <typename T, bool AKC, bool BKC, bool VEC, bool SYRK>
-static int launch_t(const GemmArgs& g, int ntiles, hipStream_t s) {
+static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   using C = Cfg<T>;
-  dim3 grid(ntiles, g.batch < 65535 ? g.batch : 65535);
-  hipLaunchKernelGGL((gemm_kernel<T, C::BM, C::BN, C::BK, C::WM, C::WN, AKC, BKC, VEC, SYRK>),
-                     grid, dim3(C::NT), 0, s, g);
-  return check_launch(SYRK ? "trnblas_hip_syrk" : "trnblas_hip_gemm");
+  auto kern = gemm_kernel<T, C::BM, C::BN, C::BK, C::WM, C::WN, AKC, BKC, VEC, SYRK>;
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, C::NT, 0) != hipSuccess) occ = 1;
+  g.sk_groups = choose_sk(g, occ, ws_bytes);
+  const int grid = g.sk_groups ? g.sk_groups : g.ntiles;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(C::NT), 0, s, g);
+  int rc = check_launch(SYRK ? "trnblas_hip_syrk" : "trnblas_hip_gemm");
+  if (rc || !g.sk_groups) return rc;
+  hipLaunchKernelGGL((gemm_fixup_kernel<T, C::BM, C::BN, SYRK>),
+                     dim3(g.ntiles - g.dp_tiles, C::BM / 8), dim3(256), 0, s, g);
+  return check_launch(SYRK ? "trnblas_hip_syrk(fixup)" : "trnblas_hip_gemm(fixup)");
 }
 
 template <typename T, bool SYRK>
-static int launch_dtype(const GemmArgs& g, bool akc, bool bkc, bool vec, int ntiles,
+static int launch_dtype(const GemmArgs& g, bool akc, bool bkc, bool vec, size_t ws_bytes,
                         hipStream_t s) {
 #define TRNBLAS_L(a, b, v)                                 \
   if (akc == a && bkc == b && vec == v)                    \
-    return launch_t<T, a, b, v, SYRK>(g, ntiles, s);
+    return launch_t<T, a, b, v, SYRK>(g, ws_bytes, s);
   TRNBLAS_L(true, true, true)
   TRNBLAS_L(true, true, false)
   TRNBLAS_L(false, false, true)
@@ -334,7 +485,7 @@ static int elem_size(int dtype) { return dtype == TRNBLAS_F32 ? 4 : 2; }
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 template <bool SYRK>
-static int dispatch(int dtype, const GemmArgs& g, bool akc, bool bkc, int ntiles,
+static int dispatch(int dtype, const GemmArgs& g, bool akc, bool bkc, size_t ws_bytes,
                     hipStream_t s) {
   const int ev = 16 / elem_size(dtype);
   // Buffer offsets inside one k-tile panel are 32-bit: the panel (tile rows
@@ -353,11 +504,11 @@ static int dispatch(int dtype, const GemmArgs& g, bool akc, bool bkc, int ntiles
                    g.sA % ev == 0 && g.sB % ev == 0 && a_ext % ev == 0 && b_ext % ev == 0;
   switch (dtype) {
     case TRNBLAS_F32:
-      return launch_dtype<float, SYRK>(g, akc, bkc, vec, ntiles, s);
+      return launch_dtype<float, SYRK>(g, akc, bkc, vec, ws_bytes, s);
     case TRNBLAS_BF16:
-      return launch_dtype<__bf16, SYRK>(g, akc, bkc, vec, ntiles, s);
+      return launch_dtype<__bf16, SYRK>(g, akc, bkc, vec, ws_bytes, s);
     case TRNBLAS_F16:
-      return launch_dtype<_Float16, SYRK>(g, akc, bkc, vec, ntiles, s);
+      return launch_dtype<_Float16, SYRK>(g, akc, bkc, vec, ws_bytes, s);
   }
   set_error("unsupported dtype %d", dtype);
   return TRNBLAS_E_ARG;
@@ -367,12 +518,17 @@ static int dispatch(int dtype, const GemmArgs& g, bool akc, bool bkc, int ntiles
 
 using namespace trnblas;
 
+extern "C" size_t trnblas_hip_gemm_workspace(void) {
+  // two fp32 partial tiles per resident workgroup slot (at most 2 per CU)
+  return (size_t)device_cus() * 2 * 2 * kSkSlotBytes;
+}
+
 extern "C" int trnblas_hip_gemm(int dtype, int transA, int transB, int64_t M, int64_t N,
                                 int64_t K, double alpha, const void* A, int64_t lda,
                                 int64_t strideA, const void* B, int64_t ldb, int64_t strideB,
                                 double beta, const void* C, int64_t ldc, int64_t strideC,
                                 void* D, int64_t ldd, int64_t strideD, int64_t batch,
-                                void* stream) {
+                                void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   TRNBLAS_CHECK_ARG(dtype == TRNBLAS_F32 || dtype == TRNBLAS_BF16 || dtype == TRNBLAS_F16,
                     "gemm: dtype %d not supported", dtype);
@@ -391,7 +547,7 @@ extern "C" int trnblas_hip_gemm(int dtype, int transA, int transB, int64_t M, in
     TRNBLAS_CHECK_ARG(C != nullptr, "gemm: beta != 0 needs C");
     TRNBLAS_CHECK_ARG(ldc >= N, "gemm: ldc too small");
   }
-  GemmArgs g;
+  GemmArgs g{};
   g.M = (int)M;
   g.N = (int)N;
   g.K = (int)K;
@@ -411,18 +567,22 @@ extern "C" int trnblas_hip_gemm(int dtype, int transA, int transB, int64_t M, in
   g.sD = strideD;
   g.batch = (int)batch;
   g.uplo = 0;
-  const int bm = 128, bn = 128;
-  g.tiles_m = (int)((M + bm - 1) / bm);
-  g.tiles_n = (int)((N + bn - 1) / bn);
-  const int64_t ntiles = (int64_t)g.tiles_m * g.tiles_n;
+  g.tiles_m = (int)((M + kTileM - 1) / kTileM);
+  g.tiles_n = (int)((N + kTileN - 1) / kTileN);
+  const int64_t ntiles = (int64_t)g.tiles_m * g.tiles_n * batch;
   TRNBLAS_CHECK_ARG(ntiles < (1ll << 31), "gemm: too many tiles");
+  g.ntiles = (int)ntiles;
+  g.nk = (int)((K + (dtype == TRNBLAS_F32 ? 15 : 31)) / (dtype == TRNBLAS_F32 ? 16 : 32));
+  g.ws = static_cast<float*>(workspace);
   // A is K-contiguous unless transposed; B is K-contiguous only when transposed.
-  return dispatch<false>(dtype, g, !transA, transB != 0, (int)ntiles, (hipStream_t)stream);
+  return dispatch<false>(dtype, g, !transA, transB != 0, workspace ? workspace_bytes : 0,
+                         (hipStream_t)stream);
 }
 
 extern "C" int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64_t K,
                                 double alpha, const void* A, int64_t lda, double beta,
-                                const void* C, int64_t ldc, void* D, int64_t ldd, void* stream) {
+                                const void* C, int64_t ldc, void* D, int64_t ldd,
+                                void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   TRNBLAS_CHECK_ARG(dtype == TRNBLAS_F32 || dtype == TRNBLAS_BF16 || dtype == TRNBLAS_F16,
                     "syrk: dtype %d not supported", dtype);
@@ -435,7 +595,7 @@ extern "C" int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64
     TRNBLAS_CHECK_ARG(lda >= (trans ? N : K), "syrk: lda too small");
   }
   if (beta != 0.0) TRNBLAS_CHECK_ARG(C != nullptr && ldc >= N, "syrk: bad C / ldc");
-  GemmArgs g;
+  GemmArgs g{};
   g.M = (int)N;
   g.N = (int)N;
   g.K = (int)K;
@@ -455,12 +615,15 @@ extern "C" int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64
   g.sD = 0;
   g.batch = 1;
   g.uplo = uplo ? 1 : 0;
-  const int t = (int)((N + 127) / 128);
+  const int t = (int)((N + kTileM - 1) / kTileM);
   g.tiles_m = g.tiles_n = t;
-  const int64_t ntri = (int64_t)t * (t + 1) / 2;
+  g.ntiles = (int)((int64_t)t * (t + 1) / 2);
+  g.nk = (int)((K + (dtype == TRNBLAS_F32 ? 15 : 31)) / (dtype == TRNBLAS_F32 ? 16 : 32));
+  g.ws = static_cast<float*>(workspace);
   // trans == 0: op(A) = A (N x K, K-contiguous) and B(k, n) = A[n][k] (K-contiguous).
   // trans != 0: op(A) = A^T with A K x N (N-contiguous), B(k, n) = A[k][n].
-  return dispatch<true>(dtype, g, !trans, !trans, (int)ntri, (hipStream_t)stream);
+  return dispatch<true>(dtype, g, !trans, !trans, workspace ? workspace_bytes : 0,
+                        (hipStream_t)stream);
 }
 
 // Which strict triangles of an n x n matrix hold a nonzero (NaN counts), for
@@ -472,24 +635,33 @@ __global__ void zero_flags_kernel(int32_t* flags) {
   if (threadIdx.x < 2) flags[threadIdx.x] = 0;
 }
 
+// A bounded grid strides over rows (4 rows per pass, one per wave; lanes
+// stride along the row, coalesced); one atomic per workgroup and flag.
 template <typename T>
 __global__ __launch_bounds__(256) void triangle_nonzero_kernel(int n, const T* C, int64_t ldc,
                                                                int32_t* flags) {
-  const int64_t total = (int64_t)n * n;
-  int up = 0, lo = 0;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    const int r = (int)(idx / n), c = (int)(idx - (int64_t)r * n);
-    const float v = (float)C[(int64_t)r * ldc + c];
-    const int nz = !(v == 0.0f);
-    up |= nz & (c > r);
-    lo |= nz & (c < r);
-  }
-  up = __any(up);
-  lo = __any(lo);
-  if ((threadIdx.x & 63) == 0) {
-    if (up) atomicOr(&flags[0], 1);
-    if (lo) atomicOr(&flags[1], 1);
+  const int lane = threadIdx.x & 63;
+  // A small grid of waves scans rows; a wave skips the side(s) already known
+  // to hold a nonzero (flags set by any wave) and stops when both are known,
+  // so a filled C is decided after a few rows per wave.
+  for (int r = blockIdx.x * 4 + (threadIdx.x >> 6); r < n; r += gridDim.x * 4) {
+    const int fu = __atomic_load_n(&flags[0], __ATOMIC_RELAXED);
+    const int fl = __atomic_load_n(&flags[1], __ATOMIC_RELAXED);
+    if (fu && fl) break;
+    const T* row = C + (int64_t)r * ldc;
+    int up = 0, lo = 0;
+    const int cb = fl ? r + 1 : 0, ce = fu ? r : n;  // columns still of interest
+    for (int c = cb + lane; c < ce; c += 64) {
+      const int nz = !((float)row[c] == 0.0f);
+      up |= nz & (c > r);
+      lo |= nz & (c < r);
+    }
+    up = __any(up);
+    lo = __any(lo);
+    if (lane == 0) {
+      if (up && !fu) atomicOr(&flags[0], 1);
+      if (lo && !fl) atomicOr(&flags[1], 1);
+    }
   }
 }
 
@@ -504,7 +676,7 @@ extern "C" int trnblas_hip_triangle_nonzero(int dtype, int64_t n, const void* C,
   hipLaunchKernelGGL(zero_flags_kernel, dim3(1), dim3(64), 0, s, flags);
   if (n == 0) return check_launch("triangle_nonzero");
   TRNBLAS_CHECK_ARG(C != nullptr && ldc >= n, "triangle_nonzero: bad C / ldc");
-  const int64_t blocks = std::min<int64_t>(((int64_t)n * n + 255) / 256, 4096);
+  const int64_t blocks = std::min<int64_t>((n + 3) / 4, 32);
   switch (dtype) {
     case TRNBLAS_F32:
       hipLaunchKernelGGL(triangle_nonzero_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, s,

@@ -28,6 +28,22 @@ def _probed_call(kernel: str, fn: str, *args) -> int:
         probe(kernel, "end")
 
 
+_gemm_ws: dict = {}
+
+
+def gemm_workspace(dev: torch.device) -> torch.Tensor:
+    """The stream-K workspace of `dev` (allocated once, reused by every GEMM /
+    SYRK launch on the device; launches on one stream are ordered)."""
+    key = (dev.index if dev.index is not None else torch.cuda.current_device())
+    ws = _gemm_ws.get(key)
+    if ws is None:
+        with torch.cuda.device(key):
+            n = _lib.load().trnblas_hip_gemm_workspace()
+        ws = torch.empty(max(n, 16), dtype=torch.uint8, device=torch.device("cuda", key))
+        _gemm_ws[key] = ws
+    return ws
+
+
 def _require_device(*ts: torch.Tensor) -> torch.device:
     dev = ts[0].device
     for t in ts:
@@ -95,6 +111,7 @@ def gemm(
         a, ta, lda = _mat_layout(A)
         b, tb, ldb = _mat_layout(B)
         D = torch.empty((M, N), dtype=A.dtype, device=dev)
+        ws = gemm_workspace(dev)
         c, ldc = None, N
         if beta != 0.0 and C is not None:
             c = C.expand(M, N)
@@ -104,7 +121,7 @@ def gemm(
         _probed_call(
             "gemm", "trnblas_hip_gemm", code, int(ta), int(tb), M, N, K, float(alpha),
             ptr(a), lda, 0, ptr(b), ldb, 0, float(beta) if c is not None else 0.0,
-            ptr(c), ldc, 0, ptr(D), N, 0, 1, stream_of(dev),
+            ptr(c), ldc, 0, ptr(D), N, 0, 1, ptr(ws), ws.numel(), stream_of(dev),
         )  # fmt: skip
         return D
     if A.dim() != 3 or B.dim() != 3:
@@ -119,6 +136,7 @@ def gemm(
     a, ta, lda, sa = _batched_layout(A)
     b, tb, ldb, sb = _batched_layout(B)
     D = torch.empty((nb, M, N), dtype=A.dtype, device=dev)
+    ws = gemm_workspace(dev)
     c, ldc, sc = None, N, 0
     if beta != 0.0 and C is not None:
         c = C.expand(nb, M, N)
@@ -128,7 +146,7 @@ def gemm(
     _probed_call(
         "gemm", "trnblas_hip_gemm", code, int(ta), int(tb), M, N, K, float(alpha),
         ptr(a), lda, sa, ptr(b), ldb, sb, float(beta) if c is not None else 0.0,
-        ptr(c), ldc, sc, ptr(D), N, M * N, nb, stream_of(dev),
+        ptr(c), ldc, sc, ptr(D), N, M * N, nb, ptr(ws), ws.numel(), stream_of(dev),
     )  # fmt: skip
     return D
 
@@ -153,6 +171,7 @@ def syrk(
     n = A.shape[1] if trans else A.shape[0]
     k = A.shape[0] if trans else A.shape[1]
     D = torch.empty((n, n), dtype=A.dtype, device=dev)
+    ws = gemm_workspace(dev)
     c, ldc = None, n
     if beta != 0.0 and C is not None:
         if C.dtype != A.dtype:
@@ -162,7 +181,7 @@ def syrk(
     _probed_call(
         "syrk", "trnblas_hip_syrk", code, 1 if uplo == "upper" else 0, int(t), n, k, float(alpha),
         ptr(a), lda, float(beta) if c is not None else 0.0, ptr(c), ldc, ptr(D), n,
-        stream_of(dev),
+        ptr(ws), ws.numel(), stream_of(dev),
     )  # fmt: skip
     return D
 
