@@ -43,7 +43,7 @@ def test_argument_errors_are_reported_without_a_gpu():
         pytest.skip("library not built")
     lib = _lib.load()
     rc = lib.trnblas_hip_gemm(7, 0, 0, 4, 4, 4, 1.0, None, 4, 0, None, 4, 0, 0.0, None, 4, 0,
-                              None, 4, 0, 1, None)
+                              None, 4, 0, 1, None, 0, None)
     assert rc == _lib.E_ARG and b"dtype" in lib.trnblas_hip_last_error()
     rc = lib.trnblas_hip_ozaki_gemm(0, 13, 4, 4, 128, 128, None, 128, 0, None, 128, 0, None,
                                     None, None, 4, 1, None)
