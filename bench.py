@@ -43,6 +43,21 @@ BATCHED_FLOP = BATCH * 2 * BM * BN * BK
 STEP_FLOP = SYRK_FLOP + BATCHED_FLOP
 
 
+def committed_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (profiles/pmc_traffic.md: FETCH_SIZE + WRITE_SIZE per dispatch,
+    scaled by the same counters' reading for a plain copy of known size), or
+    None when there is no such summary."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "pmc_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith(f"traffic_bytes_per_launch[{kernel}]"):
+                return float(line.split("=", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -215,6 +230,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument(
+        "--calibrate-copy",
+        action="store_true",
+        help="also run a plain 256 MiB device copy (the reference kernel for rocprofv3 "
+        "FETCH_SIZE / WRITE_SIZE scaling)",
+    )
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -263,11 +284,18 @@ def main():
         "peak": PEAK_FP32_MFMA,
         "unit": "TFLOP/s",
         "frac": achieved / PEAK_FP32_MFMA,
-        "traffic": None,
+        "traffic": committed_traffic("syrk"),
         "launch_ms": syrk_ms,
         "launches": len(probe.pairs),
         "algorithmic_flop_per_launch": SYRK_FLOP,
     }
+    if args.calibrate_copy:
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     # parity of the timed step (the outputs the step produced)
     S, D = step()
     torch.cuda.synchronize()
