@@ -261,3 +261,24 @@ def test_cpu_gemm_fp64_and_pair_energy():
                                       -1 - torch.rand(3, generator=g), 1 + torch.rand(8, generator=g)))
     e = nki_batched_pair_energy(Bp, eo, ev)
     assert abs(float(e) - pe.pair_energy_f64(Bp, eo, ev)) <= 1e-5 * abs(float(e))
+
+
+@pytest.mark.parametrize(
+    "threads,m,n,k,want",
+    [
+        # measured on the MI355X box: host torch.matmul vs the upload route
+        (16, 384, 384, 384, "host"),  # 0.133 ms host vs 0.169 ms upload
+        (16, 512, 512, 512, "upload"),  # 0.297 vs 0.220
+        (16, 16, 49152, 128, "host"),  # 0.579 vs 0.872
+        (16, 128, 49152, 128, "upload"),  # 2.25 vs 1.34
+        (16, 64, 4096, 4096, "upload"),  # 3.18 vs 2.81
+        (2, 192, 192, 192, "host"),  # 0.076 vs 0.211
+        (2, 256, 256, 256, "upload"),  # 0.152 vs 0.123
+        (1, 16, 49152, 128, "upload"),  # 3.03 vs 0.872
+    ],
+)
+def test_route_measured_crossovers(monkeypatch, threads, m, n, k, want):
+    _fake_gpu(monkeypatch)
+    monkeypatch.setattr(torch, "get_num_threads", lambda: threads)
+    A, B = torch.empty(m, k), torch.empty(k, n)
+    assert d._gemm_route(A, B) == want

@@ -401,7 +401,7 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs g) {
 template <typename T>
 struct Cfg {
   static constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
-  static constexpr int BK = sizeof(T) == 4 ? 16 : 32;
+  static constexpr int BK = 32;
   static constexpr int NT = (BM / WM) * (BN / WN) * 64;
 };
 
@@ -482,6 +482,9 @@ static int launch_dtype(const GemmArgs& g, bool akc, bool bkc, bool vec, size_t 
 
 static int elem_size(int dtype) { return dtype == TRNBLAS_F32 ? 4 : 2; }
 
+// k-tile of the launch configuration for `dtype`
+static int k_tile(int dtype) { return dtype == TRNBLAS_F32 ? Cfg<float>::BK : Cfg<__bf16>::BK; }
+
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 template <bool SYRK>
@@ -490,7 +493,7 @@ static int dispatch(int dtype, const GemmArgs& g, bool akc, bool bkc, size_t ws_
   const int ev = 16 / elem_size(dtype);
   // Buffer offsets inside one k-tile panel are 32-bit: the panel (tile rows
   // times the leading dimension) must stay below 2 GiB.
-  const int64_t es = elem_size(dtype), bk = es == 4 ? 16 : 32;
+  const int64_t es = elem_size(dtype), bk = k_tile(dtype);
   const int64_t span_a = (akc ? 128 : bk) * g.lda * es, span_b = (bkc ? 128 : bk) * g.ldb * es;
   if (span_a >= (int64_t)kRecords - 64 || span_b >= (int64_t)kRecords - 64) {
     set_error("gemm: leading dimension too large for 32-bit panel offsets (lda %lld, ldb %lld)",
@@ -572,7 +575,7 @@ extern "C" int trnblas_hip_gemm(int dtype, int transA, int transB, int64_t M, in
   const int64_t ntiles = (int64_t)g.tiles_m * g.tiles_n * batch;
   TRNBLAS_CHECK_ARG(ntiles < (1ll << 31), "gemm: too many tiles");
   g.ntiles = (int)ntiles;
-  g.nk = (int)((K + (dtype == TRNBLAS_F32 ? 15 : 31)) / (dtype == TRNBLAS_F32 ? 16 : 32));
+  g.nk = (int)((K + k_tile(dtype) - 1) / k_tile(dtype));
   g.ws = static_cast<float*>(workspace);
   // A is K-contiguous unless transposed; B is K-contiguous only when transposed.
   return dispatch<false>(dtype, g, !transA, transB != 0, workspace ? workspace_bytes : 0,
@@ -618,7 +621,7 @@ extern "C" int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64
   const int t = (int)((N + kTileM - 1) / kTileM);
   g.tiles_m = g.tiles_n = t;
   g.ntiles = (int)((int64_t)t * (t + 1) / 2);
-  g.nk = (int)((K + (dtype == TRNBLAS_F32 ? 15 : 31)) / (dtype == TRNBLAS_F32 ? 16 : 32));
+  g.nk = (int)((K + k_tile(dtype) - 1) / k_tile(dtype));
   g.ws = static_cast<float*>(workspace);
   // trans == 0: op(A) = A (N x K, K-contiguous) and B(k, n) = A[n][k] (K-contiguous).
   // trans != 0: op(A) = A^T with A K x N (N-contiguous), B(k, n) = A[k][n].

@@ -221,15 +221,19 @@ def _pair_result_dtype(B, eps_vir) -> torch.dtype:
 # the GPU, the kernel, the result copied back), 'aten' (torch on the GPU).
 #
 # Host-vs-device model, as the reference's `_host_gemm_wins` (:277-285):
-# for all-host fp32 operands the host wins when
-#     macs < threads / 2 * (fixed + per_byte * link_bytes),
-# `fixed` the upload + launch + download floor in host multiply-adds and
-# `per_byte` the host-link cost per byte in host multiply-adds. Fitted on the
-# MI355X box (PCIe Gen5 x16, pageable host memory; see DESIGN.md for the
-# sweep): the device floor is ~40 us and the link ~25 GB/s pageable, against
-# ~25 GMAC/s per two host threads.
+# for all-host operands the host wins when
+#     macs < (threads / 2) ** 0.7 * (fixed + per_byte * link_bytes),
+# `fixed` the upload + launch + download floor in host multiply-adds at two
+# host threads and `per_byte` the host-link cost per byte on the same scale.
+# Measured on the MI355X box over 16 shapes (square 64..4096, skinny and
+# tall) at 1, 2 and 16 host threads against the upload route (pageable H2D
+# ~29 GB/s, pinned D2H ~57 GB/s, ~0.1 ms floor, ~65 GMAC/s per host thread);
+# the exponent 0.7 carries the host's falling parallel efficiency at small
+# sizes. With these constants every one of the 48 measured cases takes the
+# faster route. bf16 uses the fp32 fit (its host rate was not measured).
 _HOST_GEMM_MODEL_THREADS = 2
-_HOST_GEMM_MODEL = {"fp32": (1.0e6, 1.0), "bf16": (2.0e6, 2.0)}
+_HOST_GEMM_THREAD_EXP = 0.7
+_HOST_GEMM_MODEL = {"fp32": (1.2e7, 1.0), "bf16": (1.2e7, 1.0)}
 _DEVICE_GEMM_DTYPES = {torch.float32: "fp32", torch.bfloat16: "bf16", torch.float16: "fp32"}
 _NATIVE_GEMM_CHOICES = ("auto", "hip", "nki", "aten", "host")
 
@@ -270,7 +274,7 @@ def _host_gemm_wins(macs: float, nbytes: int, dtype: torch.dtype) -> bool:
     if kind is None:
         return True
     fixed, per_byte = _HOST_GEMM_MODEL[kind]
-    scale = max(1, torch.get_num_threads()) / _HOST_GEMM_MODEL_THREADS
+    scale = (max(1, torch.get_num_threads()) / _HOST_GEMM_MODEL_THREADS) ** _HOST_GEMM_THREAD_EXP
     return macs < scale * (fixed + per_byte * nbytes)
 
 
@@ -309,6 +313,20 @@ def _gpu_device(*ts) -> torch.device:
 
 def _to(t, dev):
     return None if t is None else t.to(dev, non_blocking=False)
+
+
+def _to_host(t: torch.Tensor, orig: torch.device) -> torch.Tensor:
+    """A device result back on the host device `orig`: into fresh pinned
+    memory (device-to-host copies from pageable memory run ~4 GB/s on the
+    MI355X host, from pinned ~10x faster; the reference's `_host_empty` /
+    `_to_host`, nki/dispatch.py:2055-2101, makes the same choice)."""
+    if orig.type != "cpu" or t.device.type == "cpu":
+        return t.to(orig)
+    if t.numel() * t.element_size() < (1 << 20):
+        return t.cpu()
+    out = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+    out.copy_(t)
+    return out
 
 
 # ── GEMM family ──────────────────────────────────────────────────────────────
@@ -387,7 +405,7 @@ def nki_gemm(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
         dev = _gpu_device(A, B)
         orig = A.device
         try:
-            return hip_gemm(_to(A, dev), _to(B, dev)).to(orig)
+            return _to_host(hip_gemm(_to(A, dev), _to(B, dev)), orig)
         except Exception as exc:  # noqa: BLE001
             _kernel_failed(exc)
             return torch.matmul(A, B)
@@ -409,7 +427,7 @@ def nki_batched_gemm(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     try:
         a3, b3, batch = _flatten_batch(_to(A, dev), _to(B, dev))
         out = hip_gemm(a3, b3).reshape(*batch, A.shape[-2], B.shape[-1])
-        return out.to(orig) if orig != dev else out
+        return _to_host(out, orig) if orig != dev else out
     except Exception as exc:  # noqa: BLE001
         _kernel_failed(exc)
         return torch.matmul(A, B)
@@ -432,9 +450,7 @@ def gemm_scaled(alpha, a, b, beta, C):
         ad, bd = _to(a, dev), _to(b, dev)
         Cd = None if (C is None or beta == 0.0) else (C.to(dev) if C.device != dev else C)
         out = hip_gemm(ad, bd, alpha, beta, Cd)
-        if a.dim() == 2 and b.dim() == 3:
-            pass
-        return out.to(orig) if orig != dev else out
+        return _to_host(out, orig) if orig != dev else out
     except Exception as exc:  # noqa: BLE001
         _kernel_failed(exc)
         return _torch_scale_add(torch.matmul(a, b), alpha, beta, C)
@@ -458,7 +474,7 @@ def nki_syrk(A: torch.Tensor, symmetrize: bool = False) -> torch.Tensor:
 
         dev = _gpu_device(A)
         try:
-            return kernels.syrk(_to(A, dev)).to(A.device)
+            return _to_host(kernels.syrk(_to(A, dev)), A.device)
         except Exception as exc:  # noqa: BLE001
             _kernel_failed(exc)
     r = torch.matmul(A, A.mT)
@@ -481,7 +497,7 @@ def hip_syrk(alpha, A, beta, C, trans: bool, uplo: str) -> torch.Tensor | None:
     try:
         Cd = None if C is None or beta == 0.0 else _to(C, dev)
         out = kernels.syrk(_to(A, dev), alpha, beta if Cd is not None else 0.0, Cd, trans, uplo)
-        return out.to(orig) if orig != dev else out
+        return _to_host(out, orig) if orig != dev else out
     except Exception as exc:  # noqa: BLE001
         _kernel_failed(exc)
         return None
