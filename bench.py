@@ -32,6 +32,7 @@ import torch
 
 # MI355X published dense peaks (TFLOP/s or TOPS) and HBM bandwidth.
 PEAK_FP32_MFMA = 157.3
+PEAK_BF16_MFMA = 2500.0
 PEAK_FP64_MFMA = 78.6
 PEAK_INT8 = 5033.0
 PEAK_HBM_GBS = 8000.0
@@ -159,11 +160,14 @@ def run_extras(dev, tb) -> dict:
     }  # fmt: skip
     log("gemm8192", out["gemm_fp32_8192"])
     del X, Y
-    # C3: fused pair energy vs the unfused GPU baseline (hipBLASLt GEMM + torch)
+    # C3: fused pair energy vs the unfused GPU baseline (hipBLASLt GEMM + torch),
+    # in both kernel arithmetics (bf16x6 is the default)
     Bp, eo, ev = df_mp2.config3_inputs(dev)
-    tf = gpu_time_ms(lambda: kernels.pair_energy_sym(Bp, eo, ev), reps=3, warm=1)
+    tf = gpu_time_ms(lambda: kernels.pair_energy_sym(Bp, eo, ev, math="bf16x6"), reps=3, warm=1)
+    tf32 = gpu_time_ms(lambda: kernels.pair_energy_sym(Bp, eo, ev, math="fp32"), reps=3, warm=1)
     tu = gpu_time_ms(lambda: dispatch._torch_chunked_pair_energy(Bp, eo, ev), reps=3, warm=1)
-    e_hip = float(kernels.pair_energy_sym(Bp, eo, ev))
+    e_hip = float(kernels.pair_energy_sym(Bp, eo, ev, math="bf16x6"))
+    e_f32 = float(kernels.pair_energy_sym(Bp, eo, ev, math="fp32"))
     e_unf = float(dispatch._torch_chunked_pair_energy(Bp, eo, ev))
     Bd, eod, evd = Bp.double(), eo.double(), ev.double()
     e64 = torch.zeros((), dtype=torch.float64, device=dev)
@@ -187,9 +191,14 @@ def run_extras(dev, tb) -> dict:
         pe.fused_pair_cpu(Bh[0], Bh[j], float(eoh[0]), float(eoh[j]), evh)
     cpu_pair_s = (time.perf_counter() - t0) / 12
     out["pair_energy_c3_96_672_2304"] = {
-        "fused_ms": tf, "unfused_gpu_ms": tu, "speedup_vs_unfused": tu / tf,
-        "tflops_sym": fl / tf / 1e9, "frac_fp32_peak": fl / tf / 1e9 / PEAK_FP32_MFMA,
+        "fused_ms": tf, "fused_math": "bf16x6", "unfused_gpu_ms": tu,
+        "speedup_vs_unfused": tu / tf, "tflops_sym": fl / tf / 1e9,
+        "bf16_mfma_tflops": 6 * fl / tf / 1e9,
+        "frac_bf16_peak": 6 * fl / tf / 1e9 / PEAK_BF16_MFMA,
         "energy_fp64": e64, "rel_err_fused_vs_fp64": abs(e_hip - e64) / abs(e64),
+        "fused_fp32_mfma_ms": tf32, "speedup_fp32_mfma_vs_unfused": tu / tf32,
+        "frac_fp32_peak_fp32_mfma": fl / tf32 / 1e9 / PEAK_FP32_MFMA,
+        "rel_err_fused_fp32_mfma_vs_fp64": abs(e_f32 - e64) / abs(e64),
         "rel_err_unfused_fp32_vs_fp64": abs(e_unf - e64) / abs(e64), "gate": 1e-6,
         "cpu_fp32_loop_ms_est": cpu_pair_s * 96 * 96 * 1e3,
         "cpu_sample": "12 of 9216 ordered pairs of the fp32 torch loop, scaled",

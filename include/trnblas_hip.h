@@ -144,6 +144,29 @@ int trnblas_hip_pair_energy(int64_t nvir, int64_t naux, const float* Bi, int64_t
                             void* stream);
 
 /*
+ * DF-MP2 pair energies as trnblas_hip_pair_energy — same arguments, pair set,
+ * weights, outputs, workspace and determinism — with every fp32 product
+ * formed on bf16 MFMA (v_mfma_f32_16x16x32_bf16, fp32 accumulation) from the
+ * three bf16 pieces of each operand, split on the way into LDS:
+ *   x = hi + mid + lo exactly (hi = rn_bf16(x), mid = rn_bf16(x - hi),
+ *   lo = x - hi - mid), and
+ *   x y ~= hi_x hi_y + hi_x mid_y + mid_x hi_y + hi_x lo_y + mid_x mid_y + lo_x hi_y,
+ * the three dropped products being below 2^-23 |x y|. Each T entry then
+ * carries fp32 accumulation error plus that term (fp32-class accuracy) at
+ * 6/16 of the MFMA time of an fp32 product.
+ *
+ * Replaces the same reference interface as trnblas_hip_pair_energy
+ * (torch.ops.trnblas.pair_energy_sym, trnblas/nki/_native.py:221-239).
+ */
+int trnblas_hip_pair_energy_bf16x6(int64_t nvir, int64_t naux, const float* Bi, int64_t ldi_occ,
+                                   const float* Bj, int64_t ldj_occ, int64_t ld_vir,
+                                   const float* eps_i, const float* eps_j, const float* eps_vir,
+                                   int64_t nocc, int64_t npairs, const int32_t* pair_i,
+                                   const int32_t* pair_j, const double* pair_w,
+                                   double* out_pairs, double* out_total, void* workspace,
+                                   size_t workspace_bytes, void* stream);
+
+/*
  * MP2 energy of a precomputed amplitude block (no GEMM), HBM-bound.
  *
  * T[i][j][a][b] = T_flat[(i*nvir + a) * ldt + j*nvir + b] for i < ic,

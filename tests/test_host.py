@@ -282,3 +282,18 @@ def test_route_measured_crossovers(monkeypatch, threads, m, n, k, want):
     monkeypatch.setattr(torch, "get_num_threads", lambda: threads)
     A, B = torch.empty(m, k), torch.empty(k, n)
     assert d._gemm_route(A, B) == want
+
+
+def test_pair_energy_math_selection(monkeypatch):
+    from trnblas_amd.hip import kernels
+
+    monkeypatch.delenv("TRNBLAS_PAIR_ENERGY_MATH", raising=False)
+    assert kernels.pair_energy_math() == "bf16x6"
+    monkeypatch.setenv("TRNBLAS_PAIR_ENERGY_MATH", "fp32")
+    assert kernels.pair_energy_math() == "fp32"
+    assert kernels._check_math(None) == "fp32"
+    assert kernels._check_math("bf16x6") == "bf16x6"
+    monkeypatch.setenv("TRNBLAS_PAIR_ENERGY_MATH", "tf32")
+    with pytest.raises(ValueError):
+        kernels.pair_energy_math()
+    assert kernels._PE_ENTRY["bf16x6"] == "trnblas_hip_pair_energy_bf16x6"

@@ -9,6 +9,8 @@ from oracle import pair_energy as pe
 
 pytestmark = pytest.mark.gpu
 
+MATHS = ["fp32", "bf16x6"]
+
 
 def _inputs(nocc, nvir, naux, seed):
     g = torch.Generator().manual_seed(seed)
@@ -22,36 +24,43 @@ def _inputs(nocc, nvir, naux, seed):
     "nocc,nvir,naux",
     [(1, 1, 1), (3, 96, 128), (5, 97, 130), (4, 200, 77), (7, 130, 300), (2, 300, 5), (6, 33, 16)],
 )
-def test_pair_energy_sym_small(dev, nocc, nvir, naux):
+@pytest.mark.parametrize("math", MATHS)
+def test_pair_energy_sym_small(dev, nocc, nvir, naux, math):
     from trnblas_amd.hip import kernels
 
     B, eo, ev = _inputs(nocc, nvir, naux, nocc * 100 + nvir)
-    got = float(kernels.pair_energy_sym(B.to(dev), eo.to(dev), ev.to(dev)))
+    got = float(kernels.pair_energy_sym(B.to(dev), eo.to(dev), ev.to(dev), math=math))
     want = pe.pair_energy_f64(B, eo, ev)
     assert abs(got - want) <= 1e-6 * abs(want), (got, want)
 
 
-def test_pair_energy_unaligned_naux(dev):
-    # naux % 4 != 0 and a non-contiguous view: scalar-load path
+@pytest.mark.parametrize("math", MATHS)
+def test_pair_energy_unaligned_naux(dev, math):
+    # naux % 4 != 0 and a strided (non-contiguous) view: scalar-load paths
     from trnblas_amd.hip import kernels
 
     B, eo, ev = _inputs(4, 100, 63, 9)
-    Bv = B.to(dev)
-    got = float(kernels.pair_energy_sym(Bv, eo.to(dev), ev.to(dev)))
+    wide = torch.zeros(4, 100, 70)
+    wide[:, :, 3:66] = B
+    Bv = wide.to(dev)[:, :, 3:66]
+    assert not Bv.is_contiguous() and Bv.stride(1) == 70
+    got = float(kernels.pair_energy_sym(Bv, eo.to(dev), ev.to(dev), math=math))
     want = pe.pair_energy_f64(B, eo, ev)
     assert abs(got - want) <= 1e-6 * abs(want)
 
 
-def test_pair_energy_zero_B(dev):
+@pytest.mark.parametrize("math", MATHS)
+def test_pair_energy_zero_B(dev, math):
     from trnblas_amd.hip import kernels
 
     B = torch.zeros(3, 50, 40)
     eo = -torch.ones(3)
     ev = torch.ones(50)
-    assert float(kernels.pair_energy_sym(B.to(dev), eo.to(dev), ev.to(dev))) == 0.0
+    assert float(kernels.pair_energy_sym(B.to(dev), eo.to(dev), ev.to(dev), math=math)) == 0.0
 
 
-def test_pair_energies_explicit_pairs(dev):
+@pytest.mark.parametrize("math", MATHS)
+def test_pair_energies_explicit_pairs(dev, math):
     from trnblas_amd.hip import kernels
 
     B, eo, ev = _inputs(5, 150, 96, 3)
@@ -59,11 +68,77 @@ def test_pair_energies_explicit_pairs(dev):
     pi = torch.tensor([p[0] for p in pairs])
     pj = torch.tensor([p[1] for p in pairs])
     Bd = B.to(dev)
-    got = kernels.pair_energies(Bd, Bd, eo.to(dev), eo.to(dev), ev.to(dev), pi, pj).cpu()
+    got = kernels.pair_energies(Bd, Bd, eo.to(dev), eo.to(dev), ev.to(dev), pi, pj, math=math).cpu()
     want = pe.pair_energies_f64(B, B, eo, eo, ev, pairs)
     assert torch.allclose(got, want, rtol=1e-6, atol=0)
     # e_ij == e_ji (symmetry of the denominator)
     assert abs(got[1] - got[2]) <= 1e-6 * abs(got[1])
+
+
+@pytest.mark.parametrize("math", MATHS)
+def test_pair_energies_two_operands(dev, math):
+    # Bi != Bj (the j-batched surface): rows i of Bi against rows j of Bj
+    from trnblas_amd.hip import kernels
+
+    Bi, eo, ev = _inputs(3, 120, 70, 11)
+    Bj, ej, _ = _inputs(4, 120, 70, 12)
+    pairs = [(0, 3), (2, 0), (1, 1), (2, 2)]
+    pi = torch.tensor([p[0] for p in pairs])
+    pj = torch.tensor([p[1] for p in pairs])
+    got = kernels.pair_energies(
+        Bi.to(dev), Bj.to(dev), eo.to(dev), ej.to(dev), ev.to(dev), pi, pj, math=math
+    ).cpu()
+    want = pe.pair_energies_f64(Bi, Bj, eo, ej, ev, pairs)
+    assert torch.allclose(got, want, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("math", MATHS)
+def test_pair_energy_full_significands(dev, math):
+    # naux = 1, nvir = 1: T = x y exactly, e = T^2 / D. Operands with all 24
+    # significand bits set over a wide exponent range: an fp32-class product
+    # is within 2^-22 of x y; a split that lost its lo piece (2^-16) or its mid
+    # piece (2^-8) fails.
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(5)
+    n = 40
+    mant = 1.0 + torch.randint(0, 1 << 23, (n,), generator=g).double() / (1 << 23)
+    sign = torch.where(torch.rand(n, generator=g) < 0.5, -1.0, 1.0).double()
+    x = sign * mant * torch.exp2(torch.randint(-20, 20, (n,), generator=g).double())
+    B = x.float().reshape(n, 1, 1)
+    eo = -torch.rand(n, generator=g) - 0.5
+    ev = torch.tensor([0.7])
+    pairs = [(i, (i * 7 + 3) % n) for i in range(n)]
+    pi = torch.tensor([p[0] for p in pairs])
+    pj = torch.tensor([p[1] for p in pairs])
+    Bd = B.to(dev)
+    got = kernels.pair_energies(Bd, Bd, eo.to(dev), eo.to(dev), ev.to(dev), pi, pj, math=math).cpu()
+    want = pe.pair_energies_f64(B, B, eo, eo, ev, pairs)
+    rel = ((got - want).abs() / want.abs()).max().item()
+    assert rel <= 2.0**-21, rel
+
+
+def test_pair_energy_bf16x6_long_sums_unbiased(dev):
+    # nvir = 1, naux = 2304, pairs (i, i): T = sum_k x_k^2 > 0 and e = T^2 / D.
+    # The recovered T must carry no systematic error: summed slice by slice
+    # with fp32 adds its mean relative error is ~1e-10 (std ~1e-7); a long
+    # sum chained through the MFMA accumulator comes out ~1.5e-6 low.
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(0)
+    n, naux = 256, 2304
+    B = (0.05 * torch.randn(n, 1, naux, generator=g, dtype=torch.float64)).float()
+    eo, ev = -torch.ones(n), torch.tensor([0.5])
+    idx = torch.arange(n)
+    e = kernels.pair_energies(
+        B.to(dev), B.to(dev), eo.to(dev), eo.to(dev), ev.to(dev), idx, idx, math="bf16x6"
+    ).cpu()
+    T = (e * -3.0).sqrt()
+    Bd = B.double()[:, 0, :]
+    T64 = (Bd * Bd).sum(dim=1)
+    rel = (T - T64) / T64
+    assert abs(float(rel.mean())) <= 5e-8, float(rel.mean())
+    assert float(rel.abs().max()) <= 2e-6
 
 
 def test_mp2_energy_kernel(dev):
@@ -79,12 +154,13 @@ def test_mp2_energy_kernel(dev):
 
 
 @pytest.mark.parametrize("seed", [0])
-def test_pair_energy_config3_shape_subset(dev, seed):
+@pytest.mark.parametrize("math", MATHS)
+def test_pair_energy_config3_shape_subset(dev, seed, math):
     # The C3 virtual / aux sizes (672, 2304) at nocc = 6: every tile pair of
     # the production launch shape, against the fp64 closed form.
     from trnblas_amd.hip import kernels
 
     B, eo, ev = _inputs(6, 672, 2304, seed)
-    got = float(kernels.pair_energy_sym(B.to(dev), eo.to(dev), ev.to(dev)))
+    got = float(kernels.pair_energy_sym(B.to(dev), eo.to(dev), ev.to(dev), math=math))
     want = pe.pair_energy_f64(B, eo, ev)
     assert abs(got - want) <= 1e-6 * abs(want), (got, want)

@@ -300,6 +300,242 @@ __global__ __launch_bounds__(1024) void pair_total_kernel(const double* e_pair, 
   }
 }
 
+// ── bf16x6: fp32 products from three bf16 pieces on bf16 MFMA ───────────────
+//
+// x = hi + mid + lo exactly (each piece an 8-bit-significand bf16), and
+//   x y ~= hi_x hi_y + hi_x mid_y + mid_x hi_y + hi_x lo_y + mid_x mid_y + lo_x hi_y,
+// dropping mid_x lo_y + lo_x mid_y + lo_x lo_y (< 2^-23 |x y|). Each bf16
+// product is exact in fp32; the products of one 32-wide k slice are summed by
+// the MFMA, the slices by fp32 adds, so a dot product carries fp32
+// accumulation error plus that 2^-23 term. gfx950 runs
+// v_mfma_f32_16x16x32_bf16 at 16x the rate of v_mfma_f32_32x32x2_f32, so the
+// six products cost 6/16 of one fp32 MFMA product.
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// hi = rn_bf16(x), mid = rn_bf16(x - hi), lo = rn_bf16(x - hi - mid): both
+// differences are exact in fp32 and lo holds the last <= 8 bits exactly, so
+// x == hi + mid + lo for every normal x (v_cvt_pk_bf16_f32, round to
+// nearest even).
+__device__ __forceinline__ void split_bf16x3(const f32x4& x, i32x2& hi, i32x2& mid, i32x2& lo) {
+  bf16x4 h, m, l;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    h[e] = (__bf16)x[e];
+    const float r = x[e] - (float)h[e];
+    m[e] = (__bf16)r;
+    l[e] = (__bf16)(r - (float)m[e]);
+  }
+  hi = __builtin_bit_cast(i32x2, h);
+  mid = __builtin_bit_cast(i32x2, m);
+  lo = __builtin_bit_cast(i32x2, l);
+}
+
+constexpr int kX3S = 96, kX3BK = 32;
+
+// LDS slot of 16-byte group `grp` of panel row `r` (rows of 64 bytes): the
+// XOR makes every 8 (and every 16) consecutive rows of one group land on
+// distinct 16-byte bank groups, so fragment reads and stage writes are
+// conflict free without padding.
+__device__ __forceinline__ int x3_slot(int r, int grp) { return grp ^ (((r >> 1) ^ (r >> 2)) & 3); }
+
+// Work item = (pair, virtual tile pair A <= B) as in pair_energy_kernel, 96 x 96
+// tiles, 4 waves, wave w on the 48 x 48 quadrant (w & 1, w >> 1) as 3 x 3
+// blocks of 16 x 16. Off-diagonal items run two passes over k in one
+// pipeline: X = B_i[A] B_j[B]^T, then X' = B_j[A] B_i[B]^T (both held in
+// registers); diagonal items run the first pass only (B = A). The operands
+// are read as fp32 (4 bytes per element) and split into their three bf16
+// pieces on the way into LDS. A stage is one 32-wide k slice of the 3 pieces
+// x 2 panels of the running pass (36 KiB), double buffered (72 KiB, two
+// workgroups per CU); slices t+1 and t+2 are in flight in registers while
+// slice t is multiplied, one barrier per slice.
+template <bool VEC>
+__global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
+  constexpr int S = kX3S, BK = kX3BK;
+  constexpr int SIDE_V4 = S * BK / 4;    // float4 groups per panel slice (768)
+  constexpr int NV = 2 * SIDE_V4 / 256;  // float4 groups per thread per slice (6)
+  constexpr int STAGE = 6 * S * BK;      // bf16 elements: 3 pieces x 2 panels
+  static_assert(NV * 256 == 2 * SIDE_V4 && SIDE_V4 % 64 == 0, "stage split");
+  static_assert(2 * STAGE * 2 >= 2 * S * S * 4, "epilogue fits in the stage buffers");
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+  __shared__ double red[4];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int item = xcd_remap(blockIdx.x, gridDim.x);
+  const int p = item / g.nq, q = item - p * g.nq;
+  int i, j;
+  if (g.pair_i) {
+    i = g.pair_i[p];
+    j = g.pair_j[p];
+  } else {
+    tri_pair(p, g.nocc, i, j);
+  }
+  int TA, TB;
+  tri_tiles(q, g.nb, TA, TB);
+  const bool diag = TA == TB;
+  const int a0 = TA * S, b0 = TB * S;
+  const int nvir = g.nvir, naux = g.naux;
+  const int64_t ld_vir = g.ld_vir;
+  const float* Xi = g.Bi + (int64_t)i * g.ldi_occ;
+  const float* Xj = g.Bj + (int64_t)j * g.ldj_occ;
+  const int nk = (naux + BK - 1) / BK;
+  const int nsteps = diag ? nk : 2 * nk;
+
+  // Slice group index = side * 768 + row * 8 + c (c: float4 within the 32-wide
+  // row); side 0 is the A side (rows a0: B_i in pass 0, B_j in pass 1), side 1
+  // the B side (rows b0: B_j, then B_i). The 64 groups of one wave share the
+  // side, so the buffer resource is wave-uniform.
+  auto load = [&](int step, f32x4(&st)[NV]) {
+    const int pass = step >= nk ? 1 : 0, k0 = (step - pass * nk) * BK;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int base = w * 64 + v * 256;
+      const int side = base / SIDE_V4;
+      const bool use_i = (side ^ pass) == 0;
+      const int rbase = side ? b0 : a0;
+      const __amdgpu_buffer_rsrc_t rs =
+          pe_rsrc((use_i ? Xi : Xj) + (int64_t)rbase * ld_vir + k0);
+      const int local = base - side * SIDE_V4 + lane, r = local >> 3, c = (local & 7) * 4;
+      const bool rok = r < nvir - rbase;
+      const uint32_t off = (uint32_t)((r * ld_vir + c) * 4);
+      if (VEC) {
+        st[v] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (rok && c < naux - k0) ? off : kPeOob,
+                                                         0, 0));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          st[v][e] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(
+                         rs, (rok && c + e < naux - k0) ? off + 4 * e : kPeOob, 0, 0));
+      }
+    }
+  };
+  auto store = [&](int buf, const f32x4(&st)[NV]) {
+    uint16_t* dst = lds + buf * STAGE;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int base = w * 64 + v * 256;
+      const int side = base / SIDE_V4;
+      const int local = base - side * SIDE_V4 + lane, r = local >> 3, c = local & 7;
+      i32x2 h, m, l;
+      split_bf16x3(st[v], h, m, l);
+      const int e0 = (side * S + r) * BK + 8 * x3_slot(r, c >> 1) + 4 * (c & 1);
+      *reinterpret_cast<i32x2*>(dst + e0) = h;
+      *reinterpret_cast<i32x2*>(dst + 2 * S * BK + e0) = m;
+      *reinterpret_cast<i32x2*>(dst + 4 * S * BK + e0) = l;
+    }
+  };
+
+  // The fragment row of a lane is row0 + 16 blk + (lane & 15) with row0 a
+  // multiple of 16, so its LDS slot depends on the lane only.
+  const int ar0 = 48 * (w & 1), br0 = 48 * (w >> 1);
+  const int fslot = 8 * x3_slot(lane & 15, lane >> 4);
+  f32x4 accX[3][3], accP[3][3];
+#pragma unroll
+  for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 3; ++cb) accX[rb][cb] = accP[rb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto mma = [&](const uint16_t* buf, f32x4(&acc)[3][3]) {
+    auto frag = [&](int pc, int side, int r) {
+      return *reinterpret_cast<const bf16x8*>(buf + ((pc * 2 + side) * S + r) * BK + fslot);
+    };
+    bf16x8 fa[3][3];
+#pragma unroll
+    for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+      for (int pc = 0; pc < 3; ++pc) fa[rb][pc] = frag(pc, 0, ar0 + 16 * rb + (lane & 15));
+#pragma unroll
+    for (int cb = 0; cb < 3; ++cb) {
+      bf16x8 fb[3];
+#pragma unroll
+      for (int pc = 0; pc < 3; ++pc) fb[pc] = frag(pc, 1, br0 + 16 * cb + (lane & 15));
+      // The six products of this slice, smallest first, go into a fresh
+      // partial that joins the running sum through an IEEE fp32 add: chained
+      // through the MFMA accumulator, a long sum drifts (a 2304-term positive
+      // dot product came out 1.5e-6 low on average; 6e-11 this way).
+      f32x4 part[3];
+#pragma unroll
+      for (int rb = 0; rb < 3; ++rb) part[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int t = 0; t < 6; ++t) {
+        constexpr int ka[6] = {2, 1, 0, 1, 0, 0}, kb[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll
+        for (int rb = 0; rb < 3; ++rb)
+          part[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[rb][ka[t]], fb[kb[t]], part[rb],
+                                                             0, 0, 0);
+      }
+#pragma unroll
+      for (int rb = 0; rb < 3; ++rb) acc[rb][cb] += part[rb];
+    }
+  };
+
+  // Two register sets alternate (the loop is unrolled by two): at slice t,
+  // slice t + 1 is already in flight and slice t + 2 is requested.
+  f32x4 s0[NV], s1[NV];
+  if (nsteps > 0) load(0, s0);
+  if (nsteps > 1) load(1, s1);
+  if (nsteps > 0) {
+    store(0, s0);
+    __syncthreads();
+  }
+  for (int t = 0; t < nsteps; t += 2) {
+    if (t + 2 < nsteps) load(t + 2, s0);
+    if (t < nk)
+      mma(lds, accX);
+    else
+      mma(lds, accP);
+    if (t + 1 < nsteps) store(1, s1);
+    __syncthreads();
+    if (t + 1 >= nsteps) break;
+    if (t + 3 < nsteps) load(t + 3, s1);
+    if (t + 1 < nk)
+      mma(lds + STAGE, accX);
+    else
+      mma(lds + STAGE, accP);
+    if (t + 2 < nsteps) store(0, s0);
+    __syncthreads();
+  }
+
+  // Lane l of a 16 x 16 block holds column l % 16 and rows 4 (l / 16) + r.
+  // Off-diagonal: X at [0, S*S), X' at [S*S, 2 S*S), row stride S.
+  // Diagonal: X at row stride S + 1 (conflict-free transposed reads).
+  float* xs = reinterpret_cast<float*>(lds);
+  const int ldx = diag ? S + 1 : S;
+#pragma unroll
+  for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 3; ++cb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int a = ar0 + 16 * rb + 4 * (lane >> 4) + r;
+        const int b = br0 + 16 * cb + (lane & 15);
+        xs[a * ldx + b] = accX[rb][cb][r];
+        if (!diag) xs[S * S + a * S + b] = accP[rb][cb][r];
+      }
+  __syncthreads();
+
+  const double eo = (double)g.eps_i[i] + (double)g.eps_j[j];
+  double sum = 0.0;
+#pragma unroll 4
+  for (int e = 0; e < S * S / 256; ++e) {
+    const int idx = tid + 256 * e, a = idx / S, b = idx - a * S;
+    if (a0 + a < nvir && b0 + b < nvir) {
+      const double x = xs[a * ldx + b];
+      const double xp = diag ? xs[b * ldx + a] : xs[S * S + a * S + b];
+      const double d = eo - (double)g.eps_vir[a0 + a] - (double)g.eps_vir[b0 + b];
+      sum += (diag ? x * (2.0 * x - xp) : 2.0 * (x * x + xp * xp - x * xp)) / d;
+    }
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) red[w] = sum;
+  __syncthreads();
+  if (tid == 0) g.partial[item] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
 // MP2 energy of a precomputed amplitude block (the `mp2_energy` surface,
 // trnblas/nki/dispatch.py:4356-4491): one workgroup per (i, j) pair walks the
 // 32 x 32 tile pairs (A <= B) of T_ij, reading T[A,B] and T[B,A] once each
@@ -360,45 +596,43 @@ extern "C" size_t trnblas_hip_pair_energy_workspace(int64_t nvir, int64_t npairs
   return (size_t)(npairs * pe_nq(nvir) + npairs) * sizeof(double);
 }
 
-extern "C" int trnblas_hip_pair_energy(int64_t nvir, int64_t naux, const float* Bi,
-                                       int64_t ldi_occ, const float* Bj, int64_t ldj_occ,
-                                       int64_t ld_vir, const float* eps_i, const float* eps_j,
-                                       const float* eps_vir, int64_t nocc, int64_t npairs,
-                                       const int32_t* pair_i, const int32_t* pair_j,
-                                       const double* pair_w, double* out_pairs,
-                                       double* out_total, void* workspace,
-                                       size_t workspace_bytes, void* stream) {
-  clear_error();
-  hipStream_t s = (hipStream_t)stream;
-  TRNBLAS_CHECK_ARG(nvir >= 0 && naux >= 0 && nocc >= 0 && npairs >= 0,
-                    "pair_energy: negative size");
-  TRNBLAS_CHECK_ARG(nvir < (1 << 30) && naux < (1 << 30), "pair_energy: size too large");
+// Shared driver of the fp32 and bf16x6 pair-energy entry points: argument
+// checks, the fused kernel, then the per-pair and total reductions.
+static int pair_energy_run(bool x3, const char* name, int64_t nvir, int64_t naux, const float* Bi,
+                           int64_t ldi_occ, const float* Bj, int64_t ldj_occ, int64_t ld_vir, const float* eps_i, const float* eps_j,
+                           const float* eps_vir, int64_t nocc, int64_t npairs,
+                           const int32_t* pair_i, const int32_t* pair_j, const double* pair_w,
+                           double* out_pairs, double* out_total, void* workspace,
+                           size_t workspace_bytes, hipStream_t s) {
+  TRNBLAS_CHECK_ARG(nvir >= 0 && naux >= 0 && nocc >= 0 && npairs >= 0, "%s: negative size", name);
+  TRNBLAS_CHECK_ARG(nvir < (1 << 30) && naux < (1 << 30), "%s: size too large", name);
   if (pair_i == nullptr) {
     TRNBLAS_CHECK_ARG(Bi == Bj && eps_i == eps_j && ldi_occ == ldj_occ,
-                      "pair_energy: the implicit i <= j walk needs Bi == Bj, eps_i == eps_j");
+                      "%s: the implicit i <= j walk needs Bi == Bj, eps_i == eps_j", name);
     npairs = nocc * (nocc + 1) / 2;
   } else {
-    TRNBLAS_CHECK_ARG(pair_j != nullptr, "pair_energy: pair_j is NULL");
+    TRNBLAS_CHECK_ARG(pair_j != nullptr, "%s: pair_j is NULL", name);
   }
   if (npairs == 0 || nvir == 0) {
     // Empty sums: zero energies.
     if (out_total && hipMemsetAsync(out_total, 0, sizeof(double), s) != hipSuccess)
-      return check_launch("pair_energy");
+      return check_launch(name);
     if (out_pairs && npairs > 0 &&
         hipMemsetAsync(out_pairs, 0, npairs * sizeof(double), s) != hipSuccess)
-      return check_launch("pair_energy");
+      return check_launch(name);
     return TRNBLAS_OK;
   }
-  TRNBLAS_CHECK_ARG(Bi && Bj && eps_i && eps_j && eps_vir, "pair_energy: NULL operand");
-  TRNBLAS_CHECK_ARG(ld_vir >= naux, "pair_energy: ld_vir < naux");
+  TRNBLAS_CHECK_ARG(Bi && Bj && eps_i && eps_j && eps_vir, "%s: NULL operand", name);
+  TRNBLAS_CHECK_ARG(ld_vir >= naux, "%s: ld_vir < naux", name);
   TRNBLAS_CHECK_ARG((int64_t)kPeS * ld_vir * 4 < 0x7fffff00ll,
-                    "pair_energy: ld_vir too large for 32-bit panel offsets");
+                    "%s: ld_vir too large for 32-bit panel offsets", name);
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   const int64_t nq = pe_nq(nvir);
   const int64_t items = npairs * nq;
-  TRNBLAS_CHECK_ARG(items < (1ll << 31), "pair_energy: too many work items");
+  TRNBLAS_CHECK_ARG(items < (1ll << 31), "%s: too many work items", name);
   const size_t need = trnblas_hip_pair_energy_workspace(nvir, npairs);
   if (workspace == nullptr || workspace_bytes < need) {
-    set_error("pair_energy: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    set_error("%s: workspace of %zu bytes needed, %zu given", name, need, workspace_bytes);
     return TRNBLAS_E_WORKSPACE;
   }
   PairArgs g;
@@ -421,28 +655,63 @@ extern "C" int trnblas_hip_pair_energy(int64_t nvir, int64_t naux, const float* 
   g.nq = (int)nq;
   g.partial = static_cast<double*>(workspace);
   double* e_pair = out_pairs ? out_pairs : g.partial + items;
-  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   const bool vec = al16(Bi) && al16(Bj) && naux % 4 == 0 && ld_vir % 4 == 0 &&
                    ldi_occ % 4 == 0 && ldj_occ % 4 == 0;
-  constexpr int NT = kPeS / 32 * 64;
-  if (vec)
-    hipLaunchKernelGGL((pair_energy_kernel<kPeS, kPeBK, true>), dim3((unsigned)items), dim3(NT),
-                       0, s, g);
-  else
-    hipLaunchKernelGGL((pair_energy_kernel<kPeS, kPeBK, false>), dim3((unsigned)items),
-                       dim3(NT), 0, s, g);
-  int rc = check_launch("pair_energy");
+  if (x3) {
+    static_assert(kX3S == kPeS, "one tile size: one workspace layout");
+    if (vec)
+      hipLaunchKernelGGL(pair_energy_x3_kernel<true>, dim3((unsigned)items), dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL(pair_energy_x3_kernel<false>, dim3((unsigned)items), dim3(256), 0, s, g);
+  } else {
+    constexpr int NT = kPeS / 32 * 64;
+    if (vec)
+      hipLaunchKernelGGL((pair_energy_kernel<kPeS, kPeBK, true>), dim3((unsigned)items),
+                         dim3(NT), 0, s, g);
+    else
+      hipLaunchKernelGGL((pair_energy_kernel<kPeS, kPeBK, false>), dim3((unsigned)items),
+                         dim3(NT), 0, s, g);
+  }
+  int rc = check_launch(name);
   if (rc) return rc;
   hipLaunchKernelGGL(pair_sum_kernel, dim3((unsigned)((npairs + 255) / 256)), dim3(256), 0, s,
                      (const double*)g.partial, (int)npairs, (int)nq, e_pair);
-  rc = check_launch("pair_energy(sum)");
+  rc = check_launch(name);
   if (rc) return rc;
   if (out_total) {
     hipLaunchKernelGGL(pair_total_kernel, dim3(1), dim3(1024), 0, s, (const double*)e_pair,
                        (int)npairs, (int)nocc, pair_i, pair_j, pair_w, out_total);
-    rc = check_launch("pair_energy(total)");
+    rc = check_launch(name);
   }
   return rc;
+}
+
+extern "C" int trnblas_hip_pair_energy(int64_t nvir, int64_t naux, const float* Bi,
+                                       int64_t ldi_occ, const float* Bj, int64_t ldj_occ,
+                                       int64_t ld_vir, const float* eps_i, const float* eps_j,
+                                       const float* eps_vir, int64_t nocc, int64_t npairs,
+                                       const int32_t* pair_i, const int32_t* pair_j,
+                                       const double* pair_w, double* out_pairs,
+                                       double* out_total, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  clear_error();
+  return pair_energy_run(false, "pair_energy", nvir, naux, Bi, ldi_occ, Bj, ldj_occ, ld_vir, eps_i, eps_j, eps_vir, nocc, npairs, pair_i, pair_j, pair_w,
+                         out_pairs, out_total, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int trnblas_hip_pair_energy_bf16x6(int64_t nvir, int64_t naux, const float* Bi,
+                                              int64_t ldi_occ, const float* Bj, int64_t ldj_occ,
+                                              int64_t ld_vir, const float* eps_i,
+                                              const float* eps_j, const float* eps_vir,
+                                              int64_t nocc, int64_t npairs,
+                                              const int32_t* pair_i, const int32_t* pair_j,
+                                              const double* pair_w, double* out_pairs,
+                                              double* out_total, void* workspace,
+                                              size_t workspace_bytes, void* stream) {
+  clear_error();
+  return pair_energy_run(true, "pair_energy_bf16x6", nvir, naux, Bi, ldi_occ, Bj, ldj_occ,
+                         ld_vir, eps_i, eps_j, eps_vir, nocc, npairs, pair_i, pair_j, pair_w,
+                         out_pairs, out_total, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int trnblas_hip_mp2_energy(int64_t ic, int64_t nocc, int64_t nvir, const float* T_flat,

@@ -6,6 +6,8 @@ with host tensors, or without the library, raises.
 
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import _lib
@@ -198,11 +200,36 @@ def _pe_operand(X: torch.Tensor) -> torch.Tensor:
     return X
 
 
-def pair_energy_sym(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tensor):
+PAIR_ENERGY_MATH = ("fp32", "bf16x6")
+
+
+_PE_ENTRY = {"fp32": "trnblas_hip_pair_energy", "bf16x6": "trnblas_hip_pair_energy_bf16x6"}
+
+
+def pair_energy_math() -> str:
+    """Arithmetic of the fused pair-energy kernel: TRNBLAS_PAIR_ENERGY_MATH =
+    "bf16x6" (default: bf16 MFMA on three-piece splits, fp32 slice sums; the
+    faster and, measured against fp64, the more accurate) or "fp32" (fp32
+    MFMA)."""
+    return _check_math(os.environ.get("TRNBLAS_PAIR_ENERGY_MATH", "bf16x6").strip().lower())
+
+
+def _check_math(math: str | None) -> str:
+    if math is None:
+        return pair_energy_math()
+    if math not in PAIR_ENERGY_MATH:
+        raise ValueError(f"pair energy math must be one of {PAIR_ENERGY_MATH}; got {math!r}")
+    return math
+
+
+def pair_energy_sym(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tensor, math: str | None = None):
     """E = sum_{i,j} e_ij over all ordered pairs, evaluated as the i <= j walk
     (weights 1 / 2) in one launch. B (nocc, nvir, naux) fp32 on the GPU.
-    Returns a 0-d float64 device tensor."""
+    math: "fp32" (fp32 MFMA), "bf16x6" (each fp32 operand split into three
+    bf16 pieces in the kernel; six bf16 MFMA products per fp32 product) or
+    None (pair_energy_math()). Returns a 0-d float64 device tensor."""
     dev = _require_device(B, eps_occ, eps_vir)
+    math = _check_math(math)
     B = _pe_operand(B)
     nocc, nvir, naux = B.shape
     eo = eps_occ.to(torch.float32).contiguous()
@@ -213,7 +240,7 @@ def pair_energy_sym(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tenso
     work = torch.empty(max(ws, 8), dtype=torch.uint8, device=dev)
     ld_occ = B.stride(0) if nocc > 1 else nvir * naux
     _probed_call(
-        "pair_energy", "trnblas_hip_pair_energy", nvir, naux, ptr(B), ld_occ, ptr(B), ld_occ,
+        "pair_energy", _PE_ENTRY[math], nvir, naux, ptr(B), ld_occ, ptr(B), ld_occ,
         B.stride(1) if nvir > 1 else naux, ptr(eo), ptr(eo), ptr(ev), nocc, npairs,
         None, None, None, None, ptr(total), ptr(work), work.numel(), stream_of(dev),
     )  # fmt: skip
@@ -228,11 +255,13 @@ def pair_energies(
     eps_vir: torch.Tensor,
     pair_i: torch.Tensor,
     pair_j: torch.Tensor,
+    math: str | None = None,
 ) -> torch.Tensor:
     """Unweighted e_p for the pairs (pair_i[p], pair_j[p]), with T = Bi[i]
     Bj[j]^T. Bi (ni, nvir, naux), Bj (nj, nvir, naux) fp32; returns float64
-    (npairs,) on the device."""
+    (npairs,) on the device. math as in pair_energy_sym."""
     dev = _require_device(Bi, Bj, eps_i, eps_j, eps_vir)
+    math = _check_math(math)
     Bi, Bj = _pe_operand(Bi), _pe_operand(Bj)
     if Bi.shape[1:] != Bj.shape[1:]:
         raise ValueError(f"pair operands differ: {tuple(Bi.shape)} vs {tuple(Bj.shape)}")
@@ -252,7 +281,7 @@ def pair_energies(
     ev = eps_vir.to(torch.float32).contiguous()
     ld_vir = Bi.stride(1) if nvir > 1 else naux
     call(
-        "trnblas_hip_pair_energy", nvir, naux, ptr(Bi), Bi.stride(0), ptr(Bj), Bj.stride(0),
+        _PE_ENTRY[math], nvir, naux, ptr(Bi), Bi.stride(0), ptr(Bj), Bj.stride(0),
         ld_vir, ptr(ei), ptr(ej), ptr(ev), 0, npairs, ptr(pi), ptr(pj), None, ptr(out),
         None, ptr(work), work.numel(), stream_of(dev),
     )  # fmt: skip
