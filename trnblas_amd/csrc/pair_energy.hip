@@ -311,25 +311,40 @@ __global__ __launch_bounds__(1024) void pair_total_kernel(const double* e_pair, 
 // v_mfma_f32_16x16x32_bf16 at 16x the rate of v_mfma_f32_32x32x2_f32, so the
 // six products cost 6/16 of one fp32 MFMA product.
 
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 
-// hi = rn_bf16(x), mid = rn_bf16(x - hi), lo = rn_bf16(x - hi - mid): both
-// differences are exact in fp32 and lo holds the last <= 8 bits exactly, so
-// x == hi + mid + lo for every normal x (v_cvt_pk_bf16_f32, round to
-// nearest even).
+// Two floats to packed bf16, round to nearest even (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  const bf16x2 h = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// hi = rn_bf16(x), mid = rn_bf16(x - hi), lo = rn_bf16(x - hi - mid) for a
+// pair of floats, packed: both differences are exact in fp32 and lo holds the
+// last <= 8 bits exactly, so x == hi + mid + lo for every normal x. Eleven
+// VALU operations per pair.
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t& H, uint32_t& M,
+                                           uint32_t& L) {
+  // The low half goes to the top through a byte permute (v_perm_b32,
+  // [b1 b0 0 0]): written as H << 16 the compiler rebuilds it with a second
+  // conversion of x0 (two more VALU operations per pair).
+  H = cvt_pk_bf16(x0, x1);
+  const float r0 = x0 - __uint_as_float(__builtin_amdgcn_perm(H, 0u, 0x05040c0cu)),
+              r1 = x1 - __uint_as_float(H & 0xffff0000u);
+  M = cvt_pk_bf16(r0, r1);
+  const float s0 = r0 - __uint_as_float(__builtin_amdgcn_perm(M, 0u, 0x05040c0cu)),
+              s1 = r1 - __uint_as_float(M & 0xffff0000u);
+  L = cvt_pk_bf16(s0, s1);
+}
+
 __device__ __forceinline__ void split_bf16x3(const f32x4& x, i32x2& hi, i32x2& mid, i32x2& lo) {
-  bf16x4 h, m, l;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    h[e] = (__bf16)x[e];
-    const float r = x[e] - (float)h[e];
-    m[e] = (__bf16)r;
-    l[e] = (__bf16)(r - (float)m[e]);
-  }
-  hi = __builtin_bit_cast(i32x2, h);
-  mid = __builtin_bit_cast(i32x2, m);
-  lo = __builtin_bit_cast(i32x2, l);
+  uint32_t h0, m0, l0, h1, m1, l1;
+  split_pair(x[0], x[1], h0, m0, l0);
+  split_pair(x[2], x[3], h1, m1, l1);
+  hi = i32x2{(int)h0, (int)h1};
+  mid = i32x2{(int)m0, (int)m1};
+  lo = i32x2{(int)l0, (int)l1};
 }
 
 constexpr int kX3S = 96, kX3BK = 32;
@@ -383,49 +398,53 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
   const int nk = (naux + BK - 1) / BK;
   const int nsteps = diag ? nk : 2 * nk;
 
-  // Slice group index = side * 768 + row * 8 + c (c: float4 within the 32-wide
-  // row); side 0 is the A side (rows a0: B_i in pass 0, B_j in pass 1), side 1
-  // the B side (rows b0: B_j, then B_i). The 64 groups of one wave share the
-  // side, so the buffer resource is wave-uniform.
+  // Slice layout: thread tid loads the float4 at column 4 (tid & 7) of rows
+  // rr0 = tid >> 3, rr0 + 32, rr0 + 64 of both sides (v = 3 side + jj). Side 0
+  // is the A side (rows a0: B_i in pass 0, B_j in pass 1), side 1 the B side
+  // (rows b0: B_j, then B_i). Row offsets within a side are wave-uniform
+  // (scalar offset); the row bounds are fixed per item (rowmask); columns
+  // need a check only in a ragged last slice.
+  const int rr0 = tid >> 3, cc = tid & 7;
+  const uint32_t voff0 = (uint32_t)((rr0 * ld_vir + 4 * cc) * 4);
+  int rowmask = 0;
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+    if (rr0 + 32 * (v % 3) < nvir - (v < 3 ? a0 : b0)) rowmask |= 1 << v;
   auto load = [&](int step, f32x4(&st)[NV]) {
     const int pass = step >= nk ? 1 : 0, k0 = (step - pass * nk) * BK;
+    const bool ragged = k0 + BK > naux;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-      const int base = w * 64 + v * 256;
-      const int side = base / SIDE_V4;
+      const int side = v / 3, jj = v % 3;
       const bool use_i = (side ^ pass) == 0;
-      const int rbase = side ? b0 : a0;
       const __amdgpu_buffer_rsrc_t rs =
-          pe_rsrc((use_i ? Xi : Xj) + (int64_t)rbase * ld_vir + k0);
-      const int local = base - side * SIDE_V4 + lane, r = local >> 3, c = (local & 7) * 4;
-      const bool rok = r < nvir - rbase;
-      const uint32_t off = (uint32_t)((r * ld_vir + c) * 4);
+          pe_rsrc((use_i ? Xi : Xj) + (int64_t)(side ? b0 : a0) * ld_vir + k0);
+      const int soff = (int)(jj * 32 * ld_vir * 4);
+      const bool rok = (rowmask >> v) & 1;
       if (VEC) {
+        const bool ok = rok && (!ragged || 4 * cc < naux - k0);
         st[v] = __builtin_bit_cast(
-            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (rok && c < naux - k0) ? off : kPeOob,
-                                                         0, 0));
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? voff0 : kPeOob, soff, 0));
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           st[v][e] = __builtin_bit_cast(
               float, __builtin_amdgcn_raw_buffer_load_b32(
-                         rs, (rok && c + e < naux - k0) ? off + 4 * e : kPeOob, 0, 0));
+                         rs, (rok && 4 * cc + e < naux - k0) ? voff0 + 4 * e : kPeOob, soff, 0));
       }
     }
   };
+  const int lds0 = rr0 * BK + 8 * x3_slot(rr0, cc >> 1) + 4 * (cc & 1);
   auto store = [&](int buf, const f32x4(&st)[NV]) {
-    uint16_t* dst = lds + buf * STAGE;
+    uint16_t* dst = lds + buf * STAGE + lds0;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-      const int base = w * 64 + v * 256;
-      const int side = base / SIDE_V4;
-      const int local = base - side * SIDE_V4 + lane, r = local >> 3, c = local & 7;
+      const int e = ((v / 3) * S + 32 * (v % 3)) * BK;
       i32x2 h, m, l;
       split_bf16x3(st[v], h, m, l);
-      const int e0 = (side * S + r) * BK + 8 * x3_slot(r, c >> 1) + 4 * (c & 1);
-      *reinterpret_cast<i32x2*>(dst + e0) = h;
-      *reinterpret_cast<i32x2*>(dst + 2 * S * BK + e0) = m;
-      *reinterpret_cast<i32x2*>(dst + 4 * S * BK + e0) = l;
+      *reinterpret_cast<i32x2*>(dst + e) = h;
+      *reinterpret_cast<i32x2*>(dst + 2 * S * BK + e) = m;
+      *reinterpret_cast<i32x2*>(dst + 4 * S * BK + e) = l;
     }
   };
 
