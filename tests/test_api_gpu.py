@@ -205,7 +205,7 @@ def test_gemm_fp64_bitwise_vs_reference(dev, M, K, N, k, views):
         Ad = torch.from_numpy(np.ascontiguousarray(A.T)).to(dev).T
     if "B" in views:
         Bd = torch.from_numpy(np.ascontiguousarray(B.T)).to(dev).T
-    C = tb.gemm_fp64(Ad, Bd, slices=k)
+    C = tb.gemm_fp64(Ad, Bd, slices=k, mode="exact")
     assert C.dtype == torch.float64 and C.device == Ad.device
     want = oz.reference_gemm(A, B, k)
     assert np.array_equal(C.cpu().numpy().view(np.int64), want.view(np.int64))
@@ -215,8 +215,49 @@ def test_gemm_fp64_golden_from_reference(dev):
     gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "ozaki_golden.npz"))
     for c in range(5):
         A, B, Cw = gold[f"gemm{c}_A"], gold[f"gemm{c}_B"], gold[f"gemm{c}_C"]
-        C = tb.gemm_fp64(torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev), slices=int(gold[f"gemm{c}_k"]))
+        C = tb.gemm_fp64(
+            torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev), slices=int(gold[f"gemm{c}_k"]),
+            mode="exact",
+        )
         assert np.array_equal(C.cpu().numpy().view(np.int64), Cw.view(np.int64)), c
+
+
+@pytest.mark.parametrize(
+    "M,K,N,k,dist,views",
+    [(37, 300, 53, 7, "normal", ""), (130, 4100, 7, 8, "normal", ""), (200, 600, 520, 8, "logu4", "AB"),
+     (5, 4100, 3, 8, "normal", "A"), (64, 64, 64, 12, "normal", "B"), (1, 1, 1, 8, "normal", ""),
+     (70, 257, 90, 1, "normal", ""), (66, 1000, 130, 3, "logu4", ""), (129, 384, 65, 10, "logu4", "")],
+)
+def test_gemm_fp64_fast_within_bound(dev, M, K, N, k, dist, views):
+    # fast mode: every element within the k-slice truncation bound of the
+    # exact (rational) product, and no further from it than the exact mode's
+    # fp32 (hi, lo) floor
+    A, B = exact.inputs(M, K, N, dist=dist, seed=M * 5 + N + k)
+    Ad = torch.from_numpy(A).to(dev)
+    Bd = torch.from_numpy(B).to(dev)
+    if "A" in views:
+        Ad = torch.from_numpy(np.ascontiguousarray(A.T)).to(dev).T
+    if "B" in views:
+        Bd = torch.from_numpy(np.ascontiguousarray(B.T)).to(dev).T
+    C = tb.gemm_fp64(Ad, Bd, slices=k, mode="fast").cpu().numpy()
+    ref = exact.ref_exact(A, B)
+    bound = oz.error_bound(A, B, k)
+    assert (np.abs(C - ref) <= bound).all()
+    Cx = oz.reference_gemm(A, B, k)
+    AB = np.abs(A) @ np.abs(B)
+    assert (np.abs(C - Cx) <= 2.0**-45 * AB + 1e-300).all()
+
+
+def test_gemm_fp64_fast_flush_path(dev):
+    # k = 12 and K = 44032: k * K * 2^12 passes 2^31, so the int32 diagonals
+    # are flushed to fp64 once mid-K (the block path that adds into C)
+    A, B = exact.inputs(40, 44032, 24, seed=77)
+    C = tb.gemm_fp64(torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev), slices=12, mode="fast")
+    C = C.cpu().numpy()
+    ref = exact.ref_exact(A, B)
+    assert (np.abs(C - ref) <= oz.error_bound(A, B, 12)).all()
+    err = float((np.abs(C - ref) / (np.abs(A) @ np.abs(B))).max())
+    assert err <= 1e-15, err
 
 
 def test_gemm_fp64_nonfinite_and_empty(dev):
@@ -242,14 +283,17 @@ def test_config5_gemm_fp64_accuracy_full_size(dev):
         return u * torch.exp2(torch.round(4.0 * torch.randn(n, n, generator=g, device=dev, dtype=torch.float64)))
 
     A, B = draw(), draw()
-    C = tb.gemm_fp64(A, B)
     ref = A @ B
     AB = A.abs() @ B.abs()
     bound = oz.error_bound(A, B, 8, absA_absB=AB, xp=torch) + n * 2.0**-53 * AB
-    assert bool(((C - ref).abs() <= bound).all())
+    for mode in ("fast", "exact"):
+        C = tb.gemm_fp64(A, B, mode=mode)
+        assert bool(((C - ref).abs() <= bound).all()), mode
+        del C
     # on well-scaled data k = 8 is host-fp64 accurate (test_ozaki.py:179-187)
     A2 = torch.randn(4096, 4096, generator=g, device=dev, dtype=torch.float64)
     B2 = torch.randn(4096, 4096, generator=g, device=dev, dtype=torch.float64)
-    C2 = tb.gemm_fp64(A2, B2)
-    err = float(((C2 - A2 @ B2).abs() / (A2.abs() @ B2.abs())).max())
-    assert err <= 1.5e-15, err
+    for mode in ("fast", "exact"):
+        C2 = tb.gemm_fp64(A2, B2, mode=mode)
+        err = float(((C2 - A2 @ B2).abs() / (A2.abs() @ B2.abs())).max())
+        assert err <= 1.5e-15, (mode, err)

@@ -23,6 +23,8 @@
 //  * the fp64 recombination (hi + lo) 2^(eA + eB + off) is fused into the
 //    store (no (hi, lo) round trip through HBM), including the fp64 sum of K
 //    blocks for very long K (`plan`'s K blocking).
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace trnblas {
@@ -279,6 +281,7 @@ struct OzArgs {
   float* hilo;    // raw (hi, lo) planes (hilo output)
   int64_t ldc_m, ldc_n, ldh;
   int tiles_m, tiles_n;
+  int flush;      // fast mode: k-steps between int32 -> fp64 flushes of the diagonals
 };
 
 __device__ __forceinline__ void two_sum32(float& hi, float& lo, float p) {
@@ -472,6 +475,143 @@ __global__ __launch_bounds__(256) void oz_gemm_kernel(OzArgs g) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fast mode: all slices per k-step, one int32 accumulator per diagonal.
+//
+// A 64 x 64 output tile per workgroup (4 waves, one 32 x 32 MFMA block each).
+// Each 32-wide k-step stages that K slice of every digit slice of A and B in
+// LDS (2 x k x 64 rows x 32 bytes) and runs all k (k + 1) / 2 slice products
+// from it, so one load feeds (k + 1) / 2 MFMAs per slice instead of one.
+// Products on diagonal d = s + t share an int32 accumulator: with
+// |digit| <= 64 a term is <= 2^12, and the host sets `flush` so that
+// k * K_flush * 2^12 < 2^31. At a flush and at the end each diagonal is
+// converted to fp64 exactly and summed, scaled by 2^(7 (k-1-d)), smallest
+// diagonal first; flushes before the end add into C. The result is the exact
+// digit expansion up to fp64 rounding of that sum: within the truncation
+// bound of the reference's fp32 TwoSum chain, but not bitwise equal to it.
+//
+// Thread tid stages the 16-byte group (tid & 1) of row (tid >> 1) & 63 of
+// operand tid >> 7 (waves 0-1: A, 2-3: B) for every slice. LDS rows are 32
+// bytes with the two 16-byte slots swapped when ((r >> 2) ^ (r >> 3)) & 1,
+// so 16-byte fragment reads of 8 or 16 consecutive rows hit distinct banks.
+__device__ __forceinline__ int oz_slot(int r, int c) { return c ^ (((r >> 2) ^ (r >> 3)) & 1); }
+
+template <int KS>  // most slices held (8: 64 KiB LDS, 2 workgroups per CU; 12: 96 KiB)
+__global__ __launch_bounds__(256, KS <= 8 ? 2 : 1) void oz_fast_kernel(OzArgs g) {
+  constexpr int BK = 32, T = 64;
+  constexpr int SL = T * BK;   // bytes per slice tile
+  constexpr int OP = KS * SL;  // bytes per operand stage
+  constexpr int STAGE = 2 * OP;
+  __shared__ __attribute__((aligned(16))) int8_t lds[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  int tm, tn;
+  grouped_tile(t, g.tiles_m, g.tiles_n, 8, tm, tn);
+  const int m0 = tm * T, n0 = tn * T;
+  const int k = g.k;
+  const int nsteps = g.Kp / BK;
+
+  const int op = w >> 1, r = (tid >> 1) & 63, c = tid & 1;
+  const int8_t* obase = op ? g.B + (int64_t)n0 * g.ldb : g.A + (int64_t)m0 * g.lda;
+  const int64_t ld_s = op ? g.ldb_s : g.lda_s;
+  const bool rok = (op ? n0 : m0) + r < (op ? g.N : g.M);
+  const uint32_t voff = rok ? (uint32_t)(r * (op ? g.ldb : g.lda) + 16 * c) : kOzOob;
+  const int sdst = op * OP + r * BK + 16 * oz_slot(r, c);
+  i32x4 st[KS];
+  auto load = [&](int step) {
+#pragma unroll
+    for (int sl = 0; sl < KS; ++sl)
+      if (sl < k)
+        st[sl] = __builtin_amdgcn_raw_buffer_load_b128(
+            oz_rsrc(obase + sl * ld_s + (int64_t)step * BK), voff, 0, 0);
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int sl = 0; sl < KS; ++sl)
+      if (sl < k) *reinterpret_cast<i32x4*>(lds + buf * STAGE + sl * SL + sdst) = st[sl];
+  };
+
+  // Wave w: rows 32 (w & 1), columns 32 (w >> 1) of the tile. Lane l reads
+  // row l % 32 of its block, k bytes 16 (l / 32) .. +15 of the step.
+  const int ar = 32 * (w & 1) + (lane & 31), br = 32 * (w >> 1) + (lane & 31);
+  const int aoff = ar * BK + 16 * oz_slot(ar, lane >> 5);
+  const int boff = OP + br * BK + 16 * oz_slot(br, lane >> 5);
+  i32x16 acc[KS];
+#pragma unroll
+  for (int d = 0; d < KS; ++d)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[d][e] = 0;
+
+  // Lane l of a 32x32 block: column l % 32, rows 8 (e/4) + 4 (l/32) + e % 4.
+  const int off = -2 * (kSliceBits - 1) - kSliceBits * (k - 1);
+  const int n = n0 + 32 * (w >> 1) + (lane & 31);
+  const int eb = n < g.N ? g.eB[n] : 0;
+  auto flush = [&](bool first) {
+    // Convert (all accumulators die here), then scale and store.
+    double v[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      v[e] = 0.0;
+#pragma unroll
+      for (int d = KS - 1; d >= 0; --d)
+        if (d < k) v[e] += (double)acc[d][e] * pow2(kSliceBits * (k - 1 - d));
+    }
+#pragma unroll
+    for (int d = 0; d < KS; ++d)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[d][e] = 0;
+#pragma unroll 4
+    for (int e = 0; e < 16; ++e) {
+      const int m = m0 + 32 * (w & 1) + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+      if (m >= g.M || n >= g.N) continue;
+      const int ea = g.eA[m] + off;
+      double cv;
+      if (ea < 900 && ea > -900 && eb < 900 && eb > -900)
+        cv = (v[e] * pow2(ea)) * pow2(eb);
+      else
+        cv = ldexp(v[e], ea + eb);
+      double* dst = g.C + (int64_t)m * g.ldc_m + (int64_t)n * g.ldc_n;
+      *dst = first ? cv : *dst + cv;
+    }
+  };
+
+
+  // K in blocks of `flush` steps; each block drains its pipeline and then
+  // flushes (C5-size K is one block).
+  for (int s0 = 0; s0 < nsteps; s0 += g.flush) {
+    const int s1 = s0 + g.flush < nsteps ? s0 + g.flush : nsteps;
+    if (s0 > 0) __syncthreads();  // the previous block's last stage is consumed
+    load(s0);
+    store(0);
+    __syncthreads();
+    for (int s = s0; s < s1; ++s) {
+      const bool more = s + 1 < s1;
+      if (more) load(s + 1);
+      const int8_t* buf = lds + ((s - s0) & 1) * STAGE;
+      i32x4 fa[KS];
+#pragma unroll
+      for (int s2 = 0; s2 < KS; ++s2)
+        if (s2 < k) fa[s2] = *reinterpret_cast<const i32x4*>(buf + s2 * SL + aoff);
+#pragma unroll
+      for (int tt = 0; tt < KS; ++tt)
+        if (tt < k) {
+          const i32x4 fb = *reinterpret_cast<const i32x4*>(buf + tt * SL + boff);
+#pragma unroll
+          for (int s2 = 0; s2 < KS - tt; ++s2)
+            if (s2 + tt < k)
+              acc[s2 + tt] =
+                  __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s2], fb, acc[s2 + tt], 0, 0, 0);
+        }
+      if (more) store((s + 1 - s0) & 1);
+      __syncthreads();
+    }
+    flush(s0 == 0);
+  }
+  if (nsteps == 0) flush(true);
+}
+
 constexpr int kOzBM = 128, kOzBN = 128, kOzBK = 64;
 
 static int oz_launch(OzArgs& g, int out, hipStream_t s) {
@@ -486,6 +626,22 @@ static int oz_launch(OzArgs& g, int out, hipStream_t s) {
     hipLaunchKernelGGL((oz_gemm_kernel<kOzBM, kOzBN, kOzBK, 1>), dim3((unsigned)nt), dim3(256),
                        0, s, g);
   return check_launch("ozaki_gemm");
+}
+
+// Fast mode launch: 64 x 64 tiles; the int32 diagonals are flushed to fp64
+// before k * K_flush * 2^12 could reach 2^31 (K blocks are not needed).
+static int oz_fast_launch(OzArgs& g, hipStream_t s) {
+  g.tiles_m = (g.M + 63) / 64;
+  g.tiles_n = (g.N + 63) / 64;
+  const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
+  TRNBLAS_CHECK_ARG(nt < (1ll << 31), "ozaki: too many tiles");
+  const int64_t kflush = ((1ll << 31) - 1) / (4096ll * g.k);  // K terms per diagonal
+  g.flush = (int)std::max<int64_t>(1, kflush / 32);
+  if (g.k <= 8)
+    hipLaunchKernelGGL(oz_fast_kernel<8>, dim3((unsigned)nt), dim3(256), 0, s, g);
+  else
+    hipLaunchKernelGGL(oz_fast_kernel<12>, dim3((unsigned)nt), dim3(256), 0, s, g);
+  return check_launch("ozaki_gemm(fast)");
 }
 
 static int oz_check_operands(int slices, int64_t M, int64_t N, int64_t Kp, int64_t kb,
@@ -567,7 +723,7 @@ extern "C" int trnblas_hip_ozaki_gemm(int mode, int slices, int64_t M, int64_t N
                                       int64_t ldb_slice, const int32_t* eA, const int32_t* eB,
                                       double* C, int64_t ldc_m, int64_t ldc_n, void* stream) {
   clear_error();
-  TRNBLAS_CHECK_ARG(mode == 0, "ozaki_gemm: mode %d not supported", mode);
+  TRNBLAS_CHECK_ARG(mode == 0 || mode == 1, "ozaki_gemm: mode %d not supported", mode);
   if (M == 0 || N == 0) return TRNBLAS_OK;
   int rc = oz_check_operands(slices, M, N, Kp, kb, dA, lda, lda_slice, dB, ldb, ldb_slice);
   if (rc) return rc;
@@ -590,6 +746,7 @@ extern "C" int trnblas_hip_ozaki_gemm(int mode, int slices, int64_t M, int64_t N
   g.C = C;
   g.ldc_m = ldc_m;
   g.ldc_n = ldc_n;
+  if (mode == 1) return oz_fast_launch(g, (hipStream_t)stream);
   return oz_launch(g, 0, (hipStream_t)stream);
 }
 

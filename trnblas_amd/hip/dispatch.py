@@ -669,20 +669,22 @@ def _ozaki_route() -> str:
     return "kernel" if _use_hip() else "torch"
 
 
-def nki_gemm_fp64(a: torch.Tensor, b: torch.Tensor, slices: int) -> torch.Tensor:
+def nki_gemm_fp64(a: torch.Tensor, b: torch.Tensor, slices: int, mode: str | None = None) -> torch.Tensor:
     """fp64 a @ b by the Ozaki split on the device (dispatch.py:958-980).
     a (M, K), b (K, N) real tensors (any float dtype; computed as fp64).
-    Non-finite operands take a plain fp64 matmul on the device."""
+    mode: "fast", "exact" or None (ozaki.default_mode()). Non-finite operands
+    take a plain fp64 matmul on the device."""
     from .. import ozaki
 
     k = ozaki.check_slices(slices)
+    mode = ozaki.check_mode(mode)
     if _ozaki_route() == "torch":
         return torch.matmul(a.double(), b.double())
     dev = _gpu_device(a, b)
     ad = a.to(dev, torch.float64)
     bd = b.to(dev, torch.float64)
     try:
-        return ozaki.run_device(ad, bd, k)
+        return ozaki.run_device(ad, bd, k, mode)
     except ozaki.OzakiNonFinite:
         return torch.matmul(ad, bd)
     except Exception as exc:  # noqa: BLE001

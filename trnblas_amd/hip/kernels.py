@@ -347,10 +347,12 @@ def ozaki_split(X: torch.Tensor, slices: int, per: str):
 
 
 def ozaki_gemm(dA, eA, dB, eB, M: int, N: int, slices: int, kb: int | None = None,
-               out: torch.Tensor | None = None, transpose_out: bool = False) -> torch.Tensor:
+               out: torch.Tensor | None = None, transpose_out: bool = False,
+               fast: bool = False) -> torch.Tensor:
     """fp64 C (M, N) from digit stacks dA (k, >=M, Kp), dB (k, >=N, Kp)
-    (K-contiguous) and their exponents, by the bit-exact schedule. With
-    transpose_out, writes C^T into `out` (N, M) instead."""
+    (K-contiguous) and their exponents: the bit-exact schedule (fast=False,
+    K blocks of kb) or the fast one (int32 diagonals, fp64 recombination; kb
+    unused). With transpose_out, writes C^T into `out` (N, M) instead."""
     dev = _require_device(dA, dB, eA, eB)
     k, _, Kp = dA.shape
     kb = Kp if kb is None else kb
@@ -361,7 +363,7 @@ def ozaki_gemm(dA, eA, dB, eB, M: int, N: int, slices: int, kb: int | None = Non
     else:
         ldc_m, ldc_n = out.stride(0), out.stride(1)
     _probed_call(
-        "ozaki_gemm", "trnblas_hip_ozaki_gemm", 0, slices, M, N, Kp, kb, ptr(dA), dA.stride(1),
+        "ozaki_gemm", "trnblas_hip_ozaki_gemm", 1 if fast else 0, slices, M, N, Kp, kb, ptr(dA), dA.stride(1),
         dA.stride(0), ptr(dB), dB.stride(1), dB.stride(0), ptr(eA), ptr(eB), ptr(out),
         ldc_m, ldc_n, stream_of(dev),
     )  # fmt: skip

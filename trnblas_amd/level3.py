@@ -101,15 +101,19 @@ def gemm_fp64(
     slices: int = 8,
     transA: bool = False,
     transB: bool = False,
+    mode: str | None = None,
 ) -> torch.Tensor:
     """fp64-class op(A) @ op(B) by Ozaki splitting on int8 MFMA.
 
     A is split row by row and B column by column into `slices` (k) int8
     digits of 7 bits, exactly; the k (k + 1) / 2 slice products run as int8
-    MFMAs with exact int32 groups of at most 4096 terms, folded into an fp32
-    TwoSum (hi, lo) pair in the reference's order, and recombined in fp64 with
-    the power-of-two scales — all on the device. The result equals the
-    reference's `ozaki.reference_gemm` bit for bit. Accuracy (max |C - C_exact|
+    MFMAs, all on the device. mode "exact" sums exact int32 groups of at most
+    4096 terms into an fp32 TwoSum (hi, lo) pair in the reference's order and
+    recombines in fp64 with the power-of-two scales: the result equals the
+    reference's `ozaki.reference_gemm` bit for bit. mode "fast" (the default,
+    TRNBLAS_OZAKI_MODE) sums each diagonal of slice pairs exactly in int32 and
+    recombines all diagonals in fp64: same digits, same products, an error
+    within the same truncation bound, not bitwise. Accuracy (max |C - C_exact|
     / (|A| |B|), normal data): about 1e-12 at k = 6, 1e-14 at k = 7, 2e-16 to
     3e-16 at k = 8 (the default, host-fp64 level); scaling is per row of A and
     column of B, so data spread over 10^+-4 needs k = 10. 1 <= slices <= 12.
@@ -119,9 +123,10 @@ def gemm_fp64(
     set_backend("pytorch") and for non-finite operands the result is an fp64
     matmul.
     """
-    from .ozaki import check_slices
+    from .ozaki import check_mode, check_slices
 
     slices = check_slices(slices)
+    mode = check_mode(mode)
     transA, transB = trans_flag(transA, "transA"), trans_flag(transB, "transB")
     for name, X in (("A", A), ("B", B)):
         if not isinstance(X, torch.Tensor) or X.dim() != 2:
@@ -135,7 +140,7 @@ def gemm_fp64(
             f"gemm_fp64: inner dimensions differ: op(A) {tuple(a.shape)}, op(B) {tuple(b.shape)}"
         )
     device = A.device
-    return _d.nki_gemm_fp64(a.detach(), b.detach(), slices).to(device)
+    return _d.nki_gemm_fp64(a.detach(), b.detach(), slices, mode).to(device)
 
 
 def syrk(

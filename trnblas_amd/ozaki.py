@@ -18,6 +18,8 @@ has no CPU arithmetic path.
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import torch
 
@@ -140,13 +142,37 @@ def _digits_of(X: torch.Tensor, k: int, want: str):
     return split_device(X.contiguous(), k, "col")
 
 
-def run_device(A: torch.Tensor, B: torch.Tensor, slices: int = DEFAULT_SLICES) -> torch.Tensor:
+MODES = ("fast", "exact")
+
+
+def default_mode() -> str:
+    """Recombination of the slice products: TRNBLAS_OZAKI_MODE = "fast"
+    (default: each diagonal of slice pairs summed exactly in int32, all
+    diagonals recombined in fp64; within the reference's truncation bound) or
+    "exact" (the reference's groups and fp32 TwoSum order: bit-equal to
+    `ozaki.reference_gemm`)."""
+    return check_mode(os.environ.get("TRNBLAS_OZAKI_MODE", "fast").strip().lower())
+
+
+def check_mode(mode: str | None) -> str:
+    if mode is None:
+        return default_mode()
+    if mode not in MODES:
+        raise ValueError(f"Ozaki mode must be one of {MODES}; got {mode!r}")
+    return mode
+
+
+def run_device(
+    A: torch.Tensor, B: torch.Tensor, slices: int = DEFAULT_SLICES, mode: str | None = None
+) -> torch.Tensor:
     """C = A @ B in fp64 by Ozaki splitting, on the device. A (M, K), B (K, N)
-    fp64 device tensors (views allowed). Bit-equal to the reference's
-    `ozaki.reference_gemm(A, B, slices)`."""
+    fp64 device tensors (views allowed). mode "exact" is bit-equal to the
+    reference's `ozaki.reference_gemm(A, B, slices)`; "fast" has the same
+    digits and products with an fp64 recombination (see default_mode)."""
     from .hip import kernels
 
     k = check_slices(slices)
+    mode = check_mode(mode)
     M, K = A.shape
     N = B.shape[1]
     C = torch.empty((M, N), dtype=torch.float64, device=A.device)
@@ -157,9 +183,10 @@ def run_device(A: torch.Tensor, B: torch.Tensor, slices: int = DEFAULT_SLICES) -
     da, ea = _digits_of(A, k, "A")
     db, eb = _digits_of(B, k, "B")
     Kp = da.shape[2]
-    kb = k_block(Kp, k)
+    kb = k_block(Kp, k) if mode == "exact" else Kp
+    fast = mode == "fast"
     if N < SWAP_N and M > N:  # C^T = B^T A^T (ozaki.py:546-547): B's digits first
-        kernels.ozaki_gemm(db, eb, da, ea, N, M, k, kb=kb, out=C, transpose_out=True)
+        kernels.ozaki_gemm(db, eb, da, ea, N, M, k, kb=kb, out=C, transpose_out=True, fast=fast)
     else:
-        kernels.ozaki_gemm(da, ea, db, eb, M, N, k, kb=kb, out=C)
+        kernels.ozaki_gemm(da, ea, db, eb, M, N, k, kb=kb, out=C, fast=fast)
     return C
