@@ -479,8 +479,8 @@ __global__ __launch_bounds__(256) void oz_gemm_kernel(OzArgs g) {
 // Fast mode: all slices per k-step, one int32 accumulator per diagonal.
 //
 // A 64 x 64 output tile per workgroup (4 waves, one 32 x 32 MFMA block each).
-// Each 32-wide k-step stages that K slice of every digit slice of A and B in
-// LDS (2 x k x 64 rows x 32 bytes) and runs all k (k + 1) / 2 slice products
+// Each BK-wide k-step stages that K slice of every digit slice of A and B in
+// LDS (2 x k x 64 rows x BK bytes) and runs all k (k + 1) / 2 slice products
 // from it, so one load feeds (k + 1) / 2 MFMAs per slice instead of one.
 // Products on diagonal d = s + t share an int32 accumulator: with
 // |digit| <= 64 a term is <= 2^12, and the host sets `flush` so that
@@ -490,18 +490,31 @@ __global__ __launch_bounds__(256) void oz_gemm_kernel(OzArgs g) {
 // digit expansion up to fp64 rounding of that sum: within the truncation
 // bound of the reference's fp32 TwoSum chain, but not bitwise equal to it.
 //
-// Thread tid stages the 16-byte group (tid & 1) of row (tid >> 1) & 63 of
-// operand tid >> 7 (waves 0-1: A, 2-3: B) for every slice. LDS rows are 32
-// bytes with the two 16-byte slots swapped when ((r >> 2) ^ (r >> 3)) & 1,
-// so 16-byte fragment reads of 8 or 16 consecutive rows hit distinct banks.
-__device__ __forceinline__ int oz_slot(int r, int c) { return c ^ (((r >> 2) ^ (r >> 3)) & 1); }
+// Operands go from HBM straight into LDS (buffer_load_dwordx4 ... lds: lane l
+// of a wave fills the 16 bytes at the wave's LDS base + 16 l; out-of-range
+// lanes write zeros), one 1 KiB block of 1024 / BK rows of one slice of one
+// operand per instruction, so no registers hold a stage in flight. LDS rows
+// are BK bytes with the 16-byte slots XOR-swizzled by the row (lane l of a
+// block loads the global group that belongs in its slot), so 16-byte
+// fragment reads of 8 or 16 consecutive rows hit distinct banks; each row is
+// one BK-byte request.
+template <int BK>
+__device__ __forceinline__ int oz_slot(int r, int c) {
+  return BK == 64 ? c ^ (((r >> 1) ^ (r >> 2)) & 3) : c ^ (((r >> 2) ^ (r >> 3)) & 1);
+}
 
-template <int KS>  // most slices held (8: 64 KiB LDS, 2 workgroups per CU; 12: 96 KiB)
-__global__ __launch_bounds__(256, KS <= 8 ? 2 : 1) void oz_fast_kernel(OzArgs g) {
-  constexpr int BK = 32, T = 64;
-  constexpr int SL = T * BK;   // bytes per slice tile
-  constexpr int OP = KS * SL;  // bytes per operand stage
+// KS: the slice count (a template parameter, so the k (k + 1) / 2 MFMAs of a
+// k-step are straight-line code). BK = 64 for k <= 8 (128 KiB LDS), 32 above
+// (<= 96 KiB). One workgroup per CU.
+template <int KS, int BK>
+__global__ __launch_bounds__(256, 1) void oz_fast_kernel(OzArgs g) {
+  constexpr int T = 64;
+  constexpr int SL = T * BK;       // bytes per slice tile
+  constexpr int OP = KS * SL;      // bytes per operand stage
   constexpr int STAGE = 2 * OP;
+  constexpr int RPI = 1024 / BK;   // rows per 1 KiB load instruction
+  constexpr int IPS = T / RPI;     // instructions per slice tile
+  constexpr int GPR = BK / 16;     // 16-byte groups per row
   __shared__ __attribute__((aligned(16))) int8_t lds[2 * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -510,34 +523,37 @@ __global__ __launch_bounds__(256, KS <= 8 ? 2 : 1) void oz_fast_kernel(OzArgs g)
   int tm, tn;
   grouped_tile(t, g.tiles_m, g.tiles_n, 8, tm, tn);
   const int m0 = tm * T, n0 = tn * T;
-  const int k = g.k;
+  constexpr int k = KS;
   const int nsteps = g.Kp / BK;
 
-  const int op = w >> 1, r = (tid >> 1) & 63, c = tid & 1;
-  const int8_t* obase = op ? g.B + (int64_t)n0 * g.ldb : g.A + (int64_t)m0 * g.lda;
-  const int64_t ld_s = op ? g.ldb_s : g.lda_s;
-  const bool rok = (op ? n0 : m0) + r < (op ? g.N : g.M);
-  const uint32_t voff = rok ? (uint32_t)(r * (op ? g.ldb : g.lda) + 16 * c) : kOzOob;
-  const int sdst = op * OP + r * BK + 16 * oz_slot(r, c);
-  i32x4 st[KS];
-  auto load = [&](int step) {
+  // Wave w loads row block w % IPS of the slices sl with sl % (4 / IPS) ==
+  // w / IPS, of both operands: one instruction per (operand, slice).
+  constexpr int WPB = 4 / IPS;  // waves sharing one row block
+  const int blk = w % IPS, jw = w / IPS;
+  const int r = blk * RPI + lane / GPR;
+  const int cg = oz_slot<BK>(r, lane % GPR);  // the slot map is its own inverse
+  const uint32_t voffA = m0 + r < g.M ? (uint32_t)(r * g.lda + 16 * cg) : kOzOob;
+  const uint32_t voffB = n0 + r < g.N ? (uint32_t)(r * g.ldb + 16 * cg) : kOzOob;
+  const int8_t* baseA = g.A + (int64_t)m0 * g.lda;
+  const int8_t* baseB = g.B + (int64_t)n0 * g.ldb;
+  auto load = [&](int step, int buf) {
+    const int64_t koff = (int64_t)step * BK;
 #pragma unroll
     for (int sl = 0; sl < KS; ++sl)
-      if (sl < k)
-        st[sl] = __builtin_amdgcn_raw_buffer_load_b128(
-            oz_rsrc(obase + sl * ld_s + (int64_t)step * BK), voff, 0, 0);
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int sl = 0; sl < KS; ++sl)
-      if (sl < k) *reinterpret_cast<i32x4*>(lds + buf * STAGE + sl * SL + sdst) = st[sl];
+      if (sl < k && sl % WPB == jw) {
+        int8_t* dst = lds + buf * STAGE + sl * SL + blk * 1024;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            oz_rsrc(baseA + sl * g.lda_s + koff), (__attribute__((address_space(3))) void*)dst,
+            16, voffA, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            oz_rsrc(baseB + sl * g.ldb_s + koff),
+            (__attribute__((address_space(3))) void*)(dst + OP), 16, voffB, 0, 0, 0);
+      }
   };
 
   // Wave w: rows 32 (w & 1), columns 32 (w >> 1) of the tile. Lane l reads
-  // row l % 32 of its block, k bytes 16 (l / 32) .. +15 of the step.
+  // row l % 32 of its block, bytes 16 (l / 32) .. +15 of each 32-wide chunk.
   const int ar = 32 * (w & 1) + (lane & 31), br = 32 * (w >> 1) + (lane & 31);
-  const int aoff = ar * BK + 16 * oz_slot(ar, lane >> 5);
-  const int boff = OP + br * BK + 16 * oz_slot(br, lane >> 5);
   i32x16 acc[KS];
 #pragma unroll
   for (int d = 0; d < KS; ++d)
@@ -577,34 +593,40 @@ __global__ __launch_bounds__(256, KS <= 8 ? 2 : 1) void oz_fast_kernel(OzArgs g)
     }
   };
 
-
   // K in blocks of `flush` steps; each block drains its pipeline and then
-  // flushes (C5-size K is one block).
+  // flushes (C5-size K is one block). A stage is complete when every wave
+  // has waited for its own loads (vmcnt) and passed the barrier.
   for (int s0 = 0; s0 < nsteps; s0 += g.flush) {
     const int s1 = s0 + g.flush < nsteps ? s0 + g.flush : nsteps;
     if (s0 > 0) __syncthreads();  // the previous block's last stage is consumed
-    load(s0);
-    store(0);
+    load(s0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int s = s0; s < s1; ++s) {
       const bool more = s + 1 < s1;
-      if (more) load(s + 1);
+      if (more) load(s + 1, (s + 1 - s0) & 1);
       const int8_t* buf = lds + ((s - s0) & 1) * STAGE;
-      i32x4 fa[KS];
 #pragma unroll
-      for (int s2 = 0; s2 < KS; ++s2)
-        if (s2 < k) fa[s2] = *reinterpret_cast<const i32x4*>(buf + s2 * SL + aoff);
+      for (int ch = 0; ch < BK / 32; ++ch) {
+        const int c = 2 * ch + (lane >> 5);
+        const int aoff = ar * BK + 16 * oz_slot<BK>(ar, c);
+        const int boff = OP + br * BK + 16 * oz_slot<BK>(br, c);
+        i32x4 fa[KS];
 #pragma unroll
-      for (int tt = 0; tt < KS; ++tt)
-        if (tt < k) {
-          const i32x4 fb = *reinterpret_cast<const i32x4*>(buf + tt * SL + boff);
+        for (int s2 = 0; s2 < KS; ++s2)
+          if (s2 < k) fa[s2] = *reinterpret_cast<const i32x4*>(buf + s2 * SL + aoff);
 #pragma unroll
-          for (int s2 = 0; s2 < KS - tt; ++s2)
-            if (s2 + tt < k)
-              acc[s2 + tt] =
-                  __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s2], fb, acc[s2 + tt], 0, 0, 0);
-        }
-      if (more) store((s + 1 - s0) & 1);
+        for (int tt = 0; tt < KS; ++tt)
+          if (tt < k) {
+            const i32x4 fb = *reinterpret_cast<const i32x4*>(buf + tt * SL + boff);
+#pragma unroll
+            for (int s2 = 0; s2 < KS - tt; ++s2)
+              if (s2 + tt < k)
+                acc[s2 + tt] =
+                    __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s2], fb, acc[s2 + tt], 0, 0, 0);
+          }
+      }
+      __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
     flush(s0 == 0);
@@ -635,12 +657,23 @@ static int oz_fast_launch(OzArgs& g, hipStream_t s) {
   g.tiles_n = (g.N + 63) / 64;
   const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
   TRNBLAS_CHECK_ARG(nt < (1ll << 31), "ozaki: too many tiles");
+  const int bk = g.k <= 8 ? 64 : 32;
   const int64_t kflush = ((1ll << 31) - 1) / (4096ll * g.k);  // K terms per diagonal
-  g.flush = (int)std::max<int64_t>(1, kflush / 32);
-  if (g.k <= 8)
-    hipLaunchKernelGGL(oz_fast_kernel<8>, dim3((unsigned)nt), dim3(256), 0, s, g);
-  else
-    hipLaunchKernelGGL(oz_fast_kernel<12>, dim3((unsigned)nt), dim3(256), 0, s, g);
+  g.flush = (int)std::max<int64_t>(1, kflush / bk);
+  const dim3 grid((unsigned)nt), block(256);
+  switch (g.k) {
+#define OZ_FAST(KS, BK) \
+  case KS:              \
+    hipLaunchKernelGGL((oz_fast_kernel<KS, BK>), grid, block, 0, s, g); \
+    break;
+    OZ_FAST(1, 64) OZ_FAST(2, 64) OZ_FAST(3, 64) OZ_FAST(4, 64)
+    OZ_FAST(5, 64) OZ_FAST(6, 64) OZ_FAST(7, 64) OZ_FAST(8, 64)
+    OZ_FAST(9, 32) OZ_FAST(10, 32) OZ_FAST(11, 32) OZ_FAST(12, 32)
+#undef OZ_FAST
+    default:
+      set_error("ozaki_gemm(fast): slices %d not in [1, 12]", g.k);
+      return TRNBLAS_E_ARG;
+  }
   return check_launch("ozaki_gemm(fast)");
 }
 
