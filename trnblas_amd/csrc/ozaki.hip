@@ -81,17 +81,29 @@ __global__ __launch_bounds__(256) void oz_emax_row_kernel(const double* X, int64
   }
 }
 
-// Column maxima: a 64-column strip per workgroup, 4 row lanes per column.
+// Column maxima: a 64-column strip x 256-row chunk per workgroup, 4 row lanes
+// per column; the chunk's exponent (frexp is monotonic in |x|) goes into
+// exps[c] by atomicMax, a non-finite chunk as kEmaxBad (turned into
+// kNonFinite by oz_flags_kernel). exps must hold INT_MIN beforehand.
+constexpr int kEmaxRows = 256;
+constexpr int kEmaxBad = 0x7fffffff;
+
+__global__ __launch_bounds__(256) void oz_fill_kernel(int32_t* p, int n, int32_t v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
 __global__ __launch_bounds__(256) void oz_emax_col_kernel(const double* X, int64_t ldx, int R,
                                                           int C, int32_t* exps) {
   __shared__ double smax[4][64];
   __shared__ int sbad[4][64];
   const int cx = threadIdx.x & 63, ry = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + cx;
+  const int r0 = blockIdx.y * kEmaxRows, r1 = min(R, r0 + kEmaxRows);
   double m = 0.0;
   int bad = 0;
   if (c < C) {
-    for (int r = ry; r < R; r += 4) {
+    for (int r = r0 + ry; r < r1; r += 4) {
       const double v = fabs(X[(int64_t)r * ldx + c]);
       bad |= !isfinite(v);
       m = v > m ? v : m;
@@ -105,19 +117,20 @@ __global__ __launch_bounds__(256) void oz_emax_col_kernel(const double* X, int64
       m = smax[k][cx] > m ? smax[k][cx] : m;
       bad |= sbad[k][cx];
     }
-    exps[c] = bad ? kNonFinite : frexp_exp(m);
+    atomicMax(&exps[c], bad ? kEmaxBad : frexp_exp(m));
   }
 }
 
 // flags[0] = 1 when some shift 6 - e is not a normal exponent (the global
 // two-factor scaling of ozaki.py:185-188); flags[1] = 1 on non-finite input.
-__global__ __launch_bounds__(1024) void oz_flags_kernel(const int32_t* exps, int n,
-                                                        int32_t* flags) {
+// A column exponent of kEmaxBad (non-finite) is rewritten as kNonFinite.
+__global__ __launch_bounds__(1024) void oz_flags_kernel(int32_t* exps, int n, int32_t* flags) {
   __shared__ int s2[16], sn[16];
   int two = 0, nf = 0;
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
     const int e = exps[i];
-    if (e == kNonFinite) {
+    if (e == kNonFinite || e == kEmaxBad) {
+      if (e == kEmaxBad) exps[i] = kNonFinite;
       nf = 1;
     } else {
       const int sh = (kSliceBits - 1) - e;
@@ -175,41 +188,52 @@ __device__ __forceinline__ void digits_of(double x, int e, int k, bool two, int8
 }
 
 // Row split: X (R, C) row-major, one exponent per row, digits
-// out[s*ld_slice + r*ld_digit + c]. Each thread: 16 consecutive columns.
+// out[s*ld_slice + r*ld_digit + c]. A workgroup covers 1024 columns of one
+// row, each thread 4 consecutive columns: loads and the 4-byte digit stores
+// of a wave are contiguous.
 __global__ __launch_bounds__(256) void oz_digits_row_kernel(const double* X, int64_t ldx, int R,
                                                             int C, int k, const int32_t* exps,
                                                             const int32_t* flags, int8_t* out,
                                                             int64_t ld_digit, int64_t ld_slice) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int cg = (C + 15) / 16;
-  const int64_t r = gid / cg;
-  if (r >= R) return;
-  const int c0 = (int)(gid - r * cg) * 16;
+  const int cgs = (C + 1023) / 1024;
+  const int64_t r = blockIdx.x / cgs;
+  const int c0 = (int)(blockIdx.x - r * cgs) * 1024 + 4 * (int)threadIdx.x;
+  if (c0 >= C) return;
   const int e = exps[r];
   if (e == kNonFinite) return;
   const bool two = flags[0] != 0;
-  union {
-    int8_t b[16];
-    i32x4 v;
-  } u[12];
-  const double* src = X + r * ldx;
+  const double* src = X + r * ldx + c0;
+  double x[4];
+  if (c0 + 4 <= C && ((reinterpret_cast<uintptr_t>(src) & 15) == 0)) {
+    const double2 a = *reinterpret_cast<const double2*>(src);
+    const double2 b = *reinterpret_cast<const double2*>(src + 2);
+    x[0] = a.x;
+    x[1] = a.y;
+    x[2] = b.x;
+    x[3] = b.y;
+  } else {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int c = c0 + i;
+    for (int i = 0; i < 4; ++i) x[i] = c0 + i < C ? src[i] : 0.0;
+  }
+  union {
+    int8_t b[4];
+    int w;
+  } u[12];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
     int8_t d[12];
-    const double x = c < C ? src[c] : 0.0;
-    digits_of<12>(x, e, k, two, d);
+    digits_of<12>(x[i], e, k, two, d);
 #pragma unroll
     for (int s = 0; s < 12; ++s) u[s].b[i] = s < k ? d[s] : 0;
   }
-  const bool full = c0 + 16 <= C && (((uintptr_t)out + r * ld_digit + c0) & 15) == 0 &&
-                    (ld_slice & 15) == 0;
+  const bool full = c0 + 4 <= C && (((uintptr_t)out + r * ld_digit + c0) & 3) == 0 &&
+                    (ld_slice & 3) == 0;
   for (int s = 0; s < k; ++s) {
     int8_t* dst = out + (int64_t)s * ld_slice + r * ld_digit + c0;
     if (full) {
-      *reinterpret_cast<i32x4*>(dst) = u[s].v;
+      *reinterpret_cast<int*>(dst) = u[s].w;
     } else {
-      for (int i = 0; i < 16 && c0 + i < C; ++i) dst[i] = u[s].b[i];
+      for (int i = 0; i < 4 && c0 + i < C; ++i) dst[i] = u[s].b[i];
     }
   }
 }
@@ -714,7 +738,7 @@ extern "C" int trnblas_hip_ozaki_split(int per_row, int64_t R, int64_t C, const 
   const int n = per_row ? (int)R : (int)C;
   if (R == 0 || C == 0) {
     // zero exponents, no digits (the caller zero-fills the digit buffer)
-    hipLaunchKernelGGL(oz_flags_kernel, dim3(1), dim3(1024), 0, s, (const int32_t*)exps, 0,
+    hipLaunchKernelGGL(oz_flags_kernel, dim3(1), dim3(1024), 0, s, exps, 0,
                        scratch);
     if (n > 0 && hipMemsetAsync(exps, 0, n * sizeof(int32_t), s) != hipSuccess)
       return check_launch("ozaki_split");
@@ -727,21 +751,27 @@ extern "C" int trnblas_hip_ozaki_split(int per_row, int64_t R, int64_t C, const 
                        (int)C, exps);
   } else {
     TRNBLAS_CHECK_ARG(ld_digit >= R && ld_slice >= C * ld_digit, "ozaki_split: bad digit layout");
-    hipLaunchKernelGGL(oz_emax_col_kernel, dim3((unsigned)((C + 63) / 64)), dim3(256), 0, s, X,
-                       ldx, (int)R, (int)C, exps);
+    TRNBLAS_CHECK_ARG((R + kEmaxRows - 1) / kEmaxRows < 65536, "ozaki_split: too many rows");
+    hipLaunchKernelGGL(oz_fill_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, s, exps,
+                       (int)C, (int32_t)0x80000000);
+    hipLaunchKernelGGL(oz_emax_col_kernel,
+                       dim3((unsigned)((C + 63) / 64), (unsigned)((R + kEmaxRows - 1) / kEmaxRows)),
+                       dim3(256), 0, s, X, ldx, (int)R, (int)C, exps);
   }
   int rc = check_launch("ozaki_split(emax)");
   if (rc) return rc;
-  hipLaunchKernelGGL(oz_flags_kernel, dim3(1), dim3(1024), 0, s, (const int32_t*)exps, n,
+  hipLaunchKernelGGL(oz_flags_kernel, dim3(1), dim3(1024), 0, s, exps, n,
                      scratch);
   rc = check_launch("ozaki_split(flags)");
   if (rc) return rc;
   if (per_row) {
-    const int64_t threads = R * ((C + 15) / 16);
-    hipLaunchKernelGGL(oz_digits_row_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256),
+    const int64_t blocks = R * ((C + 1023) / 1024);
+    TRNBLAS_CHECK_ARG(blocks < (1ll << 31), "ozaki_split: too large");
+    hipLaunchKernelGGL(oz_digits_row_kernel, dim3((unsigned)blocks), dim3(256),
                        0, s, X, ldx, (int)R, (int)C, slices, (const int32_t*)exps,
                        (const int32_t*)scratch, digits, ld_digit, ld_slice);
   } else {
+    TRNBLAS_CHECK_ARG((R + 63) / 64 < 65536, "ozaki_split: too many rows");
     hipLaunchKernelGGL(oz_digits_col_kernel,
                        dim3((unsigned)((C + 63) / 64), (unsigned)((R + 63) / 64)), dim3(256), 0,
                        s, X, ldx, (int)R, (int)C, slices, (const int32_t*)exps,
