@@ -125,110 +125,121 @@ def cpu_baseline_level3(A, C, Ab, Bb, threads: int) -> dict:
     return {"value": STEP_FLOP / t / 1e12, "unit": "TFLOP/s", "cores": threads, "ms": t * 1e3}
 
 
-def run_extras(dev, tb) -> dict:
+def run_extras(dev, tb, only=None) -> dict:
+    """The other BASELINE workloads (C1, fp32 8192^3, C3, C5); `only` selects
+    a subset by name."""
     from trnblas_amd import df_mp2
     from trnblas_amd.hip import dispatch, kernels
 
     out = {}
-    # C1: gemm fp32 A^T B + 0.5 C at 2048^3, against the CPU path
-    A, B, C = df_mp2.config1_inputs(dev)
-    t = gpu_time_ms(lambda: tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True), reps=20, warm=3)
-    D = tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True)
-    Ah, Bh, Ch = A.cpu(), B.cpu(), C.cpu()
-    t0 = time.perf_counter()
-    cpu = Ah.T @ Bh
-    cpu.mul_(1.0).add_(Ch, alpha=0.5)
-    cpu_ms = (time.perf_counter() - t0) * 1e3
-    den = Ah.double().abs().T @ Bh.double().abs() + 0.5 * Ch.double().abs()
-    err = float(((D.cpu().double() - cpu.double()) / den).abs().max())
-    fl = 2 * 2048**3
-    out["c1_gemm_2048_transA"] = {
-        "ms": t, "tflops": fl / t / 1e9, "frac_fp32_peak": fl / t / 1e9 / PEAK_FP32_MFMA,
-        "cw_err_vs_cpu_path": err, "gate": 1e-6, "cpu_ms": cpu_ms, "cpu_threads": torch.get_num_threads(),
-    }  # fmt: skip
-    log("c1", out["c1_gemm_2048_transA"])
-    # fp32 GEMM 8192^3 (north-star target: >= 70 % of fp32 MFMA peak)
-    g = torch.Generator(device=dev).manual_seed(0)
-    X = torch.randn(8192, 8192, device=dev, generator=g)
-    Y = torch.randn(8192, 8192, device=dev, generator=g)
-    t = gpu_time_ms(lambda: tb.gemm(1.0, X, Y), reps=10, warm=2)
-    tl = gpu_time_ms(lambda: torch.matmul(X, Y), reps=10, warm=2)
-    fl = 2 * 8192**3
-    out["gemm_fp32_8192"] = {
-        "ms": t, "tflops": fl / t / 1e9, "frac_fp32_peak": fl / t / 1e9 / PEAK_FP32_MFMA,
-        "torch_hipblaslt_ms": tl, "torch_tflops": fl / tl / 1e9,
-    }  # fmt: skip
-    log("gemm8192", out["gemm_fp32_8192"])
-    del X, Y
-    # C3: fused pair energy vs the unfused GPU baseline (hipBLASLt GEMM + torch),
-    # in both kernel arithmetics (bf16x6 is the default)
-    Bp, eo, ev = df_mp2.config3_inputs(dev)
-    tf = gpu_time_ms(lambda: kernels.pair_energy_sym(Bp, eo, ev, math="bf16x6"), reps=3, warm=1)
-    tf32 = gpu_time_ms(lambda: kernels.pair_energy_sym(Bp, eo, ev, math="fp32"), reps=3, warm=1)
-    tu = gpu_time_ms(lambda: dispatch._torch_chunked_pair_energy(Bp, eo, ev), reps=3, warm=1)
-    e_hip = float(kernels.pair_energy_sym(Bp, eo, ev, math="bf16x6"))
-    e_f32 = float(kernels.pair_energy_sym(Bp, eo, ev, math="fp32"))
-    e_unf = float(dispatch._torch_chunked_pair_energy(Bp, eo, ev))
-    Bd, eod, evd = Bp.double(), eo.double(), ev.double()
-    e64 = torch.zeros((), dtype=torch.float64, device=dev)
-    for i in range(Bp.shape[0]):
-        T = torch.matmul(Bd[i].unsqueeze(0), Bd[i:].transpose(1, 2))
-        Dn = eod[i] + eod[i:, None, None] - evd[None, :, None] - evd[None, None, :]
-        e = (T * (2.0 * T - T.transpose(1, 2)) / Dn).sum(dim=(1, 2))
-        w = torch.full_like(e, 2.0)
-        w[0] = 1.0
-        e64 += (w * e).sum()
-    e64 = float(e64)
-    del Bd
-    fl = 96 * 97 / 2 * 2 * 672 * 672 * 2304
-    # CPU path sample: the reference's fp32 pair loop over 12 of the 9216
-    # ordered pairs, scaled to all pairs.
-    from oracle import pair_energy as pe
+    if only is None or "c1" in only:
+        # C1: gemm fp32 A^T B + 0.5 C at 2048^3, against the CPU path
+        A, B, C = df_mp2.config1_inputs(dev)
+        t = gpu_time_ms(lambda: tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True), reps=20, warm=3)
+        D = tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True)
+        Ah, Bh, Ch = A.cpu(), B.cpu(), C.cpu()
+        t0 = time.perf_counter()
+        cpu = Ah.T @ Bh
+        cpu.mul_(1.0).add_(Ch, alpha=0.5)
+        cpu_ms = (time.perf_counter() - t0) * 1e3
+        den = Ah.double().abs().T @ Bh.double().abs() + 0.5 * Ch.double().abs()
+        err = float(((D.cpu().double() - cpu.double()) / den).abs().max())
+        fl = 2 * 2048**3
+        out["c1_gemm_2048_transA"] = {
+            "ms": t, "tflops": fl / t / 1e9, "frac_fp32_peak": fl / t / 1e9 / PEAK_FP32_MFMA,
+            "cw_err_vs_cpu_path": err, "gate": 1e-6, "cpu_ms": cpu_ms, "cpu_threads": torch.get_num_threads(),
+        }  # fmt: skip
+        log("c1", out["c1_gemm_2048_transA"])
+    if only is None or "gemm8192" in only:
+        # fp32 GEMM 8192^3 (north-star target: >= 70 % of fp32 MFMA peak)
+        g = torch.Generator(device=dev).manual_seed(0)
+        X = torch.randn(8192, 8192, device=dev, generator=g)
+        Y = torch.randn(8192, 8192, device=dev, generator=g)
+        t = gpu_time_ms(lambda: tb.gemm(1.0, X, Y), reps=10, warm=2)
+        tl = gpu_time_ms(lambda: torch.matmul(X, Y), reps=10, warm=2)
+        fl = 2 * 8192**3
+        out["gemm_fp32_8192"] = {
+            "ms": t, "tflops": fl / t / 1e9, "frac_fp32_peak": fl / t / 1e9 / PEAK_FP32_MFMA,
+            "torch_hipblaslt_ms": tl, "torch_tflops": fl / tl / 1e9,
+        }  # fmt: skip
+        log("gemm8192", out["gemm_fp32_8192"])
+        del X, Y
+    if only is None or "c3" in only:
+        # C3: fused pair energy vs the unfused GPU baseline (hipBLASLt GEMM + torch),
+        # in both kernel arithmetics (bf16x6 is the default)
+        Bp, eo, ev = df_mp2.config3_inputs(dev)
+        tf = gpu_time_ms(lambda: kernels.pair_energy_sym(Bp, eo, ev, math="bf16x6"), reps=3, warm=1)
+        tf32 = gpu_time_ms(lambda: kernels.pair_energy_sym(Bp, eo, ev, math="fp32"), reps=3, warm=1)
+        tu = gpu_time_ms(lambda: dispatch._torch_chunked_pair_energy(Bp, eo, ev), reps=3, warm=1)
+        e_hip = float(kernels.pair_energy_sym(Bp, eo, ev, math="bf16x6"))
+        e_f32 = float(kernels.pair_energy_sym(Bp, eo, ev, math="fp32"))
+        e_unf = float(dispatch._torch_chunked_pair_energy(Bp, eo, ev))
+        Bd, eod, evd = Bp.double(), eo.double(), ev.double()
+        e64 = torch.zeros((), dtype=torch.float64, device=dev)
+        for i in range(Bp.shape[0]):
+            T = torch.matmul(Bd[i].unsqueeze(0), Bd[i:].transpose(1, 2))
+            Dn = eod[i] + eod[i:, None, None] - evd[None, :, None] - evd[None, None, :]
+            e = (T * (2.0 * T - T.transpose(1, 2)) / Dn).sum(dim=(1, 2))
+            w = torch.full_like(e, 2.0)
+            w[0] = 1.0
+            e64 += (w * e).sum()
+        e64 = float(e64)
+        del Bd
+        fl = 96 * 97 / 2 * 2 * 672 * 672 * 2304
+        # CPU path sample: the reference's fp32 pair loop over 12 of the 9216
+        # ordered pairs, scaled to all pairs.
+        from oracle import pair_energy as pe
 
-    Bh, eoh, evh = Bp[:12].cpu(), eo[:12].cpu(), ev.cpu()
-    t0 = time.perf_counter()
-    for j in range(12):
-        pe.fused_pair_cpu(Bh[0], Bh[j], float(eoh[0]), float(eoh[j]), evh)
-    cpu_pair_s = (time.perf_counter() - t0) / 12
-    out["pair_energy_c3_96_672_2304"] = {
-        "fused_ms": tf, "fused_math": "bf16x6", "unfused_gpu_ms": tu,
-        "speedup_vs_unfused": tu / tf, "tflops_sym": fl / tf / 1e9,
-        "bf16_mfma_tflops": 6 * fl / tf / 1e9,
-        "frac_bf16_peak": 6 * fl / tf / 1e9 / PEAK_BF16_MFMA,
-        "energy_fp64": e64, "rel_err_fused_vs_fp64": abs(e_hip - e64) / abs(e64),
-        "fused_fp32_mfma_ms": tf32, "speedup_fp32_mfma_vs_unfused": tu / tf32,
-        "frac_fp32_peak_fp32_mfma": fl / tf32 / 1e9 / PEAK_FP32_MFMA,
-        "rel_err_fused_fp32_mfma_vs_fp64": abs(e_f32 - e64) / abs(e64),
-        "rel_err_unfused_fp32_vs_fp64": abs(e_unf - e64) / abs(e64), "gate": 1e-6,
-        "cpu_fp32_loop_ms_est": cpu_pair_s * 96 * 96 * 1e3,
-        "cpu_sample": "12 of 9216 ordered pairs of the fp32 torch loop, scaled",
-        "cpu_threads": torch.get_num_threads(),
-    }  # fmt: skip
-    log("c3", out["pair_energy_c3_96_672_2304"])
-    del Bp
-    # C5: Ozaki gemm_fp64 at 8192^3, k = 8, against native fp64 DGEMM
-    g = torch.Generator(device=dev).manual_seed(5)
-    n = 8192
+        Bh, eoh, evh = Bp[:12].cpu(), eo[:12].cpu(), ev.cpu()
+        t0 = time.perf_counter()
+        for j in range(12):
+            pe.fused_pair_cpu(Bh[0], Bh[j], float(eoh[0]), float(eoh[j]), evh)
+        cpu_pair_s = (time.perf_counter() - t0) / 12
+        out["pair_energy_c3_96_672_2304"] = {
+            "fused_ms": tf, "fused_math": "bf16x6", "unfused_gpu_ms": tu,
+            "speedup_vs_unfused": tu / tf, "tflops_sym": fl / tf / 1e9,
+            "bf16_mfma_tflops": 6 * fl / tf / 1e9,
+            "frac_bf16_peak": 6 * fl / tf / 1e9 / PEAK_BF16_MFMA,
+            "energy_fp64": e64, "rel_err_fused_vs_fp64": abs(e_hip - e64) / abs(e64),
+            "fused_fp32_mfma_ms": tf32, "speedup_fp32_mfma_vs_unfused": tu / tf32,
+            "frac_fp32_peak_fp32_mfma": fl / tf32 / 1e9 / PEAK_FP32_MFMA,
+            "rel_err_fused_fp32_mfma_vs_fp64": abs(e_f32 - e64) / abs(e64),
+            "rel_err_unfused_fp32_vs_fp64": abs(e_unf - e64) / abs(e64), "gate": 1e-6,
+            "cpu_fp32_loop_ms_est": cpu_pair_s * 96 * 96 * 1e3,
+            "cpu_sample": "12 of 9216 ordered pairs of the fp32 torch loop, scaled",
+            "cpu_threads": torch.get_num_threads(),
+        }  # fmt: skip
+        log("c3", out["pair_energy_c3_96_672_2304"])
+        del Bp
+    if only is None or "c5" in only:
+        # C5: Ozaki gemm_fp64 at 8192^3, k = 8, against native fp64 DGEMM
+        g = torch.Generator(device=dev).manual_seed(5)
+        n = 8192
 
-    def draw():
-        u = torch.rand(n, n, generator=g, device=dev, dtype=torch.float64) * 2 - 1
-        return u * torch.exp2(torch.round(4.0 * torch.randn(n, n, generator=g, device=dev, dtype=torch.float64)))
+        def draw():
+            u = torch.rand(n, n, generator=g, device=dev, dtype=torch.float64) * 2 - 1
+            return u * torch.exp2(torch.round(4.0 * torch.randn(n, n, generator=g, device=dev, dtype=torch.float64)))
 
-    Ao, Bo = draw(), draw()
-    to = gpu_time_ms(lambda: tb.gemm_fp64(Ao, Bo), reps=3, warm=1)
-    td = gpu_time_ms(lambda: torch.matmul(Ao, Bo), reps=3, warm=1)
-    Co = tb.gemm_fp64(Ao, Bo)
-    Cd = Ao @ Bo
-    den = Ao.abs() @ Bo.abs()
-    err = float(((Co - Cd).abs() / den).max())
-    ops = 36 * 2 * n**3
-    out["ozaki_gemm_fp64_c5_8192_k8"] = {
-        "ms": to, "int8_tops": ops / to / 1e9, "frac_int8_peak": ops / to / 1e9 / PEAK_INT8,
-        "fp64_equiv_tflops": 2 * n**3 / to / 1e9, "native_dgemm_ms": td,
-        "native_dgemm_tflops": 2 * n**3 / td / 1e9, "max_cw_err_vs_dgemm": err, "gate": 1e-12,
-        "mode": "bitwise (equals the reference's ozaki.reference_gemm)",
-    }  # fmt: skip
-    log("c5", out["ozaki_gemm_fp64_c5_8192_k8"])
+        Ao, Bo = draw(), draw()
+        to = gpu_time_ms(lambda: tb.gemm_fp64(Ao, Bo, mode="fast"), reps=3, warm=1)
+        tx = gpu_time_ms(lambda: tb.gemm_fp64(Ao, Bo, mode="exact"), reps=3, warm=1)
+        td = gpu_time_ms(lambda: torch.matmul(Ao, Bo), reps=3, warm=1)
+        Cd = Ao @ Bo
+        den = Ao.abs() @ Bo.abs()
+        err = float(((tb.gemm_fp64(Ao, Bo, mode="fast") - Cd).abs() / den).max())
+        errx = float(((tb.gemm_fp64(Ao, Bo, mode="exact") - Cd).abs() / den).max())
+        ops = 36 * 2 * n**3
+        out["ozaki_gemm_fp64_c5_8192_k8"] = {
+            "ms": to, "mode": "fast (default: int32 diagonals, fp64 recombination)",
+            "int8_tops": ops / to / 1e9, "frac_int8_peak": ops / to / 1e9 / PEAK_INT8,
+            "fp64_equiv_tflops": 2 * n**3 / to / 1e9, "native_dgemm_ms": td,
+            "native_dgemm_tflops": 2 * n**3 / td / 1e9, "max_cw_err_vs_dgemm": err,
+            "exact_mode_ms": tx, "exact_mode_frac_int8_peak": ops / tx / 1e9 / PEAK_INT8,
+            "exact_mode_max_cw_err_vs_dgemm": errx,
+            "accuracy_gate": "every element within the 8-slice error bound (C5 wide-range data): "
+            "tests/test_api_gpu.py::test_config5_gemm_fp64_accuracy_full_size, both modes",
+        }  # fmt: skip
+        log("c5", out["ozaki_gemm_fp64_c5_8192_k8"])
     return out
 
 
@@ -239,6 +250,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default=None,
+                    help="comma-separated subset of the extra workloads: c1,gemm8192,c3,c5")
     ap.add_argument(
         "--calibrate-copy",
         action="store_true",
@@ -329,7 +342,8 @@ def main():
         "batched_c2b": {"ms": t_b, "tflops": BATCHED_FLOP / t_b / 1e9, "cw_err_vs_fp64": bat_err},
     }
     if not args.no_extras:
-        extra.update(run_extras(dev, tb))
+        only = None if args.only is None else set(args.only.split(","))
+        extra.update(run_extras(dev, tb, only))
     line = {
         "metric": "GEMM TFLOP/s & %MFMA peak; DF-MP2 pair-energy ms at 96/672/2304",
         "value": value,
