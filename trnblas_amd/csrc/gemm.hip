@@ -209,7 +209,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1)
   constexpr int A_SZ = A_LR * (A_LC + EV), B_SZ = B_LR * (B_LC + EV);
   constexpr int A_NV = A_LR * A_LC / EV / NT, B_NV = B_LR * B_LC / EV / NT;
   static_assert(A_NV * EV * NT == A_LR * A_LC && B_NV * EV * NT == B_LR * B_LC, "tile split");
-  __shared__ __attribute__((aligned(16))) T lds[2 * (A_SZ + B_SZ)];
+  constexpr int NB = (sizeof(T) == 4 && BK == 64) ? 1 : 2;  // LDS stages
+  __shared__ __attribute__((aligned(16))) T lds[NB * (A_SZ + B_SZ)];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
@@ -275,12 +276,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1)
     if (kb1 > kb0) {
       load_tiles(kb0 * BK);
       store_tiles(0);
+      if (NB == 1 && kb0 + 1 < kb1) load_tiles((kb0 + 1) * BK);
       __syncthreads();
     }
     for (int kt = kb0; kt < kb1; ++kt) {
-      const int cur = (kt - kb0) & 1;
+      const int cur = NB == 1 ? 0 : (kt - kb0) & 1;
       const bool more = kt + 1 < kb1;
-      if (more) load_tiles((kt + 1) * BK);
+      if (NB == 2 && more) load_tiles((kt + 1) * BK);
       const T* la = lds + cur * (A_SZ + B_SZ);
       const T* lb = la + A_SZ;
 #pragma unroll
@@ -298,8 +300,19 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1)
 #pragma unroll
           for (int j = 0; j < FN; ++j) mma_frag(acc[i][j], fa[i], fb[j], (T*)nullptr);
       }
-      if (more) store_tiles(cur ^ 1);
-      __syncthreads();
+      if (NB == 2) {
+        if (more) store_tiles(cur ^ 1);
+        __syncthreads();
+      } else {
+        // One stage: every wave is done reading before tile kt + 1 is
+        // stored; tile kt + 2 is then requested into the freed registers.
+        __syncthreads();
+        if (more) {
+          store_tiles(0);
+          if (kt + 2 < kb1) load_tiles((kt + 2) * BK);
+          __syncthreads();
+        }
+      }
     }
 
     // Lane l of an MFMA 32x32 block holds column l % 32 and rows
@@ -401,7 +414,13 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs g) {
 template <typename T>
 struct Cfg {
   static constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
-  static constexpr int BK = 32;
+  // k-tile: fp32 with 16-byte aligned operands uses 64 (one LDS stage, the
+  // next tile held in registers; two workgroups per CU cover each other's
+  // barriers); the others 32 (two LDS stages).
+  template <bool VEC>
+  static constexpr int bk() {
+    return sizeof(T) == 4 && VEC ? 64 : 32;
+  }
   static constexpr int NT = (BM / WM) * (BN / WN) * 64;
 };
 
@@ -446,7 +465,9 @@ static int choose_sk(GemmArgs& g, int occupancy, size_t ws_bytes) {
 template <typename T, bool AKC, bool BKC, bool VEC, bool SYRK>
 static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   using C = Cfg<T>;
-  auto kern = gemm_kernel<T, C::BM, C::BN, C::BK, C::WM, C::WN, AKC, BKC, VEC, SYRK>;
+  constexpr int BK = C::template bk<VEC>();
+  g.nk = (g.K + BK - 1) / BK;
+  auto kern = gemm_kernel<T, C::BM, C::BN, BK, C::WM, C::WN, AKC, BKC, VEC, SYRK>;
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, C::NT, 0) != hipSuccess) occ = 1;
   g.sk_groups = choose_sk(g, occ, ws_bytes);
@@ -482,8 +503,10 @@ static int launch_dtype(const GemmArgs& g, bool akc, bool bkc, bool vec, size_t 
 
 static int elem_size(int dtype) { return dtype == TRNBLAS_F32 ? 4 : 2; }
 
-// k-tile of the launch configuration for `dtype`
-static int k_tile(int dtype) { return dtype == TRNBLAS_F32 ? Cfg<float>::BK : Cfg<__bf16>::BK; }
+// Largest k-tile of the launch configurations for `dtype` (panel-span check).
+static int k_tile(int dtype) {
+  return dtype == TRNBLAS_F32 ? Cfg<float>::bk<true>() : Cfg<__bf16>::bk<true>();
+}
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
