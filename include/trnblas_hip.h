@@ -144,10 +144,10 @@ int trnblas_hip_pair_energy(int64_t nvir, int64_t naux, const float* Bi, int64_t
                             void* stream);
 
 /*
- * DF-MP2 pair energies as trnblas_hip_pair_energy — same arguments, pair set,
- * weights, outputs, workspace and determinism — with every fp32 product
- * formed on bf16 MFMA (v_mfma_f32_16x16x32_bf16, fp32 accumulation) from the
- * three bf16 pieces of each operand, split on the way into LDS:
+ * DF-MP2 pair energies as trnblas_hip_pair_energy — same pair set, weights,
+ * outputs and determinism — with every fp32 product formed on bf16 MFMA
+ * (v_mfma_f32_16x16x32_bf16, fp32 accumulation) from the three bf16 pieces
+ * of each operand:
  *   x = hi + mid + lo exactly (hi = rn_bf16(x), mid = rn_bf16(x - hi),
  *   lo = x - hi - mid), and
  *   x y ~= hi_x hi_y + hi_x mid_y + mid_x hi_y + hi_x lo_y + mid_x mid_y + lo_x hi_y,
@@ -155,16 +155,27 @@ int trnblas_hip_pair_energy(int64_t nvir, int64_t naux, const float* Bi, int64_t
  * carries fp32 accumulation error plus that term (fp32-class accuracy) at
  * 6/16 of the MFMA time of an fp32 product.
  *
+ * A first pass writes the pieces of Bi and Bj into the workspace (three bf16
+ * planes per operand), so the call takes the row counts of the operands:
+ * ni rows of Bi (>= every pair_i, >= nocc in the implicit mode) and nj rows
+ * of Bj (>= every pair_j), or nj == 0 when Bj == Bi with ldj_occ == ldi_occ
+ * (one set of planes serves both; required in the implicit mode); a pair
+ * index beyond these rows gives a NaN energy for its pair. workspace
+ * must hold trnblas_hip_pair_energy_bf16x6_workspace(nvir, naux, npairs, ni,
+ * nj) bytes.
+ *
  * Replaces the same reference interface as trnblas_hip_pair_energy
  * (torch.ops.trnblas.pair_energy_sym, trnblas/nki/_native.py:221-239).
  */
-int trnblas_hip_pair_energy_bf16x6(int64_t nvir, int64_t naux, const float* Bi, int64_t ldi_occ,
-                                   const float* Bj, int64_t ldj_occ, int64_t ld_vir,
-                                   const float* eps_i, const float* eps_j, const float* eps_vir,
-                                   int64_t nocc, int64_t npairs, const int32_t* pair_i,
-                                   const int32_t* pair_j, const double* pair_w,
-                                   double* out_pairs, double* out_total, void* workspace,
-                                   size_t workspace_bytes, void* stream);
+size_t trnblas_hip_pair_energy_bf16x6_workspace(int64_t nvir, int64_t naux, int64_t npairs,
+                                                int64_t ni, int64_t nj);
+int trnblas_hip_pair_energy_bf16x6(int64_t nvir, int64_t naux, const float* Bi, int64_t ni,
+                                   int64_t ldi_occ, const float* Bj, int64_t nj,
+                                   int64_t ldj_occ, int64_t ld_vir, const float* eps_i,
+                                   const float* eps_j, const float* eps_vir, int64_t nocc,
+                                   int64_t npairs, const int32_t* pair_i, const int32_t* pair_j,
+                                   const double* pair_w, double* out_pairs, double* out_total,
+                                   void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * MP2 energy of a precomputed amplitude block (no GEMM), HBM-bound.

@@ -49,3 +49,15 @@ def test_argument_errors_are_reported_without_a_gpu():
                                     None, None, 4, 1, None)
     assert rc == _lib.E_ARG and b"slices" in lib.trnblas_hip_last_error()
     assert lib.trnblas_hip_pair_energy_workspace(672, 4656) == (4656 * 28 + 4656) * 8
+    # bf16x6: partials (256-byte aligned), then 3 bf16 pieces of every
+    # (occupied, virtual) row, virtual rows in pairs, naux rounded up to 64,
+    # per operand.
+    part = -(-((4656 * 28 + 4656) * 8) // 256) * 256
+    pieces = 96 * 672 * 3 * 2304 * 2
+    assert lib.trnblas_hip_pair_energy_bf16x6_workspace(672, 2304, 4656, 96, 0) == part + pieces
+    odd = -(-(5 * 8 * 3 * 64 * 2) // 256) * 256  # nvir 7 -> 4 row pairs, naux 33 -> 64
+    assert lib.trnblas_hip_pair_energy_bf16x6_workspace(7, 33, 3, 5, 5) == 256 + 2 * odd
+    # the implicit walk shares one set of pieces (nj == 0) and needs ni >= nocc
+    rc = lib.trnblas_hip_pair_energy_bf16x6(7, 33, 16, 2, 231, 16, 0, 231, 33, 16, 16, 16, 3,
+                                            6, None, None, None, None, 16, 16, 4096, None)
+    assert rc == _lib.E_ARG and b"ni >= nocc" in lib.trnblas_hip_last_error()

@@ -28,6 +28,7 @@
 //  * items of one pair are consecutive on one XCD (shared L2 for its B_i,
 //    B_j panels).
 #include "common.hpp"
+#include <type_traits>
 
 namespace trnblas {
 
@@ -35,7 +36,11 @@ constexpr uint32_t kPeOob = 0x80000000u;
 
 struct PairArgs {
   int nvir, naux;
-  const float* Bi;
+  const float* Bi;  // fp32 operands (fp32 kernel)
+  const uint16_t* Pi;  // bf16x6 kernel: bf16 pieces of Bi / Bj (split_planes_kernel)
+  const uint16_t* Pj;
+  int ldv;             // piece row length (naux rounded up to 32)
+  int rows_i, rows_j;  // occupied rows of Pi / Pj (pair indices beyond give NaN)
   int64_t ldi_occ;
   const float* Bj;
   int64_t ldj_occ;
@@ -81,6 +86,21 @@ __device__ __forceinline__ void tri_tiles(int q, int nb, int& A, int& B) {
   B = a + rem;
 }
 
+// Work item -> pair index p (partials at p * nq + q), tile pair q, occupied
+// indices (i, j). Items of one pair are consecutive (and xcd_remap keeps
+// them on one XCD, sharing that L2 for the pair's panels).
+__device__ __forceinline__ void pe_item(const PairArgs& g, int item, int& p, int& q, int& i,
+                                        int& j) {
+  p = item / g.nq;
+  q = item - p * g.nq;
+  if (g.pair_i) {
+    i = g.pair_i[p];
+    j = g.pair_j[p];
+  } else {
+    tri_pair(p, g.nocc, i, j);
+  }
+}
+
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -104,14 +124,8 @@ __global__ __launch_bounds__(S / 32 * 64, 2) void pair_energy_kernel(PairArgs g)
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int item = xcd_remap(blockIdx.x, gridDim.x);
-  const int p = item / g.nq, q = item - p * g.nq;
-  int i, j;
-  if (g.pair_i) {
-    i = g.pair_i[p];
-    j = g.pair_j[p];
-  } else {
-    tri_pair(p, g.nocc, i, j);
-  }
+  int p, q, i, j;
+  pe_item(g, item, p, q, i, j);
   int TA, TB;
   tri_tiles(q, g.nb, TA, TB);
   const bool diag = TA == TB;
@@ -257,7 +271,7 @@ __global__ __launch_bounds__(S / 32 * 64, 2) void pair_energy_kernel(PairArgs g)
     double t = 0.0;
 #pragma unroll
     for (int k = 0; k < NW; ++k) t += red[k];
-    g.partial[item] = t;
+    g.partial[(int64_t)p * g.nq + q] = t;
   }
 }
 
@@ -355,23 +369,65 @@ constexpr int kX3S = 96, kX3BK = 32;
 // conflict free without padding.
 __device__ __forceinline__ int x3_slot(int r, int grp) { return grp ^ (((r >> 1) ^ (r >> 2)) & 3); }
 
+// fp32 operand X (n, nvir, naux), strides (ld_occ, ld_vir, 1), as its three
+// bf16 pieces p (0 hi, 1 mid, 2 lo) in 32-wide k slices s, rows taken in
+// pairs: element (o, a, p, k), a = 2 m + d, k = 32 s + c, at
+//   ((((o * nvp + m) * nk + s) * 3 + p) * 2 + d) * 32 + c,   nvp = ceil(nvir / 2),
+// nk = ldv / 32. The 64 bytes of one row's slice of one piece share a
+// 128-byte line with the other row of its pair, and the three pieces of a
+// row pair's slice are 384 contiguous bytes, so a wave's 16-row load reads
+// 8 whole lines (half lines would cost the address path twice as much).
+// Columns [naux, ldv) are zero; the second row of the last pair of an odd
+// nvir is never written (and never read). One thread per 8 consecutive k of
+// a row; `total` = n * nvir * ldv / 8 threads.
+template <bool VEC>
+__global__ __launch_bounds__(256) void split_planes_kernel(int nvir, int naux, int ldv, int total,
+                                                          const float* X, int64_t ld_occ,
+                                                          int64_t ld_vir, uint16_t* P) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= total) return;
+  const int gpr = ldv >> 3;
+  const int row = idx / gpr, k0 = (idx - row * gpr) * 8;
+  const int o = row / nvir, a = row - o * nvir;
+  const float* src = X + (int64_t)o * ld_occ + (int64_t)a * ld_vir + k0;
+  f32x4 x0, x1;
+  if (VEC && k0 + 8 <= naux) {
+    x0 = *reinterpret_cast<const f32x4*>(src);
+    x1 = *reinterpret_cast<const f32x4*>(src + 4);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x0[e] = k0 + e < naux ? src[e] : 0.0f;
+      x1[e] = k0 + 4 + e < naux ? src[4 + e] : 0.0f;
+    }
+  }
+  i32x2 h0, m0, l0, h1, m1, l1;
+  split_bf16x3(x0, h0, m0, l0);
+  split_bf16x3(x1, h1, m1, l1);
+  const int nvp = (nvir + 1) >> 1, nk = ldv >> 5;
+  uint16_t* dst = P + ((((int64_t)o * nvp + (a >> 1)) * nk + (k0 >> 5)) * 3 * 2 + (a & 1)) * 32 +
+                  (k0 & 31);
+  *reinterpret_cast<i32x4*>(dst) = i32x4{h0[0], h0[1], h1[0], h1[1]};
+  *reinterpret_cast<i32x4*>(dst + 64) = i32x4{m0[0], m0[1], m1[0], m1[1]};
+  *reinterpret_cast<i32x4*>(dst + 128) = i32x4{l0[0], l0[1], l1[0], l1[1]};
+}
+
 // Work item = (pair, virtual tile pair A <= B) as in pair_energy_kernel, 96 x 96
 // tiles, 4 waves, wave w on the 48 x 48 quadrant (w & 1, w >> 1) as 3 x 3
 // blocks of 16 x 16. Off-diagonal items run two passes over k in one
 // pipeline: X = B_i[A] B_j[B]^T, then X' = B_j[A] B_i[B]^T (both held in
 // registers); diagonal items run the first pass only (B = A). The operands
-// are read as fp32 (4 bytes per element) and split into their three bf16
-// pieces on the way into LDS. A stage is one 32-wide k slice of the 3 pieces
-// x 2 panels of the running pass (36 KiB), double buffered (72 KiB, two
-// workgroups per CU); slices t+1 and t+2 are in flight in registers while
-// slice t is multiplied, one barrier per slice.
-template <bool VEC>
+// come pre-split (split_planes_kernel), so a k-step spends no VALU on the
+// split. A stage is one 32-wide k slice of the 3 pieces x 2 panels of the
+// running pass (36 KiB); LDS holds two stages (72 KiB, two workgroups per
+// CU) and two register sets hold the next two slices in flight: slice t is
+// multiplied from LDS while slices t + 1 and t + 2 load, and slice t + 1
+// goes to LDS at the end of step t. The MFMA partial of each block spans two
+// slices (12 products) before it joins the running sum by an fp32 add.
 __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
   constexpr int S = kX3S, BK = kX3BK;
-  constexpr int SIDE_V4 = S * BK / 4;    // float4 groups per panel slice (768)
-  constexpr int NV = 2 * SIDE_V4 / 256;  // float4 groups per thread per slice (6)
-  constexpr int STAGE = 6 * S * BK;      // bf16 elements: 3 pieces x 2 panels
-  static_assert(NV * 256 == 2 * SIDE_V4 && SIDE_V4 % 64 == 0, "stage split");
+  constexpr int STAGE = 6 * S * BK;  // bf16 elements: 3 pieces x 2 panels
+  static_assert(STAGE * 2 == 36 * 1024 && S == 96 && BK == 32, "9 KiB per wave per stage");
   static_assert(2 * STAGE * 2 >= 2 * S * S * 4, "epilogue fits in the stage buffers");
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
   __shared__ double red[4];
@@ -379,88 +435,92 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int item = xcd_remap(blockIdx.x, gridDim.x);
-  const int p = item / g.nq, q = item - p * g.nq;
-  int i, j;
-  if (g.pair_i) {
-    i = g.pair_i[p];
-    j = g.pair_j[p];
-  } else {
-    tri_pair(p, g.nocc, i, j);
+  int p, q, i, j;
+  pe_item(g, item, p, q, i, j);
+  if ((unsigned)i >= (unsigned)g.rows_i || (unsigned)j >= (unsigned)g.rows_j) {
+    if (tid == 0) g.partial[(int64_t)p * g.nq + q] = __builtin_nan("");
+    return;
   }
   int TA, TB;
   tri_tiles(q, g.nb, TA, TB);
   const bool diag = TA == TB;
   const int a0 = TA * S, b0 = TB * S;
-  const int nvir = g.nvir, naux = g.naux;
-  const int64_t ld_vir = g.ld_vir;
-  const float* Xi = g.Bi + (int64_t)i * g.ldi_occ;
-  const float* Xj = g.Bj + (int64_t)j * g.ldj_occ;
-  const int nk = (naux + BK - 1) / BK;
+  const int nvir = g.nvir, ldv = g.ldv;
+  const int64_t ostride = (int64_t)((nvir + 1) >> 1) * 6 * ldv;  // pieces of one occupied row
+  const uint16_t* Xi = g.Pi + i * ostride;
+  const uint16_t* Xj = g.Pj + j * ostride;
+  const int nk = ldv / BK;  // even: ldv is a multiple of 2 BK
   const int nsteps = diag ? nk : 2 * nk;
 
-  // Slice layout: thread tid loads the float4 at column 4 (tid & 7) of rows
-  // rr0 = tid >> 3, rr0 + 32, rr0 + 64 of both sides (v = 3 side + jj). Side 0
-  // is the A side (rows a0: B_i in pass 0, B_j in pass 1), side 1 the B side
-  // (rows b0: B_j, then B_i). Row offsets within a side are wave-uniform
-  // (scalar offset); the row bounds are fixed per item (rowmask); columns
-  // need a check only in a ragged last slice.
-  const int rr0 = tid >> 3, cc = tid & 7;
-  const uint32_t voff0 = (uint32_t)((rr0 * ld_vir + 4 * cc) * 4);
-  int rowmask = 0;
+  // LDS stage layout [side][piece][row][BK], side 0 the A side (rows a0:
+  // B_i in pass 0, B_j in pass 1), side 1 the B side (rows b0: B_j, then
+  // B_i). Waves 2 s and 2 s + 1 fill side s, 18 row blocks of 16 rows x 64
+  // bytes (one 16-byte load per lane each), block e = piece * 6 + blk at
+  // stage offset e KiB; wave h = w >> 1 of the side takes e = h + 2 u. Lane
+  // l carries LDS slot l % 4 of row 16 blk + l / 4, i.e. the global 16-byte
+  // group x3_slot(row, l % 4), and stores it lane-linearly; lanes 8 v ..
+  // 8 v + 7 read one 128-byte line (a row pair of split_planes_kernel's
+  // layout). The lane's byte offset from the panel's first row pair is
+  // fixed; the slice offset (384 bytes per slice) goes into soffset and the
+  // panel (operand, rows) into the buffer resource, one per pass. Rows past
+  // nvir read as zeros.
+  const int side = w & 1, h = w >> 1;
+  const int rbase = side ? b0 : a0;
+  const int lr = lane >> 2;
+  uint32_t voff[9];
 #pragma unroll
-  for (int v = 0; v < NV; ++v)
-    if (rr0 + 32 * (v % 3) < nvir - (v < 3 ? a0 : b0)) rowmask |= 1 << v;
-  auto load = [&](int step, f32x4(&st)[NV]) {
-    const int pass = step >= nk ? 1 : 0, k0 = (step - pass * nk) * BK;
-    const bool ragged = k0 + BK > naux;
+  for (int u = 0; u < 9; ++u) {
+    const int e = h + 2 * u, pc = e / 6, r = 16 * (e - 6 * pc) + lr;
+    voff[u] = r < nvir - rbase ? (uint32_t)(((r >> 1) * nk * 192 + pc * 64 + (r & 1) * 32 +
+                                             8 * x3_slot(r, lane & 3)) *
+                                            2)
+                               : kPeOob;
+  }
+  const int64_t prow = (int64_t)(rbase >> 1) * nk * 192;  // rbase is even
+  const __amdgpu_buffer_rsrc_t rs0 = pe_rsrc((side ? Xj : Xi) + prow);
+  const __amdgpu_buffer_rsrc_t rs1 = pe_rsrc((side ? Xi : Xj) + prow);
+  // Past the last slice the loads still issue (every step issues the same
+  // 9, which keeps the compiler's wait counts exact), re-reading the last
+  // slice (L2-resident); their data is never stored.
+  i32x4 stg[2][9];  // slice t in set t & 1 between its load and its store
+  auto load = [&](int t, i32x4(&set)[9]) {
+    if (t >= nsteps) t = nsteps - 1;
+    const bool pass1 = t >= nk;
+    const int sl = pass1 ? t - nk : t;
+    const __amdgpu_buffer_rsrc_t rs = pass1 ? rs1 : rs0;
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int side = v / 3, jj = v % 3;
-      const bool use_i = (side ^ pass) == 0;
-      const __amdgpu_buffer_rsrc_t rs =
-          pe_rsrc((use_i ? Xi : Xj) + (int64_t)(side ? b0 : a0) * ld_vir + k0);
-      const int soff = (int)(jj * 32 * ld_vir * 4);
-      const bool rok = (rowmask >> v) & 1;
-      if (VEC) {
-        const bool ok = rok && (!ragged || 4 * cc < naux - k0);
-        st[v] = __builtin_bit_cast(
-            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? voff0 : kPeOob, soff, 0));
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          st[v][e] = __builtin_bit_cast(
-              float, __builtin_amdgcn_raw_buffer_load_b32(
-                         rs, (rok && 4 * cc + e < naux - k0) ? voff0 + 4 * e : kPeOob, soff, 0));
-      }
-    }
+    for (int u = 0; u < 9; ++u) set[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[u], sl * 384, 0);
   };
-  const int lds0 = rr0 * BK + 8 * x3_slot(rr0, cc >> 1) + 4 * (cc & 1);
-  auto store = [&](int buf, const f32x4(&st)[NV]) {
-    uint16_t* dst = lds + buf * STAGE + lds0;
+  auto store = [&](const i32x4(&set)[9], int buf) {
+    uint16_t* dst = lds + buf * STAGE + side * (STAGE / 2) + h * 512 + lane * 8;
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int e = ((v / 3) * S + 32 * (v % 3)) * BK;
-      i32x2 h, m, l;
-      split_bf16x3(st[v], h, m, l);
-      *reinterpret_cast<i32x2*>(dst + e) = h;
-      *reinterpret_cast<i32x2*>(dst + 2 * S * BK + e) = m;
-      *reinterpret_cast<i32x2*>(dst + 4 * S * BK + e) = l;
-    }
+    for (int u = 0; u < 9; ++u) *reinterpret_cast<i32x4*>(dst + u * 1024) = set[u];
   };
 
   // The fragment row of a lane is row0 + 16 blk + (lane & 15) with row0 a
   // multiple of 16, so its LDS slot depends on the lane only.
   const int ar0 = 48 * (w & 1), br0 = 48 * (w >> 1);
   const int fslot = 8 * x3_slot(lane & 15, lane >> 4);
-  f32x4 accX[3][3], accP[3][3];
+  f32x4 accX[3][3], accP[3][3], part[3][3];
 #pragma unroll
   for (int rb = 0; rb < 3; ++rb)
 #pragma unroll
     for (int cb = 0; cb < 3; ++cb) accX[rb][cb] = accP[rb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto mma = [&](const uint16_t* buf, f32x4(&acc)[3][3]) {
-    auto frag = [&](int pc, int side, int r) {
-      return *reinterpret_cast<const bf16x8*>(buf + ((pc * 2 + side) * S + r) * BK + fslot);
+  // Step t (global over both passes; P = t & 1 is static): slice t is in LDS
+  // buffer P (the barrier publishes it and retires every read of buffer
+  // 1 - P), set P is free (its slice t went to LDS in step t - 1) and takes
+  // slice t + 2, slice t is multiplied (the six products of each block,
+  // smallest first, into its partial, started at zero when FIRST), then set
+  // 1 - P (slice t + 1) goes to buffer 1 - P.
+  auto step = [&](auto P_, auto FIRST_, int t) {
+    constexpr int P = decltype(P_)::value;
+    constexpr bool FIRST = decltype(FIRST_)::value;
+    __syncthreads();
+    load(t + 2, stg[P]);
+    const uint16_t* buf = lds + P * STAGE;
+    auto frag = [&](int pc, int sd, int r) {
+      return *reinterpret_cast<const bf16x8*>(buf + ((sd * 3 + pc) * S + r) * BK + fslot);
     };
     bf16x8 fa[3][3];
 #pragma unroll
@@ -472,52 +532,46 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
       bf16x8 fb[3];
 #pragma unroll
       for (int pc = 0; pc < 3; ++pc) fb[pc] = frag(pc, 1, br0 + 16 * cb + (lane & 15));
-      // The six products of this slice, smallest first, go into a fresh
-      // partial that joins the running sum through an IEEE fp32 add: chained
-      // through the MFMA accumulator, a long sum drifts (a 2304-term positive
-      // dot product came out 1.5e-6 low on average; 6e-11 this way).
-      f32x4 part[3];
 #pragma unroll
-      for (int rb = 0; rb < 3; ++rb) part[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int rb = 0; rb < 3; ++rb)
+        part[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            fa[rb][2], fb[0], FIRST ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb], 0, 0, 0);
 #pragma unroll
-      for (int t = 0; t < 6; ++t) {
+      for (int e = 1; e < 6; ++e) {
         constexpr int ka[6] = {2, 1, 0, 1, 0, 0}, kb[6] = {0, 1, 2, 0, 1, 0};
 #pragma unroll
         for (int rb = 0; rb < 3; ++rb)
-          part[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[rb][ka[t]], fb[kb[t]], part[rb],
-                                                             0, 0, 0);
+          part[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[rb][ka[e]], fb[kb[e]],
+                                                                 part[rb][cb], 0, 0, 0);
       }
+    }
+    if (t + 1 < nsteps) store(stg[1 - P], 1 - P);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using T = std::true_type;
+  using F = std::false_type;
+  // One pass: slice pairs (t even, t + 1), each partial added to the pass's
+  // sum in fp32.
+  auto run_pass = [&](f32x4(&acc)[3][3], int t0) {
+    for (int u = 0; u < nk; u += 2) {
+      step(I0(), T(), t0 + u);
+      step(I1(), F(), t0 + u + 1);
 #pragma unroll
-      for (int rb = 0; rb < 3; ++rb) acc[rb][cb] += part[rb];
+      for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 3; ++cb) acc[rb][cb] += part[rb][cb];
     }
   };
 
-  // Two register sets alternate (the loop is unrolled by two): at slice t,
-  // slice t + 1 is already in flight and slice t + 2 is requested.
-  f32x4 s0[NV], s1[NV];
-  if (nsteps > 0) load(0, s0);
-  if (nsteps > 1) load(1, s1);
   if (nsteps > 0) {
-    store(0, s0);
-    __syncthreads();
+    load(0, stg[0]);
+    load(1, stg[1]);
+    store(stg[0], 0);
   }
-  for (int t = 0; t < nsteps; t += 2) {
-    if (t + 2 < nsteps) load(t + 2, s0);
-    if (t < nk)
-      mma(lds, accX);
-    else
-      mma(lds, accP);
-    if (t + 1 < nsteps) store(1, s1);
-    __syncthreads();
-    if (t + 1 >= nsteps) break;
-    if (t + 3 < nsteps) load(t + 3, s1);
-    if (t + 1 < nk)
-      mma(lds + STAGE, accX);
-    else
-      mma(lds + STAGE, accP);
-    if (t + 2 < nsteps) store(0, s0);
-    __syncthreads();
-  }
+  run_pass(accX, 0);
+  if (!diag) run_pass(accP, nk);
+  __syncthreads();  // all fragment reads done before the epilogue reuses LDS
 
   // Lane l of a 16 x 16 block holds column l % 16 and rows 4 (l / 16) + r.
   // Off-diagonal: X at [0, S*S), X' at [S*S, 2 S*S), row stride S.
@@ -552,7 +606,7 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
   sum = wave_sum(sum);
   if (lane == 0) red[w] = sum;
   __syncthreads();
-  if (tid == 0) g.partial[item] = (red[0] + red[1]) + (red[2] + red[3]);
+  if (tid == 0) g.partial[(int64_t)p * g.nq + q] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 // MP2 energy of a precomputed amplitude block (the `mp2_energy` surface,
@@ -615,10 +669,45 @@ extern "C" size_t trnblas_hip_pair_energy_workspace(int64_t nvir, int64_t npairs
   return (size_t)(npairs * pe_nq(nvir) + npairs) * sizeof(double);
 }
 
+// bf16x6 workspace: the partials of the fp32 layout, then the bf16 pieces of
+// Bi (ni x ceil(nvir / 2) row pairs of 6 x ldv), then those of Bj (nj x
+// ceil(nvir / 2); none when nj == 0, where Bj shares Bi's pieces), each
+// region 256-byte aligned.
+static int64_t x3_ldv(int64_t naux) { return (naux + 2 * kX3BK - 1) / (2 * kX3BK) * (2 * kX3BK); }
+static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
+static size_t x3_planes_bytes(int64_t n, int64_t nvir, int64_t naux) {
+  return al256((size_t)(6 * n * ((nvir + 1) / 2) * x3_ldv(naux)) * sizeof(uint16_t));
+}
+
+extern "C" size_t trnblas_hip_pair_energy_bf16x6_workspace(int64_t nvir, int64_t naux,
+                                                           int64_t npairs, int64_t ni,
+                                                           int64_t nj) {
+  if (nvir <= 0 || npairs <= 0 || naux < 0 || ni < 0 || nj < 0) return 0;
+  return al256(trnblas_hip_pair_energy_workspace(nvir, npairs)) +
+         x3_planes_bytes(ni, nvir, naux) + x3_planes_bytes(nj, nvir, naux);
+}
+
+// Split n x nvir rows (o, a) of X into the pieces at P (split_planes_kernel).
+static void x3_split(const float* X, int64_t n, int64_t ld_occ, int64_t ld_vir, int nvir,
+                     int naux, int ldv, uint16_t* P, hipStream_t s) {
+  const int64_t threads = n * nvir * (ldv / 8);
+  if (threads == 0) return;
+  const unsigned blocks = (unsigned)((threads + 255) / 256);
+  const bool vec = (reinterpret_cast<uintptr_t>(X) & 15) == 0 && ld_occ % 4 == 0 &&
+                   ld_vir % 4 == 0;
+  if (vec)
+    hipLaunchKernelGGL(split_planes_kernel<true>, dim3(blocks), dim3(256), 0, s, nvir, naux, ldv,
+                       (int)threads, X, ld_occ, ld_vir, P);
+  else
+    hipLaunchKernelGGL(split_planes_kernel<false>, dim3(blocks), dim3(256), 0, s, nvir, naux, ldv,
+                       (int)threads, X, ld_occ, ld_vir, P);
+}
+
 // Shared driver of the fp32 and bf16x6 pair-energy entry points: argument
 // checks, the fused kernel, then the per-pair and total reductions.
 static int pair_energy_run(bool x3, const char* name, int64_t nvir, int64_t naux, const float* Bi,
-                           int64_t ldi_occ, const float* Bj, int64_t ldj_occ, int64_t ld_vir, const float* eps_i, const float* eps_j,
+                           int64_t ni, int64_t ldi_occ, const float* Bj, int64_t nj,
+                           int64_t ldj_occ, int64_t ld_vir, const float* eps_i, const float* eps_j,
                            const float* eps_vir, int64_t nocc, int64_t npairs,
                            const int32_t* pair_i, const int32_t* pair_j, const double* pair_w,
                            double* out_pairs, double* out_total, void* workspace,
@@ -649,7 +738,20 @@ static int pair_energy_run(bool x3, const char* name, int64_t nvir, int64_t naux
   const int64_t nq = pe_nq(nvir);
   const int64_t items = npairs * nq;
   TRNBLAS_CHECK_ARG(items < (1ll << 31), "%s: too many work items", name);
-  const size_t need = trnblas_hip_pair_energy_workspace(nvir, npairs);
+  if (x3) {
+    TRNBLAS_CHECK_ARG(ni >= 0 && nj >= 0 && ni < (1 << 30) && nj < (1 << 30),
+                      "%s: bad row count", name);
+    TRNBLAS_CHECK_ARG(pair_i != nullptr || (ni >= nocc && nj == 0),
+                      "%s: the implicit walk needs ni >= nocc and nj == 0", name);
+    TRNBLAS_CHECK_ARG(nj > 0 || (Bj == Bi && ldj_occ == ldi_occ),
+                      "%s: nj == 0 shares Bi's pieces and needs Bj == Bi", name);
+    TRNBLAS_CHECK_ARG((int64_t)kX3S * 3 * x3_ldv(naux) * 2 < 0x7fffff00ll,
+                      "%s: naux too large for 32-bit panel offsets", name);
+    TRNBLAS_CHECK_ARG((ni > nj ? ni : nj) * nvir * (x3_ldv(naux) / 8) < (1ll << 31),
+                      "%s: operands too large for one split launch", name);
+  }
+  const size_t need = x3 ? trnblas_hip_pair_energy_bf16x6_workspace(nvir, naux, npairs, ni, nj)
+                         : trnblas_hip_pair_energy_workspace(nvir, npairs);
   if (workspace == nullptr || workspace_bytes < need) {
     set_error("%s: workspace of %zu bytes needed, %zu given", name, need, workspace_bytes);
     return TRNBLAS_E_WORKSPACE;
@@ -677,11 +779,22 @@ static int pair_energy_run(bool x3, const char* name, int64_t nvir, int64_t naux
   const bool vec = al16(Bi) && al16(Bj) && naux % 4 == 0 && ld_vir % 4 == 0 &&
                    ldi_occ % 4 == 0 && ldj_occ % 4 == 0;
   if (x3) {
-    static_assert(kX3S == kPeS, "one tile size: one workspace layout");
-    if (vec)
-      hipLaunchKernelGGL(pair_energy_x3_kernel<true>, dim3((unsigned)items), dim3(256), 0, s, g);
-    else
-      hipLaunchKernelGGL(pair_energy_x3_kernel<false>, dim3((unsigned)items), dim3(256), 0, s, g);
+    static_assert(kX3S == kPeS, "one tile size: one partials layout");
+    const int ldv = (int)x3_ldv(naux);
+    char* pieces =
+        static_cast<char*>(workspace) + al256(trnblas_hip_pair_energy_workspace(nvir, npairs));
+    uint16_t* Pi = reinterpret_cast<uint16_t*>(pieces);
+    uint16_t* Pj = nj ? reinterpret_cast<uint16_t*>(pieces + x3_planes_bytes(ni, nvir, naux)) : Pi;
+    g.Pi = Pi;
+    g.Pj = Pj;
+    g.ldv = ldv;
+    g.rows_i = (int)ni;
+    g.rows_j = (int)(nj ? nj : ni);
+    x3_split(Bi, ni, ldi_occ, ld_vir, (int)nvir, (int)naux, ldv, Pi, s);
+    if (nj) x3_split(Bj, nj, ldj_occ, ld_vir, (int)nvir, (int)naux, ldv, Pj, s);
+    int rc = check_launch(name);
+    if (rc) return rc;
+    hipLaunchKernelGGL(pair_energy_x3_kernel, dim3((unsigned)items), dim3(256), 0, s, g);
   } else {
     constexpr int NT = kPeS / 32 * 64;
     if (vec)
@@ -714,12 +827,14 @@ extern "C" int trnblas_hip_pair_energy(int64_t nvir, int64_t naux, const float* 
                                        double* out_total, void* workspace,
                                        size_t workspace_bytes, void* stream) {
   clear_error();
-  return pair_energy_run(false, "pair_energy", nvir, naux, Bi, ldi_occ, Bj, ldj_occ, ld_vir, eps_i, eps_j, eps_vir, nocc, npairs, pair_i, pair_j, pair_w,
+  return pair_energy_run(false, "pair_energy", nvir, naux, Bi, 0, ldi_occ, Bj, 0, ldj_occ, ld_vir,
+                         eps_i, eps_j, eps_vir, nocc, npairs, pair_i, pair_j, pair_w,
                          out_pairs, out_total, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int trnblas_hip_pair_energy_bf16x6(int64_t nvir, int64_t naux, const float* Bi,
-                                              int64_t ldi_occ, const float* Bj, int64_t ldj_occ,
+                                              int64_t ni, int64_t ldi_occ, const float* Bj,
+                                              int64_t nj, int64_t ldj_occ,
                                               int64_t ld_vir, const float* eps_i,
                                               const float* eps_j, const float* eps_vir,
                                               int64_t nocc, int64_t npairs,
@@ -728,7 +843,7 @@ extern "C" int trnblas_hip_pair_energy_bf16x6(int64_t nvir, int64_t naux, const 
                                               double* out_total, void* workspace,
                                               size_t workspace_bytes, void* stream) {
   clear_error();
-  return pair_energy_run(true, "pair_energy_bf16x6", nvir, naux, Bi, ldi_occ, Bj, ldj_occ,
+  return pair_energy_run(true, "pair_energy_bf16x6", nvir, naux, Bi, ni, ldi_occ, Bj, nj, ldj_occ,
                          ld_vir, eps_i, eps_j, eps_vir, nocc, npairs, pair_i, pair_j, pair_w,
                          out_pairs, out_total, workspace, workspace_bytes, (hipStream_t)stream);
 }

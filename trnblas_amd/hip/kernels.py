@@ -226,7 +226,7 @@ def pair_energy_sym(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tenso
     """E = sum_{i,j} e_ij over all ordered pairs, evaluated as the i <= j walk
     (weights 1 / 2) in one launch. B (nocc, nvir, naux) fp32 on the GPU.
     math: "fp32" (fp32 MFMA), "bf16x6" (each fp32 operand split into three
-    bf16 pieces in the kernel; six bf16 MFMA products per fp32 product) or
+    bf16 pieces by a first pass; six bf16 MFMA products per fp32 product) or
     None (pair_energy_math()). Returns a 0-d float64 device tensor."""
     dev = _require_device(B, eps_occ, eps_vir)
     math = _check_math(math)
@@ -236,15 +236,32 @@ def pair_energy_sym(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tenso
     ev = eps_vir.to(torch.float32).contiguous()
     total = torch.empty((), dtype=torch.float64, device=dev)
     npairs = nocc * (nocc + 1) // 2
-    ws = _lib.load().trnblas_hip_pair_energy_workspace(nvir, npairs)
-    work = torch.empty(max(ws, 8), dtype=torch.uint8, device=dev)
     ld_occ = B.stride(0) if nocc > 1 else nvir * naux
-    _probed_call(
-        "pair_energy", _PE_ENTRY[math], nvir, naux, ptr(B), ld_occ, ptr(B), ld_occ,
-        B.stride(1) if nvir > 1 else naux, ptr(eo), ptr(eo), ptr(ev), nocc, npairs,
-        None, None, None, None, ptr(total), ptr(work), work.numel(), stream_of(dev),
+    _pe_launch(
+        math, dev, nvir, naux, B, nocc, ld_occ, B, 0, ld_occ, B.stride(1) if nvir > 1 else naux,
+        eo, eo, ev, nocc, npairs, None, None, None, total, probed=True,
     )  # fmt: skip
     return total
+
+
+def _pe_launch(math, dev, nvir, naux, Bi, ni, ldi, Bj, nj, ldj, ld_vir, ei, ej, ev, nocc, npairs,
+               pi, pj, out_pairs, out_total, probed=False):
+    """One pair-energy launch with its workspace. ni / nj: rows of Bi / Bj
+    (nj == 0: Bj is Bi), used by the bf16x6 entry point for its planes."""
+    lib = _lib.load()
+    if math == "bf16x6":
+        ws = lib.trnblas_hip_pair_energy_bf16x6_workspace(nvir, naux, npairs, ni, nj)
+        head = (nvir, naux, ptr(Bi), ni, ldi, ptr(Bj), nj, ldj, ld_vir)
+    else:
+        ws = lib.trnblas_hip_pair_energy_workspace(nvir, npairs)
+        head = (nvir, naux, ptr(Bi), ldi, ptr(Bj), ldj, ld_vir)
+    work = torch.empty(max(ws, 8), dtype=torch.uint8, device=dev)
+    args = head + (ptr(ei), ptr(ej), ptr(ev), nocc, npairs, ptr(pi), ptr(pj), None,
+                   ptr(out_pairs), ptr(out_total), ptr(work), work.numel(), stream_of(dev))
+    if probed:
+        _probed_call("pair_energy", _PE_ENTRY[math], *args)
+    else:
+        call(_PE_ENTRY[math], *args)
 
 
 def pair_energies(
@@ -274,16 +291,14 @@ def pair_energies(
     out = torch.empty(npairs, dtype=torch.float64, device=dev)
     if npairs == 0:
         return out
-    ws = _lib.load().trnblas_hip_pair_energy_workspace(nvir, npairs)
-    work = torch.empty(max(ws, 8), dtype=torch.uint8, device=dev)
     ei = eps_i.to(torch.float32).contiguous()
     ej = eps_j.to(torch.float32).contiguous()
     ev = eps_vir.to(torch.float32).contiguous()
     ld_vir = Bi.stride(1) if nvir > 1 else naux
-    call(
-        _PE_ENTRY[math], nvir, naux, ptr(Bi), Bi.stride(0), ptr(Bj), Bj.stride(0),
-        ld_vir, ptr(ei), ptr(ej), ptr(ev), 0, npairs, ptr(pi), ptr(pj), None, ptr(out),
-        None, ptr(work), work.numel(), stream_of(dev),
+    same = Bj.data_ptr() == Bi.data_ptr() and Bj.shape == Bi.shape and Bj.stride() == Bi.stride()
+    _pe_launch(
+        math, dev, nvir, naux, Bi, Bi.shape[0], Bi.stride(0), Bj, 0 if same else Bj.shape[0],
+        Bj.stride(0), ld_vir, ei, ej, ev, 0, npairs, pi, pj, out, None,
     )  # fmt: skip
     return out
 
