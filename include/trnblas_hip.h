@@ -205,6 +205,12 @@ int trnblas_hip_mp2_energy(int64_t ic, int64_t nocc, int64_t nvir, const float* 
  *   digits[s*ld_slice + r*ld_digit + c] (K = C contiguous).
  * per_row == 0: one exponent per column (the B operand); digits are written
  *   transposed, digits[s*ld_slice + c*ld_digit + r] (K = R contiguous).
+ * per_row | 2: the interleaved layout of the fast 8-slice GEMM (mode 2 of
+ *   trnblas_hip_ozaki_gemm): digit (s, row, kk) of the digit row `row` (r or
+ *   c as above) and K index kk at
+ *   digits[row*ld_digit + (kk/64)*64*slices + s*64 + kk%64], i.e. the slices
+ *   of each 64-wide K chunk side by side; ld_digit >= round_up(K, 64) *
+ *   slices and a multiple of 16, digits 16-byte aligned; ld_slice unused.
  * The digit buffer must be zero beyond the matrix (the caller pads to the
  * kernel's tile; entries beyond R x C are not written). exps (device int32,
  * R or C entries) receives e. scratch: device int32[2] (scale-mode flag and
@@ -225,7 +231,10 @@ int trnblas_hip_ozaki_split(int per_row, int64_t R, int64_t C, const double* X, 
  * equals `ozaki.reference_gemm` bit for bit (same groups, same TwoSum order,
  * same combine, ozaki.py:418-455). Mode 1 (fast) accumulates each diagonal
  * of slice pairs exactly in int32 and recombines in fp64 (error within the
- * same bound, not bitwise).
+ * same bound, not bitwise). Mode 2 is mode 1 on interleaved digits
+ * (trnblas_hip_ozaki_split with per_row | 2; slices == 8, lda / ldb the
+ * digit row strides >= 8 Kp, lda_slice / ldb_slice unused): the same result
+ * bit for bit, with whole-cache-line loads.
  *
  * dA: digits (slices, >= M, Kp) with dA[s*lda_slice + m*lda + k];
  * dB: digits (slices, >= N, Kp) with dB[s*ldb_slice + n*ldb + k]; both K

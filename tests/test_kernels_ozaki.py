@@ -87,3 +87,43 @@ def test_ozaki_hilo_bitwise(dev):
     bt, _ = oz.split_b(B, k)
     want = oz.reference_from_digits(at, bt[:, :, :60])[:, :100, :60]
     assert np.array_equal(hilo.view(np.int32), want.view(np.int32))
+
+
+@pytest.mark.parametrize("per", ["row", "col"])
+@pytest.mark.parametrize("k", [3, 8])
+def test_split_interleaved_layout(dev, per, k):
+    # the interleaved digits are the plain split's digits with the k slices
+    # of each 64-wide K chunk of a row side by side: (rows, Kp/64, k, 64)
+    from trnblas_amd.hip import kernels
+
+    rng = np.random.default_rng(40 + k)
+    X = rng.standard_normal((150, 300)) * 10.0 ** rng.uniform(-20, 20, (150, 300))
+    Xd = torch.from_numpy(X).to(dev)
+    d, e, _ = kernels.ozaki_split(Xd, k, per)
+    di, ei, bad = kernels.ozaki_split(Xd, k, per, interleaved=True)
+    assert int(bad) == 0 and torch.equal(e, ei)
+    _, rows, Kp = d.shape
+    assert tuple(di.shape) == (rows, Kp * k)
+    got = di.cpu().numpy().reshape(rows, Kp // 64, k, 64).transpose(2, 0, 1, 3).reshape(k, rows, Kp)
+    assert np.array_equal(got, d.cpu().numpy())
+
+
+@pytest.mark.parametrize(
+    "M,K,N", [(64, 64, 64), (130, 4100, 7), (200, 9000, 31), (300, 257, 520), (1, 1, 1), (65, 129, 63)]
+)
+def test_fast_gemm_interleaved_equals_plain(dev, M, K, N):
+    # same digits, same int32 diagonal sums, same fp64 recombination order:
+    # the interleaved-digit kernel must match the plain-layout one bit for bit
+    from trnblas_amd.hip import kernels
+
+    A, B = inputs(M, K, N, seed=M + 3 * N)
+    Ad, Bd = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+    da, ea, _ = kernels.ozaki_split(Ad, 8, "row")
+    db, eb, _ = kernels.ozaki_split(Bd, 8, "col")
+    dai, _, _ = kernels.ozaki_split(Ad, 8, "row", interleaved=True)
+    dbi, _, _ = kernels.ozaki_split(Bd, 8, "col", interleaved=True)
+    C1 = kernels.ozaki_gemm(da, ea, db, eb, M, N, 8, fast=True)
+    C2 = kernels.ozaki_gemm(dai, ea, dbi, eb, M, N, 8, fast=True)
+    assert torch.equal(C1, C2)
+    C3 = kernels.ozaki_gemm(dbi, eb, dai, ea, N, M, 8, fast=True, transpose_out=True)
+    assert torch.equal(C1, C3) or bool(((C1 - C3).abs() <= 2.0**-50 * C1.abs()).all())

@@ -194,7 +194,8 @@ __device__ __forceinline__ void digits_of(double x, int e, int k, bool two, int8
 __global__ __launch_bounds__(256) void oz_digits_row_kernel(const double* X, int64_t ldx, int R,
                                                             int C, int k, const int32_t* exps,
                                                             const int32_t* flags, int8_t* out,
-                                                            int64_t ld_digit, int64_t ld_slice) {
+                                                            int64_t ld_digit, int64_t ld_slice,
+                                                            int il) {
   const int cgs = (C + 1023) / 1024;
   const int64_t r = blockIdx.x / cgs;
   const int c0 = (int)(blockIdx.x - r * cgs) * 1024 + 4 * (int)threadIdx.x;
@@ -226,11 +227,10 @@ __global__ __launch_bounds__(256) void oz_digits_row_kernel(const double* X, int
 #pragma unroll
     for (int s = 0; s < 12; ++s) u[s].b[i] = s < k ? d[s] : 0;
   }
-  const bool full = c0 + 4 <= C && (((uintptr_t)out + r * ld_digit + c0) & 3) == 0 &&
-                    (ld_slice & 3) == 0;
   for (int s = 0; s < k; ++s) {
-    int8_t* dst = out + (int64_t)s * ld_slice + r * ld_digit + c0;
-    if (full) {
+    int8_t* dst = il ? out + r * ld_digit + (int64_t)(c0 >> 6) * 64 * k + s * 64 + (c0 & 63)
+                     : out + (int64_t)s * ld_slice + r * ld_digit + c0;
+    if (c0 + 4 <= C && ((uintptr_t)dst & 3) == 0) {
       *reinterpret_cast<int*>(dst) = u[s].w;
     } else {
       for (int i = 0; i < 4 && c0 + i < C; ++i) dst[i] = u[s].b[i];
@@ -244,46 +244,48 @@ __global__ __launch_bounds__(256) void oz_digits_row_kernel(const double* X, int
 __global__ __launch_bounds__(256) void oz_digits_col_kernel(const double* X, int64_t ldx, int R,
                                                             int C, int k, const int32_t* exps,
                                                             const int32_t* flags, int8_t* out,
-                                                            int64_t ld_digit, int64_t ld_slice) {
-  __shared__ __attribute__((aligned(16))) int8_t tile[12][64][64 + 16];
+                                                            int64_t ld_digit, int64_t ld_slice,
+                                                            int il) {
+  // Block: 64 columns x 64 rows of X. Thread t: column c0 + t / 4, rows
+  // r0 + 16 (t % 4) .. +15. Both digit layouts keep the 64 rows of one
+  // (slice, column) chunk as 64 contiguous bytes, so the 4 adjacent lanes of
+  // a column write one chunk with 16-byte stores (no transpose through LDS).
   const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
-  const int cx = threadIdx.x & 63, ry = threadIdx.x >> 6;  // ry: 16-row group
-  const int c = c0 + cx;
+  const int c = c0 + (threadIdx.x >> 2), rq = (threadIdx.x & 3) * 16;
+  if (c >= C) return;
+  const int e = exps[c];
+  if (e == kNonFinite) return;
   const bool two = flags[0] != 0;
-  const int e = c < C ? exps[c] : 0;
-  const bool bad = e == kNonFinite;
-  union {
-    int8_t b[16];
-    i32x4 v;
-  } u[12];
+  // digit bytes packed into words with static indices only (a byte union
+  // indexed by the runtime slice count goes to scratch memory)
+  uint32_t u[12][4];
+#pragma unroll
+  for (int s = 0; s < 12; ++s)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) u[s][q] = 0;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int r = r0 + ry * 16 + i;
+    const int r = r0 + rq + i;
     int8_t d[12];
-    const double x = (c < C && r < R && !bad) ? X[(int64_t)r * ldx + c] : 0.0;
-    digits_of<12>(x, bad ? 0 : e, k, two, d);
+    const double x = r < R ? X[(int64_t)r * ldx + c] : 0.0;
+    digits_of<12>(x, e, k, two, d);
 #pragma unroll
-    for (int s = 0; s < 12; ++s) u[s].b[i] = s < k ? d[s] : 0;
+    for (int s = 0; s < 12; ++s) u[s][i >> 2] |= (uint32_t)(uint8_t)(s < k ? d[s] : 0) << (8 * (i & 3));
   }
-  for (int s = 0; s < k; ++s) *reinterpret_cast<i32x4*>(&tile[s][cx][ry * 16]) = u[s].v;
-  __syncthreads();
-  // write: thread -> (column cc = t / 4, 16-row chunk t % 4) per slice
-  const int cc = threadIdx.x >> 2, rq = (threadIdx.x & 3) * 16;
-  const int col = c0 + cc;
-  if (col >= C || (col < C && exps[col] == kNonFinite)) return;
-  for (int s = 0; s < k; ++s) {
-    int8_t* dst = out + (int64_t)s * ld_slice + (int64_t)col * ld_digit + r0 + rq;
-    const i32x4 v = *reinterpret_cast<const i32x4*>(&tile[s][cc][rq]);
-    const bool full = r0 + rq + 16 <= R && (((uintptr_t)dst) & 15) == 0;
-    if (full) {
-      *reinterpret_cast<i32x4*>(dst) = v;
-    } else {
-      union {
-        i32x4 v;
-        int8_t b[16];
-      } w;
-      w.v = v;
-      for (int i = 0; i < 16 && r0 + rq + i < R; ++i) dst[i] = w.b[i];
+  const bool full = r0 + rq + 16 <= R;
+#pragma unroll
+  for (int s = 0; s < 12; ++s) {
+    if (s < k) {
+      int8_t* dst = il ? out + (int64_t)c * ld_digit + (int64_t)(r0 >> 6) * 64 * k + s * 64 + rq
+                       : out + (int64_t)s * ld_slice + (int64_t)c * ld_digit + r0 + rq;
+      if (full && (((uintptr_t)dst) & 15) == 0) {
+        *reinterpret_cast<i32x4*>(dst) =
+            i32x4{(int)u[s][0], (int)u[s][1], (int)u[s][2], (int)u[s][3]};
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (r0 + rq + i < R) dst[i] = (int8_t)(u[s][i >> 2] >> (8 * (i & 3)));
+      }
     }
   }
 }
@@ -532,11 +534,21 @@ __device__ __forceinline__ int oz_slot(int r, int c) {
 // stages: 2 (double buffered, one workgroup per CU) or 1 (the load of step
 // s + 1 waits for every wave to finish step s; two workgroups per CU cover
 // each other's loads).
-template <int KS, int BK, int NB>
+// IL: the digits are in the interleaved layout of trnblas_hip_ozaki_split
+// (per_row bit 1; 8 slices): row r's 64-wide K chunk kc holds the 8 slices'
+// 64 bytes contiguously at r * ld + kc * 512 + s * 64. A load instruction
+// then covers two rows' 512 bytes (8 whole 128-byte lines, where the plain
+// layout's 64-byte row slices cost 16 half lines in the address path). The
+// operand stage is 32 such 1 KiB blocks, each followed by 16 bytes of pad,
+// and the odd row of a block keeps its 16-byte groups XOR 8: the 16 rows a
+// fragment read touches then fall on 16 distinct bank groups.
+template <int KS, int BK, int NB, bool IL = false>
 __global__ __launch_bounds__(256, NB == 1 ? 2 : 1) void oz_fast_kernel(OzArgs g) {
+  static_assert(!IL || (KS == 8 && BK == 64), "interleaved digits: 8 slices, 64-wide K chunks");
   constexpr int T = 64;
   constexpr int SL = T * BK;       // bytes per slice tile
-  constexpr int OP = KS * SL;      // bytes per operand stage
+  constexpr int IBLK = 1024 + 16;  // IL: LDS bytes per load instruction (two rows + pad)
+  constexpr int OP = IL ? 32 * IBLK : KS * SL;  // bytes per operand stage
   constexpr int STAGE = 2 * OP;
   constexpr int RPI = 1024 / BK;   // rows per 1 KiB load instruction
   constexpr int IPS = T / RPI;     // instructions per slice tile
@@ -562,8 +574,39 @@ __global__ __launch_bounds__(256, NB == 1 ? 2 : 1) void oz_fast_kernel(OzArgs g)
   const uint32_t voffB = n0 + r < g.N ? (uint32_t)(r * g.ldb + 16 * cg) : kOzOob;
   const int8_t* baseA = g.A + (int64_t)m0 * g.lda;
   const int8_t* baseB = g.B + (int64_t)n0 * g.ldb;
+  // IL: wave w loads the row pairs 8 w .. 8 w + 7 (rows 16 w .. 16 w + 15) of
+  // both operands; lane l carries row 2 q + l / 32, LDS group l % 32, i.e.
+  // the row's global group (l % 32) ^ (8 (l / 32)).
+  uint32_t ilA[IL ? 8 : 1], ilB[IL ? 8 : 1];
+  if constexpr (IL) {
+    const int d = lane >> 5, gl = 16 * ((lane & 31) ^ (8 * d));
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int rr = 16 * w + 2 * u + d;
+      ilA[u] = m0 + rr < g.M ? (uint32_t)(rr * g.lda + gl) : kOzOob;
+      ilB[u] = n0 + rr < g.N ? (uint32_t)(rr * g.ldb + gl) : kOzOob;
+    }
+  }
   auto load = [&](int step, int buf) {
     const int64_t koff = (int64_t)step * BK;
+    if constexpr (IL) {
+      // (operands as plain locals: array elements or locals of the resource
+      // type as builtin arguments fail to instantiate in the host pass of a
+      // kernel template)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        int8_t* dst = lds + buf * STAGE + (8 * w + u) * IBLK;
+        const uint32_t va = ilA[u], vb = ilB[u];
+        const int soff = step * 512;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(oz_rsrc(baseA),
+                                                 (__attribute__((address_space(3))) void*)dst, 16,
+                                                 va, soff, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(oz_rsrc(baseB),
+                                                 (__attribute__((address_space(3))) void*)(dst + OP),
+                                                 16, vb, soff, 0, 0);
+      }
+      return;
+    }
 #pragma unroll
     for (int sl = 0; sl < KS; ++sl)
       if (sl < k && sl % WPB == jw) {
@@ -647,16 +690,21 @@ __global__ __launch_bounds__(256, NB == 1 ? 2 : 1) void oz_fast_kernel(OzArgs g)
 #pragma unroll
       for (int ch = 0; ch < BK / 32; ++ch) {
         const int c = 2 * ch + (lane >> 5);
-        const int aoff = ar * BK + 16 * oz_slot<BK>(ar, c);
-        const int boff = OP + br * BK + 16 * oz_slot<BK>(br, c);
+        // byte of slice s2's group c of this lane's A / B row
+        auto fofs = [&](int row, int s2) {
+          if constexpr (IL)
+            return (row >> 1) * IBLK + (row & 1) * 512 + 16 * ((4 * s2 + c) ^ (8 * (row & 1)));
+          else
+            return s2 * SL + row * BK + 16 * oz_slot<BK>(row, c);
+        };
         i32x4 fa[KS];
 #pragma unroll
         for (int s2 = 0; s2 < KS; ++s2)
-          if (s2 < k) fa[s2] = *reinterpret_cast<const i32x4*>(buf + s2 * SL + aoff);
+          if (s2 < k) fa[s2] = *reinterpret_cast<const i32x4*>(buf + fofs(ar, s2));
 #pragma unroll
         for (int tt = 0; tt < KS; ++tt)
           if (tt < k) {
-            const i32x4 fb = *reinterpret_cast<const i32x4*>(buf + tt * SL + boff);
+            const i32x4 fb = *reinterpret_cast<const i32x4*>(buf + OP + fofs(br, tt));
 #pragma unroll
             for (int s2 = 0; s2 < KS - tt; ++s2)
               if (s2 + tt < k)
@@ -696,7 +744,7 @@ static int oz_launch(OzArgs& g, int out, hipStream_t s) {
 // (17.9 ms against 19.5 ms) than two stages and one workgroup per CU, whose
 // single wave per SIMD leaves every barrier and load wait exposed.
 constexpr int OZ_NB = 1;
-static int oz_fast_launch(OzArgs& g, hipStream_t s) {
+static int oz_fast_launch(OzArgs& g, hipStream_t s, bool il) {
   g.tiles_m = (g.M + 63) / 64;
   g.tiles_n = (g.N + 63) / 64;
   const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
@@ -705,6 +753,11 @@ static int oz_fast_launch(OzArgs& g, hipStream_t s) {
   const int64_t kflush = ((1ll << 31) - 1) / (4096ll * g.k);  // K terms per diagonal
   g.flush = (int)std::max<int64_t>(1, kflush / bk);
   const dim3 grid((unsigned)nt), block(256);
+  if (il) {
+    TRNBLAS_CHECK_ARG(g.k == 8, "ozaki_gemm(fast, interleaved): slices %d, need 8", g.k);
+    hipLaunchKernelGGL((oz_fast_kernel<8, 64, OZ_NB, true>), grid, block, 0, s, g);
+    return check_launch("ozaki_gemm(fast)");
+  }
   switch (g.k) {
 #define OZ_FAST(KS, BK) \
   case KS:              \
@@ -751,6 +804,10 @@ extern "C" int trnblas_hip_ozaki_split(int per_row, int64_t R, int64_t C, const 
                                        int32_t* scratch, void* stream) {
   clear_error();
   hipStream_t s = (hipStream_t)stream;
+  TRNBLAS_CHECK_ARG((per_row & ~3) == 0, "ozaki_split: per_row %d: bit 0 per row, bit 1 interleaved",
+                    per_row);
+  const int il = (per_row >> 1) & 1;
+  per_row &= 1;
   TRNBLAS_CHECK_ARG(slices >= 1 && slices <= 12, "ozaki_split: slices %d not in [1, 12]",
                     slices);
   TRNBLAS_CHECK_ARG(R >= 0 && C >= 0 && R < (1 << 30) && C < (1 << 30), "ozaki_split: bad size");
@@ -765,12 +822,20 @@ extern "C" int trnblas_hip_ozaki_split(int per_row, int64_t R, int64_t C, const 
     return check_launch("ozaki_split");
   }
   TRNBLAS_CHECK_ARG(X && digits && ldx >= C, "ozaki_split: bad X / digits");
+  if (il) {
+    const int64_t kd = per_row ? C : R;  // the K extent of the digits
+    TRNBLAS_CHECK_ARG(ld_digit >= (kd + 63) / 64 * 64 * slices && ld_digit % 16 == 0 &&
+                          ((uintptr_t)digits & 15) == 0,
+                      "ozaki_split: bad interleaved digit layout");
+  }
   if (per_row) {
-    TRNBLAS_CHECK_ARG(ld_digit >= C && ld_slice >= R * ld_digit, "ozaki_split: bad digit layout");
+    TRNBLAS_CHECK_ARG(il || (ld_digit >= C && ld_slice >= R * ld_digit),
+                      "ozaki_split: bad digit layout");
     hipLaunchKernelGGL(oz_emax_row_kernel, dim3((unsigned)R), dim3(256), 0, s, X, ldx, (int)R,
                        (int)C, exps);
   } else {
-    TRNBLAS_CHECK_ARG(ld_digit >= R && ld_slice >= C * ld_digit, "ozaki_split: bad digit layout");
+    TRNBLAS_CHECK_ARG(il || (ld_digit >= R && ld_slice >= C * ld_digit),
+                      "ozaki_split: bad digit layout");
     TRNBLAS_CHECK_ARG((R + kEmaxRows - 1) / kEmaxRows < 65536, "ozaki_split: too many rows");
     hipLaunchKernelGGL(oz_fill_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, s, exps,
                        (int)C, (int32_t)0x80000000);
@@ -789,13 +854,13 @@ extern "C" int trnblas_hip_ozaki_split(int per_row, int64_t R, int64_t C, const 
     TRNBLAS_CHECK_ARG(blocks < (1ll << 31), "ozaki_split: too large");
     hipLaunchKernelGGL(oz_digits_row_kernel, dim3((unsigned)blocks), dim3(256),
                        0, s, X, ldx, (int)R, (int)C, slices, (const int32_t*)exps,
-                       (const int32_t*)scratch, digits, ld_digit, ld_slice);
+                       (const int32_t*)scratch, digits, ld_digit, ld_slice, il);
   } else {
     TRNBLAS_CHECK_ARG((R + 63) / 64 < 65536, "ozaki_split: too many rows");
     hipLaunchKernelGGL(oz_digits_col_kernel,
                        dim3((unsigned)((C + 63) / 64), (unsigned)((R + 63) / 64)), dim3(256), 0,
                        s, X, ldx, (int)R, (int)C, slices, (const int32_t*)exps,
-                       (const int32_t*)scratch, digits, ld_digit, ld_slice);
+                       (const int32_t*)scratch, digits, ld_digit, ld_slice, il);
   }
   return check_launch("ozaki_split(digits)");
 }
@@ -806,10 +871,13 @@ extern "C" int trnblas_hip_ozaki_gemm(int mode, int slices, int64_t M, int64_t N
                                       int64_t ldb_slice, const int32_t* eA, const int32_t* eB,
                                       double* C, int64_t ldc_m, int64_t ldc_n, void* stream) {
   clear_error();
-  TRNBLAS_CHECK_ARG(mode == 0 || mode == 1, "ozaki_gemm: mode %d not supported", mode);
+  TRNBLAS_CHECK_ARG(mode >= 0 && mode <= 2, "ozaki_gemm: mode %d not supported", mode);
   if (M == 0 || N == 0) return TRNBLAS_OK;
   int rc = oz_check_operands(slices, M, N, Kp, kb, dA, lda, lda_slice, dB, ldb, ldb_slice);
   if (rc) return rc;
+  if (mode == 2)
+    TRNBLAS_CHECK_ARG(slices == 8 && lda >= 8 * Kp && ldb >= 8 * Kp,
+                      "ozaki_gemm: interleaved digits need 8 slices and rows of >= 8 Kp bytes");
   TRNBLAS_CHECK_ARG(Kp > 0, "ozaki_gemm: K == 0 (the caller returns zeros)");
   TRNBLAS_CHECK_ARG(C && eA && eB, "ozaki_gemm: NULL C / exponents");
   OzArgs g{};
@@ -829,7 +897,7 @@ extern "C" int trnblas_hip_ozaki_gemm(int mode, int slices, int64_t M, int64_t N
   g.C = C;
   g.ldc_m = ldc_m;
   g.ldc_n = ldc_n;
-  if (mode == 1) return oz_fast_launch(g, (hipStream_t)stream);
+  if (mode >= 1) return oz_fast_launch(g, (hipStream_t)stream, mode == 2);
   return oz_launch(g, 0, (hipStream_t)stream);
 }
 

@@ -334,12 +334,14 @@ def _round_up(n: int, m: int) -> int:
     return -(-n // m) * m
 
 
-def ozaki_split(X: torch.Tensor, slices: int, per: str):
+def ozaki_split(X: torch.Tensor, slices: int, per: str, interleaved: bool = False):
     """Digits and exponents of a device fp64 matrix X (R, C).
 
     per="row": digits (k, Rp, Cp) int8 with digit[s, r, c] (K = C contiguous);
     per="col": digits (k, Cp, Rp) int8 with digit[s, c, r] (K = R contiguous,
     the column split written transposed). Exponents int32 (R,) / (C,).
+    interleaved: digits (rows, Kp * k) instead, the k slices of each 64-wide
+    K chunk of a row side by side (the fast GEMM's 8-slice operand layout).
     Returns (digits, exps, nonfinite) where `nonfinite` is a 0-d int32 device
     flag (the digits are undefined when it is set)."""
     dev = _require_device(X)
@@ -351,12 +353,19 @@ def ozaki_split(X: torch.Tensor, slices: int, per: str):
     per_row = per == "row"
     rows, cols = (R, C) if per_row else (C, R)
     rp, cp = _round_up(max(rows, 1), OZ_ROW_PAD), _round_up(max(cols, 1), OZ_TILE)
-    digits = torch.zeros((slices, rp, cp), dtype=torch.int8, device=dev)
+    # the split writes every digit of the R x C matrix: only padding needs zeros
+    alloc = torch.empty if (rp, cp) == (rows, cols) else torch.zeros
+    if interleaved:
+        digits = alloc((rp, cp * slices), dtype=torch.int8, device=dev)
+        flags, ld_digit, ld_slice = int(per_row) | 2, cp * slices, 0
+    else:
+        digits = alloc((slices, rp, cp), dtype=torch.int8, device=dev)
+        flags, ld_digit, ld_slice = int(per_row), cp, rp * cp
     exps = torch.empty(rows, dtype=torch.int32, device=dev)
     scratch = torch.zeros(2, dtype=torch.int32, device=dev)
     call(
-        "trnblas_hip_ozaki_split", int(per_row), R, C, ptr(X), X.stride(0) if R else 1,
-        slices, ptr(digits), cp, rp * cp, ptr(exps), ptr(scratch), stream_of(dev),
+        "trnblas_hip_ozaki_split", flags, R, C, ptr(X), X.stride(0) if R else 1,
+        slices, ptr(digits), ld_digit, ld_slice, ptr(exps), ptr(scratch), stream_of(dev),
     )  # fmt: skip
     return digits, exps, scratch[1]
 
@@ -367,9 +376,19 @@ def ozaki_gemm(dA, eA, dB, eB, M: int, N: int, slices: int, kb: int | None = Non
     """fp64 C (M, N) from digit stacks dA (k, >=M, Kp), dB (k, >=N, Kp)
     (K-contiguous) and their exponents: the bit-exact schedule (fast=False,
     K blocks of kb) or the fast one (int32 diagonals, fp64 recombination; kb
-    unused). With transpose_out, writes C^T into `out` (N, M) instead."""
+    unused). 2-D dA / dB are interleaved digits (ozaki_split(interleaved=True),
+    8 slices, fast only). With transpose_out, writes C^T into `out` (N, M)
+    instead."""
     dev = _require_device(dA, dB, eA, eB)
-    k, _, Kp = dA.shape
+    interleaved = dA.dim() == 2
+    if interleaved:
+        if not fast or dB.dim() != 2:
+            raise ValueError("interleaved digits are for the fast schedule, both operands")
+        k, Kp = slices, dA.shape[1] // slices
+        mode, lda_s, ldb_s = 2, 0, 0
+    else:
+        k, _, Kp = dA.shape
+        mode, lda_s, ldb_s = (1 if fast else 0), dA.stride(0), dB.stride(0)
     kb = Kp if kb is None else kb
     if out is None:
         out = torch.empty((N, M) if transpose_out else (M, N), dtype=torch.float64, device=dev)
@@ -377,10 +396,10 @@ def ozaki_gemm(dA, eA, dB, eB, M: int, N: int, slices: int, kb: int | None = Non
         ldc_m, ldc_n = out.stride(1), out.stride(0)
     else:
         ldc_m, ldc_n = out.stride(0), out.stride(1)
+    lda, ldb = (dA.stride(0), dB.stride(0)) if interleaved else (dA.stride(1), dB.stride(1))
     _probed_call(
-        "ozaki_gemm", "trnblas_hip_ozaki_gemm", 1 if fast else 0, slices, M, N, Kp, kb, ptr(dA), dA.stride(1),
-        dA.stride(0), ptr(dB), dB.stride(1), dB.stride(0), ptr(eA), ptr(eB), ptr(out),
-        ldc_m, ldc_n, stream_of(dev),
+        "ozaki_gemm", "trnblas_hip_ozaki_gemm", mode, slices, M, N, Kp, kb, ptr(dA), lda,
+        lda_s, ptr(dB), ldb, ldb_s, ptr(eA), ptr(eB), ptr(out), ldc_m, ldc_n, stream_of(dev),
     )  # fmt: skip
     return out
 
