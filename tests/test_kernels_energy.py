@@ -2,6 +2,7 @@
 reduction kernel (C ABI via trnblas_amd.hip.kernels) against the fp64
 closed form of the oracle. Gate: relative 1e-6 (north star)."""
 
+import numpy as np
 import pytest
 import torch
 
@@ -164,3 +165,28 @@ def test_pair_energy_config3_shape_subset(dev, seed, math):
     got = float(kernels.pair_energy_sym(B.to(dev), eo.to(dev), ev.to(dev), math=math))
     want = pe.pair_energy_f64(B, eo, ev)
     assert abs(got - want) <= 1e-6 * abs(want), (got, want)
+
+
+@pytest.mark.parametrize("nocc,nvir,naux", [(5, 97, 130), (8, 200, 64), (1, 33, 40)])
+def test_pair_energy_bf16x6_implicit_walk_per_pair(dev, nocc, nvir, naux):
+    # the implicit walk runs two pairs (i, j), (i, j + 1) per workgroup; its
+    # per-pair energies (out_pairs, row-major i <= j) must match the
+    # explicit-pair kernel's, pair by pair (odd rows leave a single pair)
+    from trnblas_amd.hip import kernels
+
+    B, eo, ev = _inputs(nocc, nvir, naux, seed=nocc + nvir)
+    B, eo, ev = B.to(dev), eo.to(dev), ev.to(dev)
+    npairs = nocc * (nocc + 1) // 2
+    got = torch.empty(npairs, dtype=torch.float64, device=dev)
+    tot = torch.empty((), dtype=torch.float64, device=dev)
+    kernels._pe_launch(
+        "bf16x6", dev, nvir, naux, B, nocc, B.stride(0), B, 0, B.stride(0), B.stride(1),
+        eo, eo, ev, nocc, npairs, None, None, got, tot,
+    )  # fmt: skip
+    ii, jj = np.triu_indices(nocc)
+    want = kernels.pair_energies(B, B, eo, eo, ev, torch.from_numpy(ii), torch.from_numpy(jj), math="bf16x6")
+    torch.cuda.synchronize()
+    scale = float(want.abs().max()) + 1e-300
+    assert float((got - want).abs().max()) <= 1e-12 * scale
+    w = torch.where(torch.from_numpy(ii == jj).to(dev), 1.0, 2.0).double()
+    assert abs(float(tot) - float((w * want).sum())) <= 1e-12 * abs(float(tot))

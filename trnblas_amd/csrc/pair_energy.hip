@@ -377,21 +377,23 @@ __device__ __forceinline__ int x3_slot(int r, int grp) { return grp ^ (((r >> 1)
 // 128-byte line with the other row of its pair, and the three pieces of a
 // row pair's slice are 384 contiguous bytes, so a wave's 16-row load reads
 // 8 whole lines (half lines would cost the address path twice as much).
-// Columns [naux, ldv) are zero; the second row of the last pair of an odd
-// nvir is never written (and never read). One thread per 8 consecutive k of
-// a row; `total` = n * nvir * ldv / 8 threads.
+// Columns [naux, ldv) are zero, and so is the second row of the last pair
+// of an odd nvir. One thread per 8 consecutive k of a row (rows of the
+// padded 2 ceil(nvir / 2)); `total` = n * 2 ceil(nvir / 2) * ldv / 8 threads.
 template <bool VEC>
 __global__ __launch_bounds__(256) void split_planes_kernel(int nvir, int naux, int ldv, int total,
                                                           const float* X, int64_t ld_occ,
                                                           int64_t ld_vir, uint16_t* P) {
   const int idx = blockIdx.x * 256 + threadIdx.x;
   if (idx >= total) return;
-  const int gpr = ldv >> 3;
+  const int gpr = ldv >> 3, nv2 = (nvir + 1) & ~1;
   const int row = idx / gpr, k0 = (idx - row * gpr) * 8;
-  const int o = row / nvir, a = row - o * nvir;
+  const int o = row / nv2, a = row - o * nv2;
   const float* src = X + (int64_t)o * ld_occ + (int64_t)a * ld_vir + k0;
   f32x4 x0, x1;
-  if (VEC && k0 + 8 <= naux) {
+  if (a >= nvir) {
+    x0 = x1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  } else if (VEC && k0 + 8 <= naux) {
     x0 = *reinterpret_cast<const f32x4*>(src);
     x1 = *reinterpret_cast<const f32x4*>(src + 4);
   } else {
@@ -609,6 +611,236 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
   if (tid == 0) g.partial[(int64_t)p * g.nq + q] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+// Couples of the implicit walk: row i's pairs (i, j), j = i .. nocc - 1,
+// two at a time: couple c = (i, j0 = i + 2 h, j0 + 1) for h <
+// ceil((nocc - i) / 2); the second pair is absent when j0 + 1 == nocc. Rows
+// before i hold C(i) = sum_{t < i} ceil((nocc - t) / 2) = F(nocc + 1) -
+// F(nocc + 1 - i) couples, F(x) = sum_{u <= x} floor(u / 2).
+__device__ __forceinline__ int64_t half_floor_sum(int64_t x) {
+  const int64_t m = x >> 1;
+  return (x & 1) ? m * (m + 1) : m * m;
+}
+__host__ __device__ __forceinline__ int64_t pe_couples(int64_t n) {
+  const int64_t m = (n + 1) >> 1;  // F(n + 1)
+  return ((n + 1) & 1) ? m * (m + 1) : m * m;
+}
+__device__ __forceinline__ void couple_of(int c, int n, int& i, int& j0) {
+  auto before = [&](int r) { return half_floor_sum(n + 1) - half_floor_sum(n + 1 - r); };
+  const double nn = n + 1.0;
+  int r = (int)(nn - sqrt(fmax(0.0, nn * nn - 4.0 * (double)c)));
+  if (r < 0) r = 0;
+  if (r > n - 1) r = n - 1;
+  while (r > 0 && before(r) > c) --r;
+  while (r + 1 < n && before(r + 1) <= c) ++r;
+  i = r;
+  j0 = r + 2 * (c - (int)before(r));
+}
+
+// The implicit walk two pairs at a time: work item = (couple (i, j0, j1),
+// tile pair A <= B). Both pairs share B_i, so a k-step stages three 96-row
+// panels (54 KiB) for two 96 x 96 outputs where two single-pair workgroups
+// stage four: a quarter fewer operand bytes per product, which is what bounds
+// pair_energy_x3_kernel. 8 waves, one workgroup per CU: waves 4 g .. 4 g + 3
+// compute pair g of the couple, each the 48 x 48 quadrant (w & 1, w >> 1) as
+// in pair_energy_x3_kernel, with the same pieces, MFMA order, two-slice
+// partials and two-deep register pipeline. Stage slots: 0 = the shared panel
+// (B_i[A] in pass 0, B_i[B] in pass 1), 1 + g = pair g's (B_jg[B], then
+// B_jg[A]); a single-pair couple runs pair 0 twice and drops the copy.
+__global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
+  constexpr int S = kX3S, BK = kX3BK;
+  constexpr int SLOT = 3 * S * BK;  // bf16 elements of one panel slice, 3 pieces (9216)
+  constexpr int STAGE = 3 * SLOT;
+  constexpr int NQ = STAGE * 2 / 1024;  // 1 KiB load instructions per stage (54)
+  constexpr int NL = (NQ + 7) / 8;      // per wave (7; the 2 spare ones re-load, unstored)
+  static_assert(NQ == 54 && S == 96 && BK == 32, "stage split");
+  static_assert(2 * STAGE * 2 >= 2 * S * (S + 1) * 4, "diagonal epilogue fits");
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+  __shared__ double red[8];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int gp = w >> 2, qd = w & 3;
+  const int item = xcd_remap(blockIdx.x, gridDim.x);
+  const int c = item / g.nq, q = item - c * g.nq;
+  int i, j0;
+  couple_of(c, g.nocc, i, j0);
+  const bool two = j0 + 1 < g.nocc;
+  const int j1 = two ? j0 + 1 : j0;
+  int TA, TB;
+  tri_tiles(q, g.nb, TA, TB);
+  const bool diag = TA == TB;
+  const int a0 = TA * S, b0 = TB * S;
+  const int nvir = g.nvir, ldv = g.ldv;
+  const int nk = ldv / BK;  // even
+  const int nsteps = diag ? nk : 2 * nk;
+  const int64_t ostride = (int64_t)((nvir + 1) >> 1) * 6 * ldv;
+
+  // Load instruction qq = slot * 18 + piece * 6 + blk (rows 16 blk ..
+  // 16 blk + 15 of that slot's panel) fills stage offset qq KiB; wave w
+  // issues qq = w + 8 u. The lane offsets are those of pair_energy_x3_kernel
+  // (row-pair layout, one 128-byte line per 8 lanes) and do not depend on
+  // the panel; a panel's resource spans its valid row pairs only (the
+  // padding row of an odd nvir is zero), so rows past nvir read as zeros.
+  const int lr = lane >> 2;
+  uint32_t voff[NL];
+#pragma unroll
+  for (int u = 0; u < NL; ++u) {
+    const int qq = w + 8 * u < NQ ? w + 8 * u : w + 8 * u - 8;
+    const int e = qq % 18, pc = e / 6, r = 16 * (e - 6 * pc) + lr;
+    voff[u] = (uint32_t)(((r >> 1) * nk * 192 + pc * 64 + (r & 1) * 32 + 8 * x3_slot(r, lane & 3)) * 2);
+  }
+  // Panel (slot sl, pass ps): operand rows from rbase; its resource spans the
+  // valid row pairs only. Wave-uniform scalars, computed per load.
+  const int pairsA = min((nvir - a0 + 1) >> 1, S / 2), pairsB = min((nvir - b0 + 1) >> 1, S / 2);
+  const int64_t rowA = (int64_t)(a0 >> 1) * nk * 192, rowB = (int64_t)(b0 >> 1) * nk * 192;
+  i32x4 stg[2][NL];
+  auto load = [&](int t, i32x4(&set)[NL]) __attribute__((always_inline)) {
+    if (t >= nsteps) t = nsteps - 1;  // keeps every step at NL loads (exact wait counts)
+    const int ps = t >= nk ? 1 : 0, sl0 = ps ? t - nk : t;
+#pragma unroll
+    for (int u = 0; u < NL; ++u) {
+      const int qq = w + 8 * u < NQ ? w + 8 * u : w + 8 * u - 8;
+      const int sl = qq / 18;
+      const bool onA = (sl == 0) == (ps == 0);  // the panel's rows are the A tile's
+      // operand row i, j0 or j1 by arithmetic (a select chain becomes a table in memory)
+      const int o = i + (sl > 0) * (j0 - i) + (sl > 1) * (j1 - j0);
+      const uint16_t* base = g.Pi + o * ostride + (onA ? rowA : rowB);
+      const uint32_t v = voff[u];
+      const int soff = sl0 * 384;
+      set[u] = __builtin_amdgcn_raw_buffer_load_b128(
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0,
+                                            (onA ? pairsA : pairsB) * nk * 384, 0x00020000),
+          v, soff, 0);
+    }
+  };
+  auto store = [&](const i32x4(&set)[NL], int buf) __attribute__((always_inline)) {
+    uint16_t* dst = lds + buf * STAGE + w * 512 + lane * 8;
+#pragma unroll
+    for (int u = 0; u < NL; ++u)
+      if (w + 8 * u < NQ) *reinterpret_cast<i32x4*>(dst + u * 8 * 512) = set[u];
+  };
+
+  const int ar0 = 48 * (qd & 1), br0 = 48 * (qd >> 1);
+  const int fslot = 8 * x3_slot(lane & 15, lane >> 4);
+  f32x4 accX[3][3], accP[3][3], part[3][3];
+#pragma unroll
+  for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 3; ++cb) accX[rb][cb] = accP[rb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto step = [&](auto P_, auto FIRST_, int t) __attribute__((always_inline)) {
+    constexpr int P = decltype(P_)::value;
+    constexpr bool FIRST = decltype(FIRST_)::value;
+    __syncthreads();
+    load(t + 2, stg[P]);
+    const int ps = t >= nk ? 1 : 0;
+    const uint16_t* bufA = lds + P * STAGE + (ps ? 1 + gp : 0) * SLOT;
+    const uint16_t* bufB = lds + P * STAGE + (ps ? 0 : 1 + gp) * SLOT;
+    auto frag = [&](const uint16_t* b, int pc, int r) __attribute__((always_inline)) {
+      return *reinterpret_cast<const bf16x8*>(b + (pc * S + r) * BK + fslot);
+    };
+    bf16x8 fa[3][3];
+#pragma unroll
+    for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+      for (int pc = 0; pc < 3; ++pc) fa[rb][pc] = frag(bufA, pc, ar0 + 16 * rb + (lane & 15));
+#pragma unroll
+    for (int cb = 0; cb < 3; ++cb) {
+      bf16x8 fb[3];
+#pragma unroll
+      for (int pc = 0; pc < 3; ++pc) fb[pc] = frag(bufB, pc, br0 + 16 * cb + (lane & 15));
+#pragma unroll
+      for (int rb = 0; rb < 3; ++rb)
+        part[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            fa[rb][2], fb[0], FIRST ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb], 0, 0, 0);
+#pragma unroll
+      for (int e = 1; e < 6; ++e) {
+        constexpr int ka[6] = {2, 1, 0, 1, 0, 0}, kb[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll
+        for (int rb = 0; rb < 3; ++rb)
+          part[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[rb][ka[e]], fb[kb[e]],
+                                                                 part[rb][cb], 0, 0, 0);
+      }
+    }
+    if (t + 1 < nsteps) store(stg[1 - P], 1 - P);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using T = std::true_type;
+  using F = std::false_type;
+  auto run_pass = [&](f32x4(&acc)[3][3], int t0) __attribute__((always_inline)) {
+    for (int u = 0; u < nk; u += 2) {
+      step(I0(), T(), t0 + u);
+      step(I1(), F(), t0 + u + 1);
+#pragma unroll
+      for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 3; ++cb) acc[rb][cb] += part[rb][cb];
+    }
+  };
+
+  if (nsteps > 0) {
+    load(0, stg[0]);
+    load(1, stg[1]);
+    store(stg[0], 0);
+  }
+  run_pass(accX, 0);
+  if (!diag) run_pass(accP, nk);
+
+  // Lane l of a 16 x 16 block holds column l % 16 and rows 4 (l / 16) + r.
+  const int jg = gp ? j1 : j0;
+  const double eo = (double)g.eps_i[i] + (double)g.eps_j[jg];
+  double sum = 0.0;
+  if (!diag) {
+    // X and X' of one (a, b) sit in the same lane: the terms from registers
+#pragma unroll
+    for (int cb = 0; cb < 3; ++cb) {
+      const int b = b0 + br0 + 16 * cb + (lane & 15);
+      const double eb = b < nvir ? (double)g.eps_vir[b] : 0.0;
+#pragma unroll
+      for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int a = a0 + ar0 + 16 * rb + 4 * (lane >> 4) + r;
+          if (a < nvir && b < nvir) {
+            const double x = accX[rb][cb][r], xp = accP[rb][cb][r];
+            sum += 2.0 * (x * x + xp * xp - x * xp) / (eo - (double)g.eps_vir[a] - eb);
+          }
+        }
+    }
+  } else {
+    // diagonal tile: X^T through LDS, one 96 x 97 block per pair
+    __syncthreads();  // all fragment reads done before LDS is reused
+    float* xs = reinterpret_cast<float*>(lds) + gp * S * (S + 1);
+#pragma unroll
+    for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < 3; ++cb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          xs[(ar0 + 16 * rb + 4 * (lane >> 4) + r) * (S + 1) + br0 + 16 * cb + (lane & 15)] =
+              accX[rb][cb][r];
+    __syncthreads();
+    const int lt = tid & 255;
+#pragma unroll 4
+    for (int e = 0; e < S * S / 256; ++e) {
+      const int idx = lt + 256 * e, a = idx / S, b = idx - a * S;
+      if (a0 + a < nvir && a0 + b < nvir) {
+        const double x = xs[a * (S + 1) + b], xt = xs[b * (S + 1) + a];
+        sum += x * (2.0 * x - xt) /
+               (eo - (double)g.eps_vir[a0 + a] - (double)g.eps_vir[a0 + b]);
+      }
+    }
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) red[w] = sum;
+  __syncthreads();
+  if ((tid & 255) == 0 && (gp == 0 || two)) {
+    const int p = i * g.nocc - i * (i - 1) / 2 + (jg - i);
+    g.partial[(int64_t)p * g.nq + q] = (red[4 * gp] + red[4 * gp + 1]) + (red[4 * gp + 2] + red[4 * gp + 3]);
+  }
+}
+
 // MP2 energy of a precomputed amplitude block (the `mp2_energy` surface,
 // trnblas/nki/dispatch.py:4356-4491): one workgroup per (i, j) pair walks the
 // 32 x 32 tile pairs (A <= B) of T_ij, reading T[A,B] and T[B,A] once each
@@ -690,7 +922,7 @@ extern "C" size_t trnblas_hip_pair_energy_bf16x6_workspace(int64_t nvir, int64_t
 // Split n x nvir rows (o, a) of X into the pieces at P (split_planes_kernel).
 static void x3_split(const float* X, int64_t n, int64_t ld_occ, int64_t ld_vir, int nvir,
                      int naux, int ldv, uint16_t* P, hipStream_t s) {
-  const int64_t threads = n * nvir * (ldv / 8);
+  const int64_t threads = n * ((nvir + 1) & ~1) * (ldv / 8);
   if (threads == 0) return;
   const unsigned blocks = (unsigned)((threads + 255) / 256);
   const bool vec = (reinterpret_cast<uintptr_t>(X) & 15) == 0 && ld_occ % 4 == 0 &&
@@ -747,7 +979,7 @@ static int pair_energy_run(bool x3, const char* name, int64_t nvir, int64_t naux
                       "%s: nj == 0 shares Bi's pieces and needs Bj == Bi", name);
     TRNBLAS_CHECK_ARG((int64_t)kX3S * 3 * x3_ldv(naux) * 2 < 0x7fffff00ll,
                       "%s: naux too large for 32-bit panel offsets", name);
-    TRNBLAS_CHECK_ARG((ni > nj ? ni : nj) * nvir * (x3_ldv(naux) / 8) < (1ll << 31),
+    TRNBLAS_CHECK_ARG((ni > nj ? ni : nj) * (nvir + 1) * (x3_ldv(naux) / 8) < (1ll << 31),
                       "%s: operands too large for one split launch", name);
   }
   const size_t need = x3 ? trnblas_hip_pair_energy_bf16x6_workspace(nvir, naux, npairs, ni, nj)
@@ -794,7 +1026,14 @@ static int pair_energy_run(bool x3, const char* name, int64_t nvir, int64_t naux
     if (nj) x3_split(Bj, nj, ldj_occ, ld_vir, (int)nvir, (int)naux, ldv, Pj, s);
     int rc = check_launch(name);
     if (rc) return rc;
-    hipLaunchKernelGGL(pair_energy_x3_kernel, dim3((unsigned)items), dim3(256), 0, s, g);
+    if (pair_i == nullptr) {
+      // the implicit walk: two pairs sharing B_i per workgroup
+      const int64_t citems = pe_couples(nocc) * nq;
+      TRNBLAS_CHECK_ARG(citems < (1ll << 31), "%s: too many work items", name);
+      hipLaunchKernelGGL(pair_energy_x3c_kernel, dim3((unsigned)citems), dim3(512), 0, s, g);
+    } else {
+      hipLaunchKernelGGL(pair_energy_x3_kernel, dim3((unsigned)items), dim3(256), 0, s, g);
+    }
   } else {
     constexpr int NT = kPeS / 32 * 64;
     if (vec)
