@@ -116,32 +116,38 @@ def k_block(Kp: int, slices: int) -> int:
     return kbs[0][1]
 
 
-def split_device(X: torch.Tensor, slices: int, per: str, interleaved: bool = False):
+def split_device(X: torch.Tensor, slices: int, per: str, interleaved: bool = False,
+                 check: bool = True):
     """Device digits of `ozaki.split(X, slices, per, pad=(128, 128))`:
     int8 (k, rows, Kp) with K contiguous, where rows are X's rows (per="row")
     or columns (per="col"), and int32 exponents. interleaved: the same digits
     as (rows, Kp * k), the slices of each 64-wide K chunk side by side.
-    Raises OzakiNonFinite."""
+    check: raise OzakiNonFinite for a non-finite X (one device-to-host read);
+    otherwise return (digits, exps, flag) with the 0-d device flag, the
+    digits being undefined when it is set."""
     from .hip import kernels
 
     d, e, bad = kernels.ozaki_split(X, slices, per, interleaved)
+    if not check:
+        return d, e, bad
     if int(bad):  # one small device-to-host read
         raise OzakiNonFinite()
     return d, e
 
 
 def _digits_of(X: torch.Tensor, k: int, want: str, interleaved: bool = False):
-    """Digits for the operand role `want` ("rows of A" = per-row split of A,
-    "cols of B" = per-column split of B). A transposed view is split in its
-    own layout (as ozaki.split_a / split_b do), so no fp64 copy is made."""
+    """Digits, exponents and non-finite flag for the operand role `want`
+    ("rows of A" = per-row split of A, "cols of B" = per-column split of B).
+    A transposed view is split in its own layout (as ozaki.split_a / split_b
+    do), so no fp64 copy is made."""
     if want == "A":  # A (M, K): per row, digits (k, M, Kp)
         if X.mT.is_contiguous() and not X.is_contiguous():
-            return split_device(X.mT, k, "col", interleaved)  # A^T (K, M) by columns
-        return split_device(X.contiguous(), k, "row", interleaved)
+            return split_device(X.mT, k, "col", interleaved, False)  # A^T (K, M) by columns
+        return split_device(X.contiguous(), k, "row", interleaved, False)
     # B (K, N): per column, digits (k, N, Kp)
     if X.mT.is_contiguous() and not X.is_contiguous():
-        return split_device(X.mT, k, "row", interleaved)  # B^T (N, K) by rows
-    return split_device(X.contiguous(), k, "col", interleaved)
+        return split_device(X.mT, k, "row", interleaved, False)  # B^T (N, K) by rows
+    return split_device(X.contiguous(), k, "col", interleaved, False)
 
 
 MODES = ("fast", "exact")
@@ -185,12 +191,16 @@ def run_device(
     fast = mode == "fast"
     # the fast schedule reads 8-slice digits interleaved (whole cache lines)
     il = fast and k == 8
-    da, ea = _digits_of(A, k, "A", il)
-    db, eb = _digits_of(B, k, "B", il)
+    # the non-finite flags are read once, after the GEMM (no stall between the
+    # launches; a GEMM on undefined digits stays in bounds and is discarded)
+    da, ea, bad_a = _digits_of(A, k, "A", il)
+    db, eb, bad_b = _digits_of(B, k, "B", il)
     Kp = da.shape[1] // k if il else da.shape[2]
     kb = k_block(Kp, k) if mode == "exact" else Kp
     if N < SWAP_N and M > N:  # C^T = B^T A^T (ozaki.py:546-547): B's digits first
         kernels.ozaki_gemm(db, eb, da, ea, N, M, k, kb=kb, out=C, transpose_out=True, fast=fast)
     else:
         kernels.ozaki_gemm(da, ea, db, eb, M, N, k, kb=kb, out=C, fast=fast)
+    if int(bad_a | bad_b):  # one small device-to-host read
+        raise OzakiNonFinite()
     return C
