@@ -11,6 +11,8 @@ function citing the reference file:line it follows:
                        used to judge gemm_fp64 accuracy (tests/_ozaki_ref.py)
 * `oracle.pair_energy` the DF-MP2 pair-energy references
                        (trnblas/nki/dispatch.py, examples/df_mp2.py)
+* `oracle.metric`      trsm and the metric factor metric_inv_half
+                       (trnblas/level3.py, trnblas/nki/dispatch.py)
 
 Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of
 `bench.py` may import this package, and only as the checker (or, for

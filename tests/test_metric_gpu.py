@@ -1,0 +1,83 @@
+"""trsm / metric_inv_half on the MI355X (device-resident operands solve on
+the device in their own precision, float64 included) against
+oracle/metric.py. Gates: the residual max|J X X^T - I| (< 1e-10 in float64,
+< 1e-3 in float32; tests/test_conformance.py:1010-1018) and componentwise
+agreement with the float64 oracle."""
+
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+import trnblas_amd as tb
+from oracle import metric as om
+
+pytestmark = pytest.mark.gpu
+
+FLAGS = list(itertools.product(["left", "right"], ["upper", "lower"], [False, True], ["nonunit", "unit"]))
+
+
+@pytest.mark.parametrize("side,uplo,trans,diag", FLAGS)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_trsm_device_flags(dev, side, uplo, trans, diag, dtype):
+    g = torch.Generator().manual_seed(7)
+    n, m = 129, 33
+    # off-diagonal entries ~ 1/n keep the triangle well conditioned also for
+    # diag="unit" (N(0, 1) entries under a unit diagonal grow the solution
+    # exponentially in n)
+    A = torch.randn(n, n, generator=g, dtype=torch.float64) / n + 2 * torch.eye(n, dtype=torch.float64)
+    B = torch.randn((n, m) if side == "left" else (m, n), generator=g, dtype=torch.float64)
+    X = tb.trsm(1.25, A.to(dev, dtype), B.to(dev, dtype), side=side, uplo=uplo, trans=trans, diag=diag)
+    assert X.device.type == "cuda" and X.dtype == dtype and X.shape == B.shape
+    want = om.trsm_ref(1.25, A.numpy(), B.numpy(), side, uplo, trans, diag)
+    tol = 1e-12 if dtype == torch.float64 else 1e-4
+    assert np.abs(X.double().cpu().numpy() - want).max() <= tol * np.abs(want).max()
+
+
+def test_trsm_device_bf16_and_views(dev):
+    g = torch.Generator().manual_seed(8)
+    A = torch.randn(64, 64, generator=g, dtype=torch.float64) / 64 + 2 * torch.eye(64, dtype=torch.float64)
+    B = torch.randn(64, 16, generator=g, dtype=torch.float64)
+    want = om.trsm_ref(1.0, A.numpy(), B.numpy(), "left", "lower", True, "nonunit")
+    Ad = A.to(dev).mT.contiguous().mT  # transposed storage
+    X = tb.trsm(1.0, Ad, B.to(dev), uplo="lower", trans=True)
+    assert np.abs(X.cpu().numpy() - want).max() < 1e-12 * np.abs(want).max()
+    Xb = tb.trsm(1.0, A.to(dev, torch.bfloat16), B.to(dev, torch.bfloat16), uplo="lower", trans=True)
+    assert Xb.dtype == torch.bfloat16
+    assert np.abs(Xb.double().cpu().numpy() - want).max() < 3e-2 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("n", [1, 2, 127, 129, 1024])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_metric_inv_half_device(dev, n, dtype):
+    J = torch.from_numpy(om.spd(n, seed=60 + n))
+    X = tb.metric_inv_half(J.to(dev, dtype))
+    assert X.device.type == "cuda" and X.dtype == dtype
+    assert torch.equal(X, torch.triu(X))
+    Xd, Jd = X.double(), J.to(dev)
+    err = float((Jd @ Xd @ Xd.mT - torch.eye(n, dtype=torch.float64, device=dev)).abs().max())
+    assert err < (1e-3 if dtype == torch.float32 else 1e-10)
+    want = om.metric_inv_half_ref(J.numpy())
+    tol = 1e-12 if dtype == torch.float64 else 1e-4
+    assert np.abs(Xd.cpu().numpy() - want).max() <= tol * np.abs(want).max()
+
+
+def test_metric_inv_half_device_naux4096_fp64(dev):
+    # the DF metric size of configs 3/4 (naux <= 4096): float64 on the device
+    n = 4096
+    g = torch.Generator(device=dev).manual_seed(11)
+    S = torch.randn(n, n, generator=g, dtype=torch.float64, device=dev)
+    J = S @ S.mT / n + torch.eye(n, dtype=torch.float64, device=dev)
+    X = tb.metric_inv_half(J)
+    assert torch.equal(X, torch.triu(X))
+    err = float((J @ X @ X.mT - torch.eye(n, dtype=torch.float64, device=dev)).abs().max())
+    assert err < 1e-10, err
+
+
+def test_metric_inv_half_device_errors(dev):
+    with pytest.raises(torch.linalg.LinAlgError):
+        tb.metric_inv_half(-torch.eye(5, dtype=torch.float64, device=dev))
+    with pytest.raises(NotImplementedError):
+        tb.metric_inv_half(torch.eye(3, dtype=torch.int32, device=dev))
+    assert tb.metric_inv_half(torch.zeros(0, 0, device=dev)).shape == (0, 0)

@@ -1,7 +1,8 @@
 """trnblas_amd — the Level-3 hot path of trnsci/trnblas on AMD MI355X.
 
 A drop-in for `trnblas`'s Level-3 API on PyTorch-ROCm (`import trnblas_amd
-as trnblas`): `gemm`, `batched_gemm`, `syrk`, `gemm_fp64`, the DF-MP2 pair
+as trnblas`): `gemm`, `batched_gemm`, `syrk`, `gemm_fp64`, `trsm`,
+`metric_inv_half`, the DF-MP2 pair
 energy (`hip.nki_batched_pair_energy`), the backend switches and the
 `torch.ops.trnblas.*` op surface (`hip.get_native_ops()`). Device operands
 run hand-written gfx950 kernels from `libtrnblas_hip.so` (C ABI:
@@ -13,7 +14,7 @@ __version__ = "0.1.0"
 from . import hip  # noqa: F401
 from . import ozaki  # noqa: F401
 from .hip import get_autotune, get_backend, get_cores, set_autotune, set_backend, set_cores
-from .level3 import batched_gemm, gemm, gemm_fp64, syrk
+from .level3 import batched_gemm, gemm, gemm_fp64, metric_inv_half, syrk, trsm
 
 nki = hip  # the reference's subpackage name
 
@@ -29,6 +30,8 @@ __all__ = [
     "gemm_fp64",
     "batched_gemm",
     "syrk",
+    "trsm",
+    "metric_inv_half",
     "HAS_HIP",
     "HAS_NKI",
     "set_backend",

@@ -19,7 +19,9 @@ from .dispatch import (
     nki_gemm,
     nki_gemm_fp64,
     nki_mp2_energy,
+    nki_metric_inv_half,
     nki_syrk,
+    nki_trsm,
     set_autotune,
     set_backend,
 )
@@ -63,4 +65,6 @@ __all__ = [
     "nki_gemm_fp64",
     "nki_mp2_energy",
     "nki_syrk",
+    "nki_trsm",
+    "nki_metric_inv_half",
 ]

@@ -31,6 +31,7 @@ import warnings
 
 import torch
 
+from .._flags import diag_flag, side_flag, trans_flag, uplo_flag
 from . import _lib
 from ._lib import HipKernelError, HipLibraryError  # noqa: F401  (re-exported)
 
@@ -462,6 +463,78 @@ def gemm_scaled(alpha, a, b, beta, C):
 def _symmetrize(r: torch.Tensor) -> torch.Tensor:
     """0.5 * (r + r^T) (dispatch.py:3178-3199 values)."""
     return 0.5 * (r + r.mT)
+
+
+def _solve_dtype(*ts: torch.Tensor) -> torch.dtype:
+    """The arithmetic of a triangular solve / Cholesky: half types in fp32."""
+    dt = torch.promote_types(ts[0].dtype, ts[-1].dtype)
+    return torch.float32 if dt in (torch.bfloat16, torch.float16) else dt
+
+
+def nki_trsm(
+    A: torch.Tensor,
+    B: torch.Tensor,
+    side: str = "left",
+    uplo: str = "upper",
+    trans: bool = False,
+    diag: str = "nonunit",
+    alpha: float = 1.0,
+) -> torch.Tensor:
+    """Triangular solve with multiple right-hand sides: op(A) X = alpha B
+    (side "left") or X op(A) = alpha B (side "right"), op(A) = A or A^T.
+    Only the `uplo` triangle of A is read; diag "unit" takes its diagonal as
+    ones (the reference body, nki/dispatch.py:1707-1738). The reference's
+    device route is a blocked solve whose panels and updates it sends to
+    the host or its fp32 kernels (:1597-1704, Trainium has no fp64); on
+    MI355X a device-resident solve stays on the device in the operands' own
+    precision, float64 included (rocBLAS TRSM through
+    `torch.linalg.solve_triangular`); bf16 / fp16 solve in fp32 and return
+    in B's dtype, as the reference's host route does. Host operands solve on
+    the host. Differentiable in A and B (torch ops throughout)."""
+    side, uplo, diag = side_flag(side), uplo_flag(uplo), diag_flag(diag)
+    trans = trans_flag(trans)
+    if A.dim() != 2 or A.shape[0] != A.shape[1]:
+        raise ValueError(f"trsm: A must be square; got {tuple(A.shape)}")
+    n = A.shape[0]
+    need = B.shape[-2] if side == "left" else B.shape[-1]
+    if B.dim() < 2 or need != n:
+        raise ValueError(f"trsm: A {tuple(A.shape)} does not match B {tuple(B.shape)} for side={side!r}")
+    if not (A.is_floating_point() or A.is_complex()) or not (B.is_floating_point() or B.is_complex()):
+        raise NotImplementedError(f"trsm: expected floating point operands; got {A.dtype}, {B.dtype}")
+    cdt = _solve_dtype(A, B)
+    mat = A.mT if trans else A  # the uplo triangle of A is the other one of A^T
+    upper = (uplo == "upper") != trans
+    rhs = B.to(cdt) if alpha == 1.0 else alpha * B.to(cdt)
+    X = torch.linalg.solve_triangular(
+        mat.to(cdt), rhs, upper=upper, left=side == "left", unitriangular=diag == "unit"
+    )
+    return X.to(B.dtype)
+
+
+def nki_metric_inv_half(J: torch.Tensor) -> torch.Tensor:
+    """Cholesky inverse factor X = L^-T of an SPD metric J = L L^T, so
+    X X^T = J^-1 and `A @ X` is the density-fitting metric contraction
+    (nki/dispatch.py:1854-1905). On MI355X the Cholesky and the triangular
+    solve run on J's device in its precision (float64 native; half types in
+    fp32), where the reference sends device metrics to host LAPACK. The
+    result has J's dtype and device; X is exactly upper triangular."""
+    if not (J.is_floating_point() or J.is_complex()):
+        # every route of the reference raises for integer metrics (#86)
+        raise NotImplementedError(
+            f"metric_inv_half: expected a floating point or complex tensor; got {J.dtype}"
+        )
+    if J.dim() != 2 or J.shape[0] != J.shape[1]:
+        raise ValueError(f"metric_inv_half: J must be square; got {tuple(J.shape)}")
+    cdt = _solve_dtype(J)
+    L, info = torch.linalg.cholesky_ex(J.to(cdt))
+    if int(info) != 0:  # one small device-to-host read
+        raise torch.linalg.LinAlgError(
+            f"metric Cholesky failed: leading minor of order {int(info)} is not positive-definite"
+        )
+    eye = torch.eye(J.shape[0], dtype=cdt, device=J.device)
+    # L^-T: solve L^T X = I (the reference's trsm(L, I, uplo="lower", trans=True))
+    X = torch.linalg.solve_triangular(L.mT, eye, upper=True)
+    return X.to(J.dtype)
 
 
 def nki_syrk(A: torch.Tensor, symmetrize: bool = False) -> torch.Tensor:

@@ -1,4 +1,5 @@
-"""BLAS Level 3 on MI355X: gemm, batched_gemm, syrk, gemm_fp64.
+"""BLAS Level 3 on MI355X: gemm, batched_gemm, syrk, gemm_fp64, and the
+density-fitting metric stage trsm / metric_inv_half.
 
 Same signatures, flags and result semantics as trnblas/level3.py (drop-in):
 * `gemm` / `batched_gemm` (level3.py:69-134): C = alpha op(A) op(B) + beta C
@@ -7,7 +8,10 @@ Same signatures, flags and result semantics as trnblas/level3.py (drop-in):
   triangle of an n x n C referenced (the other-triangle fallback with a
   DeprecationWarning kept);
 * `gemm_fp64` (level3.py:137-193): fp64-class product by Ozaki splitting,
-  `slices` in [1, 12], float64 result on A's device.
+  `slices` in [1, 12], float64 result on A's device;
+* `trsm` / `metric_inv_half` (level3.py:332-380): triangular solve and the
+  Cholesky inverse factor L^-T, on the operands' device in their precision
+  (float64 native on the MI355X).
 
 On a ROCm GPU the operands run the gfx950 kernels of `libtrnblas_hip.so`
 with transposes read in place and the alpha / beta epilogue fused into the
@@ -20,7 +24,7 @@ import warnings
 
 import torch
 
-from ._flags import trans_flag, uplo_flag
+from ._flags import diag_flag, side_flag, trans_flag, uplo_flag
 from .hip import dispatch as _d
 
 
@@ -214,3 +218,36 @@ def _resolve_syrk_uplo(C: torch.Tensor, uplo: str) -> str:
         )
         return other
     return uplo
+
+
+def trsm(
+    alpha: float,
+    A: torch.Tensor,
+    B: torch.Tensor,
+    side: str = "left",
+    uplo: str = "upper",
+    trans: bool = False,
+    diag: str = "nonunit",
+) -> torch.Tensor:
+    """Triangular solve with multiple right-hand sides (level3.py:332-362):
+    op(A) @ X = alpha * B (side="left") or X @ op(A) = alpha * B
+    (side="right"), op(A) = A or A^T. Only the `uplo` triangle of A is
+    referenced; diag="unit" takes its diagonal as ones. Returns X with B's
+    dtype and device. For DF: J = L L^T, L X = (mu nu|P).
+
+    Device operands solve on the device in their own precision (float64
+    included); see `hip.dispatch.nki_trsm`.
+    """
+    side, uplo, diag = side_flag(side), uplo_flag(uplo), diag_flag(diag)
+    trans = trans_flag(trans)
+    return _d.nki_trsm(A, B, side=side, uplo=uplo, trans=trans, diag=diag, alpha=alpha)
+
+
+def metric_inv_half(J: torch.Tensor) -> torch.Tensor:
+    """Cholesky inverse factor of an SPD metric (level3.py:365-380):
+    X = L^-T where J = L @ L^T, so X @ X^T = J^-1 and `(ia|Q) @ X` is the
+    density-fitting contraction B_ia^P = sum_Q (ia|Q) [J^-1/2]_QP. X is upper
+    triangular, with J's dtype and device; a J that is not positive definite
+    raises torch.linalg.LinAlgError, an integer J NotImplementedError.
+    """
+    return _d.nki_metric_inv_half(J)
