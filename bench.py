@@ -17,7 +17,8 @@ recorded around every launch of the timed region on the launch stream.
 `extra` carries the other BASELINE configurations: C1 (2048^3 Aᵀ B parity
 and time), fp32 GEMM 8192^3 against peak, C3 (the fused DF-MP2 pair energy
 against the unfused GPU baseline, with its fp64 energy error), C5 (Ozaki
-gemm_fp64 8192^3 against native fp64 DGEMM).
+gemm_fp64 8192^3 against native fp64 DGEMM), and the metric stage
+(metric_inv_half and trsm at naux 4096 in fp64 against the host's LAPACK).
 """
 
 from __future__ import annotations
@@ -126,8 +127,8 @@ def cpu_baseline_level3(A, C, Ab, Bb, threads: int) -> dict:
 
 
 def run_extras(dev, tb, only=None) -> dict:
-    """The other BASELINE workloads (C1, fp32 8192^3, C3, C5); `only` selects
-    a subset by name."""
+    """The other BASELINE workloads (C1, fp32 8192^3, C3, C5) and the metric
+    stage; `only` selects a subset by name."""
     from trnblas_amd import df_mp2
     from trnblas_amd.hip import dispatch, kernels
 
@@ -240,6 +241,36 @@ def run_extras(dev, tb, only=None) -> dict:
             "tests/test_api_gpu.py::test_config5_gemm_fp64_accuracy_full_size, both modes",
         }  # fmt: skip
         log("c5", out["ozaki_gemm_fp64_c5_8192_k8"])
+    if only is None or "metric" in only:
+        # metric stage at C4's naux = 4096: J^-1/2 as the inverse Cholesky
+        # factor, and one trsm with naux right-hand sides, in fp64 on the
+        # device against the host's LAPACK
+        n = 4096
+        g = torch.Generator().manual_seed(7)
+        S = torch.randn(n, n, generator=g, dtype=torch.float64)
+        Jh = S @ S.T / n + torch.eye(n, dtype=torch.float64)
+        J = Jh.to(dev)
+        tm = gpu_time_ms(lambda: tb.metric_inv_half(J), reps=5, warm=2)
+        X = tb.metric_inv_half(J)
+        resid = float((X.T @ J @ X - torch.eye(n, device=dev, dtype=torch.float64)).abs().max())
+        L = torch.linalg.cholesky(J)
+        R = torch.randn(n, n, generator=g, dtype=torch.float64).to(dev)
+        tt = gpu_time_ms(lambda: tb.trsm(1.0, L, R, side="left", uplo="lower"), reps=5, warm=2)
+        Y = tb.trsm(1.0, L, R, side="left", uplo="lower")
+        tres = float(((L @ Y - R).abs().max() / R.abs().max()))
+        t0 = time.perf_counter()
+        Lh = torch.linalg.cholesky(Jh)
+        torch.linalg.solve_triangular(Lh.mT, torch.eye(n, dtype=torch.float64), upper=True)
+        cpu_ms = (time.perf_counter() - t0) * 1e3
+        fl = n**3 / 3 + n**3  # potrf + triangular solve against I (n right-hand sides)
+        out["metric_inv_half_fp64_4096"] = {
+            "ms": tm, "tflops": fl / tm / 1e9, "frac_fp64_peak": fl / tm / 1e9 / PEAK_FP64_MFMA,
+            "max_abs_XtJX_minus_I": resid, "trsm_4096x4096_ms": tt,
+            "trsm_tflops": n**3 / tt / 1e9, "trsm_rel_residual": tres,
+            "cpu_lapack_ms": cpu_ms, "cpu_threads": torch.get_num_threads(),
+        }  # fmt: skip
+        log("metric", out["metric_inv_half_fp64_4096"])
+        del J, L, R, X, Y
     return out
 
 
@@ -251,7 +282,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None,
-                    help="comma-separated subset of the extra workloads: c1,gemm8192,c3,c5")
+                    help="comma-separated subset of the extra workloads: c1,gemm8192,c3,c5,metric")
     ap.add_argument(
         "--calibrate-copy",
         action="store_true",

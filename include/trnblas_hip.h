@@ -208,8 +208,8 @@ int trnblas_hip_mp2_energy(int64_t ic, int64_t nocc, int64_t nvir, const float* 
  * per_row | 2: the interleaved layout of the fast 8-slice GEMM (mode 2 of
  *   trnblas_hip_ozaki_gemm): digit (s, row, kk) of the digit row `row` (r or
  *   c as above) and K index kk at
- *   digits[row*ld_digit + (kk/64)*64*slices + s*64 + kk%64], i.e. the slices
- *   of each 64-wide K chunk side by side; ld_digit >= round_up(K, 64) *
+ *   digits[row*ld_digit + (kk/32)*32*slices + s*32 + kk%32], i.e. the slices
+ *   of each 32-wide K chunk side by side; ld_digit >= round_up(K, 32) *
  *   slices and a multiple of 16, digits 16-byte aligned; ld_slice unused.
  * The digit buffer must be zero beyond the matrix (the caller pads to the
  * kernel's tile; entries beyond R x C are not written). exps (device int32,

@@ -93,7 +93,7 @@ def test_ozaki_hilo_bitwise(dev):
 @pytest.mark.parametrize("k", [3, 8])
 def test_split_interleaved_layout(dev, per, k):
     # the interleaved digits are the plain split's digits with the k slices
-    # of each 64-wide K chunk of a row side by side: (rows, Kp/64, k, 64)
+    # of each 32-wide K chunk of a row side by side: (rows, Kp/32, k, 32)
     from trnblas_amd.hip import kernels
 
     rng = np.random.default_rng(40 + k)
@@ -104,7 +104,7 @@ def test_split_interleaved_layout(dev, per, k):
     assert int(bad) == 0 and torch.equal(e, ei)
     _, rows, Kp = d.shape
     assert tuple(di.shape) == (rows, Kp * k)
-    got = di.cpu().numpy().reshape(rows, Kp // 64, k, 64).transpose(2, 0, 1, 3).reshape(k, rows, Kp)
+    got = di.cpu().numpy().reshape(rows, Kp // 32, k, 32).transpose(2, 0, 1, 3).reshape(k, rows, Kp)
     assert np.array_equal(got, d.cpu().numpy())
 
 

@@ -228,7 +228,7 @@ __global__ __launch_bounds__(256) void oz_digits_row_kernel(const double* X, int
     for (int s = 0; s < 12; ++s) u[s].b[i] = s < k ? d[s] : 0;
   }
   for (int s = 0; s < k; ++s) {
-    int8_t* dst = il ? out + r * ld_digit + (int64_t)(c0 >> 6) * 64 * k + s * 64 + (c0 & 63)
+    int8_t* dst = il ? out + r * ld_digit + (int64_t)(c0 >> 5) * 32 * k + s * 32 + (c0 & 31)
                      : out + (int64_t)s * ld_slice + r * ld_digit + c0;
     if (c0 + 4 <= C && ((uintptr_t)dst & 3) == 0) {
       *reinterpret_cast<int*>(dst) = u[s].w;
@@ -247,9 +247,9 @@ __global__ __launch_bounds__(256) void oz_digits_col_kernel(const double* X, int
                                                             int64_t ld_digit, int64_t ld_slice,
                                                             int il) {
   // Block: 64 columns x 64 rows of X. Thread t: column c0 + t / 4, rows
-  // r0 + 16 (t % 4) .. +15. Both digit layouts keep the 64 rows of one
-  // (slice, column) chunk as 64 contiguous bytes, so the 4 adjacent lanes of
-  // a column write one chunk with 16-byte stores (no transpose through LDS).
+  // r0 + 16 (t % 4) .. +15. Both digit layouts keep a thread's 16 rows of
+  // one (slice, column) as 16 contiguous, 16-byte aligned bytes, so each
+  // thread writes a slice with one 16-byte store (no transpose through LDS).
   const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
   const int c = c0 + (threadIdx.x >> 2), rq = (threadIdx.x & 3) * 16;
   if (c >= C) return;
@@ -276,8 +276,9 @@ __global__ __launch_bounds__(256) void oz_digits_col_kernel(const double* X, int
 #pragma unroll
   for (int s = 0; s < 12; ++s) {
     if (s < k) {
-      int8_t* dst = il ? out + (int64_t)c * ld_digit + (int64_t)(r0 >> 6) * 64 * k + s * 64 + rq
-                       : out + (int64_t)s * ld_slice + (int64_t)c * ld_digit + r0 + rq;
+      const int rr = r0 + rq;
+      int8_t* dst = il ? out + (int64_t)c * ld_digit + (int64_t)(rr >> 5) * 32 * k + s * 32 + (rr & 31)
+                       : out + (int64_t)s * ld_slice + (int64_t)c * ld_digit + rr;
       if (full && (((uintptr_t)dst) & 15) == 0) {
         *reinterpret_cast<i32x4*>(dst) =
             i32x4{(int)u[s][0], (int)u[s][1], (int)u[s][2], (int)u[s][3]};
@@ -534,21 +535,11 @@ __device__ __forceinline__ int oz_slot(int r, int c) {
 // stages: 2 (double buffered, one workgroup per CU) or 1 (the load of step
 // s + 1 waits for every wave to finish step s; two workgroups per CU cover
 // each other's loads).
-// IL: the digits are in the interleaved layout of trnblas_hip_ozaki_split
-// (per_row bit 1; 8 slices): row r's 64-wide K chunk kc holds the 8 slices'
-// 64 bytes contiguously at r * ld + kc * 512 + s * 64. A load instruction
-// then covers two rows' 512 bytes (8 whole 128-byte lines, where the plain
-// layout's 64-byte row slices cost 16 half lines in the address path). The
-// operand stage is 32 such 1 KiB blocks, each followed by 16 bytes of pad,
-// and the odd row of a block keeps its 16-byte groups XOR 8: the 16 rows a
-// fragment read touches then fall on 16 distinct bank groups.
-template <int KS, int BK, int NB, bool IL = false>
+template <int KS, int BK, int NB>
 __global__ __launch_bounds__(256, NB == 1 ? 2 : 1) void oz_fast_kernel(OzArgs g) {
-  static_assert(!IL || (KS == 8 && BK == 64), "interleaved digits: 8 slices, 64-wide K chunks");
   constexpr int T = 64;
   constexpr int SL = T * BK;       // bytes per slice tile
-  constexpr int IBLK = 1024 + 16;  // IL: LDS bytes per load instruction (two rows + pad)
-  constexpr int OP = IL ? 32 * IBLK : KS * SL;  // bytes per operand stage
+  constexpr int OP = KS * SL;      // bytes per operand stage
   constexpr int STAGE = 2 * OP;
   constexpr int RPI = 1024 / BK;   // rows per 1 KiB load instruction
   constexpr int IPS = T / RPI;     // instructions per slice tile
@@ -574,39 +565,8 @@ __global__ __launch_bounds__(256, NB == 1 ? 2 : 1) void oz_fast_kernel(OzArgs g)
   const uint32_t voffB = n0 + r < g.N ? (uint32_t)(r * g.ldb + 16 * cg) : kOzOob;
   const int8_t* baseA = g.A + (int64_t)m0 * g.lda;
   const int8_t* baseB = g.B + (int64_t)n0 * g.ldb;
-  // IL: wave w loads the row pairs 8 w .. 8 w + 7 (rows 16 w .. 16 w + 15) of
-  // both operands; lane l carries row 2 q + l / 32, LDS group l % 32, i.e.
-  // the row's global group (l % 32) ^ (8 (l / 32)).
-  uint32_t ilA[IL ? 8 : 1], ilB[IL ? 8 : 1];
-  if constexpr (IL) {
-    const int d = lane >> 5, gl = 16 * ((lane & 31) ^ (8 * d));
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int rr = 16 * w + 2 * u + d;
-      ilA[u] = m0 + rr < g.M ? (uint32_t)(rr * g.lda + gl) : kOzOob;
-      ilB[u] = n0 + rr < g.N ? (uint32_t)(rr * g.ldb + gl) : kOzOob;
-    }
-  }
   auto load = [&](int step, int buf) {
     const int64_t koff = (int64_t)step * BK;
-    if constexpr (IL) {
-      // (operands as plain locals: array elements or locals of the resource
-      // type as builtin arguments fail to instantiate in the host pass of a
-      // kernel template)
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        int8_t* dst = lds + buf * STAGE + (8 * w + u) * IBLK;
-        const uint32_t va = ilA[u], vb = ilB[u];
-        const int soff = step * 512;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(oz_rsrc(baseA),
-                                                 (__attribute__((address_space(3))) void*)dst, 16,
-                                                 va, soff, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(oz_rsrc(baseB),
-                                                 (__attribute__((address_space(3))) void*)(dst + OP),
-                                                 16, vb, soff, 0, 0);
-      }
-      return;
-    }
 #pragma unroll
     for (int sl = 0; sl < KS; ++sl)
       if (sl < k && sl % WPB == jw) {
@@ -691,12 +651,7 @@ __global__ __launch_bounds__(256, NB == 1 ? 2 : 1) void oz_fast_kernel(OzArgs g)
       for (int ch = 0; ch < BK / 32; ++ch) {
         const int c = 2 * ch + (lane >> 5);
         // byte of slice s2's group c of this lane's A / B row
-        auto fofs = [&](int row, int s2) {
-          if constexpr (IL)
-            return (row >> 1) * IBLK + (row & 1) * 512 + 16 * ((4 * s2 + c) ^ (8 * (row & 1)));
-          else
-            return s2 * SL + row * BK + 16 * oz_slot<BK>(row, c);
-        };
+        auto fofs = [&](int row, int s2) { return s2 * SL + row * BK + 16 * oz_slot<BK>(row, c); };
         i32x4 fa[KS];
 #pragma unroll
         for (int s2 = 0; s2 < KS; ++s2)
@@ -716,6 +671,159 @@ __global__ __launch_bounds__(256, NB == 1 ? 2 : 1) void oz_fast_kernel(OzArgs g)
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
       }
+    }
+    flush(s0 == 0);
+  }
+  if (nsteps == 0) flush(true);
+}
+
+// Fast mode on interleaved 8-slice digits (trnblas_hip_ozaki_split, per_row
+// bit 1): row r's 32-wide K chunk kc holds the 8 slices' 32 bytes
+// contiguously at r * ld + kc * 256 + s * 32, so one k-step of a row is 256
+// contiguous bytes (two whole cache lines) and a 1 KiB load instruction
+// covers 4 rows.
+//
+// TM x 64 output tile per workgroup, (TM / 32) x 2 waves with one 32 x 32
+// MFMA block and 8 int32 diagonal accumulators each (as oz_fast_kernel).
+// K steps of 32 through two LDS stages. A step reads every fragment it needs
+// into registers first (8 A and 8 B slices, 64 VGPRs) and only then issues
+// the DMA of the next step into the other stage, so no LDS read is ordered
+// after an outstanding LDS DMA (which would make it wait for all of them),
+// and the DMA lands while the 36 MFMAs of the step run. A stage is
+// reusable once every wave has passed the next step's barrier: its reads
+// fed that wave's MFMAs of the previous step.
+//
+// LDS: 4 rows per 1040-byte block (1024 bytes + 16 pad); row m = r % 4 of a
+// block keeps its 16-byte groups XOR 4 m, so the 16 consecutive rows of one
+// fragment read (same group) fall on 16 distinct bank groups. Lane l of a
+// load instruction fills LDS slot l (row l / 16, group l % 16), i.e. loads
+// the row's global group (l % 16) ^ (4 (l / 16)): each row's 16 lanes still
+// cover its 256 bytes exactly.
+template <int TM>
+__global__ __launch_bounds__(TM * 4, TM == 64 ? 2 : 1) void oz_fast_il_kernel(OzArgs g) {
+  constexpr int TN = 64;
+  constexpr int WM = TM / 32;                      // waves along M (2 along N)
+  constexpr int W = 2 * WM;                        // waves
+  constexpr int BLK = 1024 + 16;                   // LDS bytes per load instruction
+  constexpr int OPA = TM / 4 * BLK, OPB = TN / 4 * BLK;
+  constexpr int STAGE = OPA + OPB;
+  constexpr int LA = TM / 4 / W, LB = TN / 4 / W;  // instructions per wave and step
+  static_assert(LA >= 1 && LB >= 1 && LA * W * 4 == TM && LB * W * 4 == TN, "load split");
+  __shared__ __attribute__((aligned(16))) int8_t lds[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  int tm, tn;
+  grouped_tile(t, g.tiles_m, g.tiles_n, 8, tm, tn);
+  const int m0 = tm * TM, n0 = tn * TN;
+  const int nsteps = g.Kp / 32;
+
+  // load offsets: wave w fills A blocks w LA .. +LA-1 and B blocks
+  // w LB .. +LB-1 (block b = rows 4 b .. 4 b + 3)
+  const int gl = 16 * ((lane & 15) ^ (4 * (lane >> 4)));
+  uint32_t ilA[LA], ilB[LB];
+#pragma unroll
+  for (int u = 0; u < LA; ++u) {
+    const int rr = 4 * (w * LA + u) + (lane >> 4);
+    ilA[u] = m0 + rr < g.M ? (uint32_t)(rr * g.lda + gl) : kOzOob;
+  }
+#pragma unroll
+  for (int u = 0; u < LB; ++u) {
+    const int rr = 4 * (w * LB + u) + (lane >> 4);
+    ilB[u] = n0 + rr < g.N ? (uint32_t)(rr * g.ldb + gl) : kOzOob;
+  }
+  const int8_t* baseA = g.A + (int64_t)m0 * g.lda;
+  const int8_t* baseB = g.B + (int64_t)n0 * g.ldb;
+  auto load = [&](int step, int buf) {
+    // (operands as plain locals: array elements or locals of the resource
+    // type as builtin arguments fail to instantiate in the host pass of a
+    // kernel template)
+    const int soff = step * 256;
+#pragma unroll
+    for (int u = 0; u < LA; ++u) {
+      int8_t* dst = lds + buf * STAGE + (w * LA + u) * BLK;
+      const uint32_t va = ilA[u];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(oz_rsrc(baseA),
+                                               (__attribute__((address_space(3))) void*)dst, 16,
+                                               va, soff, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < LB; ++u) {
+      int8_t* dst = lds + buf * STAGE + OPA + (w * LB + u) * BLK;
+      const uint32_t vb = ilB[u];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(oz_rsrc(baseB),
+                                               (__attribute__((address_space(3))) void*)dst, 16,
+                                               vb, soff, 0, 0);
+    }
+  };
+
+  // Wave w: rows 32 (w % WM), columns 32 (w / WM) of the tile. Lane l reads
+  // row l % 32 of its block, bytes 16 (l / 32) .. +15 of each slice's 32.
+  const int wm = w % WM, wn = w / WM;
+  const int ar = 32 * wm + (lane & 31), br = 32 * wn + (lane & 31);
+  const int h = lane >> 5;
+  const int rowA = (ar >> 2) * BLK + (ar & 3) * 256, xa = 4 * (ar & 3);
+  const int rowB = OPA + (br >> 2) * BLK + (br & 3) * 256, xb = 4 * (br & 3);
+  i32x16 acc[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[d][e] = 0;
+
+  // Lane l of a 32x32 block: column l % 32, rows 8 (e/4) + 4 (l/32) + e % 4.
+  constexpr int k = 8;
+  const int off = -2 * (kSliceBits - 1) - kSliceBits * (k - 1);
+  const int n = n0 + 32 * wn + (lane & 31);
+  const int eb = n < g.N ? g.eB[n] : 0;
+  auto flush = [&](bool first) {
+    double v[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      v[e] = 0.0;
+#pragma unroll
+      for (int d = k - 1; d >= 0; --d) v[e] += (double)acc[d][e] * pow2(kSliceBits * (k - 1 - d));
+    }
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[d][e] = 0;
+#pragma unroll 4
+    for (int e = 0; e < 16; ++e) {
+      const int m = m0 + 32 * wm + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+      if (m >= g.M || n >= g.N) continue;
+      const int ea = g.eA[m] + off;
+      double cv;
+      if (ea < 900 && ea > -900 && eb < 900 && eb > -900)
+        cv = (v[e] * pow2(ea)) * pow2(eb);
+      else
+        cv = ldexp(v[e], ea + eb);
+      double* dst = g.C + (int64_t)m * g.ldc_m + (int64_t)n * g.ldc_n;
+      *dst = first ? cv : *dst + cv;
+    }
+  };
+
+  for (int s0 = 0; s0 < nsteps; s0 += g.flush) {
+    const int s1 = s0 + g.flush < nsteps ? s0 + g.flush : nsteps;
+    if (s0 > 0) __syncthreads();  // every wave is done with the previous block's stages
+    load(s0, 0);
+    for (int s = s0; s < s1; ++s) {
+      const int cur = (s - s0) & 1;
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA of step s has landed
+      __syncthreads();                // every wave's has; stage cur ^ 1 is free
+      const int8_t* buf = lds + cur * STAGE;
+      i32x4 fa[8], fb[8];
+#pragma unroll
+      for (int s2 = 0; s2 < 8; ++s2) {
+        fa[s2] = *reinterpret_cast<const i32x4*>(buf + rowA + 16 * (((2 * s2) ^ xa) | h));
+        fb[s2] = *reinterpret_cast<const i32x4*>(buf + rowB + 16 * (((2 * s2) ^ xb) | h));
+      }
+      if (s + 1 < s1) load(s + 1, cur ^ 1);
+#pragma unroll
+      for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+        for (int s2 = 0; s2 < 8 - tt; ++s2)
+          acc[s2 + tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s2], fb[tt], acc[s2 + tt], 0, 0, 0);
     }
     flush(s0 == 0);
   }
@@ -745,19 +853,28 @@ static int oz_launch(OzArgs& g, int out, hipStream_t s) {
 // single wave per SIMD leaves every barrier and load wait exposed.
 constexpr int OZ_NB = 1;
 static int oz_fast_launch(OzArgs& g, hipStream_t s, bool il) {
+  const int64_t kflush = ((1ll << 31) - 1) / (4096ll * g.k);  // K terms per diagonal
+  if (il) {
+    TRNBLAS_CHECK_ARG(g.k == 8, "ozaki_gemm(fast, interleaved): slices %d, need 8", g.k);
+    // 64 x 64 tiles, two workgroups per CU: measured faster at C5 (the
+    // 8192^3 call 14.2 ms against 15.0 ms) than 128 x 64 tiles with one 8-wave
+    // workgroup per CU, whose barriers stall every wave on the CU at once
+    constexpr int tmr = 64;
+    g.tiles_m = (g.M + tmr - 1) / tmr;
+    g.tiles_n = (g.N + 63) / 64;
+    const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
+    TRNBLAS_CHECK_ARG(nt < (1ll << 31), "ozaki: too many tiles");
+    g.flush = (int)std::max<int64_t>(1, kflush / 32);
+    hipLaunchKernelGGL((oz_fast_il_kernel<tmr>), dim3((unsigned)nt), dim3(4 * tmr), 0, s, g);
+    return check_launch("ozaki_gemm(fast)");
+  }
   g.tiles_m = (g.M + 63) / 64;
   g.tiles_n = (g.N + 63) / 64;
   const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
   TRNBLAS_CHECK_ARG(nt < (1ll << 31), "ozaki: too many tiles");
   const int bk = g.k <= 8 ? 64 : 32;
-  const int64_t kflush = ((1ll << 31) - 1) / (4096ll * g.k);  // K terms per diagonal
   g.flush = (int)std::max<int64_t>(1, kflush / bk);
   const dim3 grid((unsigned)nt), block(256);
-  if (il) {
-    TRNBLAS_CHECK_ARG(g.k == 8, "ozaki_gemm(fast, interleaved): slices %d, need 8", g.k);
-    hipLaunchKernelGGL((oz_fast_kernel<8, 64, OZ_NB, true>), grid, block, 0, s, g);
-    return check_launch("ozaki_gemm(fast)");
-  }
   switch (g.k) {
 #define OZ_FAST(KS, BK) \
   case KS:              \
@@ -824,7 +941,7 @@ extern "C" int trnblas_hip_ozaki_split(int per_row, int64_t R, int64_t C, const 
   TRNBLAS_CHECK_ARG(X && digits && ldx >= C, "ozaki_split: bad X / digits");
   if (il) {
     const int64_t kd = per_row ? C : R;  // the K extent of the digits
-    TRNBLAS_CHECK_ARG(ld_digit >= (kd + 63) / 64 * 64 * slices && ld_digit % 16 == 0 &&
+    TRNBLAS_CHECK_ARG(ld_digit >= (kd + 31) / 32 * 32 * slices && ld_digit % 16 == 0 &&
                           ((uintptr_t)digits & 15) == 0,
                       "ozaki_split: bad interleaved digit layout");
   }

@@ -340,7 +340,7 @@ def ozaki_split(X: torch.Tensor, slices: int, per: str, interleaved: bool = Fals
     per="row": digits (k, Rp, Cp) int8 with digit[s, r, c] (K = C contiguous);
     per="col": digits (k, Cp, Rp) int8 with digit[s, c, r] (K = R contiguous,
     the column split written transposed). Exponents int32 (R,) / (C,).
-    interleaved: digits (rows, Kp * k) instead, the k slices of each 64-wide
+    interleaved: digits (rows, Kp * k) instead, the k slices of each 32-wide
     K chunk of a row side by side (the fast GEMM's 8-slice operand layout).
     Returns (digits, exps, nonfinite) where `nonfinite` is a 0-d int32 device
     flag (the digits are undefined when it is set)."""

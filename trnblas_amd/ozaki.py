@@ -121,7 +121,7 @@ def split_device(X: torch.Tensor, slices: int, per: str, interleaved: bool = Fal
     """Device digits of `ozaki.split(X, slices, per, pad=(128, 128))`:
     int8 (k, rows, Kp) with K contiguous, where rows are X's rows (per="row")
     or columns (per="col"), and int32 exponents. interleaved: the same digits
-    as (rows, Kp * k), the slices of each 64-wide K chunk side by side.
+    as (rows, Kp * k), the slices of each 32-wide K chunk side by side.
     check: raise OzakiNonFinite for a non-finite X (one device-to-host read);
     otherwise return (digits, exps, flag) with the 0-d device flag, the
     digits being undefined when it is set."""
