@@ -331,7 +331,7 @@ def main():
     syrk_ms = probe.mean_ms()
     achieved = SYRK_FLOP / (syrk_ms * 1e-3) / 1e12
     roofline = {
-        "kernel": "gemm_kernel<float,...,SYRK> (trnblas_hip_syrk)",
+        "kernel": "gemm_f32_dma_kernel<true, true, SYRK> (trnblas_hip_syrk)",
         "bound": "mfma",
         "achieved": achieved,
         "peak": PEAK_FP32_MFMA,

@@ -9,9 +9,10 @@
 //  * a 256-thread workgroup (4 wave64s) owns a 128x128 tile of D; each wave a
 //    64x64 sub-tile as 2x2 MFMA 32x32 blocks with the accumulators in
 //    AGPR/VGPRs;
-//  * operand panels are staged in LDS, double buffered: the global loads of
-//    k-tile t+1 are in flight while the MFMAs of k-tile t run, one barrier
-//    per k-tile;
+//  * operand panels are staged in LDS, double buffered: the loads of k-tile
+//    t+1 are in flight while the MFMAs of k-tile t run, one barrier per
+//    k-tile (fp32 on 16-byte aligned operands: direct-to-LDS DMA,
+//    gemm_f32_dma_kernel; otherwise through registers, gemm_kernel);
 //  * an operand whose K dimension is contiguous in HBM is kept K-contiguous
 //    in LDS (rows padded by 16 bytes, so each 16-byte fragment read is
 //    bank-conflict free); one whose M / N dimension is contiguous (a
@@ -189,6 +190,41 @@ __device__ __forceinline__ int64_t sk_start(int w, int64_t total, int groups) {
   return (int64_t)w * total / groups;
 }
 
+// Epilogue of one segment: alpha / beta into D (slot < 0, whole tile) or the
+// raw partial into workspace slot `slot` of workgroup w (stream-K).
+// Lane l of an MFMA 32x32 block holds column l % 32 and rows
+// 8 (r / 4) + 4 (l / 32) + r % 4 of its 16 registers r.
+template <typename T, bool SYRK, int FM, int FN, int BM, int BN>
+__device__ __forceinline__ void store_tile(const GemmArgs& g, const f32x16 (&acc)[FM][FN], int bat,
+                                           int m0, int n0, int wm0, int wn0, int lane, int slot,
+                                           int w) {
+  if (slot < 0) {
+    const T* C = static_cast<const T*>(g.C) + (g.C ? bat * g.sC : 0);
+    T* D = static_cast<T*>(g.D) + bat * g.sD;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int mb = m0 + wm0 + i * 32 + (lane >> 5) * 4;
+        const int n = n0 + wn0 + j * 32 + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          store_out<T, SYRK>(g, C, D, mb + (r >> 2) * 8 + (r & 3), n, acc[i][j][r]);
+      }
+  } else {
+    float* P = g.ws + ((int64_t)w * 2 + slot) * (BM * BN);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int mb = wm0 + i * 32 + (lane >> 5) * 4;
+        const int n = wn0 + j * 32 + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) P[(mb + (r >> 2) * 8 + (r & 3)) * BN + n] = acc[i][j][r];
+      }
+  }
+}
+
 // Each workgroup computes whole tiles (data-parallel: one tile per
 // workgroup) or, under stream-K, a contiguous range of the k-iterations of
 // all tiles: whole tiles it covers get the epilogue directly, the partial
@@ -315,33 +351,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1)
       }
     }
 
-    // Lane l of an MFMA 32x32 block holds column l % 32 and rows
-    // 8 (r / 4) + 4 (l / 32) + r % 4 of its 16 registers r.
-    if (slot < 0) {
-      const T* C = static_cast<const T*>(g.C) + (g.C ? bat * g.sC : 0);
-      T* D = static_cast<T*>(g.D) + bat * g.sD;
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int mb = m0 + wm0 + i * 32 + (lane >> 5) * 4;
-          const int n = n0 + wn0 + j * 32 + (lane & 31);
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            store_out<T, SYRK>(g, C, D, mb + (r >> 2) * 8 + (r & 3), n, acc[i][j][r]);
-        }
-    } else {
-      float* P = g.ws + ((int64_t)w * 2 + slot) * (BM * BN);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int mb = wm0 + i * 32 + (lane >> 5) * 4;
-          const int n = wn0 + j * 32 + (lane & 31);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) P[(mb + (r >> 2) * 8 + (r & 3)) * BN + n] = acc[i][j][r];
-        }
-    }
+    store_tile<T, SYRK, FM, FN, BM, BN>(g, acc, bat, m0, n0, wm0, wn0, lane, slot, w);
   };
 
   if (g.sk_groups == 0) {
@@ -362,6 +372,187 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1)
     const bool whole = kb0 == 0 && kb1 == nk;
     segment(g.dp_tiles + tt, kb0, kb1, whole ? -1 : (x == x0 ? 0 : 1), w);
     x += kb1 - kb0;
+  }
+}
+
+// fp32 GEMM / SYRK on 16-byte aligned operands: the tile, wave split, MFMA
+// (v_mfma_f32_32x32x2_f32) and k order of gemm_kernel, with the operand
+// panels moved by LDS DMA (buffer_load_dwordx4 ... lds) instead of through
+// registers. 32-wide k-tiles in two LDS stages; after the barrier that
+// publishes k-tile t every wave reads all its fragments of k-tile t, then
+// issues the DMA of k-tile t + 1 into the other stage, which lands behind
+// k-tile t's MFMAs: one barrier per k-tile, no staging registers and no LDS
+// stores. (The compiler makes an LDS read that follows an outstanding LDS
+// DMA wait for it, so no read may follow the DMA inside a k-tile.)
+//
+// The panels have no row padding; their 16-byte groups are XOR-swizzled, so
+// a 1 KiB DMA block (lane l writes bytes 16 l .. 16 l + 15) is a set of
+// whole rows and the fragment reads are bank-conflict free:
+//  * K-contiguous panel, 128 rows of 32 k (128 bytes): group q of row r sits
+//    in slot q ^ ((r >> 1) & 7); a DMA block is 8 rows;
+//  * M/N-contiguous panel, 32 rows k of 128 columns (512 bytes): group q of
+//    row k sits in slot q ^ (8 ((k >> 2) & 1)); a DMA block is 2 rows.
+// Lane l of a DMA block loads the global group that belongs in its slot
+// (the swizzles are their own inverses), so each row's lanes still read the
+// row's bytes exactly once. Ragged edges: a group outside the matrix gets
+// an offset past the buffer's records and reads as zeros (VEC operands:
+// every 16-byte group is wholly inside or outside).
+template <bool AKC, bool BKC, bool SYRK>
+__global__ __launch_bounds__(256, 2) void gemm_f32_dma_kernel(GemmArgs g) {
+  constexpr int BM = 128, BN = 128, BK = 32, WM = 64, WN = 64, FM = 2, FN = 2;
+  constexpr int PANEL = 128 * BK;  // floats of one operand panel (16 KiB)
+  __shared__ __attribute__((aligned(16))) float st0[2 * PANEL];
+  __shared__ __attribute__((aligned(16))) float st1[2 * PANEL];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+  const int M = g.M, N = g.N, K = g.K, nk = g.nk;
+
+  auto segment = [&](int t, int kb0, int kb1, int slot, int w) {
+    // The lane index is made opaque per segment: otherwise every per-lane LDS
+    // address of the segment is hoisted out of the work loop and kept live
+    // across it, which spills.
+    int lane = tid & 63;
+    asm volatile("" : "+v"(lane));
+    int bat, tm, tn;
+    decode_tile<SYRK>(g, t, bat, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const float* A = static_cast<const float*>(g.A) + bat * g.sA;
+    const float* B = static_cast<const float*>(g.B) + bat * g.sB;
+
+    // the DMA of k-tile kt into stage st (A panel, then B panel)
+    auto dma = [&](float* st, int kt) {
+      const int k0 = kt * BK;
+      const float* pa = AKC ? A + (int64_t)m0 * g.lda + k0 : A + (int64_t)k0 * g.lda + m0;
+      const float* pb = BKC ? B + (int64_t)n0 * g.ldb + k0 : B + (int64_t)k0 * g.ldb + n0;
+      // rows / columns of the matrix left from the panel's corner
+      const int ra = AKC ? M - m0 : K - k0, ca = AKC ? K - k0 : M - m0;
+      const int rb = BKC ? N - n0 : K - k0, cb = BKC ? K - k0 : N - n0;
+      // wave w fills blocks 4 w .. 4 w + 3 of each panel. KC block b: row
+      // 8 b + l / 8, global group (l % 8) ^ swizzle; MN block b: row
+      // 2 b + l / 32, global group (l % 32) ^ swizzle.
+      auto geo = [&](bool kc, int u, int& row, int& grp) __attribute__((always_inline)) {
+        const int b = 4 * wave + u;
+        if (kc) {
+          row = 8 * b + (lane >> 3);
+          grp = (lane & 7) ^ ((row >> 1) & 7);
+        } else {
+          row = 2 * b + (lane >> 5);
+          grp = (lane & 31) ^ (8 * ((row >> 2) & 1));
+        }
+      };
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        int rw, gp;
+        geo(AKC, u, rw, gp);
+        const bool oka = rw < ra && 4 * gp < ca;
+        const uint32_t va = oka ? (uint32_t)((int64_t)rw * g.lda * 4 + 16 * gp) : kOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            make_rsrc(pa), (__attribute__((address_space(3))) void*)(st + (4 * wave + u) * 256), 16,
+            va, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        int rw, gp;
+        geo(BKC, u, rw, gp);
+        const bool okb = rw < rb && 4 * gp < cb;
+        const uint32_t vb = okb ? (uint32_t)((int64_t)rw * g.ldb * 4 + 16 * gp) : kOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            make_rsrc(pb),
+            (__attribute__((address_space(3))) void*)(st + PANEL + (4 * wave + u) * 256), 16, vb,
+            0, 0, 0);
+      }
+    };
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // Fragment of the lane's row r (32 rows per MFMA block) at k offset kk
+    // (4 consecutive k, kk a multiple of 4): one 16-byte read from a
+    // K-contiguous panel, 4 column reads from an M/N-contiguous one.
+    auto frag = [&](const float* p, bool kc, int r, int kk) __attribute__((always_inline)) {
+      if (kc) return *reinterpret_cast<const i32x4*>(p + r * 32 + 4 * ((kk >> 2) ^ ((r >> 1) & 7)));
+      const float* q = p + 4 * ((r >> 2) ^ (8 * ((kk >> 2) & 1))) + (r & 3);
+      f32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = q[(kk + e) * 128];
+      return __builtin_bit_cast(i32x4, v);
+    };
+    // One k-tile from stage `cur`: every fragment of the k-tile is read into
+    // registers (64 VGPRs) before the DMA of k-tile `next` (< 0: none) into
+    // the other stage issues, then the 64 MFMAs run behind that DMA.
+    auto step = [&](const float* cur, float* oth, int next) __attribute__((always_inline)) {
+      i32x4 fa[BK / 8][FM], fb[BK / 8][FN];
+#pragma unroll
+      for (int c = 0; c < BK / 8; ++c) {
+        const int kk = c * 8 + (lane >> 5) * 4;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) fa[c][i] = frag(cur, AKC, wm0 + i * 32 + (lane & 31), kk);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          fb[c][j] = frag(cur + PANEL, BKC, wn0 + j * 32 + (lane & 31), kk);
+      }
+      if (next >= 0) dma(oth, next);
+#pragma unroll
+      for (int c = 0; c < BK / 8; ++c)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) mma_frag(acc[i][j], fa[c][i], fb[c][j], (float*)nullptr);
+    };
+
+    __syncthreads();  // a previous segment's reads of both stages are done
+    if (kb1 > kb0) dma(st0, kb0);
+    for (int kt = kb0; kt < kb1; kt += 2) {
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA of k-tile kt has landed
+      __syncthreads();                // every wave's has; every read of st1 is done
+      step(st0, st1, kt + 1 < kb1 ? kt + 1 : -1);
+      if (kt + 1 >= kb1) break;
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      step(st1, st0, kt + 2 < kb1 ? kt + 2 : -1);
+    }
+    store_tile<float, SYRK, FM, FN, BM, BN>(g, acc, bat, m0, n0, wm0, wn0, lane, slot, w);
+  };
+
+  // Work of this workgroup, walked with one call site of `segment` (two
+  // inlined copies of it do not fit the register budget): data-parallel, the
+  // tile w; under stream-K, whole tiles w, w + G, ... below dp_tiles, then
+  // the k-iteration range [x0, x1) of the remaining tiles.
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const bool sk = g.sk_groups != 0;
+  const int G = sk ? g.sk_groups : 1;
+  const int64_t total = sk ? (int64_t)(g.ntiles - g.dp_tiles) * nk : 0;
+  int64_t x = sk ? sk_start(w, total, G) : 0;
+  const int64_t x1 = sk ? sk_start(w + 1, total, G) : 0;
+  const int64_t x0 = x;
+  int tw = w;  // next whole tile
+  const int tw_end = sk ? g.dp_tiles : w + 1;
+  for (;;) {
+    int t, kb0, kb1, slot;
+    if (tw < tw_end) {
+      t = tw;
+      kb0 = 0;
+      kb1 = nk;
+      slot = -1;
+      tw += G;
+    } else if (x < x1) {
+      const int tt = (int)(x / nk);
+      kb0 = (int)(x - (int64_t)tt * nk);
+      kb1 = (int)((int64_t)kb0 + (x1 - x) < nk ? kb0 + (x1 - x) : nk);
+      t = g.dp_tiles + tt;
+      slot = (kb0 == 0 && kb1 == nk) ? -1 : (x == x0 ? 0 : 1);
+      x += kb1 - kb0;
+    } else {
+      break;
+    }
+    segment(t, kb0, kb1, slot, w);
   }
 }
 
@@ -414,12 +605,11 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs g) {
 template <typename T>
 struct Cfg {
   static constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
-  // k-tile: fp32 with 16-byte aligned operands uses 64 (one LDS stage, the
-  // next tile held in registers; two workgroups per CU cover each other's
-  // barriers); the others 32 (two LDS stages).
+  // k-tile of gemm_kernel: 32 (two LDS stages). (fp32 with 16-byte aligned
+  // operands runs gemm_f32_dma_kernel, also with 32-wide k-tiles.)
   template <bool VEC>
   static constexpr int bk() {
-    return sizeof(T) == 4 && VEC ? 64 : 32;
+    return 32;
   }
   static constexpr int NT = (BM / WM) * (BN / WN) * 64;
 };
@@ -465,9 +655,14 @@ static int choose_sk(GemmArgs& g, int occupancy, size_t ws_bytes) {
 template <typename T, bool AKC, bool BKC, bool VEC, bool SYRK>
 static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   using C = Cfg<T>;
-  constexpr int BK = C::template bk<VEC>();
+  constexpr bool DMA = sizeof(T) == 4 && VEC;  // fp32 on aligned operands: gemm_f32_dma_kernel
+  constexpr int BK = DMA ? 32 : C::template bk<VEC>();
   g.nk = (g.K + BK - 1) / BK;
-  auto kern = gemm_kernel<T, C::BM, C::BN, BK, C::WM, C::WN, AKC, BKC, VEC, SYRK>;
+  void (*kern)(GemmArgs);
+  if constexpr (DMA)
+    kern = gemm_f32_dma_kernel<AKC, BKC, SYRK>;
+  else
+    kern = gemm_kernel<T, C::BM, C::BN, BK, C::WM, C::WN, AKC, BKC, VEC, SYRK>;
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, C::NT, 0) != hipSuccess) occ = 1;
   g.sk_groups = choose_sk(g, occ, ws_bytes);
