@@ -261,6 +261,23 @@ int trnblas_hip_ozaki_hilo(int slices, int64_t M, int64_t N, int64_t Kp, const i
                            int64_t lda, int64_t lda_slice, const int8_t* dB, int64_t ldb,
                            int64_t ldb_slice, float* hilo, int64_t ldh, void* stream);
 
+/*
+ * One diagonal block of the blocked Cholesky of metric_inv_half, fp64:
+ * A (nb x nb, 0 <= nb <= 128, row-major, leading dimension lda; only its lower
+ * triangle is read) is overwritten in its lower triangle by the Cholesky
+ * factor L (A = L L^T) and Linv (nb x nb, ldl) receives L^-1, lower
+ * triangular with zeros above. A pivot that is not positive (A not positive
+ * definite, or NaN) sets *info = offset + its 1-based column unless *info is
+ * already nonzero (the host zeroes info once and checks it after the last
+ * block); L and Linv are then garbage. Device pointers, asynchronous on
+ * `stream`. Replaces the factorisation inside metric_inv_half
+ * (trnblas/level3.py:365-380: torch.linalg.cholesky + trsm,
+ * trnblas/nki/dispatch.py:1854-1881); the panels, trailing updates and the
+ * block inverse of L around it are DGEMMs on the host side of the op.
+ */
+int trnblas_hip_chol_block(int64_t nb, double* A, int64_t lda, double* Linv, int64_t ldl,
+                           int32_t* info, int64_t offset, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -81,3 +81,73 @@ def test_metric_inv_half_device_errors(dev):
     with pytest.raises(NotImplementedError):
         tb.metric_inv_half(torch.eye(3, dtype=torch.int32, device=dev))
     assert tb.metric_inv_half(torch.zeros(0, 0, device=dev)).shape == (0, 0)
+
+
+@pytest.mark.parametrize("nb", [1, 5, 64, 127, 128])
+def test_chol_block_kernel(dev, nb):
+    # one diagonal block through the C ABI: L L^T = A, L L^-1 = I, L^-1 equal
+    # to the oracle's inverse Cholesky factor; the strict upper triangle of
+    # A is neither read nor written
+    from trnblas_amd.hip import kernels
+
+    J = om.spd(nb, seed=nb)
+    A = torch.from_numpy(J).to(dev)
+    A_up = torch.triu(torch.full((nb, nb), 7.0, dtype=torch.float64, device=dev), 1)
+    A = torch.tril(A) + A_up
+    Li = torch.empty(nb, nb, dtype=torch.float64, device=dev)
+    info = torch.zeros(1, dtype=torch.int32, device=dev)
+    kernels.chol_block(A, Li, info, 0)
+    assert int(info) == 0
+    assert torch.equal(torch.triu(A, 1), A_up)
+    L = torch.tril(A).cpu().numpy()
+    assert np.abs(L @ L.T - J).max() <= 1e-13 * np.abs(J).max()
+    Lin = Li.cpu().numpy()
+    assert np.array_equal(Lin, np.tril(Lin))
+    assert np.abs(L @ Lin - np.eye(nb)).max() <= 1e-13
+    want = om.metric_inv_half_ref(J).T  # L^-1
+    assert np.abs(Lin - want).max() <= 1e-12 * np.abs(want).max()
+
+
+def test_chol_block_info(dev):
+    # the first non-positive pivot, offset by the block's position, and an
+    # info already set by an earlier block is kept
+    from trnblas_amd.hip import kernels
+
+    A = torch.eye(10, dtype=torch.float64, device=dev)
+    A[6, 6] = -1.0
+    Li = torch.empty_like(A)
+    info = torch.zeros(1, dtype=torch.int32, device=dev)
+    kernels.chol_block(A.clone(), Li, info, 100)
+    assert int(info) == 107
+    kernels.chol_block(A.clone(), Li, info, 500)
+    assert int(info) == 107
+    info.zero_()
+    A[6, 6] = float("nan")
+    kernels.chol_block(A.clone(), Li, info, 0)
+    assert int(info) == 7
+
+
+@pytest.mark.parametrize("n", [300, 385])
+@pytest.mark.parametrize("cond", [1e2, 1e8])
+def test_metric_inv_half_blocked_conditioning(dev, n, cond):
+    # several 128-wide blocks, a ragged last one, and RI-like conditioning:
+    # the residual stays within a small factor of LAPACK's on the same J
+    rng = np.random.default_rng(int(n + np.log10(cond)))
+    Q, _ = np.linalg.qr(rng.standard_normal((n, n)))
+    J = (Q * np.geomspace(1.0, 1.0 / cond, n)) @ Q.T
+    J = (J + J.T) / 2
+    X = tb.metric_inv_half(torch.from_numpy(J).to(dev)).cpu().numpy()
+    assert np.array_equal(X, np.triu(X))
+    res = np.abs(X.T @ J @ X - np.eye(n)).max()
+    Xh = om.metric_inv_half_ref(J)
+    res_h = np.abs(Xh.T @ J @ Xh - np.eye(n)).max()
+    assert res <= 20 * res_h + 1e-13, (res, res_h)
+    assert np.abs(X - Xh).max() <= 1e-14 * cond * np.abs(Xh).max()
+
+
+def test_metric_inv_half_device_error_later_block(dev):
+    # a failing leading minor inside the third block is reported by its order
+    J = torch.eye(300, dtype=torch.float64, device=dev)
+    J[261, 261] = -2.0
+    with pytest.raises(torch.linalg.LinAlgError, match="order 262"):
+        tb.metric_inv_half(J)

@@ -19,7 +19,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 _PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("TRNBLAS_HIP_LIB", _PKG / "lib" / "libtrnblas_hip.so"))
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 F32, BF16, F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
@@ -81,6 +81,10 @@ SIGNATURES = {
         _c_int,
         [_c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64]
         + [_c_ptr, _c_i64, _c_ptr],
+    ),
+    "trnblas_hip_chol_block": (
+        _c_int,
+        [_c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
     ),
 }
 

@@ -511,13 +511,56 @@ def nki_trsm(
     return X.to(B.dtype)
 
 
+def _metric_inv_half_blocked(J: torch.Tensor) -> torch.Tensor:
+    """X = L^-T of a real SPD J on the ROCm device, in fp64: a right-looking
+    blocked Cholesky whose diagonal blocks (128 wide) are factored and
+    inverted by the HIP kernel `trnblas_hip_chol_block`, whose panels
+    (L_ik = J_ik L_kk^-T) and trailing updates are DGEMMs, then the block
+    inverse of L by rows, L^-1_ij = -L_ii^-1 (sum_m L_im L^-1_mj), also
+    DGEMMs. Returns float64."""
+    from . import kernels
+
+    n = J.shape[0]
+    dev = J.device
+    W = J.to(torch.float64).clone(memory_format=torch.contiguous_format)
+    nb = kernels.CHOL_NB
+    nblk = -(-n // nb)
+    Li = torch.empty(nblk, nb, nb, dtype=torch.float64, device=dev)
+    info = torch.zeros(1, dtype=torch.int32, device=dev)
+    for b in range(nblk):
+        k0, k1 = b * nb, min(n, (b + 1) * nb)
+        Lkk = Li[b, : k1 - k0, : k1 - k0]
+        kernels.chol_block(W[k0:k1, k0:k1], Lkk, info, k0)
+        if k1 < n:
+            P = W[k1:, k0:k1] @ Lkk.mT  # the panel of L
+            W[k1:, k0:k1] = P
+            W[k1:, k1:].addmm_(P, P.mT, alpha=-1.0)  # lower triangle used; upper is scratch
+    bad = int(info)  # one small device-to-host read
+    if bad != 0:
+        raise torch.linalg.LinAlgError(
+            f"metric Cholesky failed: leading minor of order {bad} is not positive-definite"
+        )
+    X = torch.zeros_like(W)  # L^-1, lower triangular
+    for b in range(nblk):
+        k0, k1 = b * nb, min(n, (b + 1) * nb)
+        Lkk = Li[b, : k1 - k0, : k1 - k0]
+        X[k0:k1, k0:k1] = Lkk
+        if k0:
+            X[k0:k1, :k0] = -(Lkk @ (W[k0:k1, :k0] @ X[:k0, :k0]))
+    return X.mT.contiguous()
+
+
 def nki_metric_inv_half(J: torch.Tensor) -> torch.Tensor:
     """Cholesky inverse factor X = L^-T of an SPD metric J = L L^T, so
     X X^T = J^-1 and `A @ X` is the density-fitting metric contraction
-    (nki/dispatch.py:1854-1905). On MI355X the Cholesky and the triangular
-    solve run on J's device in its precision (float64 native; half types in
-    fp32), where the reference sends device metrics to host LAPACK. The
-    result has J's dtype and device; X is exactly upper triangular."""
+    (nki/dispatch.py:1854-1905). On MI355X a real J on the device is factored
+    and inverted there in fp64 (`_metric_inv_half_blocked`: a HIP kernel for
+    the diagonal blocks, DGEMMs around it), where the reference sends device
+    metrics to host LAPACK or runs torch.linalg.cholesky + trsm in the
+    metric's precision; complex metrics and host tensors take torch's
+    Cholesky and triangular solve (host LAPACK for host tensors, the
+    reference's own host route). The result has J's dtype and device; X is
+    exactly upper triangular."""
     if not (J.is_floating_point() or J.is_complex()):
         # every route of the reference raises for integer metrics (#86)
         raise NotImplementedError(
@@ -525,6 +568,8 @@ def nki_metric_inv_half(J: torch.Tensor) -> torch.Tensor:
         )
     if J.dim() != 2 or J.shape[0] != J.shape[1]:
         raise ValueError(f"metric_inv_half: J must be square; got {tuple(J.shape)}")
+    if J.is_cuda and J.is_floating_point():
+        return _metric_inv_half_blocked(J).to(J.dtype)
     cdt = _solve_dtype(J)
     L, info = torch.linalg.cholesky_ex(J.to(cdt))
     if int(info) != 0:  # one small device-to-host read

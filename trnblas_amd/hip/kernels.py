@@ -324,6 +324,33 @@ def mp2_energy_pairs(T_flat, eps_occ_chunk, eps_occ_full, eps_vir) -> torch.Tens
     return out
 
 
+# ── metric stage ─────────────────────────────────────────────────────────────
+
+CHOL_NB = 128  # largest diagonal block of trnblas_hip_chol_block
+
+
+def chol_block(A: torch.Tensor, Linv: torch.Tensor, info: torch.Tensor, offset: int) -> None:
+    """One diagonal block (nb <= 128) of the blocked metric Cholesky, in
+    place on the device: A's lower triangle becomes L (A = L L^T), Linv
+    becomes L^-1 (lower, zeros above), and info[0] becomes offset + the first
+    non-positive pivot (1-based) unless it is already nonzero. A and Linv are
+    (nb, nb) float64 views with unit column stride; info is int32."""
+    dev = _require_device(A, Linv, info)
+    if A.dtype != torch.float64 or Linv.dtype != torch.float64 or info.dtype != torch.int32:
+        raise TypeError("chol_block takes float64 A / Linv and an int32 info")
+    nb = A.shape[0]
+    if A.dim() != 2 or A.shape[1] != nb or tuple(Linv.shape) != (nb, nb):
+        raise ValueError("chol_block: A and Linv must both be (nb, nb)")
+    if nb > CHOL_NB:
+        raise ValueError(f"chol_block: nb {nb} > {CHOL_NB}")
+    if nb and (A.stride(1) != 1 or Linv.stride(1) != 1):
+        raise ValueError("chol_block: A and Linv need unit column stride")
+    call(
+        "trnblas_hip_chol_block", nb, ptr(A), A.stride(0) if nb else 1, ptr(Linv),
+        Linv.stride(0) if nb else 1, ptr(info), offset, stream_of(dev),
+    )  # fmt: skip
+
+
 # ── Ozaki ────────────────────────────────────────────────────────────────────
 
 OZ_TILE = 128  # K padding of the digit stacks (ozaki.TILE_K)
