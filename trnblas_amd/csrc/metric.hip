@@ -8,44 +8,68 @@
 // of one updated diagonal block (nb <= 128) and its inverse L_kk^-1, which
 // turns the panel solve into a GEMM and seeds the block inverse of L.
 //
-// One 1024-thread workgroup per block. The owner of tile (br, bc), br >= bc,
-// keeps the 4 x 4 tile at rows 4 br .., columns 4 bc .. of the 128 x 128
-// block (padded with the identity past nb) in registers. Both phases are
-// right-looking with
-// one barrier per column: the owners of the column (and, for the inverse,
-// of the row) publish it into an LDS vector (double buffered, so a vector is
-// rewritten only two barriers after it was read), every owner then applies
-// the rank-1 update to its tile.
+// One workgroup of 576 threads per block, blocked by 4 x 4 tiles: the owner of
+// tile (br, bc), br >= bc, keeps the tile at rows 4 br .., columns 4 bc .. of
+// the 128 x 128 block (padded with the identity past nb) in registers.
+// Cholesky, per tile column jb: (A) the owner of the diagonal tile factors
+// it (4 x 4 Cholesky) and inverts its factor into an LDS table; (B) the
+// panel tiles below it become A_ij L_jj^-T and are published; (C) every
+// trailing tile loses P_i P_j^T. Inverse X = L^-1, per tile row ib: the
+// unscaled row of X and the column M_m = L_m,ib L_ib,ib^-1 are published,
+// then the row becomes L_ib,ib^-1 X_ib and every later row m loses
+// M_m X_ib (unscaled). Waves whose tiles all lie above the current tile row
+// skip the arithmetic (those tiles are final) but keep the barriers.
 #include "common.hpp"
 
 namespace trnblas {
 
 constexpr int kCholNB = 128;
+constexpr int kCholNT = kCholNB / 4;
+constexpr int kCholTiles = kCholNT * (kCholNT + 1) / 2;
 
-__global__ __launch_bounds__(1024) void chol_block_kernel(int nb, double* A, int64_t lda,
+constexpr int kCholThreads = (kCholTiles + 63) / 64 * 64;  // 9 waves
+
+// 1 / sqrt(d) for d > 0: the hardware estimate (v_rsq_f64) refined by two
+// Newton-Raphson steps y <- y (3 - d y^2) / 2, each of which doubles the
+// correct bits; a short FMA chain in place of a correctly rounded sqrt and
+// a division on the serial path of the diagonal tile. NaN for d <= 0.
+__device__ __forceinline__ double rsqrt_nr(double d) {
+  double y = __builtin_amdgcn_rsq(d);
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const double h = 0.5 * d * y;
+    y = fma(-h, y, 1.5) * y;
+  }
+  return d > 0.0 ? y : __builtin_nan("");
+}
+
+__global__ __launch_bounds__(kCholThreads) void chol_block_kernel(int nb, double* A, int64_t lda,
                                                           double* Li, int64_t ldl, int32_t* info,
                                                           int offset) {
-  __shared__ double col[2][kCholNB];
-  __shared__ double row[2][kCholNB];
-  // Thread t < 528 owns lower tile t of the 32 x 32 tile grid in row-major
-  // triangle order (br (br + 1) / 2 + bc = t); the others own nothing. A
-  // wave whose tiles all lie above the current row skips the update (the
-  // tiles of a finished row never change again) but keeps the barriers.
+  __shared__ double dinv[kCholNT][16];    // L_jj^-1 of every diagonal tile, row-major
+  __shared__ double pan[kCholNT][16];     // Cholesky: the panel column of tiles
+  __shared__ double mcol[2][kCholNT][16]; // inverse: M_m of the current tile row
+  __shared__ double xrow[2][kCholNT][16]; // inverse: the unscaled tile row of X
+  __shared__ int sbad;
+
+  // Thread t < 528 owns lower tile t in row-major triangle order
+  // (br (br + 1) / 2 + bc = t); the rest of the last wave owns nothing.
   const int t = threadIdx.x;
-  constexpr int kTiles = 32 * 33 / 2;
-  const bool own = t < kTiles;
+  const bool own = t < kCholTiles;
   int br = (int)((sqrtf(8.0f * (float)t + 1.0f) - 1.0f) * 0.5f);
   while (br * (br + 1) / 2 > t) --br;
   while ((br + 1) * (br + 2) / 2 <= t) ++br;
   int bc = t - br * (br + 1) / 2;
   if (!own) br = bc = 0;  // (reads stay in range; nothing is published or written)
   // largest tile row in this wave (wave-uniform; -1 for a wave with no tile)
-  const int tl = min((int)(t | 63), kTiles - 1);
+  const int tl = min((int)(t | 63), kCholTiles - 1);
   int wrow = (int)((sqrtf(8.0f * (float)tl + 1.0f) - 1.0f) * 0.5f);
   while (wrow * (wrow + 1) / 2 > tl) --wrow;
   while ((wrow + 1) * (wrow + 2) / 2 <= tl) ++wrow;
-  if ((t & ~63) >= kTiles) wrow = -1;
+  if ((t & ~63) >= kCholTiles) wrow = -1;
   wrow = __builtin_amdgcn_readfirstlane(wrow);
+  const int ntr = (nb + 3) >> 2;  // tile rows holding matrix entries
+  if (t == 0) sbad = 0x7fffffff;
 
   double a[4][4];
 #pragma unroll
@@ -58,93 +82,145 @@ __global__ __launch_bounds__(1024) void chol_block_kernel(int nb, double* A, int
       a[r][c] = v;
     }
 
-  // Cholesky: at column j the tile entries (i, k), j < k <= i, lose
-  // a_ij a_kj / a_jj; column j becomes a_ij / sqrt(a_jj), its diagonal
-  // sqrt(a_jj). A pivot that is not positive (or NaN) is recorded
-  // (1-based, plus the block's offset in J) and the factor is garbage.
-  int bad = 0;
-  for (int j = 0; j < nb; ++j) {
-    double* cv = col[j & 1];
-    if (own && bc == (j >> 2)) {
-      // (static indices only: a runtime index into the tile puts it in scratch)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        double v = a[r][0];
-#pragma unroll
-        for (int c = 1; c < 4; ++c) v = (j & 3) == c ? a[r][c] : v;
-        cv[4 * br + r] = v;
-      }
-    }
-    __syncthreads();
-    // every value the step needs is read at once, and the tile is updated
-    // with selects: per-entry branches around the LDS reads serialise them
-    const double d = cv[j];
-    double ci[4], ck[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) ci[r] = cv[4 * br + r];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) ck[c] = cv[4 * bc + c];
-    if (!(d > 0.0) && bad == 0) bad = j + 1;
-    if (wrow < (j >> 2)) continue;
-    const double rt = sqrt(d), rinv = 1.0 / rt, dinv = rinv * rinv;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
+  for (int jb = 0; jb < ntr; ++jb) {
+    // (A) diagonal tile: factor (lower part only) and invert
+    if (own && br == jb && bc == jb) {
+      double rinv[4];  // 1 / l_cc
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const int i = 4 * br + r, k = 4 * bc + c;
-        const double upd = a[r][c] - ci[r] * ck[c] * dinv;
-        const double cj = i == j ? rt : ci[r] * rinv;
-        a[r][c] = (k == j && i >= j) ? cj : ((k > j && i >= k) ? upd : a[r][c]);
+        const double d = a[c][c];
+        if (!(d > 0.0) && 4 * jb + c < nb) atomicMin(&sbad, 4 * jb + c + 1);
+        rinv[c] = rsqrt_nr(d);
+        a[c][c] = d * rinv[c];
+#pragma unroll
+        for (int r = c + 1; r < 4; ++r) a[r][c] *= rinv[c];
+#pragma unroll
+        for (int r = c + 1; r < 4; ++r)
+#pragma unroll
+          for (int q = c + 1; q <= r; ++q) a[r][q] -= a[r][c] * a[q][c];
       }
+      double m[4][4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int r = 0; r < c; ++r) m[r][c] = 0.0;
+        m[c][c] = rinv[c];
+#pragma unroll
+        for (int r = c + 1; r < 4; ++r) {
+          double sum = 0.0;
+#pragma unroll
+          for (int q = c; q < r; ++q) sum += a[r][q] * m[q][c];
+          m[r][c] = -sum * rinv[r];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          dinv[jb][4 * r + c] = m[r][c];
+          if (c > r) a[r][c] = 0.0;
+        }
+    }
+    __syncthreads();
+    // (B) panel tiles: A_ij L_jj^-T, published
+    if (wrow > jb && own && bc == jb && br > jb) {
+      double m[4][4], p[4][4];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) m[e >> 2][e & 3] = dinv[jb][e];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          double sum = 0.0;
+#pragma unroll
+          for (int q = 0; q <= c; ++q) sum += a[r][q] * m[c][q];
+          p[r][c] = sum;
+        }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          a[r][c] = p[r][c];
+          pan[br][4 * r + c] = p[r][c];
+        }
+    }
+    __syncthreads();
+    // (C) trailing tiles: A_ik -= P_i P_k^T (diagonal tiles: their upper part
+    // is never read)
+    if (wrow > jb && own && bc > jb) {
+      double pk[4][4];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) pk[e >> 2][e & 3] = pan[bc][e];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        double pi[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pi[q] = pan[br][4 * r + q];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          double sum = 0.0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) sum += pi[q] * pk[c][q];
+          a[r][c] -= sum;
+        }
+      }
+    }
   }
 
-  // Inverse X = L^-1 (lower), forward substitution by rows: at row i the row
-  // is complete up to the factor 1 / l_ii; every later row m loses
-  // (l_mi / l_ii) x_i. Row i of X and column i of L are published together.
   double x[4][4];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) x[r][c] = (own && 4 * br + r == 4 * bc + c) ? 1.0 : 0.0;
-  for (int i = 0; i < nb; ++i) {
-    double* lc = col[(nb + i) & 1];
-    double* xr = row[i & 1];
-    if (own && bc == (i >> 2)) {
+    for (int c = 0; c < 4; ++c) x[r][c] = (own && br == bc && r == c) ? 1.0 : 0.0;
+  for (int ib = 0; ib < ntr; ++ib) {
+    double(*mc)[16] = mcol[ib & 1];
+    double(*xr)[16] = xrow[ib & 1];
+    if (own && br == ib) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        double v = a[r][0];
-#pragma unroll
-        for (int c = 1; c < 4; ++c) v = (i & 3) == c ? a[r][c] : v;
-        lc[4 * br + r] = v;
-      }
+      for (int e = 0; e < 16; ++e) xr[bc][e] = x[e >> 2][e & 3];
     }
-    if (own && br == (i >> 2)) {
+    if (wrow > ib && own && bc == ib && br > ib) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        double v = x[0][c];
+      for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int r = 1; r < 4; ++r) v = (i & 3) == r ? x[r][c] : v;
-        xr[4 * bc + c] = v;
-      }
+        for (int c = 0; c < 4; ++c) {
+          double sum = 0.0;
+#pragma unroll
+          for (int q = c; q < 4; ++q) sum += a[r][q] * dinv[ib][4 * q + c];
+          mc[br][4 * r + c] = sum;
+        }
     }
     __syncthreads();
-    if (wrow < (i >> 2)) continue;
-    const double inv = 1.0 / lc[i];
-    double lm[4], xk[4];
+    if (wrow < ib || !own || bc > ib || br < ib) continue;
+    double xk[4][4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) lm[r] = lc[4 * br + r];
+    for (int e = 0; e < 16; ++e) xk[e >> 2][e & 3] = xr[bc][e];
+    if (br == ib) {
+      // the final row: L_ib,ib^-1 X_ib
 #pragma unroll
-    for (int c = 0; c < 4; ++c) xk[c] = xr[4 * bc + c];
+      for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+        for (int c = 0; c < 4; ++c) {
+          double sum = 0.0;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int m = 4 * br + r, k = 4 * bc + c;
-        // X is lower triangular: row i is zero past column i (and those
-        // entries of the published row are stale), so columns k > i stay
-        const double v = m == i ? x[r][c] * inv : x[r][c] - lm[r] * inv * xk[c];
-        x[r][c] = (k <= i && m >= i) ? v : x[r][c];
+          for (int q = 0; q <= r; ++q) sum += dinv[ib][4 * r + q] * xk[q][c];
+          x[r][c] = sum;
+        }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        double mr[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) mr[q] = mc[br][4 * r + q];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          double sum = 0.0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) sum += mr[q] * xk[q][c];
+          x[r][c] -= sum;
+        }
       }
+    }
   }
 
 #pragma unroll
@@ -159,7 +235,8 @@ __global__ __launch_bounds__(1024) void chol_block_kernel(int nb, double* A, int
         if (br > bc) Li[(int64_t)k * ldl + i] = 0.0;
       }
     }
-  if (t == 0 && bad && info[0] == 0) info[0] = offset + bad;
+  __syncthreads();
+  if (t == 0 && sbad != 0x7fffffff && info[0] == 0) info[0] = offset + sbad;
 }
 
 }  // namespace trnblas
@@ -175,7 +252,7 @@ extern "C" int trnblas_hip_chol_block(int64_t nb, double* A, int64_t lda, double
   TRNBLAS_CHECK_ARG(A && Linv && info, "chol_block: NULL pointer");
   TRNBLAS_CHECK_ARG(lda >= nb && ldl >= nb, "chol_block: leading dimension below nb");
   TRNBLAS_CHECK_ARG(offset >= 0 && offset < (1ll << 30), "chol_block: bad offset");
-  hipLaunchKernelGGL(chol_block_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, (int)nb, A,
+  hipLaunchKernelGGL(chol_block_kernel, dim3(1), dim3(kCholThreads), 0, (hipStream_t)stream, (int)nb, A,
                      lda, Linv, ldl, info, (int)offset);
   return check_launch("chol_block");
 }

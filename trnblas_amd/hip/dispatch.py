@@ -511,13 +511,21 @@ def nki_trsm(
     return X.to(B.dtype)
 
 
+_METRIC_LOOKAHEAD = True  # overlap the diagonal-block kernel with the trailing update
+
+
 def _metric_inv_half_blocked(J: torch.Tensor) -> torch.Tensor:
     """X = L^-T of a real SPD J on the ROCm device, in fp64: a right-looking
     blocked Cholesky whose diagonal blocks (128 wide) are factored and
     inverted by the HIP kernel `trnblas_hip_chol_block`, whose panels
-    (L_ik = J_ik L_kk^-T) and trailing updates are DGEMMs, then the block
-    inverse of L by rows, L^-1_ij = -L_ii^-1 (sum_m L_im L^-1_mj), also
-    DGEMMs. Returns float64."""
+    (L_ik = J_ik L_kk^-T) and trailing updates are DGEMMs, then the inverse
+    of L by halves, [[X11, 0], [-X22 L21 X11, X22]], also DGEMMs. Returns
+    float64.
+
+    Look-ahead: after a panel only the next block column is updated on the
+    calling stream, so the next diagonal block (one workgroup) is factored
+    while a second stream applies the rest of the trailing update with the
+    other CUs; the calling stream waits for it before it next writes there."""
     from . import kernels
 
     n = J.shape[0]
@@ -527,26 +535,60 @@ def _metric_inv_half_blocked(J: torch.Tensor) -> torch.Tensor:
     nblk = -(-n // nb)
     Li = torch.empty(nblk, nb, nb, dtype=torch.float64, device=dev)
     info = torch.zeros(1, dtype=torch.int32, device=dev)
+    main = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(dev) if nblk > 2 and _METRIC_LOOKAHEAD else None
+    rest_done = None  # the side stream's update of W[k1:, k1:] minus the next block column
     for b in range(nblk):
         k0, k1 = b * nb, min(n, (b + 1) * nb)
         Lkk = Li[b, : k1 - k0, : k1 - k0]
         kernels.chol_block(W[k0:k1, k0:k1], Lkk, info, k0)
-        if k1 < n:
-            P = W[k1:, k0:k1] @ Lkk.mT  # the panel of L
-            W[k1:, k0:k1] = P
-            W[k1:, k1:].addmm_(P, P.mT, alpha=-1.0)  # lower triangle used; upper is scratch
+        if k1 == n:
+            break
+        k2 = min(n, k1 + nb)
+        P = W[k1:, k0:k1] @ Lkk.mT  # the panel of L
+        W[k1:, k0:k1] = P
+        if rest_done is not None:
+            main.wait_event(rest_done)  # the next block column is in the side's region
+        # the next block column (lower triangle used; its upper part is scratch)
+        W[k1:, k1:k2].addmm_(P, P[: k2 - k1].mT, alpha=-1.0)
+        rest_done = None
+        if k2 < n:
+            R = P[k2 - k1 :]
+            if side is None:
+                W[k2:, k2:].addmm_(R, R.mT, alpha=-1.0)
+            else:
+                ready = torch.cuda.Event()
+                ready.record(main)
+                side.wait_event(ready)
+                with torch.cuda.stream(side):
+                    W[k2:, k2:].addmm_(R, R.mT, alpha=-1.0)
+                P.record_stream(side)
+                rest_done = torch.cuda.Event()
+                rest_done.record(side)
+    if rest_done is not None:
+        main.wait_event(rest_done)
     bad = int(info)  # one small device-to-host read
     if bad != 0:
         raise torch.linalg.LinAlgError(
             f"metric Cholesky failed: leading minor of order {bad} is not positive-definite"
         )
     X = torch.zeros_like(W)  # L^-1, lower triangular
-    for b in range(nblk):
-        k0, k1 = b * nb, min(n, (b + 1) * nb)
-        Lkk = Li[b, : k1 - k0, : k1 - k0]
-        X[k0:k1, k0:k1] = Lkk
-        if k0:
-            X[k0:k1, :k0] = -(Lkk @ (W[k0:k1, :k0] @ X[:k0, :k0]))
+
+    def inverse(b0: int, b1: int) -> None:
+        # X over block rows / columns [b0, b1): halves on a block boundary,
+        # X_21 = -X_22 L_21 X_11 (large DGEMMs at the top of the recursion)
+        k0, k1 = b0 * nb, min(n, b1 * nb)
+        if b1 - b0 == 1:
+            X[k0:k1, k0:k1] = Li[b0, : k1 - k0, : k1 - k0]
+            return
+        bm = (b0 + b1) // 2
+        km = bm * nb
+        inverse(b0, bm)
+        inverse(bm, b1)
+        X[km:k1, k0:km] = -(X[km:k1, km:k1] @ (W[km:k1, k0:km] @ X[k0:km, k0:km]))
+
+    if nblk:
+        inverse(0, nblk)
     return X.mT.contiguous()
 
 
