@@ -13,6 +13,9 @@ function citing the reference file:line it follows:
                        (trnblas/nki/dispatch.py, examples/df_mp2.py)
 * `oracle.metric`      trsm and the metric factor metric_inv_half
                        (trnblas/level3.py, trnblas/nki/dispatch.py)
+* `oracle.df_mp2`      the example's whole DF-MP2 calculation: metric factor,
+                       half-transforms, metric contraction, energy
+                       (examples/df_mp2.py)
 
 Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of
 `bench.py` may import this package, and only as the checker (or, for

@@ -5,6 +5,11 @@ The MI355X counterpart of the energy step of examples/df_mp2.py:
   chunked `gemm(B_chunk, B_flat, transB=True)` + torch reduction;
 * `energy_reduction_batched_pair` — its `--batched-pair-energy` path
   (df_mp2.py:131-144): one fused HIP launch for every pair;
+* `df_mp2_energy` — the example's whole calculation (df_mp2.py:147-233):
+  metric factor, half-transforms, metric contraction, energy, with its four
+  energy paths (`energy_reduction` with / without `use_fused`,
+  `energy_reduction_fused_gemm`, `energy_reduction_batched_pair`), and its
+  `flops` / `make_inputs` helpers;
 * `half_transform` / `df_mp2_chain_energy` — the config-4 chain: the two
   half-transforms of a P-major 3-center tensor as two one-launch batched
   GEMMs writing B directly in the (nocc, nvir, naux) layout the fused energy
@@ -22,21 +27,39 @@ from . import level3
 from .hip import dispatch as _d
 
 
-def energy_reduction(B, eps_occ, eps_vir, *, mem_budget_bytes: int = 1_500_000_000) -> float:
+def energy_reduction(
+    B, eps_occ, eps_vir, *, mem_budget_bytes: int = 1_500_000_000, use_fused: bool = False
+) -> float:
     """E = sum_{ijab} T_ijab (2 T_ijab - T_ijba) / D_ijab by chunked GEMM
     (one `gemm(..., transB=True)` per i-chunk, B_flat^T read in place) and a
-    torch reduction (examples/df_mp2.py:51-99)."""
+    torch reduction, or with `use_fused` the `mp2_energy` HIP reduction of
+    each T chunk (examples/df_mp2.py:51-99)."""
     nocc, nvir, naux = B.shape
     i_block = max(1, min(nocc, int(mem_budget_bytes // (4 * nvir * nocc * nvir))))
     flat = B.reshape(nocc * nvir, naux)
-    eo2 = eps_occ.view(nocc, 1, 1, 1) + eps_occ.view(1, nocc, 1, 1)
-    ev2 = eps_vir.view(1, 1, nvir, 1) + eps_vir.view(1, 1, 1, nvir)
+    if not use_fused:
+        eo2 = eps_occ.view(nocc, 1, 1, 1) + eps_occ.view(1, nocc, 1, 1)
+        ev2 = eps_vir.view(1, 1, nvir, 1) + eps_vir.view(1, 1, 1, nvir)
     e = torch.zeros((), dtype=B.dtype, device=B.device)
     for i0 in range(0, nocc, i_block):
         i1 = min(i0 + i_block, nocc)
-        T = level3.gemm(1.0, flat[i0 * nvir : i1 * nvir], flat, transB=True)
-        T = T.reshape(i1 - i0, nvir, nocc, nvir).permute(0, 2, 1, 3)
+        T_flat = level3.gemm(1.0, flat[i0 * nvir : i1 * nvir], flat, transB=True)
+        if use_fused:
+            e = e + _d.nki_mp2_energy(T_flat, eps_occ[i0:i1], eps_occ, eps_vir)
+            continue
+        T = T_flat.reshape(i1 - i0, nvir, nocc, nvir).permute(0, 2, 1, 3)
         e = e + (T * (2.0 * T - T.transpose(-2, -1)) / (eo2[i0:i1] - ev2)).sum()
+    return float(e)
+
+
+def energy_reduction_fused_gemm(B, eps_occ, eps_vir) -> float:
+    """The per-pair fused GEMM + energy loop over all nocc^2 ordered pairs
+    (examples/df_mp2.py:102-128), one fused HIP launch per pair."""
+    nocc = B.shape[0]
+    e = torch.zeros((), dtype=B.dtype, device=B.device)
+    for i in range(nocc):
+        for j in range(nocc):
+            e = e + _d.nki_fused_gemm_energy(B[i], B[j], float(eps_occ[i]), float(eps_occ[j]), eps_vir)
     return float(e)
 
 
@@ -76,6 +99,102 @@ def df_mp2_chain_energy(eri, C_occ, C_vir, eps_occ, eps_vir, timings: dict | Non
     if timings is not None:
         timings.update(half=t1 - t0, energy=t2 - t1)
     return e
+
+
+def df_mp2_energy(
+    C_occ: torch.Tensor,
+    C_vir: torch.Tensor,
+    eri_3c: torch.Tensor,
+    J_metric: torch.Tensor,
+    eps_occ: torch.Tensor,
+    eps_vir: torch.Tensor,
+    timings: dict | None = None,
+    use_fused: bool = False,
+    use_fused_gemm: bool = False,
+    use_batched_pair: bool = False,
+) -> float:
+    """DF-MP2 correlation energy (examples/df_mp2.py:147-233), the
+    reference's layout and steps: eri_3c is (nbasis, nbasis, naux), C_occ
+    (nbasis, nocc), C_vir (nbasis, nvir), J_metric (naux, naux).
+
+    1. X = metric_inv_half(J) (X = L^-T, J = L L^T; fp64 on the device);
+    2a. (i nu|P) = C_occ^T (mu nu|P): one GEMM on the (nbasis, nbasis naux)
+        view of eri (transA, read in place);
+    2b. (ia|P) = C_vir^T (i nu|P)_i: one batched GEMM whose C_vir^T operand
+        is a stride-0 broadcast (no per-batch copies);
+    3. B_i = (ia|P)_i X: one batched GEMM, X broadcast the same way;
+    4. the energy, by `use_batched_pair` (the fused pair-energy kernel, one
+       launch), `use_fused_gemm` (one fused launch per ordered pair),
+       `use_fused` (chunked GEMM + the HIP mp2_energy reduction) or the
+       default chunked GEMM + torch reduction.
+    `timings` receives seconds per step (chol, half, metric, energy)."""
+    import time
+
+    nbasis, nocc = C_occ.shape
+    nvir = C_vir.shape[1]
+    naux = J_metric.shape[0]
+    dev = C_occ.device
+
+    def sync():
+        if timings is not None and dev.type == "cuda":
+            torch.cuda.synchronize(dev)
+
+    t0 = time.perf_counter()
+    X = level3.metric_inv_half(J_metric)
+    sync()
+    t_chol = time.perf_counter() - t0
+
+    t0 = time.perf_counter()
+    eri_flat = eri_3c.reshape(nbasis, nbasis * naux)
+    iv_P = level3.gemm(1.0, C_occ, eri_flat, transA=True).reshape(nocc, nbasis, naux)
+    ia_P = level3.batched_gemm(1.0, C_vir.mT.unsqueeze(0).expand(nocc, nvir, nbasis), iv_P)
+    sync()
+    t_half = time.perf_counter() - t0
+
+    t0 = time.perf_counter()
+    B = level3.batched_gemm(1.0, ia_P, X.to(ia_P.dtype).unsqueeze(0).expand(nocc, naux, naux))
+    sync()
+    t_metric = time.perf_counter() - t0
+
+    t0 = time.perf_counter()
+    if use_batched_pair:
+        e = energy_reduction_batched_pair(B, eps_occ, eps_vir)
+    elif use_fused_gemm:
+        e = energy_reduction_fused_gemm(B, eps_occ, eps_vir)
+    else:
+        e = energy_reduction(B, eps_occ, eps_vir, use_fused=use_fused)
+    t_energy = time.perf_counter() - t0
+    if timings is not None:
+        timings.update(chol=t_chol, half=t_half, metric=t_metric, energy=t_energy)
+    return float(e)
+
+
+def flops(nbasis: int, nocc: int, naux: int) -> int:
+    """Approximate flops of one df_mp2_energy (examples/df_mp2.py:236-242):
+    steps 2a, 2b, 3 and the ordered-pair energy GEMMs."""
+    nvir = nbasis - nocc
+    return (
+        2 * nbasis * nbasis * nocc * naux
+        + 2 * nocc * nvir * nbasis * naux
+        + 2 * nocc * nvir * naux * naux
+        + 2 * nocc * nocc * nvir * nvir * naux
+    )
+
+
+def make_inputs(nbasis: int, nocc: int, naux: int, seed: int = 42, device: str = "cpu"):
+    """The example's synthetic inputs (examples/df_mp2.py:245-266): the same
+    draws in the same order from torch's global generator on the host, then
+    moved to `device`. Returns (C_occ, C_vir, eri_3c, J_metric, eps_occ,
+    eps_vir)."""
+    torch.manual_seed(seed)
+    C_occ = torch.randn(nbasis, nocc) * 0.1
+    C_vir = torch.randn(nbasis, nbasis - nocc) * 0.1
+    eri_3c = torch.randn(nbasis, nbasis, naux) * 0.01
+    J_raw = torch.randn(naux, naux) * 0.01
+    J_metric = J_raw @ J_raw.T + naux * torch.eye(naux)
+    eps_occ = -torch.sort(torch.rand(nocc))[0] - 0.5
+    eps_vir = torch.sort(torch.rand(nbasis - nocc))[0] + 0.1
+    return tuple(t.to(device) for t in (C_occ, C_vir, eri_3c, J_metric, eps_occ, eps_vir))
 
 
 def chain_flops(nao: int, nocc: int, nvir: int, naux: int) -> dict:
