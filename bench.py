@@ -164,7 +164,19 @@ def run_extras(dev, tb, only=None) -> dict:
             "torch_hipblaslt_ms": tl, "torch_tflops": fl / tl / 1e9,
         }  # fmt: skip
         log("gemm8192", out["gemm_fp32_8192"])
+        # the same product in bf16 (fp32 accumulate), NN and NT (B^T read in place)
+        Xb, Yb = X.bfloat16(), Y.bfloat16()
         del X, Y
+        tb_nn = gpu_time_ms(lambda: tb.gemm(1.0, Xb, Yb), reps=10, warm=2)
+        tb_nt = gpu_time_ms(lambda: tb.gemm(1.0, Xb, Yb, transB=True), reps=10, warm=2)
+        tlb = gpu_time_ms(lambda: torch.matmul(Xb, Yb), reps=10, warm=2)
+        out["gemm_bf16_8192"] = {
+            "nn_ms": tb_nn, "nn_tflops": fl / tb_nn / 1e9, "nt_ms": tb_nt, "nt_tflops": fl / tb_nt / 1e9,
+            "frac_bf16_peak_nt": fl / tb_nt / 1e9 / PEAK_BF16_MFMA,
+            "torch_hipblaslt_nn_ms": tlb, "torch_tflops": fl / tlb / 1e9,
+        }  # fmt: skip
+        log("gemm8192bf16", out["gemm_bf16_8192"])
+        del Xb, Yb
     if only is None or "c3" in only:
         # C3: fused pair energy vs the unfused GPU baseline (hipBLASLt GEMM + torch),
         # in both kernel arithmetics (bf16x6 is the default)
@@ -331,7 +343,7 @@ def main():
     syrk_ms = probe.mean_ms()
     achieved = SYRK_FLOP / (syrk_ms * 1e-3) / 1e12
     roofline = {
-        "kernel": "gemm_f32_dma_kernel<true, true, SYRK> (trnblas_hip_syrk)",
+        "kernel": "gemm_dma_kernel<float, true, true, SYRK> (trnblas_hip_syrk)",
         "bound": "mfma",
         "achieved": achieved,
         "peak": PEAK_FP32_MFMA,

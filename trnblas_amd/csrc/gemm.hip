@@ -11,8 +11,8 @@
 //    AGPR/VGPRs;
 //  * operand panels are staged in LDS, double buffered: the loads of k-tile
 //    t+1 are in flight while the MFMAs of k-tile t run, one barrier per
-//    k-tile (fp32 on 16-byte aligned operands: direct-to-LDS DMA,
-//    gemm_f32_dma_kernel; otherwise through registers, gemm_kernel);
+//    k-tile (16-byte aligned operands: direct-to-LDS DMA, gemm_dma_kernel;
+//    otherwise through registers, gemm_kernel);
 //  * an operand whose K dimension is contiguous in HBM is kept K-contiguous
 //    in LDS (rows padded by 16 bytes, so each 16-byte fragment read is
 //    bank-conflict free); one whose M / N dimension is contiguous (a
@@ -375,34 +375,52 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1)
   }
 }
 
-// fp32 GEMM / SYRK on 16-byte aligned operands: the tile, wave split, MFMA
-// (v_mfma_f32_32x32x2_f32) and k order of gemm_kernel, with the operand
-// panels moved by LDS DMA (buffer_load_dwordx4 ... lds) instead of through
-// registers. 32-wide k-tiles in two LDS stages; after the barrier that
-// publishes k-tile t every wave reads all its fragments of k-tile t, then
-// issues the DMA of k-tile t + 1 into the other stage, which lands behind
-// k-tile t's MFMAs: one barrier per k-tile, no staging registers and no LDS
-// stores. (The compiler makes an LDS read that follows an outstanding LDS
-// DMA wait for it, so no read may follow the DMA inside a k-tile.)
+// One 16-byte-per-lane LDS DMA (buffer_load_dwordx4 ... lds) of the wave:
+// lane l's group at offset voff of the resource lands at lds + 16 l. (A
+// non-template helper: the builtin with a type-dependent LDS pointer does
+// not instantiate in a kernel template's host pass.)
+__device__ __forceinline__ void lds_dma16(const void* base, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(base),
+                                           (__attribute__((address_space(3))) void*)lds, 16, voff,
+                                           0, 0, 0);
+}
+
+// GEMM / SYRK on 16-byte aligned operands (fp32, bf16, fp16): the tile,
+// wave split, MFMA (v_mfma_f32_32x32x2_f32, v_mfma_f32_32x32x16_{bf16,f16})
+// and k order of gemm_kernel, with the operand panels moved by LDS DMA
+// (buffer_load_dwordx4 ... lds) instead of through registers. k-tiles of
+// 128 bytes per K-contiguous row (32 fp32 / 64 bf16 or fp16 values) in two
+// LDS stages; after the barrier that publishes k-tile t every wave reads all
+// its fragments of k-tile t, then issues the DMA of k-tile t + 1 into the
+// other stage, which lands behind k-tile t's MFMAs: one barrier per k-tile,
+// no staging registers and no LDS stores. (The compiler makes an LDS read
+// that follows an outstanding LDS DMA wait for it, so no read may follow
+// the DMA inside a k-tile.)
 //
 // The panels have no row padding; their 16-byte groups are XOR-swizzled, so
 // a 1 KiB DMA block (lane l writes bytes 16 l .. 16 l + 15) is a set of
 // whole rows and the fragment reads are bank-conflict free:
-//  * K-contiguous panel, 128 rows of 32 k (128 bytes): group q of row r sits
-//    in slot q ^ ((r >> 1) & 7); a DMA block is 8 rows;
-//  * M/N-contiguous panel, 32 rows k of 128 columns (512 bytes): group q of
-//    row k sits in slot q ^ (8 ((k >> 2) & 1)); a DMA block is 2 rows.
+//  * K-contiguous panel, 128 rows of 128 bytes: group q of row r sits in
+//    slot q ^ ((r >> 1) & 7); a DMA block is 8 rows;
+//  * M/N-contiguous panel, rows k of 128 values (512 or 256 bytes): group q
+//    of row k sits in slot q ^ (2 sizeof(T) ((k / EV) & 1)), which moves the
+//    second lane half's column reads (k + EV) onto the other half of the
+//    banks; a DMA block is 2 (fp32) or 4 rows.
 // Lane l of a DMA block loads the global group that belongs in its slot
 // (the swizzles are their own inverses), so each row's lanes still read the
 // row's bytes exactly once. Ragged edges: a group outside the matrix gets
 // an offset past the buffer's records and reads as zeros (VEC operands:
 // every 16-byte group is wholly inside or outside).
-template <bool AKC, bool BKC, bool SYRK>
-__global__ __launch_bounds__(256, 2) void gemm_f32_dma_kernel(GemmArgs g) {
-  constexpr int BM = 128, BN = 128, BK = 32, WM = 64, WN = 64, FM = 2, FN = 2;
-  constexpr int PANEL = 128 * BK;  // floats of one operand panel (16 KiB)
-  __shared__ __attribute__((aligned(16))) float st0[2 * PANEL];
-  __shared__ __attribute__((aligned(16))) float st1[2 * PANEL];
+template <typename T, bool AKC, bool BKC, bool SYRK>
+__global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
+  constexpr int EV = 16 / sizeof(T);  // values per 16-byte group
+  constexpr int BM = 128, BN = 128, BK = 128 / sizeof(T), WM = 64, WN = 64, FM = 2, FN = 2;
+  constexpr int CH = 2 * EV;          // k per fragment chunk (both lane halves)
+  constexpr int PANEL = 128 * BK;     // values of one operand panel (16 KiB)
+  constexpr int MG = 128 / EV;        // 16-byte groups in an M/N-contiguous row
+  constexpr int MSW = 2 * sizeof(T);  // M/N swizzle (groups)
+  __shared__ __attribute__((aligned(16))) T st0[2 * PANEL];
+  __shared__ __attribute__((aligned(16))) T st1[2 * PANEL];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -418,50 +436,47 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dma_kernel(GemmArgs g) {
     int bat, tm, tn;
     decode_tile<SYRK>(g, t, bat, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const float* A = static_cast<const float*>(g.A) + bat * g.sA;
-    const float* B = static_cast<const float*>(g.B) + bat * g.sB;
+    const T* A = static_cast<const T*>(g.A) + bat * g.sA;
+    const T* B = static_cast<const T*>(g.B) + bat * g.sB;
 
     // the DMA of k-tile kt into stage st (A panel, then B panel)
-    auto dma = [&](float* st, int kt) {
+    auto dma = [&](T* st, int kt) {
       const int k0 = kt * BK;
-      const float* pa = AKC ? A + (int64_t)m0 * g.lda + k0 : A + (int64_t)k0 * g.lda + m0;
-      const float* pb = BKC ? B + (int64_t)n0 * g.ldb + k0 : B + (int64_t)k0 * g.ldb + n0;
+      const T* pa = AKC ? A + (int64_t)m0 * g.lda + k0 : A + (int64_t)k0 * g.lda + m0;
+      const T* pb = BKC ? B + (int64_t)n0 * g.ldb + k0 : B + (int64_t)k0 * g.ldb + n0;
       // rows / columns of the matrix left from the panel's corner
       const int ra = AKC ? M - m0 : K - k0, ca = AKC ? K - k0 : M - m0;
       const int rb = BKC ? N - n0 : K - k0, cb = BKC ? K - k0 : N - n0;
       // wave w fills blocks 4 w .. 4 w + 3 of each panel. KC block b: row
       // 8 b + l / 8, global group (l % 8) ^ swizzle; MN block b: row
-      // 2 b + l / 32, global group (l % 32) ^ swizzle.
+      // (64 / MG) b + l / MG, global group (l % MG) ^ swizzle.
       auto geo = [&](bool kc, int u, int& row, int& grp) __attribute__((always_inline)) {
         const int b = 4 * wave + u;
         if (kc) {
           row = 8 * b + (lane >> 3);
           grp = (lane & 7) ^ ((row >> 1) & 7);
         } else {
-          row = 2 * b + (lane >> 5);
-          grp = (lane & 31) ^ (8 * ((row >> 2) & 1));
+          row = (64 / MG) * b + lane / MG;
+          grp = (lane % MG) ^ (MSW * ((row / EV) & 1));
         }
       };
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         int rw, gp;
         geo(AKC, u, rw, gp);
-        const bool oka = rw < ra && 4 * gp < ca;
-        const uint32_t va = oka ? (uint32_t)((int64_t)rw * g.lda * 4 + 16 * gp) : kOob;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            make_rsrc(pa), (__attribute__((address_space(3))) void*)(st + (4 * wave + u) * 256), 16,
-            va, 0, 0, 0);
+        const bool oka = rw < ra && EV * gp < ca;
+        const uint32_t va =
+            oka ? (uint32_t)((int64_t)rw * g.lda * (int64_t)sizeof(T) + 16 * gp) : kOob;
+        lds_dma16(pa, st + (4 * wave + u) * (1024 / sizeof(T)), va);
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         int rw, gp;
         geo(BKC, u, rw, gp);
-        const bool okb = rw < rb && 4 * gp < cb;
-        const uint32_t vb = okb ? (uint32_t)((int64_t)rw * g.ldb * 4 + 16 * gp) : kOob;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            make_rsrc(pb),
-            (__attribute__((address_space(3))) void*)(st + PANEL + (4 * wave + u) * 256), 16, vb,
-            0, 0, 0);
+        const bool okb = rw < rb && EV * gp < cb;
+        const uint32_t vb =
+            okb ? (uint32_t)((int64_t)rw * g.ldb * (int64_t)sizeof(T) + 16 * gp) : kOob;
+        lds_dma16(pb, st + PANEL + (4 * wave + u) * (1024 / sizeof(T)), vb);
       }
     };
 
@@ -474,24 +489,28 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dma_kernel(GemmArgs g) {
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     // Fragment of the lane's row r (32 rows per MFMA block) at k offset kk
-    // (4 consecutive k, kk a multiple of 4): one 16-byte read from a
-    // K-contiguous panel, 4 column reads from an M/N-contiguous one.
-    auto frag = [&](const float* p, bool kc, int r, int kk) __attribute__((always_inline)) {
-      if (kc) return *reinterpret_cast<const i32x4*>(p + r * 32 + 4 * ((kk >> 2) ^ ((r >> 1) & 7)));
-      const float* q = p + 4 * ((r >> 2) ^ (8 * ((kk >> 2) & 1))) + (r & 3);
-      f32x4 v;
+    // (EV consecutive k, kk a multiple of EV): one 16-byte read from a
+    // K-contiguous panel, EV column reads from an M/N-contiguous one.
+    auto frag = [&](const T* p, bool kc, int r, int kk) __attribute__((always_inline)) {
+      if (kc)
+        return *reinterpret_cast<const i32x4*>(p + r * BK + EV * ((kk / EV) ^ ((r >> 1) & 7)));
+      const T* q = p + EV * ((r / EV) ^ (MSW * ((kk / EV) & 1))) + (r % EV);
+      union {
+        i32x4 v;
+        T e[EV];
+      } u;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = q[(kk + e) * 128];
-      return __builtin_bit_cast(i32x4, v);
+      for (int e = 0; e < EV; ++e) u.e[e] = q[(kk + e) * 128];
+      return u.v;
     };
     // One k-tile from stage `cur`: every fragment of the k-tile is read into
     // registers (64 VGPRs) before the DMA of k-tile `next` (< 0: none) into
     // the other stage issues, then the 64 MFMAs run behind that DMA.
-    auto step = [&](const float* cur, float* oth, int next) __attribute__((always_inline)) {
-      i32x4 fa[BK / 8][FM], fb[BK / 8][FN];
+    auto step = [&](const T* cur, T* oth, int next) __attribute__((always_inline)) {
+      i32x4 fa[BK / CH][FM], fb[BK / CH][FN];
 #pragma unroll
-      for (int c = 0; c < BK / 8; ++c) {
-        const int kk = c * 8 + (lane >> 5) * 4;
+      for (int c = 0; c < BK / CH; ++c) {
+        const int kk = c * CH + (lane >> 5) * EV;
 #pragma unroll
         for (int i = 0; i < FM; ++i) fa[c][i] = frag(cur, AKC, wm0 + i * 32 + (lane & 31), kk);
 #pragma unroll
@@ -500,11 +519,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dma_kernel(GemmArgs g) {
       }
       if (next >= 0) dma(oth, next);
 #pragma unroll
-      for (int c = 0; c < BK / 8; ++c)
+      for (int c = 0; c < BK / CH; ++c)
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-          for (int j = 0; j < FN; ++j) mma_frag(acc[i][j], fa[c][i], fb[c][j], (float*)nullptr);
+          for (int j = 0; j < FN; ++j) mma_frag(acc[i][j], fa[c][i], fb[c][j], (T*)nullptr);
     };
 
     __syncthreads();  // a previous segment's reads of both stages are done
@@ -518,7 +537,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dma_kernel(GemmArgs g) {
       __syncthreads();
       step(st1, st0, kt + 2 < kb1 ? kt + 2 : -1);
     }
-    store_tile<float, SYRK, FM, FN, BM, BN>(g, acc, bat, m0, n0, wm0, wn0, lane, slot, w);
+    store_tile<T, SYRK, FM, FN, BM, BN>(g, acc, bat, m0, n0, wm0, wn0, lane, slot, w);
   };
 
   // Work of this workgroup, walked with one call site of `segment` (two
@@ -605,8 +624,8 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs g) {
 template <typename T>
 struct Cfg {
   static constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
-  // k-tile of gemm_kernel: 32 (two LDS stages). (fp32 with 16-byte aligned
-  // operands runs gemm_f32_dma_kernel, also with 32-wide k-tiles.)
+  // k-tile of gemm_kernel: 32 (two LDS stages). (16-byte aligned operands
+  // run gemm_dma_kernel, with 128-byte k-tiles.)
   template <bool VEC>
   static constexpr int bk() {
     return 32;
@@ -655,12 +674,12 @@ static int choose_sk(GemmArgs& g, int occupancy, size_t ws_bytes) {
 template <typename T, bool AKC, bool BKC, bool VEC, bool SYRK>
 static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   using C = Cfg<T>;
-  constexpr bool DMA = sizeof(T) == 4 && VEC;  // fp32 on aligned operands: gemm_f32_dma_kernel
-  constexpr int BK = DMA ? 32 : C::template bk<VEC>();
+  constexpr bool DMA = VEC;  // aligned operands: gemm_dma_kernel
+  constexpr int BK = DMA ? 128 / (int)sizeof(T) : C::template bk<VEC>();
   g.nk = (g.K + BK - 1) / BK;
   void (*kern)(GemmArgs);
   if constexpr (DMA)
-    kern = gemm_f32_dma_kernel<AKC, BKC, SYRK>;
+    kern = gemm_dma_kernel<T, AKC, BKC, SYRK>;
   else
     kern = gemm_kernel<T, C::BM, C::BN, BK, C::WM, C::WN, AKC, BKC, VEC, SYRK>;
   int occ = 0;
@@ -700,7 +719,7 @@ static int elem_size(int dtype) { return dtype == TRNBLAS_F32 ? 4 : 2; }
 
 // Largest k-tile of the launch configurations for `dtype` (panel-span check).
 static int k_tile(int dtype) {
-  return dtype == TRNBLAS_F32 ? Cfg<float>::bk<true>() : Cfg<__bf16>::bk<true>();
+  return 128 / elem_size(dtype);  // gemm_dma_kernel's (gemm_kernel's is 32, no larger)
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
