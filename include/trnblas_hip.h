@@ -98,9 +98,24 @@ int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64_t K, doubl
                      void* stream);
 
 /*
+ * SYRK as trnblas_hip_syrk, with the referenced triangle of C chosen on the
+ * device from `flags` (device int32[2] as written by
+ * trnblas_hip_triangle_nonzero on the same stream): the `uplo` triangle, or
+ * the other one when only that one holds off-diagonal entries. Replaces
+ * `_resolve_syrk_uplo` + syrk of trnblas/level3.py:285-287, :305-329 without
+ * a host round trip between the triangle check and the product (the host
+ * reads the flags afterwards, for the DeprecationWarning). flags may be NULL
+ * only when beta == 0.
+ */
+int trnblas_hip_syrk_flagged(int dtype, int uplo, int trans, int64_t N, int64_t K, double alpha,
+                             const void* A, int64_t lda, double beta, const void* C, int64_t ldc,
+                             void* D, int64_t ldd, const int32_t* flags, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/*
  * Which strict triangles of the n x n matrix C hold a nonzero entry (NaN
  * counts as nonzero): flags[0] = strictly upper, flags[1] = strictly lower
- * (device int32[2], written by this call). The triangle rule of SYRK's C
+ * (device int32[2], 8-byte aligned, written by this call). The triangle rule of SYRK's C
  * argument, trnblas/level3.py:305-329 (`_resolve_syrk_uplo`), as one pass
  * over C on the device. dtype as in trnblas_hip_gemm.
  */

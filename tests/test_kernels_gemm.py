@@ -137,3 +137,107 @@ def test_syrk_stream_k(dev, n, k, uplo):
     den = Ad.abs() @ Ad.abs().T + 0.5 * Cs.double().abs()
     tol = max(1e-6, 2 * k**0.5 * 2.0**-24)
     assert ((D.double() - ref).abs() / den).max().item() <= tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2.0**-8), (torch.float16, 2.0**-11)])
+@pytest.mark.parametrize("n,k", [(384, 200), (300, 77)])
+@pytest.mark.parametrize("uplo", ["lower", "upper"])
+def test_syrk_16bit(dev, dtype, tol, n, k, uplo):
+    # 16-bit SYRK: (384, 200) runs the direct-to-LDS kernel with whole
+    # interior tiles (vector mirrored stores of 8 bytes), (300, 77) the
+    # register-staged kernel with ragged edges. The only rounding beyond
+    # fp32 accumulation is the final one to the 16-bit output.
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(n * 7 + k)
+    A = torch.randn(n, k, generator=g).to(dtype)
+    X = torch.randn(n, n, generator=g).to(dtype)
+    D = kernels.syrk(A.to(dev), 1.0, 0.5, X.to(dev), uplo=uplo).cpu()
+    assert D.dtype == dtype and torch.equal(D, D.T)
+    Xd = X.double()
+    Cs = torch.tril(Xd) + torch.tril(Xd, -1).T if uplo == "lower" else torch.triu(Xd) + torch.triu(Xd, 1).T
+    Ad = A.double()
+    ref = Ad @ Ad.T + 0.5 * Cs
+    den = Ad.abs() @ Ad.abs().T + 0.5 * Cs.abs()
+    assert ((D.double() - ref).abs() / den).max().item() <= tol
+
+
+def _tri_flags_ref(X):
+    up = bool((torch.triu(X, 1) != 0).any())
+    lo = bool((torch.tril(X, -1) != 0).any())
+    return up, lo
+
+
+@pytest.mark.parametrize("n", [1, 2, 77, 1024, 1500, 2100])
+def test_triangle_nonzero_patterns(dev, n):
+    # one pass of the device check against torch on patterns that make it
+    # scan everything (empty triangles, a single entry in the far corner of
+    # a triangle) and ones it decides early (filled C); NaN counts as nonzero
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(n)
+    full = torch.randn(n, n, generator=g)
+    pats = {"full": full, "lower": torch.tril(full), "upper": torch.triu(full),
+            "diag": torch.diag(torch.diagonal(full)), "zero": torch.zeros(n, n)}
+    if n > 1:
+        one_lo = torch.zeros(n, n)
+        one_lo[n - 1, 0] = 3.0
+        one_up = torch.zeros(n, n)
+        one_up[0, n - 1] = float("nan")
+        pats["corner_lo"] = one_lo
+        pats["corner_up_nan"] = one_up
+    for name, X in pats.items():
+        for dtype in (torch.float32, torch.bfloat16):
+            Xd = X.to(dtype).to(dev)
+            for uplo in ("upper", "lower"):
+                up, lo = _tri_flags_ref(X)
+                want = (up, lo) if uplo == "upper" else (lo, up)
+                assert kernels.triangle_nonzero(Xd, uplo) == want, (name, dtype, uplo)
+
+
+@pytest.mark.parametrize("n,k", [(512, 96), (300, 77)])
+@pytest.mark.parametrize("stored", ["full", "lower", "upper", "diag"])
+@pytest.mark.parametrize("uplo", ["upper", "lower"])
+def test_syrk_checked_triangle_rule(dev, n, k, stored, uplo):
+    # the referenced triangle decided on the device: the flags returned and
+    # the product must follow the host rule (level3.py:305-329)
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(n + k)
+    A = torch.randn(n, k, generator=g)
+    full = torch.randn(n, n, generator=g)
+    X = {"full": full, "lower": torch.tril(full), "upper": torch.triu(full),
+         "diag": torch.diag(torch.diagonal(full))}[stored]
+    D, mine, theirs = kernels.syrk_checked(A.to(dev), 1.0, 0.5, X.to(dev), uplo=uplo)
+    up, lo = _tri_flags_ref(X)
+    assert (mine, theirs) == ((up, lo) if uplo == "upper" else (lo, up))
+    other = "lower" if uplo == "upper" else "upper"
+    side = other if (theirs and not mine) else uplo
+    D = D.cpu()
+    assert torch.equal(D, D.T)
+    Xd = X.double()
+    Cs = torch.tril(Xd) + torch.tril(Xd, -1).T if side == "lower" else torch.triu(Xd) + torch.triu(Xd, 1).T
+    Ad = A.double()
+    ref = Ad @ Ad.T + 0.5 * Cs
+    den = Ad.abs() @ Ad.abs().T + 0.5 * Cs.abs()
+    tol = max(1e-6, 2 * k**0.5 * 2.0**-24)
+    assert ((D.double() - ref).abs() / den).max().item() <= tol
+    # the same product through the fixed-triangle entry point, bit for bit
+    D2 = kernels.syrk(A.to(dev), 1.0, 0.5, X.to(dev), uplo=side).cpu()
+    assert torch.equal(D, D2)
+
+
+def test_syrk_unaligned_c_ld(dev):
+    # a C whose leading dimension is not a multiple of 4 (no vector access
+    # to C or D's mirror): the scalar epilogue, same values
+    from trnblas_amd.hip import kernels
+
+    n, k = 384, 64
+    g = torch.Generator().manual_seed(5)
+    A = torch.randn(n, k, generator=g).to(dev)
+    big = torch.randn(n, n + 3, generator=g).to(dev)
+    Xv = big[:, :n]  # ldc = n + 3
+    D1 = kernels.syrk(A, 1.0, 0.5, Xv, uplo="upper")
+    D2 = kernels.syrk(A, 1.0, 0.5, Xv.contiguous(), uplo="upper")
+    torch.cuda.synchronize()
+    assert torch.equal(D1, D2)

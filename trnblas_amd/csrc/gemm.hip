@@ -49,6 +49,8 @@ struct GemmArgs {
   int ntiles;            // tiles of the launch (all batch entries, or the SYRK triangle)
   int nk;                // k-tiles per tile
   int uplo;              // SYRK: 0 = lower triangle of C referenced, 1 = upper
+  const int32_t* tri;    // SYRK: triangle flags of C (device), or null; see syrk_upper
+  int vec4;              // SYRK: C and D take 4-element vector accesses (aligned, ld % 4 == 0)
   int sk_groups;         // stream-K workgroups (0 = data-parallel)
   int dp_tiles;          // under stream-K: leading tiles computed whole
   float* ws;             // stream-K partial tiles [sk_groups][2][BM * BN]
@@ -148,17 +150,32 @@ __device__ __forceinline__ void tri_tile(int t, int& tm, int& tn) {
   tn = t - r * (r + 1) / 2;
 }
 
+// SYRK: whether the upper triangle of C is the one referenced: g.uplo, or,
+// with triangle flags (flags[0]: the strict upper triangle holds a nonzero,
+// flags[1]: the strict lower one), the other triangle when only that one
+// holds off-diagonal entries (the rule of trnblas/level3.py:305-329, decided
+// on the device so the host need not wait for the flags before the launch).
+__device__ __forceinline__ int syrk_upper(const GemmArgs& g) {
+  int up = g.uplo;
+  if (g.tri != nullptr) {
+    const int has_up = g.tri[0], has_lo = g.tri[1];
+    if (up ? (has_lo && !has_up) : (has_up && !has_lo)) up ^= 1;
+  }
+  return up;
+}
+
 // D = alpha acc + beta C for one output element (C not read when beta == 0);
-// SYRK: m >= n only, written to both triangles, C read from the uplo side.
+// SYRK: m >= n only, written to both triangles, C read from the side `up`
+// (syrk_upper).
 template <typename T, bool SYRK>
 __device__ __forceinline__ void store_out(const GemmArgs& g, const T* C, T* D, int m, int n,
-                                          float acc) {
+                                          float acc, int up = 0) {
   if (SYRK) {
     if (m < g.M && n <= m) {
       float v = g.alpha * acc;
       if (g.beta != 0.0f) {
-        const int64_t ci = g.uplo ? (int64_t)n * g.ldc + m : (int64_t)m * g.ldc + n;
-        v += g.beta * to_f32(C[ci]);
+        const int64_t ci = up ? (int64_t)n * g.ldc + m : (int64_t)m * g.ldc + n;
+        v = __builtin_fmaf(g.beta, to_f32(C[ci]), v);  // one rounding, in every epilogue
       }
       const T o = (T)v;
       D[(int64_t)m * g.ldd + n] = o;
@@ -166,9 +183,40 @@ __device__ __forceinline__ void store_out(const GemmArgs& g, const T* C, T* D, i
     }
   } else if (m < g.M && n < g.N) {
     float v = g.alpha * acc;
-    if (g.beta != 0.0f) v += g.beta * to_f32(C[(int64_t)m * g.ldc + n]);
+    if (g.beta != 0.0f) v = __builtin_fmaf(g.beta, to_f32(C[(int64_t)m * g.ldc + n]), v);
     D[(int64_t)m * g.ldd + n] = (T)v;
   }
+}
+
+// Four consecutive values of T at p (4-element aligned) as floats, and back
+// (one 16-byte access for fp32, 8 bytes for 16-bit types).
+template <typename T>
+__device__ __forceinline__ void load4(const T* p, float (&v)[4]) {
+  union {
+    u32x2 u2;
+    f32x4 f;
+    T e[4];
+  } x;
+  if constexpr (sizeof(T) == 4)
+    x.f = *reinterpret_cast<const f32x4*>(p);
+  else
+    x.u2 = *reinterpret_cast<const u32x2*>(p);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = to_f32(x.e[e]);
+}
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const float (&v)[4]) {
+  union {
+    u32x2 u2;
+    f32x4 f;
+    T e[4];
+  } x;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) x.e[e] = (T)v[e];
+  if constexpr (sizeof(T) == 4)
+    *reinterpret_cast<f32x4*>(p) = x.f;
+  else
+    *reinterpret_cast<u32x2*>(p) = x.u2;
 }
 
 // Tile t -> (batch, tile row, tile column).
@@ -201,6 +249,43 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const f32x16 (&acc
   if (slot < 0) {
     const T* C = static_cast<const T*>(g.C) + (g.C ? bat * g.sC : 0);
     T* D = static_cast<T*>(g.D) + bat * g.sD;
+    const int up = SYRK ? syrk_upper(g) : 0;
+    if (SYRK && m0 > n0 && m0 + BM <= g.M && g.vec4) {
+      // A SYRK tile strictly below the diagonal with every row inside: each
+      // lane's registers r = 4 s .. 4 s + 3 are 4 consecutive rows of one
+      // column, so the mirrored values D[n][m .. m + 3] (and C[n][m .. m + 3]
+      // when the upper triangle is referenced) move as one vector per lane.
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int mb = m0 + wm0 + i * 32 + (lane >> 5) * 4;
+          const int n = n0 + wn0 + j * 32 + (lane & 31);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int m = mb + 8 * s;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = g.alpha * acc[i][j][4 * s + e];
+            if (g.beta != 0.0f) {
+              if (up) {
+                float c[4];
+                load4(C + (int64_t)n * g.ldc + m, c);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = __builtin_fmaf(g.beta, c[e], v[e]);
+              } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  v[e] = __builtin_fmaf(g.beta, to_f32(C[(int64_t)(m + e) * g.ldc + n]), v[e]);
+              }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) D[(int64_t)(m + e) * g.ldd + n] = (T)v[e];
+            store4(D + (int64_t)n * g.ldd + m, v);
+          }
+        }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -209,7 +294,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const f32x16 (&acc
         const int n = n0 + wn0 + j * 32 + (lane & 31);
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          store_out<T, SYRK>(g, C, D, mb + (r >> 2) * 8 + (r & 3), n, acc[i][j][r]);
+          store_out<T, SYRK>(g, C, D, mb + (r >> 2) * 8 + (r & 3), n, acc[i][j][r], up);
       }
   } else {
     float* P = g.ws + ((int64_t)w * 2 + slot) * (BM * BN);
@@ -506,24 +591,33 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
     // One k-tile from stage `cur`: every fragment of the k-tile is read into
     // registers (64 VGPRs) before the DMA of k-tile `next` (< 0: none) into
     // the other stage issues, then the 64 MFMAs run behind that DMA.
+    // On a SYRK diagonal tile the wave of rows 0-63, columns 64-127 holds
+    // only entries above the diagonal: it moves its share of the panels and
+    // keeps the barriers, but reads no fragments and runs no MFMAs (its
+    // accumulators stay zero and its store writes nothing).
+    const bool busy = !(SYRK && tm == tn && wn0 > wm0);
     auto step = [&](const T* cur, T* oth, int next) __attribute__((always_inline)) {
       i32x4 fa[BK / CH][FM], fb[BK / CH][FN];
+      if (busy) {
 #pragma unroll
-      for (int c = 0; c < BK / CH; ++c) {
-        const int kk = c * CH + (lane >> 5) * EV;
+        for (int c = 0; c < BK / CH; ++c) {
+          const int kk = c * CH + (lane >> 5) * EV;
 #pragma unroll
-        for (int i = 0; i < FM; ++i) fa[c][i] = frag(cur, AKC, wm0 + i * 32 + (lane & 31), kk);
+          for (int i = 0; i < FM; ++i) fa[c][i] = frag(cur, AKC, wm0 + i * 32 + (lane & 31), kk);
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-          fb[c][j] = frag(cur + PANEL, BKC, wn0 + j * 32 + (lane & 31), kk);
+          for (int j = 0; j < FN; ++j)
+            fb[c][j] = frag(cur + PANEL, BKC, wn0 + j * 32 + (lane & 31), kk);
+        }
       }
       if (next >= 0) dma(oth, next);
+      if (busy) {
 #pragma unroll
-      for (int c = 0; c < BK / CH; ++c)
+        for (int c = 0; c < BK / CH; ++c)
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+          for (int i = 0; i < FM; ++i)
 #pragma unroll
-          for (int j = 0; j < FN; ++j) mma_frag(acc[i][j], fa[c][i], fb[c][j], (T*)nullptr);
+            for (int j = 0; j < FN; ++j) mma_frag(acc[i][j], fa[c][i], fb[c][j], (T*)nullptr);
+      }
     };
 
     __syncthreads();  // a previous segment's reads of both stages are done
@@ -615,10 +709,11 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs g) {
   const int r = blockIdx.y * ROWS + threadIdx.x / (BN / 4);
   const int c = (threadIdx.x % (BN / 4)) * 4;
   const int e = r * BN + c;
+  const int up = SYRK ? syrk_upper(g) : 0;
   f32x4 v = *reinterpret_cast<const f32x4*>(g.ws + src[0] + e);
   for (int q = 1; q < nc; ++q) v += *reinterpret_cast<const f32x4*>(g.ws + src[q] + e);
 #pragma unroll
-  for (int u = 0; u < 4; ++u) store_out<T, SYRK>(g, C, D, m0 + r, n0 + c + u, v[u]);
+  for (int u = 0; u < 4; ++u) store_out<T, SYRK>(g, C, D, m0 + r, n0 + c + u, v[u], up);
 }
 
 template <typename T>
@@ -819,11 +914,10 @@ extern "C" int trnblas_hip_gemm(int dtype, int transA, int transB, int64_t M, in
                          (hipStream_t)stream);
 }
 
-extern "C" int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64_t K,
-                                double alpha, const void* A, int64_t lda, double beta,
-                                const void* C, int64_t ldc, void* D, int64_t ldd,
-                                void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
+static int syrk_impl(int dtype, int uplo, int trans, int64_t N, int64_t K, double alpha,
+                     const void* A, int64_t lda, double beta, const void* C, int64_t ldc, void* D,
+                     int64_t ldd, const int32_t* tri, void* workspace, size_t workspace_bytes,
+                     void* stream) {
   TRNBLAS_CHECK_ARG(dtype == TRNBLAS_F32 || dtype == TRNBLAS_BF16 || dtype == TRNBLAS_F16,
                     "syrk: dtype %d not supported", dtype);
   TRNBLAS_CHECK_ARG(N >= 0 && K >= 0, "syrk: negative size");
@@ -855,6 +949,10 @@ extern "C" int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64
   g.sD = 0;
   g.batch = 1;
   g.uplo = uplo ? 1 : 0;
+  g.tri = beta != 0.0 ? tri : nullptr;
+  const size_t vb = 4 * (size_t)elem_size(dtype);
+  g.vec4 = (ldd % 4 == 0) && ((uintptr_t)D % vb == 0) &&
+           (beta == 0.0 || ((ldc % 4 == 0) && ((uintptr_t)C % vb == 0)));
   const int t = (int)((N + kTileM - 1) / kTileM);
   g.tiles_m = g.tiles_n = t;
   g.ntiles = (int)((int64_t)t * (t + 1) / 2);
@@ -866,69 +964,170 @@ extern "C" int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64
                         (hipStream_t)stream);
 }
 
+extern "C" int trnblas_hip_syrk(int dtype, int uplo, int trans, int64_t N, int64_t K,
+                                double alpha, const void* A, int64_t lda, double beta,
+                                const void* C, int64_t ldc, void* D, int64_t ldd,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  return syrk_impl(dtype, uplo, trans, N, K, alpha, A, lda, beta, C, ldc, D, ldd, nullptr,
+                   workspace, workspace_bytes, stream);
+}
+
+extern "C" int trnblas_hip_syrk_flagged(int dtype, int uplo, int trans, int64_t N, int64_t K,
+                                        double alpha, const void* A, int64_t lda, double beta,
+                                        const void* C, int64_t ldc, void* D, int64_t ldd,
+                                        const int32_t* flags, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  clear_error();
+  TRNBLAS_CHECK_ARG(flags != nullptr || beta == 0.0, "syrk_flagged: NULL flags");
+  return syrk_impl(dtype, uplo, trans, N, K, alpha, A, lda, beta, C, ldc, D, ldd, flags,
+                   workspace, workspace_bytes, stream);
+}
+
 // Which strict triangles of an n x n matrix hold a nonzero (NaN counts), for
 // the SYRK triangle rule (trnblas/level3.py:305-329): flags[0] = upper,
 // flags[1] = lower.
 namespace trnblas {
 
-__global__ void zero_flags_kernel(int32_t* flags) {
-  if (threadIdx.x < 2) flags[threadIdx.x] = 0;
+// Sets the flags from a sample: wave w reads the 1024 columns around the
+// diagonal of row {n/2, n/4, 3n/4, n-1}[w] (n = 0: zeros). A C with entries
+// in both triangles is decided here, by two plain stores, so the waves of
+// the full pass that follows find both flags set and stop at once (stores
+// from thousands of waves to one address serialise in the L2).
+template <typename T>
+__global__ __launch_bounds__(256) void tri_sample_kernel(int n, const T* C, int64_t ldc,
+                                                         int32_t* flags) {
+  __shared__ int s_up[4], s_lo[4];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int up = 0, lo = 0;
+  if (n > 0) {
+    const int rows[4] = {n / 2, n / 4, (int)((3ll * n) / 4), n - 1};
+    const int r = __builtin_amdgcn_readfirstlane(w == 0 ? rows[0] : w == 1 ? rows[1] : w == 2 ? rows[2] : rows[3]);
+    const int cb = r - 512;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(C + (int64_t)r * ldc);
+    T v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int c = cb + 64 * u + lane;
+      const uint32_t off = (c >= 0 && c < n && c != r) ? (uint32_t)c * (uint32_t)sizeof(T) : kOob;
+      if constexpr (sizeof(T) == 4) {
+        v[u] = __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+      } else {
+        v[u] = __builtin_bit_cast(T, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int c = cb + 64 * u + lane;
+      const int nz = !(to_f32(v[u]) == 0.0f);
+      up |= nz & (c > r);
+      lo |= nz & (c < r);
+    }
+  }
+  up = __any(up);
+  lo = __any(lo);
+  if (lane == 0) {
+    s_up[w] = up;
+    s_lo[w] = lo;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    flags[0] = s_up[0] | s_up[1] | s_up[2] | s_up[3];
+    flags[1] = s_lo[0] | s_lo[1] | s_lo[2] | s_lo[3];
+  }
 }
 
-// A bounded grid strides over rows (4 rows per pass, one per wave; lanes
-// stride along the row, coalesced); one atomic per workgroup and flag.
+// Work items are (row, 1024-column chunk) pairs, one per wave at a time
+// over a grid of 2048 waves; a wave's lanes read 16 columns each (64 apart,
+// all loads in flight at once; columns outside the row's strict triangles
+// of interest read as zero through the buffer resource, with no access).
+// Before each item a wave reads both flags (one 8-byte load at device scope)
+// and skips the triangles already known to hold a nonzero; it stops once
+// both are known, from the flags or from its own items. A flag is set by a
+// plain store of 1 (every writer writes the same value: no read-modify-
+// write, so thousands of waves finding entries at once do not serialise on
+// atomics). A filled C is decided after about one item per wave; an empty
+// triangle costs one pass over it.
 template <typename T>
 __global__ __launch_bounds__(256) void triangle_nonzero_kernel(int n, const T* C, int64_t ldc,
                                                                int32_t* flags) {
   const int lane = threadIdx.x & 63;
-  // A small grid of waves scans rows; a wave skips the side(s) already known
-  // to hold a nonzero (flags set by any wave) and stops when both are known,
-  // so a filled C is decided after a few rows per wave.
-  for (int r = blockIdx.x * 4 + (threadIdx.x >> 6); r < n; r += gridDim.x * 4) {
-    const int fu = __atomic_load_n(&flags[0], __ATOMIC_RELAXED);
-    const int fl = __atomic_load_n(&flags[1], __ATOMIC_RELAXED);
+  const int nch = (n + 1023) >> 10;
+  const int64_t items = (int64_t)n * nch;
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  int64_t* both = reinterpret_cast<int64_t*>(flags);
+  int fu = 0, fl = 0;  // known by this wave
+  for (int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); q < items; q += stride) {
+    const int64_t f = __hip_atomic_load(both, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    fu |= (int)(f & 0xffffffff) != 0;
+    fl |= (int)(f >> 32) != 0;
+    fu = __builtin_amdgcn_readfirstlane(fu);
+    fl = __builtin_amdgcn_readfirstlane(fl);
     if (fu && fl) break;
-    const T* row = C + (int64_t)r * ldc;
+    const int r = (int)(q / nch);
+    const int c0 = (int)(q - (int64_t)r * nch) * 1024;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(C + (int64_t)r * ldc);
+    T v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int c = c0 + 64 * u + lane;
+      const bool want = c < n && ((c > r && !fu) || (c < r && !fl));
+      const uint32_t off = want ? (uint32_t)c * (uint32_t)sizeof(T) : kOob;
+      if constexpr (sizeof(T) == 4) {
+        v[u] = __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+      } else {
+        v[u] = __builtin_bit_cast(T, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0));
+      }
+    }
     int up = 0, lo = 0;
-    const int cb = fl ? r + 1 : 0, ce = fu ? r : n;  // columns still of interest
-    for (int c = cb + lane; c < ce; c += 64) {
-      const int nz = !((float)row[c] == 0.0f);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int c = c0 + 64 * u + lane;
+      const int nz = !(to_f32(v[u]) == 0.0f);  // NaN counts as nonzero
       up |= nz & (c > r);
       lo |= nz & (c < r);
     }
     up = __any(up);
     lo = __any(lo);
     if (lane == 0) {
-      if (up && !fu) atomicOr(&flags[0], 1);
-      if (lo && !fl) atomicOr(&flags[1], 1);
+      if (up && !fu) __hip_atomic_store(&flags[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lo && !fl) __hip_atomic_store(&flags[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    fu |= up;
+    fl |= lo;
   }
 }
 
 }  // namespace trnblas
+
+template <typename T>
+static void launch_triangle(int64_t n, const void* C, int64_t ldc, int32_t* flags, hipStream_t s) {
+  const T* c = static_cast<const T*>(C);
+  hipLaunchKernelGGL(tri_sample_kernel<T>, dim3(1), dim3(256), 0, s, (int)n, c, ldc, flags);
+  if (n < 2) return;
+  const int64_t items = n * ((n + 1023) / 1024);
+  const int64_t blocks = std::min<int64_t>((items + 3) / 4, 512);
+  hipLaunchKernelGGL(triangle_nonzero_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s, (int)n,
+                     c, ldc, flags);
+}
 
 extern "C" int trnblas_hip_triangle_nonzero(int dtype, int64_t n, const void* C, int64_t ldc,
                                             int32_t* flags, void* stream) {
   clear_error();
   hipStream_t s = (hipStream_t)stream;
   TRNBLAS_CHECK_ARG(n >= 0 && n < (1 << 30), "triangle_nonzero: bad n");
-  TRNBLAS_CHECK_ARG(flags != nullptr, "triangle_nonzero: NULL flags");
-  hipLaunchKernelGGL(zero_flags_kernel, dim3(1), dim3(64), 0, s, flags);
-  if (n == 0) return check_launch("triangle_nonzero");
-  TRNBLAS_CHECK_ARG(C != nullptr && ldc >= n, "triangle_nonzero: bad C / ldc");
-  const int64_t blocks = std::min<int64_t>((n + 3) / 4, 32);
+  TRNBLAS_CHECK_ARG(flags != nullptr && (uintptr_t)flags % 8 == 0,
+                    "triangle_nonzero: flags NULL or not 8-byte aligned");
+  if (n > 0) TRNBLAS_CHECK_ARG(C != nullptr && ldc >= n, "triangle_nonzero: bad C / ldc");
   switch (dtype) {
     case TRNBLAS_F32:
-      hipLaunchKernelGGL(triangle_nonzero_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, s,
-                         (int)n, (const float*)C, ldc, flags);
+      launch_triangle<float>(n, C, ldc, flags, s);
       break;
     case TRNBLAS_BF16:
-      hipLaunchKernelGGL(triangle_nonzero_kernel<__bf16>, dim3((unsigned)blocks), dim3(256), 0,
-                         s, (int)n, (const __bf16*)C, ldc, flags);
+      launch_triangle<__bf16>(n, C, ldc, flags, s);
       break;
     case TRNBLAS_F16:
-      hipLaunchKernelGGL(triangle_nonzero_kernel<_Float16>, dim3((unsigned)blocks), dim3(256), 0,
-                         s, (int)n, (const _Float16*)C, ldc, flags);
+      launch_triangle<_Float16>(n, C, ldc, flags, s);
       break;
     default:
       set_error("triangle_nonzero: dtype %d not supported", dtype);

@@ -19,7 +19,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 _PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("TRNBLAS_HIP_LIB", _PKG / "lib" / "libtrnblas_hip.so"))
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 F32, BF16, F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
@@ -48,6 +48,11 @@ SIGNATURES = {
         _c_int,
         [_c_int, _c_int, _c_int, _c_i64, _c_i64, _c_dbl, _c_ptr, _c_i64, _c_dbl, _c_ptr]
         + [_c_i64, _c_ptr, _c_i64, _c_ptr, _c_size, _c_ptr],
+    ),
+    "trnblas_hip_syrk_flagged": (
+        _c_int,
+        [_c_int, _c_int, _c_int, _c_i64, _c_i64, _c_dbl, _c_ptr, _c_i64, _c_dbl, _c_ptr]
+        + [_c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr],
     ),
     "trnblas_hip_triangle_nonzero": (_c_int, [_c_int, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr]),
     "trnblas_hip_pair_energy_workspace": (_c_size, [_c_i64, _c_i64]),

@@ -663,6 +663,28 @@ def hip_syrk(alpha, A, beta, C, trans: bool, uplo: str) -> torch.Tensor | None:
         return None
 
 
+def hip_syrk_checked(alpha, A, beta, C, trans: bool, uplo: str):
+    """SYRK with beta != 0 and an n x n C of A's dtype whose referenced
+    triangle is decided on the device (`kernels.syrk_checked`): (D, the uplo
+    triangle has an off-diagonal nonzero, the other triangle has one), or
+    None when the route is not a kernel route."""
+    n = A.shape[1] if trans else A.shape[0]
+    k = A.shape[0] if trans else A.shape[1]
+    route = _gemm_route(A, C, op="syrk", macs=n * n * k, nbytes=(n * k + 2 * n * n) * A.element_size())
+    if route not in ("hip", "upload"):
+        return None
+    from . import kernels
+
+    dev = _gpu_device(A, C)
+    orig = A.device
+    try:
+        out, mine, theirs = kernels.syrk_checked(_to(A, dev), alpha, beta, _to(C, dev), trans, uplo)
+        return (_to_host(out, orig) if orig != dev else out), mine, theirs
+    except Exception as exc:  # noqa: BLE001
+        _kernel_failed(exc)
+        return None
+
+
 # ── DF-MP2 energies ──────────────────────────────────────────────────────────
 
 _PAIR_ENERGY_CHOICES = ("auto", "hip", "sym", "aten", "legacy")

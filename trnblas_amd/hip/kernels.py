@@ -188,6 +188,72 @@ def syrk(
     return D
 
 
+_side_streams: dict = {}
+
+
+def _side_stream(dev: torch.device) -> "torch.cuda.Stream":
+    """A second stream of `dev` (default priority) for small host reads that
+    must not wait behind the main stream's later work."""
+    s = _side_streams.get(dev.index)
+    if s is None:
+        s = _side_streams[dev.index] = torch.cuda.Stream(dev)
+    return s
+
+
+def syrk_checked(
+    A: torch.Tensor,
+    alpha: float,
+    beta: float,
+    C: torch.Tensor,
+    trans: bool = False,
+    uplo: str = "upper",
+) -> tuple[torch.Tensor, bool, bool]:
+    """`syrk` with beta != 0 and the triangle rule of an n x n C decided on
+    the device: returns (D, uplo triangle has an off-diagonal nonzero, the
+    other triangle has one). The triangle check, then the SYRK reading its
+    flags, run back to back on the current stream; the flags reach the host
+    over a side stream, so the host waits for the check only, not for the
+    product."""
+    dev = _require_device(A, C)
+    code = _lib.DTYPE_CODES.get(A.dtype)
+    if code is None:
+        raise TypeError(f"syrk: dtype {A.dtype} not supported by the HIP kernel")
+    if C.dtype != A.dtype:
+        raise TypeError("syrk: C dtype differs from A")
+    a, t, lda = _mat_layout(A)
+    t = t != bool(trans)
+    n = A.shape[1] if trans else A.shape[0]
+    k = A.shape[0] if trans else A.shape[1]
+    if tuple(C.shape) != (n, n):
+        raise ValueError(f"syrk: C must be {n} x {n}, got {tuple(C.shape)}")
+    c = C if (C.stride(1) == 1 and C.stride(0) >= n) else C.contiguous()
+    ldc = c.stride(0)
+    D = torch.empty((n, n), dtype=A.dtype, device=dev)
+    ws = gemm_workspace(dev)
+    flags = torch.empty(2, dtype=torch.int32, device=dev)
+    main = torch.cuda.current_stream(dev)
+    call("trnblas_hip_triangle_nonzero", code, n, ptr(c), ldc, ptr(flags), stream_of(dev))
+    checked = torch.cuda.Event()
+    checked.record(main)
+    side = _side_stream(dev)
+    side.wait_event(checked)
+    host = torch.empty(2, dtype=torch.int32, pin_memory=True)
+    with torch.cuda.stream(side):
+        host.copy_(flags, non_blocking=True)
+        landed = torch.cuda.Event()
+        landed.record(side)
+    flags.record_stream(side)
+    _probed_call(
+        "syrk", "trnblas_hip_syrk_flagged", code, 1 if uplo == "upper" else 0, int(t), n, k,
+        float(alpha), ptr(a), lda, float(beta), ptr(c), ldc, ptr(D), n, ptr(flags),
+        ptr(ws), ws.numel(), stream_of(dev),
+    )  # fmt: skip
+    landed.synchronize()
+    up, lo = (bool(v) for v in host.tolist())
+    mine, theirs = (up, lo) if uplo == "upper" else (lo, up)
+    return D, mine, theirs
+
+
 # ── DF-MP2 pair energy ───────────────────────────────────────────────────────
 
 

@@ -170,11 +170,13 @@ def syrk(
     n = A.shape[1] if trans else A.shape[0]
     add = C is not None and beta != 0.0
     if add and C.dim() == 2 and tuple(C.shape) == (n, n):
-        side = _resolve_syrk_uplo(C, uplo)
         if C.dtype == A.dtype:
-            out = _d.hip_syrk(alpha, A, beta, C, trans, side)
-            if out is not None:
+            res = _d.hip_syrk_checked(alpha, A, beta, C, trans, uplo)
+            if res is not None:
+                out, mine, theirs = res
+                _syrk_side(uplo, mine, theirs)
                 return out
+        side = _resolve_syrk_uplo(C, uplo)
         Cs = _sym_from_triangle(C, side)
         A_eff = A.mT if trans else A
         return _scale_add(_d.nki_syrk(A_eff, symmetrize=True), alpha, beta, Cs)
@@ -206,6 +208,12 @@ def _resolve_syrk_uplo(C: torch.Tensor, uplo: str) -> str:
         up = bool(torch.triu(C, diagonal=1).ne(0).any())
         lo = bool(torch.tril(C, diagonal=-1).ne(0).any())
         mine, theirs = (up, lo) if uplo == "upper" else (lo, up)
+    return _syrk_side(uplo, mine, theirs, stacklevel=4)
+
+
+def _syrk_side(uplo: str, mine: bool, theirs: bool, stacklevel: int = 3) -> str:
+    """The triangle rule (level3.py:305-329): `uplo`, or the other triangle,
+    with a DeprecationWarning, when only that one holds off-diagonal entries."""
     other = "lower" if uplo == "upper" else "upper"
     if theirs and not mine:
         warnings.warn(
@@ -214,7 +222,7 @@ def _resolve_syrk_uplo(C: torch.Tensor, uplo: str) -> str:
             "Only the uplo triangle of C is referenced when both are stored, and "
             "this fallback will be removed.",
             DeprecationWarning,
-            stacklevel=3,
+            stacklevel=stacklevel,
         )
         return other
     return uplo
