@@ -241,3 +241,38 @@ def test_syrk_unaligned_c_ld(dev):
     D2 = kernels.syrk(A, 1.0, 0.5, Xv.contiguous(), uplo="upper")
     torch.cuda.synchronize()
     assert torch.equal(D1, D2)
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 32768), (256, 128, 20000), (1024, 1024, 1024), (64, 300, 4096)])
+def test_gemm_stream_k_few_tiles(dev, M, N, K):
+    # a handful of tiles with long K: every tile is split over many
+    # workgroups (up to the fixup's 64 contributors per tile)
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(M + N + K)
+    A = torch.randn(M, K, generator=g)
+    B = torch.randn(K, N, generator=g)
+    C = torch.randn(M, N, generator=g)
+    D1 = kernels.gemm(A.to(dev), B.to(dev), 1.0, 0.5, C.to(dev))
+    D2 = kernels.gemm(A.to(dev), B.to(dev), 1.0, 0.5, C.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(D1, D2)  # deterministic
+    err = _cw_err(D1.cpu(), A, B, 1.0, 0.5, C)
+    assert err <= 1e-6, err
+
+
+@pytest.mark.parametrize("n,k", [(128, 32768), (300, 8192)])
+def test_syrk_stream_k_few_tiles(dev, n, k):
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(n + k)
+    A = torch.randn(n, k, generator=g)
+    X = torch.randn(n, n, generator=g)
+    D = kernels.syrk(A.to(dev), 1.0, 0.5, X.to(dev), uplo="upper").cpu()
+    assert torch.equal(D, D.T)
+    Cs = torch.triu(X) + torch.triu(X, 1).T
+    Ad = A.double()
+    ref = Ad @ Ad.T + 0.5 * Cs.double()
+    den = Ad.abs() @ Ad.abs().T + 0.5 * Cs.double().abs()
+    tol = max(1e-6, 2 * k**0.5 * 2.0**-24)
+    assert ((D.double() - ref).abs() / den).max().item() <= tol

@@ -675,7 +675,7 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
 // thread and contributor (all contributors' loads in flight at once).
 template <typename T, int BM, int BN, bool SYRK>
 __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs g) {
-  constexpr int MAXC = 64;  // contributors per tile (>= 4 k-iterations each)
+  constexpr int MAXC = 64;  // contributors per tile (choose_sk keeps to it)
   constexpr int ROWS = 8;
   static_assert(ROWS * BN / 4 == 256, "one float4 per thread");
   __shared__ int64_t src[MAXC];
@@ -754,12 +754,19 @@ static int choose_sk(GemmArgs& g, int occupancy, size_t ws_bytes) {
   const int64_t slots = (int64_t)device_cus() * (occupancy > 0 ? occupancy : 1);
   const int64_t rounds = (g.ntiles + slots - 1) / slots;
   const double eff = (double)g.ntiles / (double)(rounds * slots);
-  // Tiles that give every CU at most one workgroup are already balanced.
-  if (eff >= 0.9 || rounds > 8 || g.ntiles <= device_cus()) return 0;
+  // At most one tile per CU leaves one wave per SIMD (no second workgroup to
+  // fill the MFMA pipe behind the barriers): split it too when each tile has
+  // k-iterations enough (32) for the partial-tile traffic to pay (1024^2 x
+  // 4096 fp32: 277 -> 83 us; 2048^3 with its 256 tiles: 175 -> 163 us).
+  if (eff >= 0.9 || rounds > 8 || (g.ntiles <= device_cus() && g.nk < 32)) return 0;
   int64_t groups = slots;
   const int64_t dp = (g.ntiles / groups) * groups;  // whole rounds
   const int64_t tail = (int64_t)(g.ntiles - dp) * g.nk;
-  if (tail / groups < 4) groups = tail / 4;  // at least 4 k-iterations each
+  // at least 4 k-iterations per group, and few enough groups per tile for
+  // gemm_fixup_kernel's 64 contributors (a tile spans at most
+  // ceil(nk / per) + 1 groups)
+  const int64_t per = std::max<int64_t>(4, (g.nk + 62) / 63);
+  if (tail / groups < per) groups = tail / per;
   if (groups < 1 || (size_t)groups * 2 * kSkSlotBytes > ws_bytes) return 0;
   if (dp > 0 && groups != slots) return 0;  // keep one workgroup per slot
   g.dp_tiles = (int)dp;
