@@ -141,13 +141,32 @@ __device__ __forceinline__ i32x4 read_frag(const T* buf, int row, int kk) {
   }
 }
 
-// Lower-triangle tile t -> (tm, tn), tm >= tn, row-major over the triangle.
-__device__ __forceinline__ void tri_tile(int t, int& tm, int& tn) {
-  int r = (int)((sqrtf(8.0f * (float)t + 1.0f) - 1.0f) * 0.5f);
-  while (r * (r + 1) / 2 > t) --r;
-  while ((r + 1) * (r + 2) / 2 <= t) ++r;
-  tm = r;
-  tn = t - r * (r + 1) / 2;
+// Lower-triangle tile t -> (tm, tn), tm >= tn, of a triangle T tiles on a
+// side, in groups of 8 tile rows: group G (rows 8G .. 8G + R - 1, R = 8 but
+// for the last) lists its whole columns tn < 8G (R tiles each, top to
+// bottom), then its own R-row triangle column by column; groups start at
+// tile 32 G^2 + 4 G. Consecutive tiles (one XCD's share of a round) then
+// cover an 8-row, 8-column block of operand panels (13-20 distinct panels per
+// 64 tiles of a 32-tile side, against ~35 for a row-major walk).
+__device__ __forceinline__ void tri_tile(int t, int T, int& tm, int& tn) {
+  int G = (int)((sqrtf(16.0f + 128.0f * (float)t) - 4.0f) * (1.0f / 64.0f));
+  while (G > 0 && 32 * G * G + 4 * G > t) --G;
+  while ((G + 1) * 8 < T && 32 * (G + 1) * (G + 1) + 4 * (G + 1) <= t) ++G;
+  int u = t - (32 * G * G + 4 * G);
+  const int R = min(8, T - 8 * G);
+  if (u < 8 * G * R) {
+    tm = 8 * G + u % R;
+    tn = u / R;
+    return;
+  }
+  u -= 8 * G * R;
+  int c = 0;
+  while (u >= R - c) {
+    u -= R - c;
+    ++c;
+  }
+  tm = 8 * G + c + u;
+  tn = 8 * G + c;
 }
 
 // SYRK: whether the upper triangle of C is the one referenced: g.uplo, or,
@@ -224,7 +243,7 @@ template <bool SYRK>
 __device__ __forceinline__ void decode_tile(const GemmArgs& g, int t, int& bat, int& tm, int& tn) {
   if (SYRK) {
     bat = 0;
-    tri_tile(t, tm, tn);
+    tri_tile(t, g.tiles_m, tm, tn);
   } else {
     const int per = g.tiles_m * g.tiles_n;
     bat = t / per;
@@ -710,8 +729,18 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs g) {
   const int c = (threadIdx.x % (BN / 4)) * 4;
   const int e = r * BN + c;
   const int up = SYRK ? syrk_upper(g) : 0;
+  // contributors summed in order; their loads issued 8 at a time (a plain
+  // loop would wait for each load before the next add)
   f32x4 v = *reinterpret_cast<const f32x4*>(g.ws + src[0] + e);
-  for (int q = 1; q < nc; ++q) v += *reinterpret_cast<const f32x4*>(g.ws + src[q] + e);
+  int q = 1;
+  for (; q + 8 <= nc; q += 8) {
+    f32x4 p[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) p[u] = *reinterpret_cast<const f32x4*>(g.ws + src[q + u] + e);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v += p[u];
+  }
+  for (; q < nc; ++q) v += *reinterpret_cast<const f32x4*>(g.ws + src[q] + e);
 #pragma unroll
   for (int u = 0; u < 4; ++u) store_out<T, SYRK>(g, C, D, m0 + r, n0 + c + u, v[u], up);
 }
