@@ -276,3 +276,30 @@ def test_syrk_stream_k_few_tiles(dev, n, k):
     den = Ad.abs() @ Ad.abs().T + 0.5 * Cs.double().abs()
     tol = max(1e-6, 2 * k**0.5 * 2.0**-24)
     assert ((D.double() - ref).abs() / den).max().item() <= tol
+
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2.0**-8), (torch.float16, 2.0**-11)])
+@pytest.mark.parametrize(
+    "batch,M,N,K",
+    [(1, 4000, 2176, 1000), (16, 1000, 1024, 512), (1, 4096, 2176, 8192)],
+)
+def test_gemm_16bit_large(dev, dtype, tol, batch, M, N, K):
+    # 16-bit A B^T (both K-contiguous) on aligned operands at sizes that fill
+    # the GPU: ragged M, a batch, and (last) a stream-K tail; fp32
+    # accumulation, one rounding to the 16-bit output
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(M + K)
+    A = torch.randn(batch, M, K, generator=g).to(dtype)
+    Bt = torch.randn(batch, N, K, generator=g).to(dtype)
+    C = torch.randn(batch, M, N, generator=g).to(dtype)
+    Ad, Bd, Cd = A.to(dev), Bt.to(dev), C.to(dev)
+    if batch == 1:
+        Ad, Bd, Cd = Ad[0], Bd[0], Cd[0]
+    D = kernels.gemm(Ad, Bd.mT, 1.0, 0.5, Cd)
+    torch.cuda.synchronize()
+    D = D.cpu().double().reshape(batch, M, N)
+    ref = A.double() @ Bt.double().mT + 0.5 * C.double()
+    den = A.double().abs() @ Bt.double().abs().mT + 0.5 * C.double().abs()
+    assert ((D - ref).abs() / den).max().item() <= tol
