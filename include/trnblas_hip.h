@@ -75,7 +75,9 @@ int trnblas_hip_gemm(int dtype, int transA, int transB, int64_t M, int64_t N, in
  * whose tiles do not fill the GPU evenly (stream-K: the k-iterations of all
  * tiles are split evenly over the resident workgroups; split tiles are summed
  * by a second, deterministic kernel). Bytes for the current device; with a
- * NULL or smaller workspace the calls run one tile per workgroup.
+ * NULL or smaller workspace the calls run one tile per workgroup. Calls on
+ * one stream may share a workspace; calls that can overlap (other streams)
+ * need one each.
  */
 size_t trnblas_hip_gemm_workspace(void);
 

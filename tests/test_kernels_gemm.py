@@ -303,3 +303,26 @@ def test_gemm_16bit_large(dev, dtype, tol, batch, M, N, K):
     ref = A.double() @ Bt.double().mT + 0.5 * C.double()
     den = A.double().abs() @ Bt.double().abs().mT + 0.5 * C.double().abs()
     assert ((D - ref).abs() / den).max().item() <= tol
+
+
+def test_stream_k_two_streams(dev):
+    # split-k GEMMs launched on two streams may run at the same time: each
+    # stream has its own partial-tile workspace, so both match the results
+    # of the same calls made one after the other, bit for bit
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator(device=dev).manual_seed(11)
+    ops = [(torch.randn(1024, 4096, device=dev, generator=g), torch.randn(4096, 1024, device=dev, generator=g))
+           for _ in range(2)]
+    want = [kernels.gemm(a, b) for a, b in ops]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(dev), torch.cuda.Stream(dev)]
+    got = [[], []]
+    for _ in range(4):
+        for s, (a, b), out in zip(streams, ops, got):
+            with torch.cuda.stream(s):
+                out.append(kernels.gemm(a, b))
+    torch.cuda.synchronize()
+    for w, outs in zip(want, got):
+        for o in outs:
+            assert torch.equal(o, w)

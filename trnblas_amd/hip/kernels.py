@@ -34,15 +34,18 @@ _gemm_ws: dict = {}
 
 
 def gemm_workspace(dev: torch.device) -> torch.Tensor:
-    """The stream-K workspace of `dev` (allocated once, reused by every GEMM /
-    SYRK launch on the device; launches on one stream are ordered)."""
+    """The stream-K workspace of `dev` for torch's current stream there
+    (allocated once per stream and reused by every GEMM / SYRK launch on it:
+    launches on one stream are ordered, launches on two streams may overlap,
+    so each stream has its own)."""
     key = (dev.index if dev.index is not None else torch.cuda.current_device())
-    ws = _gemm_ws.get(key)
+    stream = torch.cuda.current_stream(key).cuda_stream
+    ws = _gemm_ws.get((key, stream))
     if ws is None:
         with torch.cuda.device(key):
             n = _lib.load().trnblas_hip_gemm_workspace()
         ws = torch.empty(max(n, 16), dtype=torch.uint8, device=torch.device("cuda", key))
-        _gemm_ws[key] = ws
+        _gemm_ws[(key, stream)] = ws
     return ws
 
 
