@@ -11,10 +11,12 @@
 // One workgroup of 576 threads per block, blocked by 4 x 4 tiles: the owner of
 // tile (br, bc), br >= bc, keeps the tile at rows 4 br .., columns 4 bc .. of
 // the 128 x 128 block (padded with the identity past nb) in registers.
-// Cholesky, per tile column jb: (A) the owner of the diagonal tile factors
-// it (4 x 4 Cholesky) and inverts its factor into an LDS table; (B) the
-// panel tiles below it become A_ij L_jj^-T and are published; (C) every
-// trailing tile loses P_i P_j^T. Inverse X = L^-1, per tile row ib: the
+// Cholesky, per tile column jb, one barrier: (A) the owner of the diagonal
+// tile factors it (4 x 4 Cholesky) and publishes L_jj^-1 and
+// A_jj^-1 = L_jj^-T L_jj^-1; after the barrier (B) the panel tiles below it
+// become L_ij = A_ij L_jj^-T while (C) every trailing tile loses
+// A_ij A_jj^-1 A_kj^T (= L_ij L_kj^T) from column jb's unscaled tiles, and
+// the tiles of column jb + 1 publish themselves for the next step. Inverse X = L^-1, per tile row ib: the
 // unscaled row of X and the column M_m = L_m,ib L_ib,ib^-1 are published,
 // then the row becomes L_ib,ib^-1 X_ib and every later row m loses
 // M_m X_ib (unscaled). Waves whose tiles all lie above the current tile row
@@ -47,7 +49,8 @@ __global__ __launch_bounds__(kCholThreads) void chol_block_kernel(int nb, double
                                                           double* Li, int64_t ldl, int32_t* info,
                                                           int offset) {
   __shared__ double dinv[kCholNT][16];    // L_jj^-1 of every diagonal tile, row-major
-  __shared__ double pan[kCholNT][16];     // Cholesky: the panel column of tiles
+  __shared__ double ainv[2][16];          // Cholesky: A_jj^-1 = L_jj^-T L_jj^-1 of column j
+  __shared__ double pan[2][kCholNT][16];  // Cholesky: column j's tiles before their scaling
   __shared__ double mcol[2][kCholNT][16]; // inverse: M_m of the current tile row
   __shared__ double xrow[2][kCholNT][16]; // inverse: the unscaled tile row of X
   __shared__ int sbad;
@@ -82,8 +85,17 @@ __global__ __launch_bounds__(kCholThreads) void chol_block_kernel(int nb, double
       a[r][c] = v;
     }
 
+  // Column 0's tiles below the diagonal, as they are
+  if (own && bc == 0 && br > 0) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) pan[0][br][e] = a[e >> 2][e & 3];
+  }
   for (int jb = 0; jb < ntr; ++jb) {
-    // (A) diagonal tile: factor (lower part only) and invert
+    double(*pj)[16] = pan[jb & 1];
+    double(*pn)[16] = pan[(jb + 1) & 1];
+    double* aj = ainv[jb & 1];
+    // (A) diagonal tile (updated through column jb - 1 by this same thread):
+    // factor (lower part only), invert, and publish L_jj^-1 and A_jj^-1
     if (own && br == jb && bc == jb) {
       double rinv[4];  // 1 / l_cc
 #pragma unroll
@@ -119,11 +131,15 @@ __global__ __launch_bounds__(kCholThreads) void chol_block_kernel(int nb, double
         for (int c = 0; c < 4; ++c) {
           dinv[jb][4 * r + c] = m[r][c];
           if (c > r) a[r][c] = 0.0;
+          double sum = 0.0;  // (m^T m)[r][c]
+#pragma unroll
+          for (int q = 0; q < 4; ++q) sum += m[q][r] * m[q][c];
+          aj[4 * r + c] = sum;
         }
     }
-    __syncthreads();
-    // (B) panel tiles: A_ij L_jj^-T, published
+    __syncthreads();  // L_jj^-1, A_jj^-1 and column jb's tiles are published
     if (wrow > jb && own && bc == jb && br > jb) {
+      // (B) panel tile: L_ij = A_ij L_jj^-T
       double m[4][4], p[4][4];
 #pragma unroll
       for (int e = 0; e < 16; ++e) m[e >> 2][e & 3] = dinv[jb][e];
@@ -139,30 +155,43 @@ __global__ __launch_bounds__(kCholThreads) void chol_block_kernel(int nb, double
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          a[r][c] = p[r][c];
-          pan[br][4 * r + c] = p[r][c];
-        }
-    }
-    __syncthreads();
-    // (C) trailing tiles: A_ik -= P_i P_k^T (diagonal tiles: their upper part
-    // is never read)
-    if (wrow > jb && own && bc > jb) {
-      double pk[4][4];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) pk[e >> 2][e & 3] = pan[bc][e];
+        for (int c = 0; c < 4; ++c) a[r][c] = p[r][c];
+    } else if (wrow > jb && own && bc > jb) {
+      // (C) trailing tile: A_ik -= (A_ij A_jj^-1) A_kj^T, from column jb's
+      // unscaled tiles (L_ij L_kj^T = A_ij A_jj^-1 A_kj^T), so the panel's
+      // scaling (B) runs beside this update instead of before it
+      double q4[4][4];  // A_ij A_jj^-1
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        double pi[4];
+        double ai[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) pi[q] = pan[br][4 * r + q];
+        for (int q = 0; q < 4; ++q) ai[q] = pj[br][4 * r + q];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           double sum = 0.0;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) sum += pi[q] * pk[c][q];
+          for (int q = 0; q < 4; ++q) sum += ai[q] * aj[4 * q + c];
+          q4[r][c] = sum;
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        double ak[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ak[q] = pj[bc][4 * c + q];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          double sum = 0.0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) sum += q4[r][q] * ak[q];
           a[r][c] -= sum;
         }
+      }
+      // column jb + 1's tiles below the diagonal are now as the next step
+      // needs them
+      if (bc == jb + 1 && br > bc) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) pn[br][e] = a[e >> 2][e & 3];
       }
     }
   }
