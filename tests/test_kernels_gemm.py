@@ -326,3 +326,20 @@ def test_stream_k_two_streams(dev):
     for w, outs in zip(want, got):
         for o in outs:
             assert torch.equal(o, w)
+
+
+def test_batched_stream_k_few_tiles(dev):
+    # a batch of single-tile products with long K (split over many
+    # workgroups per tile, partial tiles summed per batch entry), with a
+    # stride-0 broadcast B and beta * C
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(21)
+    A = torch.randn(3, 100, 8192, generator=g)
+    B = torch.randn(8192, 120, generator=g)
+    C = torch.randn(3, 100, 120, generator=g)
+    D = kernels.gemm(A.to(dev), B.to(dev).unsqueeze(0).expand(3, 8192, 120), 1.0, 0.5, C.to(dev))
+    torch.cuda.synchronize()
+    for b in range(3):
+        err = _cw_err(D[b].cpu(), A[b], B, 1.0, 0.5, C[b])
+        assert err <= 1e-6, (b, err)
