@@ -489,6 +489,16 @@ __device__ __forceinline__ void lds_dma16(const void* base, void* lds, uint32_t 
                                            0, 0, 0);
 }
 
+// Lane layout of ds_read_b64_tr_b16 (gfx950), measured with an in-bounds
+// probe: in each group of 16 lanes every lane loads 8 bytes (four 16-bit
+// values) at its own address, and lane i receives, for j = 0..3, value i % 4
+// of the 8 bytes loaded by lane 4 j + i / 4 of its group.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ s16x4 lds_tr16(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(const_cast<void*>(p)));
+}
+
 // GEMM / SYRK on 16-byte aligned operands (fp32, bf16, fp16): the tile,
 // wave split, MFMA (v_mfma_f32_32x32x2_f32, v_mfma_f32_32x32x16_{bf16,f16})
 // and k order of gemm_kernel, with the operand panels moved by LDS DMA
@@ -598,6 +608,23 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
     auto frag = [&](const T* p, bool kc, int r, int kk) __attribute__((always_inline)) {
       if (kc)
         return *reinterpret_cast<const i32x4*>(p + r * BK + EV * ((kk / EV) ^ ((r >> 1) & 7)));
+      if constexpr (sizeof(T) == 2) {
+        // Two transposing reads: in each 16-lane group (rows rb .. rb + 15,
+        // one k-octet) lane i loads row k + i / 4, columns rb + 4 (i % 4) ..
+        // + 3 of the panel (8 bytes of one swizzled 16-byte slot), and
+        // receives column rb + i of rows k .. k + 3.
+        const int i = lane & 15;
+        const int c0 = r - i + 4 * (i & 3);
+        const int k1 = kk + (i >> 2);
+        const T* s0 = p + k1 * 128 + EV * ((c0 / EV) ^ (MSW * ((kk / EV) & 1))) + (c0 & 4);
+        union {
+          s16x4 h[2];
+          i32x4 v;
+        } u;
+        u.h[0] = lds_tr16(s0);
+        u.h[1] = lds_tr16(s0 + 4 * 128);
+        return u.v;
+      }
       const T* q = p + EV * ((r / EV) ^ (MSW * ((kk / EV) & 1))) + (r % EV);
       union {
         i32x4 v;
