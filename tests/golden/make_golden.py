@@ -7,8 +7,8 @@ exponents of `split` (per row and per column, extreme / zero / subnormal
 rows, the two-factor scaling), the (hi, lo) of `reference_from_digits`, and
 the fp64 result of `reference_gemm` (including the narrow-N swap, K >= 4096
 group cuts and multi-pair groups). These are the functions whose bitwise
-output no closed form pins; everything else is pinned by
-invariants and closed forms in the tests.
+output no closed form pins; everything else is pinned by invariants and
+closed forms in the tests.
 
     python tests/golden/make_golden.py      # writes tests/golden/ozaki_golden.npz
 """
