@@ -61,3 +61,24 @@ def test_argument_errors_are_reported_without_a_gpu():
     rc = lib.trnblas_hip_pair_energy_bf16x6(7, 33, 16, 2, 231, 16, 0, 231, 33, 16, 16, 16, 3,
                                             6, None, None, None, None, 16, 16, 4096, None)
     assert rc == _lib.E_ARG and b"ni >= nocc" in lib.trnblas_hip_last_error()
+
+
+def test_syrk_and_triangle_argument_errors_without_a_gpu():
+    # the device-decided triangle rule needs its flags when beta != 0, and
+    # the triangle check needs an aligned int32[2]; both are refused before
+    # any HIP call (the chol_block size bound too)
+    import ctypes
+
+    from trnblas_amd.hip import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("library not built")
+    lib = _lib.load()
+    fake = ctypes.c_void_p(4096)  # never dereferenced: the calls fail their argument checks
+    rc = lib.trnblas_hip_syrk_flagged(0, 0, 0, 8, 8, 1.0, fake, 8, 0.5, fake, 8, fake, 8, None,
+                                      None, 0, None)
+    assert rc == _lib.E_ARG and b"flags" in lib.trnblas_hip_last_error()
+    rc = lib.trnblas_hip_triangle_nonzero(0, 8, fake, 8, ctypes.c_void_p(4100), None)
+    assert rc == _lib.E_ARG and b"aligned" in lib.trnblas_hip_last_error()
+    rc = lib.trnblas_hip_chol_block(129, fake, 129, fake, 129, fake, 0, None)
+    assert rc == _lib.E_ARG and b"nb" in lib.trnblas_hip_last_error()
