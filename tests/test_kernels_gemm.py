@@ -343,3 +343,44 @@ def test_batched_stream_k_few_tiles(dev):
     for b in range(3):
         err = _cw_err(D[b].cpu(), A[b], B, 1.0, 0.5, C[b])
         assert err <= 1e-6, (b, err)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2.0**-8), (torch.float16, 2.0**-11)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_gemm_16bit_aligned_layouts(dev, dtype, tol, ta, tb):
+    # 16-byte aligned rows in every layout: the direct-to-LDS kernel, whose
+    # M/N-contiguous fragments use the transposing LDS read; ragged M and N
+    from trnblas_amd.hip import kernels
+
+    M, N, K = 392, 264, 512
+    g = torch.Generator().manual_seed(7)
+    A0 = torch.randn((K, M) if ta else (M, K), generator=g).to(dtype)
+    B0 = torch.randn((N, K) if tb else (K, N), generator=g).to(dtype)
+    C = torch.randn(M, N, generator=g).to(dtype)
+    A = (A0.mT if ta else A0).to(dev)
+    B = (B0.mT if tb else B0).to(dev)
+    D = kernels.gemm(A, B, 1.5, -0.5, C.to(dev))
+    torch.cuda.synchronize()
+    Ad, Bd = A.cpu().double(), B.cpu().double()
+    ref = 1.5 * (Ad @ Bd) - 0.5 * C.double()
+    den = 1.5 * (Ad.abs() @ Bd.abs()) + 0.5 * C.double().abs()
+    assert ((D.cpu().double() - ref).abs() / den).max().item() <= tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2.0**-8), (torch.float16, 2.0**-11)])
+def test_syrk_16bit_trans_aligned(dev, dtype, tol):
+    # op(A) = A^T with A (k, n) N-contiguous and aligned: both SYRK panels
+    # are M/N-contiguous (transposing LDS reads)
+    from trnblas_amd.hip import kernels
+
+    n, k = 392, 200
+    g = torch.Generator().manual_seed(9)
+    A = torch.randn(k, n, generator=g).to(dtype)
+    X = torch.randn(n, n, generator=g).to(dtype)
+    D = kernels.syrk(A.to(dev), 1.0, 0.5, X.to(dev), trans=True, uplo="lower").cpu()
+    assert torch.equal(D, D.T)
+    Ad, Xd = A.double().T, X.double()
+    Cs = torch.tril(Xd) + torch.tril(Xd, -1).T
+    ref = Ad @ Ad.T + 0.5 * Cs
+    den = Ad.abs() @ Ad.abs().T + 0.5 * Cs.abs()
+    assert ((D.double() - ref).abs() / den).max().item() <= tol
