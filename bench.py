@@ -136,7 +136,7 @@ def run_extras(dev, tb, only=None) -> dict:
     if only is None or "c1" in only:
         # C1: gemm fp32 A^T B + 0.5 C at 2048^3, against the CPU path
         A, B, C = df_mp2.config1_inputs(dev)
-        t = gpu_time_ms(lambda: tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True), reps=20, warm=3)
+        t = gpu_time_ms(lambda: tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True), reps=20, warm=20)
         D = tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True)
         Ah, Bh, Ch = A.cpu(), B.cpu(), C.cpu()
         t0 = time.perf_counter()
@@ -375,7 +375,7 @@ def main():
     denb = Ab.double().abs() @ Bb.double().abs()
     bat_err = float(((D.double() - refb) / denb).abs().max())
     del ref, den, refb, denb, Ad
-    t_b = gpu_time_ms(lambda: tb.batched_gemm(1.0, Ab, Bb), reps=10)
+    t_b = gpu_time_ms(lambda: tb.batched_gemm(1.0, Ab, Bb), reps=20, warm=20)  # past the clock ramp
     cpu = None
     if not args.no_cpu:
         threads = torch.get_num_threads()
