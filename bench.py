@@ -43,6 +43,7 @@ BATCH, BM, BK, BN = 64, 512, 2048, 512
 SYRK_FLOP = SYRK_N * (SYRK_N + 1) * SYRK_K  # triangle count
 BATCHED_FLOP = BATCH * 2 * BM * BN * BK
 STEP_FLOP = SYRK_FLOP + BATCHED_FLOP
+SETTLE_S = 0.3  # untimed steps before the warm-up (clock ramp), seconds of wall time
 
 
 def committed_traffic(kernel: str):
@@ -290,10 +291,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    # 30 untimed steps (~50 ms): the GPU's clocks ramp up over the first
-    # ~20 steps after an idle spell; timing inside the ramp understates the
-    # steady rate by ~6 %.
-    ap.add_argument("--warmup", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None,
@@ -329,6 +327,17 @@ def main():
         D = tb.batched_gemm(1.0, Ab, Bb)
         return S, D
 
+    # Clock settle: after an idle spell the GPU's clocks ramp up over ~50 ms
+    # of this step (the SYRK launch falls from 1.26 to 1.10 ms, then stays);
+    # steps run untimed for SETTLE_S seconds of wall time first, then the W
+    # warm-up steps, so the timed steps see the steady clocks at any --warmup.
+    t_settle = time.perf_counter()
+    settle_steps = 0
+    while time.perf_counter() - t_settle < SETTLE_S:
+        for _ in range(5):
+            step()
+        torch.cuda.synchronize()
+        settle_steps += 5
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -397,6 +406,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"seconds": SETTLE_S, "steps": settle_steps},
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",

@@ -53,11 +53,40 @@ def test_config2_syrk_and_batched(dev):
     Ad = A.double()
     ref = Ad @ Ad.T + 0.5 * (torch.tril(C.double()) + torch.tril(C.double(), -1).T)
     den = Ad.abs() @ Ad.abs().T + 0.5 * C.double().abs()
-    tol = max(1e-6, 2 * 8192**0.5 * 2.0**-24)  # diagonal sums of k positive terms
-    assert _cw(S, ref, den) <= tol
+    assert _cw(S, ref, den) <= 1e-6  # north-star gate vs fp64
+    # ... and vs the reference's CPU path (fp32 torch.matmul + the epilogue)
+    Sh = S.cpu()
+    cpu = blas.syrk_cpu(1.0, A.cpu(), 0.5, C.cpu(), uplo="lower")
+    assert _cw(Sh, cpu.double(), den.cpu()) <= 1e-6
     refb = Ab.double() @ Bb.double()
     denb = Ab.double().abs() @ Bb.double().abs()
     assert _cw(Db, refb, denb) <= 1e-6
+    cpub = blas.gemm_cpu(1.0, Ab.cpu(), Bb.cpu())
+    assert _cw(Db.cpu(), cpub.double(), denb.cpu()) <= 1e-6
+
+
+def test_gemm_same_sign_long_k(dev):
+    # U(0, 1) operands: every output is a sum of K same-sign products, the
+    # case in which the rounding of one long fp32 accumulation chain adds up
+    # (cancelling N(0, 1) data hides it). Gate: 1e-6 |A||B| against fp64 and
+    # against the reference's CPU path.
+    g = torch.Generator().manual_seed(11)
+    K = 8192
+    A = torch.rand(1024, K, generator=g)
+    B = torch.rand(K, 768, generator=g)
+    C = torch.rand(1024, 768, generator=g)
+    D = tb.gemm(1.0, A.to(dev), B.to(dev), beta=0.5, C=C.to(dev)).cpu()
+    ref = blas.gemm_f64(1.0, A, B, 0.5, C)
+    den = blas.gemm_cw_den(1.0, A, B, 0.5, C)
+    assert _cw(D, ref, den) <= 1e-6
+    cpu = blas.gemm_cpu(1.0, A, B, 0.5, C)
+    assert _cw(D, cpu.double(), den) <= 1e-6
+    # transposed read paths (C1's layout) and SYRK on the same data
+    Dt = tb.gemm(1.0, A.T.contiguous().to(dev), B.to(dev), transA=True).cpu()
+    assert _cw(Dt, A.double() @ B.double(), A.double() @ B.double()) <= 1e-6
+    S = tb.syrk(1.0, A[:640].to(dev), uplo="lower").cpu()
+    As = A[:640].double()
+    assert _cw(S, As @ As.T, As @ As.T) <= 1e-6
 
 
 # ── GEMM semantics and edge cases ────────────────────────────────────────────

@@ -54,6 +54,7 @@ struct GemmArgs {
   int sk_groups;         // stream-K workgroups (0 = data-parallel)
   int dp_tiles;          // under stream-K: leading tiles computed whole
   float* ws;             // stream-K partial tiles [sk_groups][2][BM * BN]
+  int span;              // k-tiles per MFMA accumulation chain (chain_length / k-tile)
 };
 
 template <typename T>
@@ -100,6 +101,26 @@ __device__ __forceinline__ i32x4 load_group(__amdgpu_buffer_rsrc_t rs, uint32_t 
       u.h[e] = __builtin_amdgcn_raw_buffer_load_b16(rs, o, 0, 0);
   }
   return u.v;
+}
+
+// Accumulation: the MFMA accumulator of a tile restarts from zero every
+// chain_length(K) k values and each finished chain is added into a separate
+// fp32 sum with a VALU add (fold_span). One chain over all of K rounds the
+// running sum at every step: a sum of 8192 same-sign products (a SYRK
+// diagonal) came out 5.3e-6 off. With chains of L values folded into the sum
+// the error is that of L chain steps plus K / L folds; L near 2 sqrt(K)
+// balances them, and at K = 8192 the result stays near 3e-7, the error of
+// the host's blocked fp32 matmul. (A multiple of every k-tile, 128 k.)
+static inline int chain_length(int64_t K) {
+  return K < 16384 ? 256 : K < 65536 ? 512 : 1024;
+}
+
+__device__ __forceinline__ void fold_span(f32x16& sum, f32x16& acc) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    sum[r] += acc[r];
+    acc[r] = 0.0f;
+  }
 }
 
 // acc += a * b over one fragment: 4 fp32 MFMAs (one per element) or one
@@ -336,7 +357,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const f32x16 (&acc
 // and summed by gemm_fixup_kernel.
 template <typename T, int BM, int BN, int BK, int WM, int WN, bool AKC, bool BKC, bool VEC,
           bool SYRK>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1) void gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1) void gemm_kernel(GemmArgs g) {
   constexpr int EV = 16 / sizeof(T);
   constexpr int NT = (BM / WM) * (BN / WN) * 64;
   constexpr int WAVES_N = BN / WN;
@@ -405,13 +426,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1)
       }
     };
 
-    f32x16 acc[FM][FN];
+    f32x16 acc[FM][FN], sum[FM][FN];  // current MFMA chain, folded chains
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = sum[i][j][r] = 0.0f;
 
     if (kb1 > kb0) {
       load_tiles(kb0 * BK);
@@ -419,6 +440,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1)
       if (NB == 1 && kb0 + 1 < kb1) load_tiles((kb0 + 1) * BK);
       __syncthreads();
     }
+    int chain = g.span;  // k-tiles left in the current MFMA chain
     for (int kt = kb0; kt < kb1; ++kt) {
       const int cur = NB == 1 ? 0 : (kt - kb0) & 1;
       const bool more = kt + 1 < kb1;
@@ -440,6 +462,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1)
 #pragma unroll
           for (int j = 0; j < FN; ++j) mma_frag(acc[i][j], fa[i], fb[j], (T*)nullptr);
       }
+      if (--chain == 0) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) fold_span(sum[i][j], acc[i][j]);
+        chain = g.span;
+      }
       if (NB == 2) {
         if (more) store_tiles(cur ^ 1);
         __syncthreads();
@@ -454,8 +483,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, sizeof(T) == 4 ? 2 : 1)
         }
       }
     }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) fold_span(sum[i][j], acc[i][j]);
 
-    store_tile<T, SYRK, FM, FN, BM, BN>(g, acc, bat, m0, n0, wm0, wn0, lane, slot, w);
+    store_tile<T, SYRK, FM, FN, BM, BN>(g, sum, bat, m0, n0, wm0, wn0, lane, slot, w);
   };
 
   if (g.sk_groups == 0) {
@@ -594,13 +627,19 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
       }
     };
 
-    f32x16 acc[FM][FN];
+    f32x16 acc[FM][FN], sum[FM][FN];  // current MFMA chain, folded chains
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = sum[i][j][r] = 0.0f;
+    auto fold = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) fold_span(sum[i][j], acc[i][j]);
+    };
 
     // Fragment of the lane's row r (32 rows per MFMA block) at k offset kk
     // (EV consecutive k, kk a multiple of EV): one 16-byte read from a
@@ -641,7 +680,13 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
     // only entries above the diagonal: it moves its share of the panels and
     // keeps the barriers, but reads no fragments and runs no MFMAs (its
     // accumulators stay zero and its store writes nothing).
-    const bool busy = !(SYRK && tm == tn && wn0 > wm0);
+    // `busy` is also a runtime (opaque) condition for GEMM: as a branch it
+    // keeps the fragment reads, the DMA and the MFMAs of a k-tile in separate
+    // blocks; scheduled as one block they hold the folded sums, the chain and
+    // the fragments live together with hoisted addresses, and spill.
+    int on = 1;
+    asm volatile("" : "+s"(on));
+    const bool busy = SYRK ? !(tm == tn && wn0 > wm0) : on != 0;
     auto step = [&](const T* cur, T* oth, int next) __attribute__((always_inline)) {
       i32x4 fa[BK / CH][FM], fb[BK / CH][FN];
       if (busy) {
@@ -668,6 +713,7 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
 
     __syncthreads();  // a previous segment's reads of both stages are done
     if (kb1 > kb0) dma(st0, kb0);
+    int chain = g.span;  // k-tiles left in the current MFMA chain (span is even)
     for (int kt = kb0; kt < kb1; kt += 2) {
       __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA of k-tile kt has landed
       __syncthreads();                // every wave's has; every read of st1 is done
@@ -676,8 +722,14 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       step(st1, st0, kt + 2 < kb1 ? kt + 2 : -1);
+      chain -= 2;
+      if (chain == 0) {
+        fold();
+        chain = g.span;
+      }
     }
-    store_tile<T, SYRK, FM, FN, BM, BN>(g, acc, bat, m0, n0, wm0, wn0, lane, slot, w);
+    fold();
+    store_tile<T, SYRK, FM, FN, BM, BN>(g, sum, bat, m0, n0, wm0, wn0, lane, slot, w);
   };
 
   // Work of this workgroup, walked with one call site of `segment` (two
@@ -835,6 +887,7 @@ static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   constexpr bool DMA = VEC;  // aligned operands: gemm_dma_kernel
   constexpr int BK = DMA ? 128 / (int)sizeof(T) : C::template bk<VEC>();
   g.nk = (g.K + BK - 1) / BK;
+  g.span = chain_length(g.K) / BK;  // even for every k-tile (32, 64)
   void (*kern)(GemmArgs);
   if constexpr (DMA)
     kern = gemm_dma_kernel<T, AKC, BKC, SYRK>;
