@@ -195,6 +195,30 @@ int trnblas_hip_pair_energy_bf16x6(int64_t nvir, int64_t naux, const float* Bi, 
                                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * trnblas_hip_pair_energy without a workspace argument: same arguments
+ * (minus workspace), pair set, weights, outputs, kernels and bits. It
+ * allocates nothing: the fp64 partials live in a static device array of
+ * trnblas_hip_pair_energy_noalloc_max_bytes() bytes (16 MiB) per GPU, held
+ * until the process ends, so npairs * (nb (nb + 1) / 2 + 1) * 8 bytes, with
+ * nb = ceil(nvir / 96), must fit (C3: 1.1 MB; nocc 256 / nvir 768: 9.7 MB);
+ * larger calls return TRNBLAS_E_WORKSPACE. Nothing needs clearing between
+ * calls (every partial is written before it is read), but calls that overlap
+ * on one GPU share the array and race.
+ *
+ * No counterpart in the reference: this is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).
+ */
+size_t trnblas_hip_pair_energy_noalloc_max_bytes(void);
+int trnblas_hip_pair_energy_noalloc(int64_t nvir, int64_t naux, const float* Bi, int64_t ldi_occ,
+                                    const float* Bj, int64_t ldj_occ, int64_t ld_vir,
+                                    const float* eps_i, const float* eps_j,
+                                    const float* eps_vir, int64_t nocc, int64_t npairs,
+                                    const int32_t* pair_i, const int32_t* pair_j,
+                                    const double* pair_w, double* out_pairs, double* out_total,
+                                    void* stream);
+
+/*
  * MP2 energy of a precomputed amplitude block (no GEMM), HBM-bound.
  *
  * T[i][j][a][b] = T_flat[(i*nvir + a) * ldt + j*nvir + b] for i < ic,

@@ -28,6 +28,7 @@
 //  * items of one pair are consecutive on one XCD (shared L2 for its B_i,
 //    B_j panels).
 #include "common.hpp"
+#include <mutex>
 #include <type_traits>
 
 namespace trnblas {
@@ -284,6 +285,13 @@ __global__ __launch_bounds__(256) void pair_sum_kernel(const double* partial, in
   double s = 0.0;
   for (int q = 0; q < nq; ++q) s += src[q];
   e_pair[p] = s;
+}
+
+// Zero fill (the empty-sum results): a kernel rather than hipMemsetAsync, so
+// the call records no memset node when a caller captures it in a graph.
+__global__ __launch_bounds__(256) void zero_f64_kernel(double* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0;
 }
 
 __global__ __launch_bounds__(1024) void pair_total_kernel(const double* e_pair, int npairs,
@@ -955,12 +963,11 @@ static int pair_energy_run(bool x3, const char* name, int64_t nvir, int64_t naux
   }
   if (npairs == 0 || nvir == 0) {
     // Empty sums: zero energies.
-    if (out_total && hipMemsetAsync(out_total, 0, sizeof(double), s) != hipSuccess)
-      return check_launch(name);
-    if (out_pairs && npairs > 0 &&
-        hipMemsetAsync(out_pairs, 0, npairs * sizeof(double), s) != hipSuccess)
-      return check_launch(name);
-    return TRNBLAS_OK;
+    if (out_total) hipLaunchKernelGGL(zero_f64_kernel, dim3(1), dim3(256), 0, s, out_total, 1);
+    if (out_pairs && npairs > 0)
+      hipLaunchKernelGGL(zero_f64_kernel, dim3((unsigned)((npairs + 255) / 256)), dim3(256), 0, s,
+                         out_pairs, npairs);
+    return check_launch(name);
   }
   TRNBLAS_CHECK_ARG(Bi && Bj && eps_i && eps_j && eps_vir, "%s: NULL operand", name);
   TRNBLAS_CHECK_ARG(ld_vir >= naux, "%s: ld_vir < naux", name);
@@ -1085,6 +1092,77 @@ extern "C" int trnblas_hip_pair_energy_bf16x6(int64_t nvir, int64_t naux, const 
   return pair_energy_run(true, "pair_energy_bf16x6", nvir, naux, Bi, ni, ldi_occ, Bj, nj, ldj_occ,
                          ld_vir, eps_i, eps_j, eps_vir, nocc, npairs, pair_i, pair_j, pair_w,
                          out_pairs, out_total, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+// ── No-allocation variant of trnblas_hip_pair_energy ───────────────────────
+//
+// The partials live in `scratch`, a file-scope device array: each GPU the
+// library runs on holds its own copy at its own address until the process
+// ends. In host code `scratch` names a host-side stand-in, never the device
+// memory, so its device address is looked up per device (hipGetSymbolAddress,
+// with that device current, on the first call there) and only that address
+// is handed to the kernels. Every partial is written before it is read, so
+// nothing needs clearing between calls; calls that overlap on one GPU (other
+// streams, other host threads) share the array and race.
+constexpr size_t kPeScratchBytes = (size_t)16 << 20;  // 2 Mi fp64 partials
+static __device__ __align__(256) double scratch[kPeScratchBytes / sizeof(double)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+}  // namespace
+
+static int scratch_address(const char* name, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("%s: no current device (or device index >= %d)", name, kMaxDevices);
+    return TRNBLAS_E_LAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("%s: hipGetSymbolAddress(scratch) on device %d: %s", name, dev,
+                hipGetErrorString(e));
+      return TRNBLAS_E_LAUNCH;
+    }
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return TRNBLAS_OK;
+}
+
+extern "C" size_t trnblas_hip_pair_energy_noalloc_max_bytes(void) { return kPeScratchBytes; }
+
+extern "C" int trnblas_hip_pair_energy_noalloc(int64_t nvir, int64_t naux, const float* Bi,
+                                               int64_t ldi_occ, const float* Bj, int64_t ldj_occ,
+                                               int64_t ld_vir, const float* eps_i,
+                                               const float* eps_j, const float* eps_vir,
+                                               int64_t nocc, int64_t npairs,
+                                               const int32_t* pair_i, const int32_t* pair_j,
+                                               const double* pair_w, double* out_pairs,
+                                               double* out_total, void* stream) {
+  clear_error();
+  static const char* name = "pair_energy_noalloc";
+  TRNBLAS_CHECK_ARG(nvir >= 0 && nocc >= 0 && npairs >= 0 && nvir < (1 << 30) &&
+                        nocc < (1 << 30),
+                    "%s: bad size", name);
+  const int64_t np = pair_i == nullptr ? nocc * (nocc + 1) / 2 : npairs;
+  const size_t need = trnblas_hip_pair_energy_workspace(nvir, np);
+  if (need > kPeScratchBytes) {
+    set_error("%s: %lld pairs at nvir %lld need %zu bytes of partials; the static scratch holds "
+              "%zu (use trnblas_hip_pair_energy with a workspace)",
+              name, (long long)np, (long long)nvir, need, kPeScratchBytes);
+    return TRNBLAS_E_WORKSPACE;
+  }
+  void* ws = nullptr;
+  const int rc = scratch_address(name, &ws);
+  if (rc) return rc;
+  return pair_energy_run(false, name, nvir, naux, Bi, 0, ldi_occ, Bj, 0, ldj_occ, ld_vir, eps_i,
+                         eps_j, eps_vir, nocc, npairs, pair_i, pair_j, pair_w, out_pairs,
+                         out_total, ws, kPeScratchBytes, (hipStream_t)stream);
 }
 
 extern "C" int trnblas_hip_mp2_energy(int64_t ic, int64_t nocc, int64_t nvir, const float* T_flat,

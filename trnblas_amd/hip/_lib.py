@@ -19,7 +19,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 _PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("TRNBLAS_HIP_LIB", _PKG / "lib" / "libtrnblas_hip.so"))
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 F32, BF16, F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
@@ -67,6 +67,12 @@ SIGNATURES = {
         [_c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64]
         + [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
         + [_c_ptr, _c_size, _c_ptr],
+    ),
+    "trnblas_hip_pair_energy_noalloc_max_bytes": (_c_size, []),
+    "trnblas_hip_pair_energy_noalloc": (
+        _c_int,
+        [_c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr],
     ),
     "trnblas_hip_mp2_energy": (
         _c_int,
