@@ -200,15 +200,34 @@ def run_extras(dev, tb, only=None) -> dict:
         e64 = float(e64)
         del Bd
         fl = 96 * 97 / 2 * 2 * 672 * 672 * 2304
-        # CPU path sample: the reference's fp32 pair loop over 12 of the 9216
-        # ordered pairs, scaled to all pairs.
+        # the fused entry point's launches (split + fused kernel + sums), timed
+        # with HIP events on the launch stream
+        probe = LaunchEvents("pair_energy")
+        kernels._launch_probe = probe
+        for _ in range(3):
+            kernels.pair_energy_sym(Bp, eo, ev, math="bf16x6")
+        kernels._launch_probe = None
+        torch.cuda.synchronize()
+        t_launch = probe.mean_ms()
+        roof = {
+            "kernel": "split_planes_kernel + pair_energy_x3c_kernel (trnblas_hip_pair_energy_bf16x6)",
+            "bound": "mfma", "launch_ms": t_launch,
+            "achieved": 6 * fl / t_launch / 1e9, "peak": PEAK_BF16_MFMA, "unit": "TFLOP/s (bf16 MFMA)",
+            "frac": 6 * fl / t_launch / 1e9 / PEAK_BF16_MFMA,
+            "achieved_fp32_equiv": fl / t_launch / 1e9, "ceiling_fp32_equiv": PEAK_BF16_MFMA / 6,
+            "frac_fp32_peak": fl / t_launch / 1e9 / PEAK_FP32_MFMA,
+            "algorithmic_flop_per_launch": fl, "traffic": None,
+        }  # fmt: skip
+        # The reference's CPU path (the fp32 torch pair loop of
+        # dispatch.py:2514-2533, restated in oracle/pair_energy.py) over all
+        # 9216 ordered pairs, once.
         from oracle import pair_energy as pe
 
-        Bh, eoh, evh = Bp[:12].cpu(), eo[:12].cpu(), ev.cpu()
+        Bh, eoh, evh = Bp.cpu(), eo.cpu(), ev.cpu()
         t0 = time.perf_counter()
-        for j in range(12):
-            pe.fused_pair_cpu(Bh[0], Bh[j], float(eoh[0]), float(eoh[j]), evh)
-        cpu_pair_s = (time.perf_counter() - t0) / 12
+        e_cpu = float(pe.batched_pair_cpu(Bh, eoh, evh))
+        cpu_loop_ms = (time.perf_counter() - t0) * 1e3
+        del Bh
         out["pair_energy_c3_96_672_2304"] = {
             "fused_ms": tf, "fused_math": "bf16x6", "unfused_gpu_ms": tu,
             "speedup_vs_unfused": tu / tf, "tflops_sym": fl / tf / 1e9,
@@ -219,22 +238,42 @@ def run_extras(dev, tb, only=None) -> dict:
             "frac_fp32_peak_fp32_mfma": fl / tf32 / 1e9 / PEAK_FP32_MFMA,
             "rel_err_fused_fp32_mfma_vs_fp64": abs(e_f32 - e64) / abs(e64),
             "rel_err_unfused_fp32_vs_fp64": abs(e_unf - e64) / abs(e64), "gate": 1e-6,
-            "cpu_fp32_loop_ms_est": cpu_pair_s * 96 * 96 * 1e3,
-            "cpu_sample": "12 of 9216 ordered pairs of the fp32 torch loop, scaled",
-            "cpu_threads": torch.get_num_threads(),
+            "cpu_fp32_loop_ms": cpu_loop_ms, "rel_err_cpu_fp32_loop_vs_fp64": abs(e_cpu - e64) / abs(e64),
+            "cpu_sample": "the whole fp32 torch pair loop (9216 ordered pairs), once",
+            "cpu_threads": torch.get_num_threads(), "roofline": roof,
         }  # fmt: skip
         log("c3", out["pair_energy_c3_96_672_2304"])
         del Bp
+    if only is None or "c4" in only:
+        # C4: the DF-MP2 chain at its real size (nao 1024, nocc 256, nvir 768,
+        # naux 4096): two half-transform batched GEMMs into B, then the fused
+        # pair energy (bf16x6); 1.63e14 algorithmic flop (i <= j pair count)
+        nao, nocc, nvir, naux = 1024, 256, 768, 4096
+        eri, Co, Cv, eo4, ev4 = df_mp2.chain_inputs(nao, nocc, nvir, naux, dev, seed=4)
+        th = gpu_time_ms(lambda: df_mp2.half_transform(eri, Co, Cv), reps=3, warm=1)
+        B4 = df_mp2.half_transform(eri, Co, Cv)
+        del eri
+        te = gpu_time_ms(lambda: kernels.pair_energy_sym(B4, eo4, ev4, math="bf16x6"), reps=2, warm=1)
+        e4 = float(kernels.pair_energy_sym(B4, eo4, ev4, math="bf16x6"))
+        fl = df_mp2.chain_flops(nao, nocc, nvir, naux)
+        tot = fl["half1"] + fl["half2"] + fl["energy"]
+        t_all = th + te
+        out["df_mp2_chain_c4_1024_256_768_4096"] = {
+            "half_transform_ms": th, "energy_ms": te, "chain_ms": t_all, "energy": e4,
+            "flop": tot, "tflops": tot / t_all / 1e9,
+            "half_transform_tflops": (fl["half1"] + fl["half2"]) / th / 1e9,
+            "energy_tflops_sym": fl["energy"] / te / 1e9, "energy_math": "bf16x6",
+            "frac_fp32_peak": tot / t_all / 1e9 / PEAK_FP32_MFMA,
+            "energy_frac_bf16x6_ceiling": 6 * fl["energy"] / te / 1e9 / PEAK_BF16_MFMA,
+            "parity": "tests/test_config4_gpu.py: rel <= 1e-6 against the fp64 chain on the device",
+        }  # fmt: skip
+        log("c4", out["df_mp2_chain_c4_1024_256_768_4096"])
+        del B4
+        torch.cuda.empty_cache()
     if only is None or "c5" in only:
         # C5: Ozaki gemm_fp64 at 8192^3, k = 8, against native fp64 DGEMM
-        g = torch.Generator(device=dev).manual_seed(5)
         n = 8192
-
-        def draw():
-            u = torch.rand(n, n, generator=g, device=dev, dtype=torch.float64) * 2 - 1
-            return u * torch.exp2(torch.round(4.0 * torch.randn(n, n, generator=g, device=dev, dtype=torch.float64)))
-
-        Ao, Bo = draw(), draw()
+        Ao, Bo = df_mp2.config5_inputs(dev, n, seed=5)
         to = gpu_time_ms(lambda: tb.gemm_fp64(Ao, Bo, mode="fast"), reps=3, warm=1)
         tx = gpu_time_ms(lambda: tb.gemm_fp64(Ao, Bo, mode="exact"), reps=3, warm=1)
         td = gpu_time_ms(lambda: torch.matmul(Ao, Bo), reps=3, warm=1)
@@ -243,13 +282,27 @@ def run_extras(dev, tb, only=None) -> dict:
         err = float(((tb.gemm_fp64(Ao, Bo, mode="fast") - Cd).abs() / den).max())
         errx = float(((tb.gemm_fp64(Ao, Bo, mode="exact") - Cd).abs() / den).max())
         ops = 36 * 2 * n**3
+        # slice counts 8..12 (fast mode): time and max |C - DGEMM| / (|A||B|);
+        # the difference to DGEMM settles at DGEMM's own error once the
+        # truncation is below it (tests/test_config5_slices_gpu.py judges each
+        # k against a near-exact product: host-fp64 accuracy needs k = 11 on
+        # this data)
+        sweep = []
+        for k in range(8, 13):
+            tk = gpu_time_ms(lambda: tb.gemm_fp64(Ao, Bo, slices=k, mode="fast"), reps=3, warm=1)
+            ek = float(((tb.gemm_fp64(Ao, Bo, slices=k, mode="fast") - Cd).abs() / den).max())
+            opk = k * (k + 1) // 2 * 2 * n**3
+            sweep.append({
+                "k": k, "ms": tk, "int8_tops": opk / tk / 1e9, "frac_int8_peak": opk / tk / 1e9 / PEAK_INT8,
+                "fp64_equiv_tflops": 2 * n**3 / tk / 1e9, "max_cw_diff_vs_dgemm": ek,
+            })  # fmt: skip
         out["ozaki_gemm_fp64_c5_8192_k8"] = {
             "ms": to, "mode": "fast (default: int32 diagonals, fp64 recombination)",
             "int8_tops": ops / to / 1e9, "frac_int8_peak": ops / to / 1e9 / PEAK_INT8,
             "fp64_equiv_tflops": 2 * n**3 / to / 1e9, "native_dgemm_ms": td,
             "native_dgemm_tflops": 2 * n**3 / td / 1e9, "max_cw_err_vs_dgemm": err,
             "exact_mode_ms": tx, "exact_mode_frac_int8_peak": ops / tx / 1e9 / PEAK_INT8,
-            "exact_mode_max_cw_err_vs_dgemm": errx,
+            "exact_mode_max_cw_err_vs_dgemm": errx, "slice_sweep_fast": sweep,
             "accuracy_gate": "every element within the 8-slice error bound (C5 wide-range data): "
             "tests/test_api_gpu.py::test_config5_gemm_fp64_accuracy_full_size, both modes",
         }  # fmt: skip
@@ -295,7 +348,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None,
-                    help="comma-separated subset of the extra workloads: c1,gemm8192,c3,c5,metric")
+                    help="comma-separated subset of the extra workloads: c1,gemm8192,c3,c4,c5,metric")
     ap.add_argument(
         "--calibrate-copy",
         action="store_true",

@@ -304,14 +304,9 @@ def test_config5_gemm_fp64_accuracy_full_size(dev):
     # reference's k-slice error bound (oracle.ozaki.error_bound: the
     # per-row / per-column truncation of ozaki.py:123-139 plus the
     # double-fp32 floor), against native fp64 DGEMM.
-    g = torch.Generator(device=dev).manual_seed(5)
     n = 8192
-
-    def draw():
-        u = torch.rand(n, n, generator=g, device=dev, dtype=torch.float64) * 2 - 1
-        return u * torch.exp2(torch.round(4.0 * torch.randn(n, n, generator=g, device=dev, dtype=torch.float64)))
-
-    A, B = draw(), draw()
+    A, B = df_mp2.config5_inputs(dev, n, seed=5)
+    g = torch.Generator(device=dev).manual_seed(6)
     ref = A @ B
     AB = A.abs() @ B.abs()
     bound = oz.error_bound(A, B, 8, absA_absB=AB, xp=torch) + n * 2.0**-53 * AB

@@ -250,6 +250,21 @@ def config3_inputs(device, seed: int = 3):
     return pair_inputs(96, 672, 2304, device, seed)
 
 
+def config5_inputs(device, n: int = 8192, seed: int = 5):
+    """C5 rules: A, B (n x n) fp64, each entry U(-1, 1) 2^round(N(0, 4^2)),
+    drawn on the device from a seeded device generator (A's two draws, then
+    B's)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def draw():
+        u = torch.rand(n, n, generator=g, device=device, dtype=torch.float64) * 2 - 1
+        e = torch.round(4.0 * torch.randn(n, n, generator=g, device=device, dtype=torch.float64))
+        return u * torch.exp2(e)
+
+    A = draw()
+    return A, draw()
+
+
 def chain_inputs(nao: int, nocc: int, nvir: int, naux: int, device, seed: int = 4):
     """C4 rules: eri (naux, nao, nao) = 0.02 N(0,1) symmetrised in its last two
     indices as (X + X^T) / sqrt(2) (so entries stay N(0, 0.02^2) off the
