@@ -285,7 +285,7 @@ def run_extras(dev, tb, only=None) -> dict:
         # slice counts 8..12 (fast mode): time and max |C - DGEMM| / (|A||B|);
         # the difference to DGEMM settles at DGEMM's own error once the
         # truncation is below it (tests/test_config5_slices_gpu.py judges each
-        # k against a near-exact product: host-fp64 accuracy needs k = 11 on
+        # k against a near-exact product: k = 10 meets the reference's host gate on
         # this data)
         sweep = []
         for k in range(8, 13):

@@ -246,7 +246,7 @@ int trnblas_hip_mp2_energy(int64_t ic, int64_t nocc, int64_t nvir, const float* 
  *   digits[s*ld_slice + r*ld_digit + c] (K = C contiguous).
  * per_row == 0: one exponent per column (the B operand); digits are written
  *   transposed, digits[s*ld_slice + c*ld_digit + r] (K = R contiguous).
- * per_row | 2: the interleaved layout of the fast 8-slice GEMM (mode 2 of
+ * per_row | 2: the interleaved layout of the fast GEMM (mode 2 of
  *   trnblas_hip_ozaki_gemm): digit (s, row, kk) of the digit row `row` (r or
  *   c as above) and K index kk at
  *   digits[row*ld_digit + (kk/32)*32*slices + s*32 + kk%32], i.e. the slices
@@ -273,9 +273,9 @@ int trnblas_hip_ozaki_split(int per_row, int64_t R, int64_t C, const double* X, 
  * same combine, ozaki.py:418-455). Mode 1 (fast) accumulates each diagonal
  * of slice pairs exactly in int32 and recombines in fp64 (error within the
  * same bound, not bitwise). Mode 2 is mode 1 on interleaved digits
- * (trnblas_hip_ozaki_split with per_row | 2; slices == 8, lda / ldb the
- * digit row strides >= 8 Kp, lda_slice / ldb_slice unused): the same result
- * bit for bit, with whole-cache-line loads.
+ * (trnblas_hip_ozaki_split with per_row | 2; any slice count, lda / ldb
+ * the digit row strides >= slices * Kp, lda_slice / ldb_slice unused): the
+ * same result bit for bit, each row's k-step one contiguous load.
  *
  * dA: digits (slices, >= M, Kp) with dA[s*lda_slice + m*lda + k];
  * dB: digits (slices, >= N, Kp) with dB[s*ldb_slice + n*ldb + k]; both K

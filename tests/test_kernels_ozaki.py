@@ -109,21 +109,25 @@ def test_split_interleaved_layout(dev, per, k):
 
 
 @pytest.mark.parametrize(
-    "M,K,N", [(64, 64, 64), (130, 4100, 7), (200, 9000, 31), (300, 257, 520), (1, 1, 1), (65, 129, 63)]
+    "M,K,N,k",
+    [(64, 64, 64, 8), (130, 4100, 7, 8), (200, 9000, 31, 8), (300, 257, 520, 8), (1, 1, 1, 8),
+     (65, 129, 63, 8), (200, 9000, 31, 1), (130, 4100, 70, 3), (300, 257, 520, 9),
+     (200, 9000, 31, 10), (65, 129, 63, 11), (130, 4100, 70, 12), (33, 50000, 20, 12)],
 )
-def test_fast_gemm_interleaved_equals_plain(dev, M, K, N):
+def test_fast_gemm_interleaved_equals_plain(dev, M, K, N, k):
     # same digits, same int32 diagonal sums, same fp64 recombination order:
     # the interleaved-digit kernel must match the plain-layout one bit for bit
+    # (K = 50000 at k = 12 crosses the int32 flush of the diagonals)
     from trnblas_amd.hip import kernels
 
-    A, B = inputs(M, K, N, seed=M + 3 * N)
+    A, B = inputs(M, K, N, seed=M + 3 * N + k)
     Ad, Bd = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
-    da, ea, _ = kernels.ozaki_split(Ad, 8, "row")
-    db, eb, _ = kernels.ozaki_split(Bd, 8, "col")
-    dai, _, _ = kernels.ozaki_split(Ad, 8, "row", interleaved=True)
-    dbi, _, _ = kernels.ozaki_split(Bd, 8, "col", interleaved=True)
-    C1 = kernels.ozaki_gemm(da, ea, db, eb, M, N, 8, fast=True)
-    C2 = kernels.ozaki_gemm(dai, ea, dbi, eb, M, N, 8, fast=True)
+    da, ea, _ = kernels.ozaki_split(Ad, k, "row")
+    db, eb, _ = kernels.ozaki_split(Bd, k, "col")
+    dai, _, _ = kernels.ozaki_split(Ad, k, "row", interleaved=True)
+    dbi, _, _ = kernels.ozaki_split(Bd, k, "col", interleaved=True)
+    C1 = kernels.ozaki_gemm(da, ea, db, eb, M, N, k, fast=True)
+    C2 = kernels.ozaki_gemm(dai, ea, dbi, eb, M, N, k, fast=True)
     assert torch.equal(C1, C2)
-    C3 = kernels.ozaki_gemm(dbi, eb, dai, ea, N, M, 8, fast=True, transpose_out=True)
+    C3 = kernels.ozaki_gemm(dbi, eb, dai, ea, N, M, k, fast=True, transpose_out=True)
     assert torch.equal(C1, C3) or bool(((C1 - C3).abs() <= 2.0**-50 * C1.abs()).all())

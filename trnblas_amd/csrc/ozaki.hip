@@ -677,38 +677,35 @@ __global__ __launch_bounds__(256, NB == 1 ? 2 : 1) void oz_fast_kernel(OzArgs g)
   if (nsteps == 0) flush(true);
 }
 
-// Fast mode on interleaved 8-slice digits (trnblas_hip_ozaki_split, per_row
-// bit 1): row r's 32-wide K chunk kc holds the 8 slices' 32 bytes
-// contiguously at r * ld + kc * 256 + s * 32, so one k-step of a row is 256
-// contiguous bytes (two whole cache lines) and a 1 KiB load instruction
-// covers 4 rows.
+// Fast mode on interleaved digits of any slice count KS (1..12): row r's
+// 32-wide K chunk kc holds the KS slices' 32 bytes side by side at
+// r * ld + kc * 32 KS + s * 32 (trnblas_hip_ozaki_split, per_row bit 1), so
+// a k-step of a row is 32 KS contiguous bytes.
 //
-// TM x 64 output tile per workgroup, (TM / 32) x 2 waves with one 32 x 32
-// MFMA block and 8 int32 diagonal accumulators each (as oz_fast_kernel).
-// K steps of 32 through two LDS stages. A step reads every fragment it needs
-// into registers first (8 A and 8 B slices, 64 VGPRs) and only then issues
-// the DMA of the next step into the other stage, so no LDS read is ordered
-// after an outstanding LDS DMA (which would make it wait for all of them),
-// and the DMA lands while the 36 MFMAs of the step run. A stage is
-// reusable once every wave has passed the next step's barrier: its reads
-// fed that wave's MFMAs of the previous step.
+// A 64 x 64 output tile per workgroup, 4 waves with one 32 x 32 MFMA block
+// and KS int32 diagonal accumulators each (the arithmetic and bits of
+// oz_fast_kernel), K steps of 32 through two LDS stages. A step reads every
+// fragment it needs into registers first and only then issues the DMA of
+// the next step into the other stage, so no LDS read is ordered after an
+// outstanding LDS DMA (which would make it wait for all of them) and the
+// DMA lands while the step's KS (KS + 1) / 2 MFMAs run. Up to 9 slices the
+// accumulators and fragments (24 KS VGPRs) leave two waves per SIMD; above,
+// one (a second fragment set read ahead of the MFMAs measured slower: 27.1
+// against 25.8 ms at C5, k = 10).
 //
-// LDS: 4 rows per 1040-byte block (1024 bytes + 16 pad); row m = r % 4 of a
-// block keeps its 16-byte groups XOR 4 m, so the 16 consecutive rows of one
-// fragment read (same group) fall on 16 distinct bank groups. Lane l of a
-// load instruction fills LDS slot l (row l / 16, group l % 16), i.e. loads
-// the row's global group (l % 16) ^ (4 (l / 16)): each row's 16 lanes still
-// cover its 256 bytes exactly.
-template <int TM>
-__global__ __launch_bounds__(TM * 4, TM == 64 ? 2 : 1) void oz_fast_il_kernel(OzArgs g) {
-  constexpr int TN = 64;
-  constexpr int WM = TM / 32;                      // waves along M (2 along N)
-  constexpr int W = 2 * WM;                        // waves
-  constexpr int BLK = 1024 + 16;                   // LDS bytes per load instruction
-  constexpr int OPA = TM / 4 * BLK, OPB = TN / 4 * BLK;
-  constexpr int STAGE = OPA + OPB;
-  constexpr int LA = TM / 4 / W, LB = TN / 4 / W;  // instructions per wave and step
-  static_assert(LA >= 1 && LB >= 1 && LA * W * 4 == TM && LB * W * 4 == TN, "load split");
+// LDS rows are 2 KS + 1 groups of 16 bytes (one pad group): with an odd
+// pitch the 16 consecutive rows of a fragment read fall on 16 distinct bank
+// groups. A panel is loaded as consecutive 1 KiB DMA blocks: lane l of
+// block b fills slot q = 64 b + l, i.e. group q % (2 KS + 1) of row
+// q / (2 KS + 1); pad slots and rows outside the matrix read zeros without a
+// memory access.
+template <int KS>
+__global__ __launch_bounds__(256, KS <= 9 ? 2 : 1) void oz_fast_ilk_kernel(OzArgs g) {
+  constexpr int T = 64, W = 4;
+  constexpr int RG = 2 * KS, PG = RG + 1;  // groups of a row's step, LDS pitch in groups
+  constexpr int NIP = (T * PG + 63) / 64;  // 1 KiB DMA blocks per panel
+  constexpr int OPA = NIP * 1024, STAGE = 2 * OPA;
+  constexpr int PER = (NIP + W - 1) / W;   // blocks per wave, panel and step
   __shared__ __attribute__((aligned(16))) int8_t lds[2 * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -716,63 +713,51 @@ __global__ __launch_bounds__(TM * 4, TM == 64 ? 2 : 1) void oz_fast_il_kernel(Oz
   const int t = xcd_remap(blockIdx.x, gridDim.x);
   int tm, tn;
   grouped_tile(t, g.tiles_m, g.tiles_n, 8, tm, tn);
-  const int m0 = tm * TM, n0 = tn * TN;
+  const int m0 = tm * T, n0 = tn * T;
   const int nsteps = g.Kp / 32;
 
-  // load offsets: wave w fills A blocks w LA .. +LA-1 and B blocks
-  // w LB .. +LB-1 (block b = rows 4 b .. 4 b + 3)
-  const int gl = 16 * ((lane & 15) ^ (4 * (lane >> 4)));
-  uint32_t ilA[LA], ilB[LB];
+  // wave w moves blocks w, w + W, ... of each panel: per block its lane's
+  // row offset and group (or kOzOob)
+  uint32_t voffA[PER], voffB[PER];
 #pragma unroll
-  for (int u = 0; u < LA; ++u) {
-    const int rr = 4 * (w * LA + u) + (lane >> 4);
-    ilA[u] = m0 + rr < g.M ? (uint32_t)(rr * g.lda + gl) : kOzOob;
-  }
-#pragma unroll
-  for (int u = 0; u < LB; ++u) {
-    const int rr = 4 * (w * LB + u) + (lane >> 4);
-    ilB[u] = n0 + rr < g.N ? (uint32_t)(rr * g.ldb + gl) : kOzOob;
+  for (int u = 0; u < PER; ++u) {
+    const int q = 64 * (w + u * W) + lane, r = q / PG, j = q % PG;
+    const bool in = j < RG && r < T;
+    voffA[u] = (in && m0 + r < g.M) ? (uint32_t)(r * g.lda + 16 * j) : kOzOob;
+    voffB[u] = (in && n0 + r < g.N) ? (uint32_t)(r * g.ldb + 16 * j) : kOzOob;
   }
   const int8_t* baseA = g.A + (int64_t)m0 * g.lda;
   const int8_t* baseB = g.B + (int64_t)n0 * g.ldb;
   auto load = [&](int step, int buf) {
-    // (operands as plain locals: array elements or locals of the resource
-    // type as builtin arguments fail to instantiate in the host pass of a
-    // kernel template)
-    const int soff = step * 256;
+    const int soff = step * 32 * KS;
 #pragma unroll
-    for (int u = 0; u < LA; ++u) {
-      int8_t* dst = lds + buf * STAGE + (w * LA + u) * BLK;
-      const uint32_t va = ilA[u];
+    for (int u = 0; u < PER; ++u) {
+      if (NIP % W != 0 && u + 1 == PER && w + u * W >= NIP) break;
+      int8_t* dst = lds + buf * STAGE + (w + u * W) * 1024;
+      const uint32_t va = voffA[u], vb = voffB[u];
       __builtin_amdgcn_raw_ptr_buffer_load_lds(oz_rsrc(baseA),
                                                (__attribute__((address_space(3))) void*)dst, 16,
                                                va, soff, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < LB; ++u) {
-      int8_t* dst = lds + buf * STAGE + OPA + (w * LB + u) * BLK;
-      const uint32_t vb = ilB[u];
       __builtin_amdgcn_raw_ptr_buffer_load_lds(oz_rsrc(baseB),
-                                               (__attribute__((address_space(3))) void*)dst, 16,
-                                               vb, soff, 0, 0);
+                                               (__attribute__((address_space(3))) void*)(dst + OPA),
+                                               16, vb, soff, 0, 0);
     }
   };
 
-  // Wave w: rows 32 (w % WM), columns 32 (w / WM) of the tile. Lane l reads
+  // Wave w: rows 32 (w & 1), columns 32 (w >> 1) of the tile. Lane l reads
   // row l % 32 of its block, bytes 16 (l / 32) .. +15 of each slice's 32.
-  const int wm = w % WM, wn = w / WM;
-  const int ar = 32 * wm + (lane & 31), br = 32 * wn + (lane & 31);
+  const int wm = w & 1, wn = w >> 1;
   const int h = lane >> 5;
-  const int rowA = (ar >> 2) * BLK + (ar & 3) * 256, xa = 4 * (ar & 3);
-  const int rowB = OPA + (br >> 2) * BLK + (br & 3) * 256, xb = 4 * (br & 3);
-  i32x16 acc[8];
+  const int rowA = (32 * wm + (lane & 31)) * 16 * PG + 16 * h;
+  const int rowB = OPA + (32 * wn + (lane & 31)) * 16 * PG + 16 * h;
+  i32x16 acc[KS];
 #pragma unroll
-  for (int d = 0; d < 8; ++d)
+  for (int d = 0; d < KS; ++d)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[d][e] = 0;
 
   // Lane l of a 32x32 block: column l % 32, rows 8 (e/4) + 4 (l/32) + e % 4.
-  constexpr int k = 8;
+  constexpr int k = KS;
   const int off = -2 * (kSliceBits - 1) - kSliceBits * (k - 1);
   const int n = n0 + 32 * wn + (lane & 31);
   const int eb = n < g.N ? g.eB[n] : 0;
@@ -785,7 +770,7 @@ __global__ __launch_bounds__(TM * 4, TM == 64 ? 2 : 1) void oz_fast_il_kernel(Oz
       for (int d = k - 1; d >= 0; --d) v[e] += (double)acc[d][e] * pow2(kSliceBits * (k - 1 - d));
     }
 #pragma unroll
-    for (int d = 0; d < 8; ++d)
+    for (int d = 0; d < KS; ++d)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[d][e] = 0;
 #pragma unroll 4
@@ -803,6 +788,21 @@ __global__ __launch_bounds__(TM * 4, TM == 64 ? 2 : 1) void oz_fast_il_kernel(Oz
     }
   };
 
+  auto read = [&](const int8_t* buf, i32x4 (&fa)[KS], i32x4 (&fb)[KS]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s2 = 0; s2 < KS; ++s2) {
+      fa[s2] = *reinterpret_cast<const i32x4*>(buf + rowA + 32 * s2);
+      fb[s2] = *reinterpret_cast<const i32x4*>(buf + rowB + 32 * s2);
+    }
+  };
+  auto mfmas = [&](const i32x4 (&fa)[KS], const i32x4 (&fb)[KS]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int tt = 0; tt < KS; ++tt)
+#pragma unroll
+      for (int s2 = 0; s2 < KS - tt; ++s2)
+        acc[s2 + tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s2], fb[tt], acc[s2 + tt], 0, 0, 0);
+  };
+
   for (int s0 = 0; s0 < nsteps; s0 += g.flush) {
     const int s1 = s0 + g.flush < nsteps ? s0 + g.flush : nsteps;
     if (s0 > 0) __syncthreads();  // every wave is done with the previous block's stages
@@ -811,19 +811,10 @@ __global__ __launch_bounds__(TM * 4, TM == 64 ? 2 : 1) void oz_fast_il_kernel(Oz
       const int cur = (s - s0) & 1;
       __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA of step s has landed
       __syncthreads();                // every wave's has; stage cur ^ 1 is free
-      const int8_t* buf = lds + cur * STAGE;
-      i32x4 fa[8], fb[8];
-#pragma unroll
-      for (int s2 = 0; s2 < 8; ++s2) {
-        fa[s2] = *reinterpret_cast<const i32x4*>(buf + rowA + 16 * (((2 * s2) ^ xa) | h));
-        fb[s2] = *reinterpret_cast<const i32x4*>(buf + rowB + 16 * (((2 * s2) ^ xb) | h));
-      }
+      i32x4 fa[KS], fb[KS];
+      read(lds + cur * STAGE, fa, fb);
       if (s + 1 < s1) load(s + 1, cur ^ 1);
-#pragma unroll
-      for (int tt = 0; tt < 8; ++tt)
-#pragma unroll
-        for (int s2 = 0; s2 < 8 - tt; ++s2)
-          acc[s2 + tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s2], fb[tt], acc[s2 + tt], 0, 0, 0);
+      mfmas(fa, fb);
     }
     flush(s0 == 0);
   }
@@ -855,17 +846,28 @@ constexpr int OZ_NB = 1;
 static int oz_fast_launch(OzArgs& g, hipStream_t s, bool il) {
   const int64_t kflush = ((1ll << 31) - 1) / (4096ll * g.k);  // K terms per diagonal
   if (il) {
-    TRNBLAS_CHECK_ARG(g.k == 8, "ozaki_gemm(fast, interleaved): slices %d, need 8", g.k);
-    // 64 x 64 tiles, two workgroups per CU: measured faster at C5 (the
-    // 8192^3 call 14.2 ms against 15.0 ms) than 128 x 64 tiles with one 8-wave
-    // workgroup per CU, whose barriers stall every wave on the CU at once
-    constexpr int tmr = 64;
-    g.tiles_m = (g.M + tmr - 1) / tmr;
+    // 64 x 64 tiles (two workgroups per CU up to 9 slices): measured faster
+    // at C5 (the 8192^3 call 14.2 ms against 15.0 ms) than 128 x 64 tiles
+    // with one 8-wave workgroup per CU, whose barriers stall every wave on
+    // the CU at once
+    g.tiles_m = (g.M + 63) / 64;
     g.tiles_n = (g.N + 63) / 64;
     const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
     TRNBLAS_CHECK_ARG(nt < (1ll << 31), "ozaki: too many tiles");
     g.flush = (int)std::max<int64_t>(1, kflush / 32);
-    hipLaunchKernelGGL((oz_fast_il_kernel<tmr>), dim3((unsigned)nt), dim3(4 * tmr), 0, s, g);
+    const dim3 grid((unsigned)nt), block(256);
+    switch (g.k) {
+#define OZ_IL(KS) \
+  case KS:        \
+    hipLaunchKernelGGL((oz_fast_ilk_kernel<KS>), grid, block, 0, s, g); \
+    break;
+      OZ_IL(1) OZ_IL(2) OZ_IL(3) OZ_IL(4) OZ_IL(5) OZ_IL(6)
+      OZ_IL(7) OZ_IL(8) OZ_IL(9) OZ_IL(10) OZ_IL(11) OZ_IL(12)
+#undef OZ_IL
+      default:
+        set_error("ozaki_gemm(fast): slices %d not in [1, 12]", g.k);
+        return TRNBLAS_E_ARG;
+    }
     return check_launch("ozaki_gemm(fast)");
   }
   g.tiles_m = (g.M + 63) / 64;
@@ -993,8 +995,8 @@ extern "C" int trnblas_hip_ozaki_gemm(int mode, int slices, int64_t M, int64_t N
   int rc = oz_check_operands(slices, M, N, Kp, kb, dA, lda, lda_slice, dB, ldb, ldb_slice);
   if (rc) return rc;
   if (mode == 2)
-    TRNBLAS_CHECK_ARG(slices == 8 && lda >= 8 * Kp && ldb >= 8 * Kp,
-                      "ozaki_gemm: interleaved digits need 8 slices and rows of >= 8 Kp bytes");
+    TRNBLAS_CHECK_ARG(lda >= slices * Kp && ldb >= slices * Kp,
+                      "ozaki_gemm: interleaved digits need rows of >= slices * Kp bytes");
   TRNBLAS_CHECK_ARG(Kp > 0, "ozaki_gemm: K == 0 (the caller returns zeros)");
   TRNBLAS_CHECK_ARG(C && eA && eB, "ozaki_gemm: NULL C / exponents");
   OzArgs g{};

@@ -437,7 +437,7 @@ def ozaki_split(X: torch.Tensor, slices: int, per: str, interleaved: bool = Fals
     per="col": digits (k, Cp, Rp) int8 with digit[s, c, r] (K = R contiguous,
     the column split written transposed). Exponents int32 (R,) / (C,).
     interleaved: digits (rows, Kp * k) instead, the k slices of each 32-wide
-    K chunk of a row side by side (the fast GEMM's 8-slice operand layout).
+    K chunk of a row side by side (the fast GEMM's operand layout).
     Returns (digits, exps, nonfinite) where `nonfinite` is a 0-d int32 device
     flag (the digits are undefined when it is set)."""
     dev = _require_device(X)
@@ -473,7 +473,7 @@ def ozaki_gemm(dA, eA, dB, eB, M: int, N: int, slices: int, kb: int | None = Non
     (K-contiguous) and their exponents: the bit-exact schedule (fast=False,
     K blocks of kb) or the fast one (int32 diagonals, fp64 recombination; kb
     unused). 2-D dA / dB are interleaved digits (ozaki_split(interleaved=True),
-    8 slices, fast only). With transpose_out, writes C^T into `out` (N, M)
+    fast only). With transpose_out, writes C^T into `out` (N, M)
     instead."""
     dev = _require_device(dA, dB, eA, eB)
     interleaved = dA.dim() == 2

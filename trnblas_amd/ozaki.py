@@ -189,8 +189,9 @@ def run_device(
     if K == 0:
         return C.zero_()
     fast = mode == "fast"
-    # the fast schedule reads 8-slice digits interleaved (whole cache lines)
-    il = fast and k == 8
+    # the fast schedule reads the digits interleaved (a row's k slices of a
+    # 32-wide K chunk side by side)
+    il = fast
     # the non-finite flags are read once, after the GEMM (no stall between the
     # launches; a GEMM on undefined digits stays in bounds and is discarded)
     da, ea, bad_a = _digits_of(A, k, "A", il)
