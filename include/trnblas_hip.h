@@ -280,8 +280,8 @@ int trnblas_hip_ozaki_split(int per_row, int64_t R, int64_t C, const double* X, 
  * dA: digits (slices, >= M, Kp) with dA[s*lda_slice + m*lda + k];
  * dB: digits (slices, >= N, Kp) with dB[s*ldb_slice + n*ldb + k]; both K
  * contiguous, zero beyond M / N / K. Kp is K padded to 128. kb: K block
- * (a multiple of 128 dividing into Kp blocks, `ozaki.plan`), blocks summed
- * in fp64 in order. C element (m, n) at C[m*ldc_m + n*ldc_n] (ldc_m, ldc_n
+ * (a multiple of 128, `ozaki.plan`; the last block holds what remains of
+ * Kp), blocks summed in fp64 in order. C element (m, n) at C[m*ldc_m + n*ldc_n] (ldc_m, ldc_n
  * let the caller write C^T for the narrow-N swap of `ozaki.run`).
  * Replaces torch.ops.trnblas.ozaki_gemm (trnblas/nki/_native.py:77-85;
  * kernel dispatch.py:3887-3918) and the host `combine`.

@@ -224,7 +224,7 @@ def test_config4_chain_small(dev):
 @pytest.mark.parametrize(
     "M,K,N,k,views",
     [(37, 300, 53, 7, ""), (130, 4100, 7, 8, ""), (200, 600, 520, 8, "AB"), (5, 4100, 3, 8, "A"),
-     (64, 64, 64, 12, "B"), (1, 1, 1, 8, "")],
+     (64, 64, 64, 12, "B"), (1, 1, 1, 8, ""), (600, 700, 650, 8, ""), (6, 90000, 3, 12, "")],
 )
 def test_gemm_fp64_bitwise_vs_reference(dev, M, K, N, k, views):
     A, B = exact.inputs(M, K, N, seed=M * 3 + N)

@@ -309,6 +309,7 @@ struct OzArgs {
   int64_t ldc_m, ldc_n, ldh;
   int tiles_m, tiles_n;
   int flush;      // fast mode: k-steps between int32 -> fp64 flushes of the diagonals
+  int64_t hl_rs, hl_cs, hl_lo;  // oz_exact_kernel: (hi, lo) output strides (floats)
 };
 
 __device__ __forceinline__ void two_sum32(float& hi, float& lo, float p) {
@@ -334,6 +335,10 @@ struct OzStep {
   int d, s, ks;
 };
 
+// Exact mode over K blocks (`plan`'s K blocking, K beyond ~2^16: each block
+// its own (hi, lo) chain, the blocks summed in fp64 into C): register-staged
+// 64-byte k-steps, one pair's tiles per step. Single-block calls take
+// oz_exact_kernel.
 template <int BM, int BN, int BK, int OUT>  // OUT: 0 combine into C, 1 raw hilo
 __global__ __launch_bounds__(256) void oz_gemm_kernel(OzArgs g) {
   constexpr int NT = 256;
@@ -353,12 +358,10 @@ __global__ __launch_bounds__(256) void oz_gemm_kernel(OzArgs g) {
   grouped_tile(t, g.tiles_m, g.tiles_n, 8, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int k = g.k;
-  const int nkb = g.Kp / g.kb;
-  const int kt = g.kb / kTileK;  // 128-tiles per slice in a K block
-  const int steps_per_pair = kt * SUB;
+  const int nkb = (g.Kp + g.kb - 1) / g.kb;  // the last block may be shorter
   const int npairs = k * (k + 1) / 2;
-  const int total = npairs * steps_per_pair;
-  const int per = kt >= kGroupTiles ? 1 : kGroupTiles / kt;
+  // per K block: 128-tiles per slice, and the group cut that follows from it
+  int kt = 0, steps_per_pair = 0, total = 0, per = 1;
 
   i32x4 ra[NVA], rb[NVB];
   int kbase = 0;
@@ -414,6 +417,10 @@ __global__ __launch_bounds__(256) void oz_gemm_kernel(OzArgs g) {
 
   for (int kbi = 0; kbi < nkb; ++kbi) {
     kbase = kbi * g.kb;
+    kt = (g.Kp - kbase < g.kb ? g.Kp - kbase : g.kb) / kTileK;
+    steps_per_pair = kt * SUB;
+    total = npairs * steps_per_pair;
+    per = kt >= kGroupTiles ? 1 : kGroupTiles / kt;
     i32x16 acc[FM][FN];
     float hi[FM][FN][16], lo[FM][FN][16];
 #pragma unroll
@@ -821,6 +828,210 @@ __global__ __launch_bounds__(256, KS <= 9 ? 2 : 1) void oz_fast_ilk_kernel(OzArg
   if (nsteps == 0) flush(true);
 }
 
+// Exact mode, streamed by slice pair: the reference's groups and fp32 TwoSum
+// order (bit for bit the arithmetic of `reference_gemm`), on a 128 x 128
+// output tile.
+//
+// 4 waves (2 x 2), each a 64 x 64 block as 2 x 2 MFMA 32 x 32 blocks with
+// its int32 group accumulators and fp32 (hi, lo) pairs in registers (192
+// VGPRs); two workgroups per CU, so one computes while the other waits at
+// a barrier. The walk is the schedule's (diagonal, pair, K tile) order; each
+// step is one 128-byte K tile of the pair's A and B slices, moved by LDS DMA
+// (buffer_load_dwordx4 ... lds) into one of two LDS stages. A step reads
+// the fragments of its first two 32-byte chunks, runs their MFMAs, reads
+// the last two chunks and only then issues the DMA of the next step into
+// the other stage (an LDS read ordered after an outstanding LDS DMA would
+// wait for it), then runs the last MFMAs: at most two chunks' fragments
+// (32 VGPRs) are live.
+//
+// LDS rows are 128 bytes with the 16-byte groups XOR ((r >> 1) & 7) per
+// row r (as the GEMM kernel's K-contiguous panels), so a 1 KiB DMA block is
+// 8 whole rows and the 16 rows of a fragment read fall on distinct bank
+// groups. Lane l of block b loads row 8 b + l / 8, global group
+// (l % 8) ^ ((row >> 1) & 7): within a wave's blocks that is two per-lane
+// offsets (even and odd blocks) plus a uniform row offset; rows past M / N
+// read zeros.
+__global__ __launch_bounds__(256, 2) void oz_exact_kernel(OzArgs g) {
+  constexpr int TM = 128, TN = 128;
+  constexpr int PA = TM * 128, STG = PA + TN * 128;  // bytes: A panel, stage
+  __shared__ __attribute__((aligned(16))) int8_t lds[2 * STG];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int lane = tid & 63;
+  const int wm0 = (wave >> 1) * 64, wn0 = (wave & 1) * 64;
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  int tm, tn;
+  grouped_tile(t, g.tiles_m, g.tiles_n, 8, tm, tn);
+  const int m0 = tm * TM, n0 = tn * TN;
+  const int k = g.k;
+  const int kt = g.Kp / kTileK;  // K tiles per slice (one K block: kb == Kp)
+  const int total = k * (k + 1) / 2 * kt;
+  const int per = kt >= kGroupTiles ? 1 : kGroupTiles / kt;
+
+  // wave w fills blocks 4 w .. 4 w + 3 of each panel: block 4 w + u holds
+  // rows 8 (4 w + u) + l / 8, whose swizzle is ((l / 8) >> 1) + 4 (u & 1)
+  const int lr = lane >> 3, lq = lane & 7;
+  const uint32_t vA0 = (uint32_t)(lr * g.lda + 16 * (lq ^ (lr >> 1)));
+  const uint32_t vA1 = (uint32_t)(lr * g.lda + 16 * (lq ^ ((lr >> 1) + 4)));
+  const uint32_t vB0 = (uint32_t)(lr * g.ldb + 16 * (lq ^ (lr >> 1)));
+  const uint32_t vB1 = (uint32_t)(lr * g.ldb + 16 * (lq ^ ((lr >> 1) + 4)));
+  auto dma = [&](int8_t* st, int d, int sp, int ks) __attribute__((always_inline)) {
+    const int64_t koff = (int64_t)ks * kTileK;
+    const int8_t* pa = g.A + sp * g.lda_s + (int64_t)m0 * g.lda + koff;
+    const int8_t* pb = g.B + (d - sp) * g.ldb_s + (int64_t)n0 * g.ldb + koff;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int rows = 8 * (4 * wave + u);
+      int8_t* dst = st + (4 * wave + u) * 1024;
+      // rows past M / N (an edge tile) read zeros without a memory access
+      const uint32_t va = m0 + rows + lr < g.M ? ((u & 1) ? vA1 : vA0) : kOzOob;
+      const uint32_t vb = n0 + rows + lr < g.N ? ((u & 1) ? vB1 : vB0) : kOzOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(oz_rsrc(pa),
+                                               (__attribute__((address_space(3))) void*)dst, 16,
+                                               va, rows * (int)g.lda, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          oz_rsrc(pb), (__attribute__((address_space(3))) void*)(dst + PA), 16, vb,
+          rows * (int)g.ldb, 0, 0);
+    }
+  };
+
+  {
+    // the lane index is made opaque: otherwise the per-lane addresses of
+    // the whole walk are hoisted and kept live
+    asm volatile("" : "+v"(lane));
+    i32x16 acc[2][2];
+    float hi[2][2][16], lo[2][2][16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          acc[i][j][r] = 0;
+          hi[i][j][r] = 0.0f;
+          lo[i][j][r] = 0.0f;
+        }
+    // fragments of chunk c: the lane's rows (32 per MFMA block), global
+    // group 2 c + l / 32 (rows 32 apart share the swizzle)
+    const int sw = ((lane & 31) >> 1) & 7;
+    const int ra = (wm0 + (lane & 31)) * 128, rb = PA + (wn0 + (lane & 31)) * 128;
+    auto rd = [&](const int8_t* cur, int c, i32x4 (&f)[4]) __attribute__((always_inline)) {
+      const int o = 16 * ((2 * c + (lane >> 5)) ^ sw);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        f[i] = *reinterpret_cast<const i32x4*>(cur + ra + o + 32 * 128 * i);
+        f[2 + i] = *reinterpret_cast<const i32x4*>(cur + rb + o + 32 * 128 * i);
+      }
+    };
+    auto mm = [&](const i32x4 (&f)[4]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[i], f[2 + j], acc[i][j], 0, 0, 0);
+    };
+
+    int d = k - 1, sp = 0, ks = 0;  // the step being computed
+    dma(lds, d, sp, ks);
+    for (int n = 0; n < total; ++n) {
+      int8_t* cur = lds + (n & 1) * STG;
+      int8_t* oth = lds + ((n & 1) ^ 1) * STG;
+      // the next step of the walk: K tiles, then pairs s = 0 .. d (t = d - s),
+      // then diagonals d = k-1 .. 0
+      int nd = d, ns = sp, nk = ks + 1;
+      if (nk == kt) {
+        nk = 0;
+        if (++ns > nd) {
+          ns = 0;
+          --nd;
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA of step n has landed
+      __syncthreads();                // every wave's has; every read of `oth` is done
+      i32x4 f0[4], f1[4];
+      rd(cur, 0, f0);
+      rd(cur, 1, f1);
+      mm(f0);
+      mm(f1);
+      rd(cur, 2, f0);
+      rd(cur, 3, f1);
+      if (n + 1 < total) dma(oth, nd, ns, nk);
+      mm(f0);
+      mm(f1);
+      // a group closes after this step (ozaki.py:337-355): fold its exact
+      // int32 sums, scaled by 2^(7 (k - 1 - d)), into (hi, lo)
+      const bool end = kt >= kGroupTiles ? ((ks + 1) % kGroupTiles == 0 || ks + 1 == kt)
+                                         : (ks + 1 == kt && ((sp + 1) % per == 0 || sp == d));
+      if (end) {
+        const float scale = __int_as_float((127 + kSliceBits * (k - 1 - d)) << 23);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const float pv = (float)acc[i][j][r] * scale;  // exact: |G| <= 2^24
+              two_sum32(hi[i][j][r], lo[i][j][r], pv);
+              acc[i][j][r] = 0;
+            }
+      }
+      d = nd, sp = ns, ks = nk;
+    }
+
+    // Epilogue: the raw (hi, lo) pairs (lane l of a 32x32 block: column
+    // l % 32, rows 8 (r/4) + 4 (l/32) + r % 4), into two planes (the hilo
+    // surface) or as the two words of C's own 8 bytes per element (the fp64
+    // recombination is then oz_combine_kernel, which reads them in place).
+    asm volatile("" : "+v"(lane));
+    // (one base address per 32 x 32 block; the row offsets are uniform)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn0 + j * 32 + (lane & 31);
+        const int mb = m0 + wm0 + i * 32 + (lane >> 5) * 4;
+        if (n >= g.N) continue;
+        // (hi, lo) of element (m, n) at hilo[m rs + n cs] and lo_off floats on
+        float* hb = g.hilo + (int64_t)mb * g.hl_rs + (int64_t)n * g.hl_cs;
+        const int64_t rs = g.hl_rs, lo_off = g.hl_lo;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dm = (r >> 2) * 8 + (r & 3);
+          if (mb + dm >= g.M) continue;
+          hb[dm * rs] = hi[i][j][r];
+          hb[dm * rs + lo_off] = lo[i][j][r];
+        }
+      }
+  }
+}
+
+// The fp64 recombination of the exact mode (ozaki.py:418-455, `combine`):
+// C[m][n] = ((double) hi + (double) lo) 2^(eA[m] + eB[n] + off), reading the
+// float2 (hi, lo) that oz_exact_kernel left in C's own 8 bytes and writing
+// the fp64 value in its place. One element per thread.
+__global__ __launch_bounds__(256) void oz_combine_kernel(int M, int N, int k, const int32_t* eA,
+                                                         const int32_t* eB, double* C,
+                                                         int64_t ldc_m, int64_t ldc_n) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)M * N) return;
+  // consecutive threads along C's contiguous dimension
+  const bool n_fast = ldc_n == 1;
+  const int m = n_fast ? (int)(idx / N) : (int)(idx % M);
+  const int n = n_fast ? (int)(idx % N) : (int)(idx / M);
+  double* dst = C + (int64_t)m * ldc_m + (int64_t)n * ldc_n;
+  const float2 hl = *reinterpret_cast<const float2*>(dst);
+  const int off = -2 * (kSliceBits - 1) - kSliceBits * (k - 1);
+  const int ea = eA[m] + off, eb = eB[n];
+  const double v = (double)hl.x + (double)hl.y;
+  double c;
+  if (ea < 900 && ea > -900 && eb < 900 && eb > -900)
+    c = (v * pow2(ea)) * pow2(eb);
+  else
+    c = ldexp(v, ea + eb);
+  *dst = c;
+}
+
 constexpr int kOzBM = 128, kOzBN = 128, kOzBK = 64;
 
 static int oz_launch(OzArgs& g, int out, hipStream_t s) {
@@ -828,6 +1039,28 @@ static int oz_launch(OzArgs& g, int out, hipStream_t s) {
   g.tiles_n = (g.N + kOzBN - 1) / kOzBN;
   const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
   TRNBLAS_CHECK_ARG(nt < (1ll << 31), "ozaki: too many tiles");
+  if (g.kb == g.Kp) {
+    // one K block (K up to ~2^16): the streamed kernel (C5: 22.7 ms against
+    // 63.8 ms for oz_gemm_kernel, bit-equal), then (into C) the fp64 combine
+    if (out == 0) {
+      g.hilo = reinterpret_cast<float*>(g.C);
+      g.hl_rs = 2 * g.ldc_m;
+      g.hl_cs = 2 * g.ldc_n;
+      g.hl_lo = 1;
+    } else {
+      g.hl_rs = g.ldh;
+      g.hl_cs = 1;
+      g.hl_lo = (int64_t)g.M * g.ldh;
+    }
+    hipLaunchKernelGGL(oz_exact_kernel, dim3((unsigned)nt), dim3(256), 0, s, g);
+    int rc = check_launch("ozaki_gemm");
+    if (rc || out != 0) return rc;
+    const int64_t n = (int64_t)g.M * g.N;
+    TRNBLAS_CHECK_ARG((n + 255) / 256 < (1ll << 31), "ozaki: too many elements");
+    hipLaunchKernelGGL(oz_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g.M,
+                       g.N, g.k, g.eA, g.eB, g.C, g.ldc_m, g.ldc_n);
+    return check_launch("ozaki_gemm(combine)");
+  }
   if (out == 0)
     hipLaunchKernelGGL((oz_gemm_kernel<kOzBM, kOzBN, kOzBK, 0>), dim3((unsigned)nt), dim3(256),
                        0, s, g);
@@ -900,8 +1133,8 @@ static int oz_check_operands(int slices, int64_t M, int64_t N, int64_t Kp, int64
   TRNBLAS_CHECK_ARG(M >= 0 && N >= 0 && Kp >= 0 && M < (1 << 30) && N < (1 << 30),
                     "ozaki: bad size");
   TRNBLAS_CHECK_ARG(Kp % kTileK == 0, "ozaki: Kp %lld not a multiple of 128", (long long)Kp);
-  TRNBLAS_CHECK_ARG(kb > 0 && kb % kTileK == 0 && Kp % kb == 0,
-                    "ozaki: K block %lld must be a multiple of 128 dividing Kp", (long long)kb);
+  TRNBLAS_CHECK_ARG(kb > 0 && kb % kTileK == 0,
+                    "ozaki: K block %lld must be a positive multiple of 128", (long long)kb);
   TRNBLAS_CHECK_ARG(dA && dB, "ozaki: NULL digits");
   TRNBLAS_CHECK_ARG(lda >= Kp && ldb >= Kp && lda % 16 == 0 && ldb % 16 == 0 &&
                         lda_slice % 16 == 0 && ldb_slice % 16 == 0,
