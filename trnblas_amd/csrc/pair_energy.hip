@@ -747,29 +747,41 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
     auto frag = [&](const uint16_t* b, int pc, int r) __attribute__((always_inline)) {
       return *reinterpret_cast<const bf16x8*>(b + (pc * S + r) * BK + fslot);
     };
+    constexpr int ka[6] = {2, 1, 0, 1, 0, 0}, kb[6] = {0, 1, 2, 0, 1, 0};
     bf16x8 fa[3][3];
+    // Blocks (rb, cb) in the order cb-major; before a block's six MFMAs
+    // the fragments the next block adds (A rows of rb + 1 in column block
+    // 0, B columns of cb + 1 at rb = 2) are read, and scheduling barriers
+    // keep that order: the LDS reads of a step are spread over its MFMAs
+    // instead of all preceding them (C3: 55.5 against 56.4 ms).
+    bf16x8 fb[3][3];
 #pragma unroll
-    for (int rb = 0; rb < 3; ++rb)
-#pragma unroll
-      for (int pc = 0; pc < 3; ++pc) fa[rb][pc] = frag(bufA, pc, ar0 + 16 * rb + (lane & 15));
-#pragma unroll
-    for (int cb = 0; cb < 3; ++cb) {
-      bf16x8 fb[3];
-#pragma unroll
-      for (int pc = 0; pc < 3; ++pc) fb[pc] = frag(bufB, pc, br0 + 16 * cb + (lane & 15));
-#pragma unroll
-      for (int rb = 0; rb < 3; ++rb)
-        part[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            fa[rb][2], fb[0], FIRST ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb], 0, 0, 0);
-#pragma unroll
-      for (int e = 1; e < 6; ++e) {
-        constexpr int ka[6] = {2, 1, 0, 1, 0, 0}, kb[6] = {0, 1, 2, 0, 1, 0};
-#pragma unroll
-        for (int rb = 0; rb < 3; ++rb)
-          part[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[rb][ka[e]], fb[kb[e]],
-                                                                 part[rb][cb], 0, 0, 0);
-      }
+    for (int pc = 0; pc < 3; ++pc) {
+      fb[0][pc] = frag(bufB, pc, br0 + (lane & 15));
+      fa[0][pc] = frag(bufA, pc, ar0 + (lane & 15));
     }
+#pragma unroll
+    for (int cb = 0; cb < 3; ++cb)
+#pragma unroll
+      for (int rb = 0; rb < 3; ++rb) {
+        if (cb == 0 && rb < 2) {
+#pragma unroll
+          for (int pc = 0; pc < 3; ++pc)
+            fa[rb + 1][pc] = frag(bufA, pc, ar0 + 16 * (rb + 1) + (lane & 15));
+        } else if (rb == 2 && cb < 2) {
+#pragma unroll
+          for (int pc = 0; pc < 3; ++pc)
+            fb[cb + 1][pc] = frag(bufB, pc, br0 + 16 * (cb + 1) + (lane & 15));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        part[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            fa[rb][2], fb[cb][0], FIRST ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb], 0, 0, 0);
+#pragma unroll
+        for (int e = 1; e < 6; ++e)
+          part[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[rb][ka[e]], fb[cb][kb[e]],
+                                                                 part[rb][cb], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     if (t + 1 < nsteps) store(stg[1 - P], 1 - P);
   };
   using I0 = std::integral_constant<int, 0>;
