@@ -77,6 +77,46 @@ def test_route_table(monkeypatch):
         d._gemm_route(big, big)
 
 
+@pytest.mark.parametrize(
+    "a_shape,b_shape,dtype,contig,op,want",
+    [
+        ((8192, 8192), (8192, 8192), torch.float32, True, "gemm", False),  # fp32: accuracy gate
+        ((8192, 8192), (8192, 8192), torch.bfloat16, True, "gemm", True),
+        ((2048, 2048), (2048, 2048), torch.bfloat16, True, "gemm", True),
+        ((2048, 128), (128, 2048), torch.bfloat16, True, "gemm", False),  # short K: the kernel
+        ((1024, 8192), (8192, 1024), torch.bfloat16, True, "gemm", False),  # long K: the kernel
+        ((256, 8192), (8192, 8192), torch.float16, True, "gemm", False),
+        ((8192, 256), (256, 8192), torch.bfloat16, False, "gemm", False),  # K 256 < 512
+        ((8192, 1024), (1024, 8192), torch.bfloat16, False, "gemm", True),  # 2-D views are fine
+        ((64, 512, 2048), (64, 2048, 512), torch.bfloat16, True, "batched_gemm", True),  # C2b
+        ((64, 512, 2048), (64, 2048, 512), torch.bfloat16, False, "batched_gemm", False),
+        ((64, 512, 2048), (64, 2048, 512), torch.float32, True, "batched_gemm", False),
+        ((4096, 8192), (8192, 4096), torch.bfloat16, True, "syrk", False),  # triangle
+    ],
+)
+def test_device_route_known_answers(a_shape, b_shape, dtype, contig, op, want):
+    # the measured hipBLASLt-vs-kernel crossover of device-resident GEMMs
+    assert d._aten_gemm_wins(a_shape, b_shape, dtype, contig, op) is want
+
+
+@pytest.mark.parametrize(
+    "shape,want",
+    [
+        ((96, 672, 2304), "hip"),  # C3
+        ((256, 768, 4096), "hip"),  # C4's energy
+        ((16, 128, 1536), "hip"),
+        ((4, 448, 1536), "hip"),
+        ((2, 448, 1536), "aten"),  # 30 work items on 256 CUs
+        ((64, 32, 1536), "aten"),  # nvir far below the 96-row tile
+        ((1, 672, 2304), "aten"),  # one pair: one item's k-steps are the whole run
+    ],
+)
+def test_pair_energy_route_known_answers(monkeypatch, shape, want):
+    # the measured fused-vs-unfused crossover (estimates in ms)
+    fused, unfused = d._pair_energy_estimates(*shape)
+    assert ("aten" if unfused < fused else "hip") == want
+
+
 def test_route_grad_goes_to_torch(monkeypatch):
     _fake_gpu(monkeypatch)
     A = torch.randn(512, 512, requires_grad=True)

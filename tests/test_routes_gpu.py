@@ -1,0 +1,120 @@
+"""The routes of the public API on the GPU box: host operands large enough
+for the upload route (the reference's `_upload` / `_to_host`,
+nki/dispatch.py:254-274, :2075-2101) come back on the host in pinned memory
+and match the reference's CPU path at 1e-6 |A||B|; device-resident calls
+take the kernel or hipBLASLt as the measured crossover says (the
+reference's `_gemm_route` / `_lnc_gemm_wins`, :633-727), and the pair energy
+takes the fused kernel or the unfused path by its crossover (:2680-2703)."""
+
+import pytest
+import torch
+
+import trnblas_amd as tb
+from oracle import blas
+from oracle import pair_energy as pe
+from trnblas_amd import df_mp2
+from trnblas_amd.hip import dispatch as d
+from trnblas_amd.hip import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def _cw(D, ref, den):
+    den = torch.where(den > 0, den, torch.ones_like(den))
+    return float(((D.double() - ref) / den).abs().max())
+
+
+class _Launches:
+    """Names of the HIP kernel families launched while active."""
+
+    def __init__(self):
+        self.names = []
+
+    def __call__(self, kernel, phase):
+        if phase == "begin":
+            self.names.append(kernel)
+
+    def __enter__(self):
+        kernels._launch_probe = self
+        return self
+
+    def __exit__(self, *exc):
+        kernels._launch_probe = None
+
+
+def test_upload_route_gemm_batched_syrk(dev):
+    g = torch.Generator().manual_seed(21)
+    A = torch.randn(2048, 1536, generator=g)
+    B = torch.randn(1536, 1024, generator=g)
+    C = torch.randn(2048, 1024, generator=g)
+    assert d._gemm_route(A, B) == "upload"
+    with _Launches() as seen:
+        D = tb.gemm(1.0, A, B, beta=0.5, C=C)
+    assert "gemm" in seen.names  # the kernel ran on the GPU
+    assert D.device.type == "cpu" and D.is_pinned()
+    den = blas.gemm_cw_den(1.0, A, B, 0.5, C)
+    assert _cw(D, blas.gemm_cpu(1.0, A, B, 0.5, C).double(), den) <= 1e-6
+    assert _cw(D, blas.gemm_f64(1.0, A, B, 0.5, C), den) <= 1e-6
+
+    A3 = torch.randn(8, 512, 1024, generator=g)
+    B3 = torch.randn(8, 1024, 512, generator=g)
+    assert d._gemm_route(A3, B3, op="batched_gemm") == "upload"
+    with _Launches() as seen:
+        D3 = tb.batched_gemm(1.0, A3, B3)
+    assert "gemm" in seen.names
+    assert D3.device.type == "cpu" and D3.is_pinned()
+    ref3 = A3.double() @ B3.double()
+    assert _cw(D3, ref3, A3.double().abs() @ B3.double().abs()) <= 1e-6
+
+    As = torch.randn(1536, 2048, generator=g)
+    X = torch.randn(1536, 1536, generator=g)
+    Cs = torch.tril(X) + torch.tril(X, -1).T
+    with _Launches() as seen:
+        S = tb.syrk(1.0, As, beta=0.5, C=Cs, uplo="lower")
+    assert "syrk" in seen.names
+    assert S.device.type == "cpu" and S.is_pinned() and torch.equal(S, S.T)
+    ref = blas.syrk_f64(1.0, As, 0.5, Cs, uplo="lower")
+    den = As.double().abs() @ As.double().abs().T + 0.5 * Cs.double().abs()
+    assert _cw(S, ref, den) <= 1e-6
+    assert _cw(S, blas.syrk_cpu(1.0, As, 0.5, Cs, uplo="lower").double(), den) <= 1e-6
+
+
+def test_device_gemm_route_by_dtype_and_shape(dev):
+    g = torch.Generator(device=dev).manual_seed(22)
+    # fp32: the kernel at every size (the 1e-6 gate)
+    A = torch.randn(4096, 4096, device=dev, generator=g)
+    with _Launches() as seen:
+        D = tb.gemm(1.0, A, A)
+    assert seen.names == ["gemm"]
+    # bf16 at 4096^3: hipBLASLt (measured 0.72-0.80 of the kernel's time)
+    Ab = A.bfloat16()
+    with _Launches() as seen:
+        Db = tb.gemm(1.0, Ab, Ab)
+    assert seen.names == []
+    ref = (Ab.float() @ Ab.float()).double()
+    den = Ab.float().abs() @ Ab.float().abs()
+    assert _cw(Db.float(), ref, den.double()) <= 2.0**-8
+    # bf16 with a short K: the kernel
+    As, Bs = Ab[:, :128].contiguous(), Ab[:128].contiguous()
+    with _Launches() as seen:
+        tb.gemm(1.0, As, Bs)
+    assert seen.names == ["gemm"]
+    # bf16 SYRK: always the kernel (the triangle)
+    with _Launches() as seen:
+        tb.syrk(1.0, Ab[:2048])
+    assert seen.names == ["syrk"]
+    del A, D, Ab, Db
+
+
+def test_pair_energy_route_small_shape_takes_unfused(dev):
+    B, eo, ev = df_mp2.pair_inputs(2, 448, 1536, seed=23)
+    Bd, eod, evd = B.to(dev), eo.to(dev), ev.to(dev)
+    assert d._pair_energy_route(Bd) == "aten"
+    with _Launches() as seen:
+        e = d.nki_batched_pair_energy(Bd, eod, evd)
+    assert "pair_energy" not in seen.names
+    want = pe.pair_energy_f64(B, eo, ev)
+    assert abs(float(e) - want) <= 1e-6 * abs(want)
+    # and the fused kernel on the same inputs agrees
+    got = float(kernels.pair_energy_sym(Bd, eod, evd))
+    assert abs(got - want) <= 1e-6 * abs(want)

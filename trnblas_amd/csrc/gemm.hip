@@ -864,9 +864,10 @@ static int choose_sk(GemmArgs& g, int occupancy, size_t ws_bytes) {
   const double eff = (double)g.ntiles / (double)(rounds * slots);
   // At most one tile per CU leaves one wave per SIMD (no second workgroup to
   // fill the MFMA pipe behind the barriers): split it too when each tile has
-  // k-iterations enough (32) for the partial-tile traffic to pay (1024^2 x
-  // 4096 fp32: 277 -> 83 us; 2048^3 with its 256 tiles: 175 -> 163 us).
-  if (eff >= 0.9 || rounds > 8 || (g.ntiles <= device_cus() && g.nk < 32)) return 0;
+  // k-iterations enough (16) for the partial-tile traffic to pay (1024^2 x
+  // 4096 fp32: 277 -> 83 us; 2048^3 with its 256 tiles: 175 -> 163 us;
+  // 512^3: 51.5 -> 28.7 us, 768^3: 67 -> 35 us; below 16 no further gain).
+  if (eff >= 0.9 || rounds > 8 || (g.ntiles <= device_cus() && g.nk < 16)) return 0;
   int64_t groups = slots;
   const int64_t dp = (g.ntiles / groups) * groups;  // whole rounds
   const int64_t tail = (int64_t)(g.ntiles - dp) * g.nk;

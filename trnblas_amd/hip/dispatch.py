@@ -279,6 +279,38 @@ def _host_gemm_wins(macs: float, nbytes: int, dtype: torch.dtype) -> bool:
     return macs < scale * (fixed + per_byte * nbytes)
 
 
+# Device-resident GEMMs under `auto` (the reference's `_lnc_gemm_wins`,
+# nki/dispatch.py:707-727, picks its kernel only where it measured a win;
+# re-measured here against hipBLASLt through torch.matmul on the MI355X,
+# warm medians, 2-D NN / NT / TN and the C2 shapes):
+#  * fp32 stays on the HIP kernel: hipBLASLt is 8-12 % faster from 2048^3 up
+#    (1.1-2x below 1024^3), but on same-sign operands at K = 8192 its result
+#    is 6.0e-6 |A||B| off against fp64 where the kernel's is 2.9e-7: it misses
+#    the 1e-6 componentwise gate the fp32 path is held to.
+#  * SYRK stays on the kernel (the triangle: 1.2-1.7x faster than the full
+#    product on hipBLASLt, C2a).
+#  * bf16 / fp16 go to hipBLASLt when batch * M * N >= 2^22 and K >= 512
+#    (0.66-0.88 of the kernel's time at 2048^3 .. 8192^3 and 8192^2 x 256;
+#    C2b batched 0.74); the kernel keeps the small, short-K and long-K shapes
+#    (2048^2 x 128: 0.8x, 1024^2 x 8192 and 256 x 8192^2: 0.65-0.75x of
+#    hipBLASLt's time). Batched products go to hipBLASLt only with contiguous
+#    operands (a transposed right operand of a 16-bit bmm is avoided).
+_ATEN_16BIT_MIN_MN = 1 << 22
+_ATEN_16BIT_MIN_K = 512
+
+
+def _aten_gemm_wins(a_shape, b_shape, dtype: torch.dtype, contiguous: bool, op: str = "gemm") -> bool:
+    """True when a device-resident GEMM of these operands runs faster on
+    hipBLASLt than on the HIP kernel at the same accuracy (table above)."""
+    if op == "syrk" or dtype not in (torch.bfloat16, torch.float16):
+        return False
+    M, K, N = a_shape[-2], a_shape[-1], b_shape[-1]
+    nb = math.prod(torch.broadcast_shapes(tuple(a_shape[:-2]), tuple(b_shape[:-2])))
+    if nb > 1 and not contiguous:
+        return False
+    return nb * M * N >= _ATEN_16BIT_MIN_MN and K >= _ATEN_16BIT_MIN_K
+
+
 def _gemm_route(*tensors, op: str = "gemm", macs: float | None = None, nbytes: int | None = None):
     """'torch', 'hip', 'host', 'upload' or 'aten' for a GEMM-family call."""
     if not _use_hip() or _mixed_dtypes(*tensors) or _wants_grad(*tensors):
@@ -288,7 +320,13 @@ def _gemm_route(*tensors, op: str = "gemm", macs: float | None = None, nbytes: i
         return "torch"  # float64 / complex / integer: torch where the data is
     policy = _native_gemm_policy()
     if _on_gpu(*tensors):
-        return "aten" if policy == "aten" else "hip"
+        if policy == "aten":
+            return "aten"
+        if policy == "auto" and _backend == "auto" and len(tensors) >= 2:
+            a, b = tensors[0], tensors[1]
+            if _aten_gemm_wins(a.shape, b.shape, a.dtype, a.is_contiguous() and b.is_contiguous(), op):
+                return "aten"
+        return "hip"
     if not _on_host(*tensors):
         return "upload"  # mixed residency: compute on the GPU operand's device
     if policy == "host":
@@ -740,6 +778,43 @@ def _torch_chunked_pair_energy(B, eps_occ, eps_vir, mem_budget_bytes: int = 1_50
     return e
 
 
+# Fused kernel vs the unfused chunked path (hipBLASLt GEMM + torch
+# elementwise) under `auto`, as the reference's row-flop / SBUF rule
+# (nki/dispatch.py:2680-2703) re-measured for MI355X: over 90 small shapes
+# (nocc 2..64, nvir 32..448, naux 128..1536) the fused kernel loses only
+# where its work items (pairs of occupied rows x 96-row tile pairs) fill a
+# fraction of the 256 CUs, so one item's k-steps (~1.9 us each, two passes
+# off the tile diagonal) form the whole critical path, or where nvir is far
+# below the 96-row tile; the unfused path costs a ~0.115 ms floor plus its
+# ordered-pair GEMM (~100 TFLOP/s) and six fp32 passes over T (~3 TB/s).
+# The model below picks the faster route in 87 of the 90 cases (mean loss
+# 0.7 %); at C3 / C4 it keeps the fused kernel by a wide margin.
+_PE_STEP_MS = 1.9e-3
+_PE_FUSED_FLOOR_MS = 0.02
+_PE_UNFUSED_FLOOR_MS = 0.115
+_PE_UNFUSED_GEMM_FLOPS = 100e12
+_PE_UNFUSED_T_BYTES_PER_S = 3e12
+_PE_TILE = 96
+_PE_CUS = 256
+
+
+def _pair_energy_estimates(nocc: int, nvir: int, naux: int) -> tuple[float, float]:
+    """(fused, unfused) estimated milliseconds for B (nocc, nvir, naux)."""
+    nb = -(-nvir // _PE_TILE)
+    nq = nb * (nb + 1) // 2
+    couples = sum((nocc - i + 1) // 2 for i in range(nocc))  # pairs i <= j, two per item
+    nk = -(-naux // 32)
+    steps = (nk * nb + 2 * nk * (nq - nb)) / nq  # mean k-steps per item
+    fused = _PE_FUSED_FLOOR_MS + math.ceil(couples * nq / _PE_CUS) * steps * _PE_STEP_MS
+    m = nocc * nvir
+    unfused = (
+        _PE_UNFUSED_FLOOR_MS
+        + 2.0 * m * m * naux / _PE_UNFUSED_GEMM_FLOPS * 1e3
+        + 24.0 * m * m / _PE_UNFUSED_T_BYTES_PER_S * 1e3
+    )
+    return fused, unfused
+
+
 def _pair_energy_route(B) -> str:
     """'hip' (fused kernel), 'aten' (chunked torch on the GPU) or 'torch'."""
     choice = _pair_energy_choice()
@@ -747,6 +822,10 @@ def _pair_energy_route(B) -> str:
         return "torch"
     if choice == "aten":
         return "aten" if B.device.type == "cuda" else "torch"
+    if choice == "auto" and _backend == "auto" and B.device.type == "cuda" and B.dim() == 3:
+        fused, unfused = _pair_energy_estimates(*B.shape)
+        if unfused < fused:
+            return "aten"
     return "hip"
 
 
