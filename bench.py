@@ -171,9 +171,15 @@ def run_extras(dev, tb, only=None) -> dict:
         tb_nn = gpu_time_ms(lambda: tb.gemm(1.0, Xb, Yb), reps=10, warm=2)
         tb_nt = gpu_time_ms(lambda: tb.gemm(1.0, Xb, Yb, transB=True), reps=10, warm=2)
         tlb = gpu_time_ms(lambda: torch.matmul(Xb, Yb), reps=10, warm=2)
+        # the HIP kernel itself (the public call above takes the measured route)
+        tk_nn = gpu_time_ms(lambda: kernels.gemm(Xb, Yb, 1.0, 0.0, None), reps=10, warm=2)
+        tk_nt = gpu_time_ms(lambda: kernels.gemm(Xb, Yb.mT, 1.0, 0.0, None), reps=10, warm=2)
         out["gemm_bf16_8192"] = {
+            "route_nn": dispatch._gemm_route(Xb, Yb), "route_nt": dispatch._gemm_route(Xb, Yb.mT),
             "nn_ms": tb_nn, "nn_tflops": fl / tb_nn / 1e9, "nt_ms": tb_nt, "nt_tflops": fl / tb_nt / 1e9,
             "frac_bf16_peak_nt": fl / tb_nt / 1e9 / PEAK_BF16_MFMA,
+            "kernel_nn_ms": tk_nn, "kernel_nn_tflops": fl / tk_nn / 1e9,
+            "kernel_nt_ms": tk_nt, "kernel_nt_tflops": fl / tk_nt / 1e9,
             "torch_hipblaslt_nn_ms": tlb, "torch_tflops": fl / tlb / 1e9,
         }  # fmt: skip
         log("gemm8192bf16", out["gemm_bf16_8192"])

@@ -260,11 +260,13 @@ def test_schedule_matches_oracle(kt, k):
     assert ozaki.n_groups(k, kt) == oracle_ozaki.n_groups(k, kt)
 
 
-def test_plan_and_k_block():
+def test_k_block():
     assert ozaki.k_block(8192, 8) == 8192
-    assert [b for b in ozaki.plan(4096, 4096, 4096, 8)[1]] == [(0, 4096)]
-    kb = ozaki.k_block(1 << 20, 8)
-    assert oracle_ozaki.plan_k_blocks(1 << 20, 8)[0][1] == kb
+    assert ozaki.k_block(4096, 12) == 4096
+    for Kp, k in ((1 << 20, 8), (1 << 17, 12), (131072 + 128, 8), (1 << 18, 1)):
+        kb = ozaki.k_block(Kp, k)
+        assert oracle_ozaki.plan_k_blocks(Kp, k)[0][1] == kb
+        assert kb % ozaki.TILE_K == 0 and kb <= Kp
     for bad in (0, 13, 2.0, True, "8"):
         with pytest.raises((ValueError, TypeError)):
             ozaki.check_slices(bad)

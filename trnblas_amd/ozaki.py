@@ -32,8 +32,6 @@ MAX_SLICES = 12
 DEFAULT_SLICES = 8
 BLOCK_BYTES = 1 << 31
 SWAP_N = 512
-LAUNCH_M = 1024
-LAUNCH_N = 1024
 
 
 class OzakiNonFinite(Exception):
@@ -92,28 +90,17 @@ def exponent_offset(slices: int) -> int:
     return -2 * (SLICE_BITS - 1) - SLICE_BITS * (slices - 1)
 
 
-def _blocks(total: int, step: int) -> list:
-    return [(i, min(step, total - i)) for i in range(0, total, step)]
-
-
-def plan(Mp, Kp, N, slices, limit=BLOCK_BYTES, max_m=LAUNCH_M, max_n=LAUNCH_N):
-    """The reference's launch blocks (ozaki.py:486-511). On the device only
-    the K blocks matter (they are separate (hi, lo) chains summed in fp64);
-    M / N blocks change nothing in the arithmetic and are not used."""
-    k = check_slices(slices)
-    cap = limit // (2 * k)
-    Kb = Kp if Kp * 1024 <= cap else max(TILE_K, (cap // 1024) // TILE_K * TILE_K)
-    Mb = max(TILE_K, min(Mp, max_m // TILE_K * TILE_K, (cap // Kb) // TILE_K * TILE_K))
-    Nb = max(1, min(N, max_n, cap // Kb))
-    if 8 * Mb * Nb > limit:
-        Nb = max(1, min(Nb, limit // (8 * Mb)))
-    return _blocks(Mp, Mb), _blocks(Kp, Kb), _blocks(N, Nb)
-
-
-def k_block(Kp: int, slices: int) -> int:
-    """The K block of `plan` (Kp itself unless K is about 2^17 or more)."""
-    kbs = plan(TILE_K, Kp, 1, slices)[1]
-    return kbs[0][1]
+def k_block(Kp: int, slices: int, limit: int = BLOCK_BYTES) -> int:
+    """The K block of the reference's launch plan (ozaki.py:486-511): Kp
+    itself unless a 1024-row launch over all of K would pass `limit` (K of
+    about 2^17 or more), else the largest multiple of TILE_K that fits; the
+    last block may be shorter. The reference's M / N blocks change nothing in
+    the arithmetic (each block's (hi, lo) chains are the same), so only the
+    K block is computed."""
+    cap = limit // (2 * check_slices(slices))
+    if Kp * 1024 <= cap:
+        return Kp
+    return max(TILE_K, (cap // 1024) // TILE_K * TILE_K)
 
 
 def split_device(X: torch.Tensor, slices: int, per: str, interleaved: bool = False,
