@@ -29,6 +29,7 @@ extern "C" {
 #define TRNBLAS_F32 0
 #define TRNBLAS_BF16 1
 #define TRNBLAS_F16 2
+#define TRNBLAS_F64 3 /* trnblas_hip_tri_inv_blocks only (fp64 work has its own entry points) */
 
 /* error codes */
 #define TRNBLAS_OK 0
@@ -61,7 +62,8 @@ const char* trnblas_hip_last_error(void);
  * beta == 0 (then C is not read, as in BLAS). Any M, N, K >= 0 (ragged edges
  * are handled in the kernel; K == 0 gives D = beta * C). Batch strides are in
  * elements; a stride of 0 broadcasts that operand over the batch. D must not
- * overlap A, B or C.
+ * overlap A or B; it may be C itself (an in-place update: each element of C
+ * is read and written by the same thread), but must not partly overlap C.
  */
 int trnblas_hip_gemm(int dtype, int transA, int transB, int64_t M, int64_t N, int64_t K,
                      double alpha, const void* A, int64_t lda, int64_t strideA,
@@ -318,6 +320,95 @@ int trnblas_hip_ozaki_hilo(int slices, int64_t M, int64_t N, int64_t Kp, const i
  */
 int trnblas_hip_chol_block(int64_t nb, double* A, int64_t lda, double* Linv, int64_t ldl,
                            int32_t* info, int64_t offset, void* stream);
+
+/*
+ * Inverses of the 128 x 128 diagonal blocks of a triangular n x n matrix T
+ * (trsm's diagonal solves, as GEMMs with these inverses): element (i, k) of
+ * T at T[i * ldt_r + k * ldt_c] (any two positive strides: a transposed view
+ * is passed as is); upper != 0: T is upper triangular, else lower; only
+ * that triangle is read, and with unit != 0 its diagonal is taken as ones.
+ * Dinv receives ceil(n / 128) row-major 128 x 128 blocks: block b is the
+ * inverse of T[128 b : 128 b + 128, 128 b : 128 b + 128] (zeros in the other
+ * triangle; the identity past n). dtype TRNBLAS_F32 or TRNBLAS_F64 (T and
+ * Dinv); the arithmetic is fp64 either way. A zero pivot gives inf / NaN, as
+ * a triangular solve does. Replaces the per-block
+ * torch.linalg.solve_triangular calls of the reference's blocked trsm
+ * (`_nki_trsm_left`, trnblas/nki/dispatch.py:1740-1799).
+ */
+int trnblas_hip_tri_inv_blocks(int dtype, int64_t n, int upper, int unit, const void* T,
+                               int64_t ldt_r, int64_t ldt_c, void* Dinv, void* stream);
+
+/* operand triangles of trnblas_hip_dgemm (bits of `tri`) */
+#define TRNBLAS_TRI_A_LOWER 1 /* A[m][k] == 0 for k > m: a tile reads k < m0 + tile */
+#define TRNBLAS_TRI_A_UPPER 2 /* A[m][k] == 0 for k < m: a tile reads k >= m0 */
+#define TRNBLAS_TRI_B_LOWER 4 /* B[k][n] == 0 for k < n: a tile reads k >= n0 */
+#define TRNBLAS_TRI_B_UPPER 8 /* B[k][n] == 0 for k > n: a tile reads k < n0 + tile */
+
+/*
+ * fp64 GEMM, strided-batched: D[b] = alpha * op(A[b]) * op(B[b]) + beta * C[b]
+ * on the fp64 MFMA. The products of the metric stage: the reference runs
+ * them as the GEMM updates of its blocked trsm (`_nki_trsm_left`,
+ * trnblas/nki/dispatch.py:1740-1799, `mm(...)`) after torch.linalg.cholesky
+ * (`_device_inv_chol_factor`, :1866-1870); here they are the panels and
+ * trailing updates of the blocked Cholesky, the block products of the
+ * triangular inverse and trsm's block solves and updates.
+ *
+ * op(A) is M x K: row-major M x K (lda >= K) when transA == 0, row-major
+ * K x M (lda >= M) otherwise; likewise op(B) K x N. C and D are row-major
+ * M x N (ldc, ldd >= N); D may be C itself (an in-place update); C is not
+ * read when beta == 0. A and B need 16-byte aligned bases and even leading
+ * dimensions, batch strides and contiguous extents (K when K is the
+ * contiguous dimension, else M / N). lower != 0 (M == N, batch <= 1): only
+ * the elements m >= n of D are computed and written. tri: TRNBLAS_TRI_* bits
+ * of triangular operands whose zero blocks are skipped (their other
+ * triangle must hold zeros).
+ */
+int trnblas_hip_dgemm(int transA, int transB, int64_t M, int64_t N, int64_t K, double alpha,
+                      const double* A, int64_t lda, int64_t strideA, const double* B,
+                      int64_t ldb, int64_t strideB, double beta, const double* C, int64_t ldc,
+                      int64_t strideC, double* D, int64_t ldd, int64_t strideD, int64_t batch,
+                      int lower, int tri, void* stream);
+
+/*
+ * metric_inv_half: X = L^-T for an SPD n x n fp64 J = L L^T (row-major,
+ * ldj; only its lower triangle is read), X row-major (ldx), exactly upper
+ * triangular. Replaces `nki_metric_inv_half` (trnblas/nki/dispatch.py:
+ * 1883-1905; its device route `_device_inv_chol_factor` :1866-1870 is
+ * torch.linalg.cholesky + the blocked trsm against the identity). One call
+ * issues the whole sequence: a right-looking blocked Cholesky (128-wide
+ * blocks; trnblas_hip_chol_block on the diagonal, trnblas_hip_dgemm panels
+ * and lower-triangle trailing updates, the trailing update on a second
+ * stream of the same device so the next diagonal block runs beside it),
+ * then L^-1 by recursive doubling over block halves and its transpose.
+ * info (device int32) is set to the order of the first leading minor that
+ * is not positive definite, else 0 (X is then garbage). workspace: at least
+ * trnblas_hip_metric_inv_half_workspace(n) bytes, 256-byte aligned. Calls on
+ * one device share its second stream and are serialised on the host.
+ */
+size_t trnblas_hip_metric_inv_half_workspace(int64_t n);
+int trnblas_hip_metric_inv_half(int64_t n, const double* J, int64_t ldj, double* X, int64_t ldx,
+                                int32_t* info, void* workspace, size_t workspace_bytes,
+                                void* stream);
+
+/*
+ * Triangular solve T X = alpha B, T n x n triangular (upper != 0: upper,
+ * else lower; only that triangle read; unit != 0: its diagonal taken as
+ * ones), B n x nrhs, X n x nrhs; element (i, j) of each matrix at
+ * base[i * ld_r + j * ld_c] (any positive strides: a transposed view is
+ * passed as is, which is how the left / right and trans forms of trsm map
+ * to this one). dtype TRNBLAS_F32 or TRNBLAS_F64. Replaces the reference's
+ * blocked `_nki_trsm_left` (trnblas/nki/dispatch.py:1740-1799): the
+ * 128 x 128 diagonal blocks are all inverted in one launch
+ * (trnblas_hip_tri_inv_blocks), then the solve recurses over block halves
+ * with GEMM updates (fp64: trnblas_hip_dgemm; fp32: trnblas_hip_gemm).
+ * workspace: at least trnblas_hip_trsm_workspace(dtype, n, nrhs) bytes,
+ * 256-byte aligned. X may not overlap T or B.
+ */
+size_t trnblas_hip_trsm_workspace(int dtype, int64_t n, int64_t nrhs);
+int trnblas_hip_trsm(int dtype, int64_t n, int64_t nrhs, int upper, int unit, double alpha,
+                     const void* T, int64_t ldt_r, int64_t ldt_c, const void* B, int64_t ldb_r,
+                     int64_t ldb_c, void* X, int64_t ldx_r, int64_t ldx_c, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,40 +1,54 @@
-// Diagonal blocks of the metric factorisation, fp64, for gfx950.
+// 128-wide diagonal blocks of the metric stage, fp64, for gfx950.
 //
 // metric_inv_half (trnblas/level3.py:365-380; the reference's device route is
 // torch.linalg.cholesky + a blocked trsm, trnblas/nki/dispatch.py:1854-1881)
-// returns X = L^-T for J = L L^T. On the device this build factors J by a
-// right-looking blocked Cholesky whose trailing updates and panels are
-// DGEMMs; this kernel is the step those cannot do: the Cholesky factor L_kk
-// of one updated diagonal block (nb <= 128) and its inverse L_kk^-1, which
-// turns the panel solve into a GEMM and seeds the block inverse of L.
+// returns X = L^-T for J = L L^T, and trsm (level3.py:332-362, the blocked
+// solve of dispatch.py:1740-1799) solves with a triangular matrix. On the
+// device both are blocked by 128: the panels, trailing updates and block
+// products are fp64 GEMMs (dgemm.hip); these kernels do what a GEMM cannot,
+// on one 128 x 128 diagonal block per workgroup:
+//  * chol128_kernel: the Cholesky factor L of an updated SPD block and L^-1
+//    (the panel solve then is a GEMM with L^-1, and L^-1 seeds the block
+//    inverse of the whole factor);
+//  * trinv128_kernel: the inverse of each 128 x 128 diagonal block of a
+//    triangular matrix (trsm's diagonal solves become GEMMs).
 //
-// One workgroup of 576 threads per block, blocked by 4 x 4 tiles: the owner of
-// tile (br, bc), br >= bc, keeps the tile at rows 4 br .., columns 4 bc .. of
-// the 128 x 128 block (padded with the identity past nb) in registers.
-// Cholesky, per tile column jb, one barrier: (A) the owner of the diagonal
-// tile factors it (4 x 4 Cholesky) and publishes L_jj^-1 and
-// A_jj^-1 = L_jj^-T L_jj^-1; after the barrier (B) the panel tiles below it
-// become L_ij = A_ij L_jj^-T while (C) every trailing tile loses
-// A_ij A_jj^-1 A_kj^T (= L_ij L_kj^T) from column jb's unscaled tiles, and
-// the tiles of column jb + 1 publish themselves for the next step. Inverse X = L^-1, per tile row ib: the
-// unscaled row of X and the column M_m = L_m,ib L_ib,ib^-1 are published,
-// then the row becomes L_ib,ib^-1 X_ib and every later row m loses
-// M_m X_ib (unscaled). Waves whose tiles all lie above the current tile row
-// skip the arithmetic (those tiles are final) but keep the barriers.
+// Inside a workgroup (8 waves) the block is a grid of 8 x 8 sub-blocks of
+// 16 x 16 in LDS, lower sub-blocks only, each column-major with column pitch
+// 17 doubles. With that pitch the three access patterns of the 16x16x4 f64
+// MFMA are cheap: an A fragment (lane l: X[l % 16][4 q + l / 16]) reads 16
+// consecutive doubles per 16-lane group, a B fragment (X[4 q + l / 16][l % 16])
+// and the accumulator layout (lane l, register e: row 4 e + l / 16, column
+// l % 16) fall on distinct banks.
+//
+// Cholesky, per 16-wide block column p (one barrier after each phase):
+//  1. one wave factors the 16 x 16 diagonal sub-block and inverts it
+//     (diag16: column by column, the column and the multipliers' row
+//     exchanged through LDS; the inverse is built from the same row
+//     operations applied to the identity);
+//  2. the sub-blocks below it become L_ip = A_ip (L_pp^-1)^T (MFMA);
+//  3. the trailing sub-blocks lose L_ip L_kp^T (MFMA).
+// Inverse (both kernels), with the diagonal sub-blocks' inverses in place:
+// recursive doubling over halves of 16, 32 and 64,
+// Y21 = -Y22 (L21 Y11), in place over L21, through an LDS scratch for the
+// intermediate product.
 #include "common.hpp"
 
 namespace trnblas {
 
-constexpr int kCholNB = 128;
-constexpr int kCholNT = kCholNB / 4;
-constexpr int kCholTiles = kCholNT * (kCholNT + 1) / 2;
+typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kCholThreads = (kCholTiles + 63) / 64 * 64;  // 9 waves
+constexpr int kCholNB = 128;
+constexpr int kSP = 17;          // column pitch of a sub-block (doubles)
+constexpr int kSB = 16 * kSP;    // doubles per sub-block
+constexpr int kNS = 8;           // sub-blocks per side
+constexpr int kNLow = kNS * (kNS + 1) / 2;  // lower sub-blocks
+constexpr int kThreads = 512;    // 8 waves
+
+__device__ __forceinline__ int sidx(int i, int j) { return i * (i + 1) / 2 + j; }  // i >= j
 
 // 1 / sqrt(d) for d > 0: the hardware estimate (v_rsq_f64) refined by two
-// Newton-Raphson steps y <- y (3 - d y^2) / 2, each of which doubles the
-// correct bits; a short FMA chain in place of a correctly rounded sqrt and
-// a division on the serial path of the diagonal tile. NaN for d <= 0.
+// Newton-Raphson steps y <- y (3 - d y^2) / 2; NaN for d <= 0.
 __device__ __forceinline__ double rsqrt_nr(double d) {
   double y = __builtin_amdgcn_rsq(d);
 #pragma unroll
@@ -45,227 +59,271 @@ __device__ __forceinline__ double rsqrt_nr(double d) {
   return d > 0.0 ? y : __builtin_nan("");
 }
 
-__global__ __launch_bounds__(kCholThreads) void chol_block_kernel(int nb, double* A, int64_t lda,
-                                                          double* Li, int64_t ldl, int32_t* info,
-                                                          int offset) {
-  __shared__ double dinv[kCholNT][16];    // L_jj^-1 of every diagonal tile, row-major
-  __shared__ double ainv[2][16];          // Cholesky: A_jj^-1 = L_jj^-T L_jj^-1 of column j
-  __shared__ double pan[2][kCholNT][16];  // Cholesky: column j's tiles before their scaling
-  __shared__ double mcol[2][kCholNT][16]; // inverse: M_m of the current tile row
-  __shared__ double xrow[2][kCholNT][16]; // inverse: the unscaled tile row of X
-  __shared__ int sbad;
-
-  // Thread t < 528 owns lower tile t in row-major triangle order
-  // (br (br + 1) / 2 + bc = t); the rest of the last wave owns nothing.
-  const int t = threadIdx.x;
-  const bool own = t < kCholTiles;
-  int br = (int)((sqrtf(8.0f * (float)t + 1.0f) - 1.0f) * 0.5f);
-  while (br * (br + 1) / 2 > t) --br;
-  while ((br + 1) * (br + 2) / 2 <= t) ++br;
-  int bc = t - br * (br + 1) / 2;
-  if (!own) br = bc = 0;  // (reads stay in range; nothing is published or written)
-  // largest tile row in this wave (wave-uniform; -1 for a wave with no tile)
-  const int tl = min((int)(t | 63), kCholTiles - 1);
-  int wrow = (int)((sqrtf(8.0f * (float)tl + 1.0f) - 1.0f) * 0.5f);
-  while (wrow * (wrow + 1) / 2 > tl) --wrow;
-  while ((wrow + 1) * (wrow + 2) / 2 <= tl) ++wrow;
-  if ((t & ~63) >= kCholTiles) wrow = -1;
-  wrow = __builtin_amdgcn_readfirstlane(wrow);
-  const int ntr = (nb + 3) >> 2;  // tile rows holding matrix entries
-  if (t == 0) sbad = 0x7fffffff;
-
-  double a[4][4];
+// 1 / d: the hardware estimate (v_rcp_f64) refined by two Newton-Raphson
+// steps y <- y + y (1 - d y).
+__device__ __forceinline__ double rcp_nr(double d) {
+  double y = __builtin_amdgcn_rcp(d);
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int i = 4 * br + r, k = 4 * bc + c;
-      double v = 0.0;
-      if (own && k <= i) v = (i < nb) ? A[(int64_t)i * lda + k] : (i == k ? 1.0 : 0.0);
-      a[r][c] = v;
-    }
-
-  // Column 0's tiles below the diagonal, as they are
-  if (own && bc == 0 && br > 0) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) pan[0][br][e] = a[e >> 2][e & 3];
+  for (int it = 0; it < 2; ++it) {
+    const double e = fma(-d, y, 1.0);
+    y = fma(y, e, y);
   }
-  for (int jb = 0; jb < ntr; ++jb) {
-    double(*pj)[16] = pan[jb & 1];
-    double(*pn)[16] = pan[(jb + 1) & 1];
-    double* aj = ainv[jb & 1];
-    // (A) diagonal tile (updated through column jb - 1 by this same thread):
-    // factor (lower part only), invert, and publish L_jj^-1 and A_jj^-1
-    if (own && br == jb && bc == jb) {
-      double rinv[4];  // 1 / l_cc
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const double d = a[c][c];
-        if (!(d > 0.0) && 4 * jb + c < nb) atomicMin(&sbad, 4 * jb + c + 1);
-        rinv[c] = rsqrt_nr(d);
-        a[c][c] = d * rinv[c];
-#pragma unroll
-        for (int r = c + 1; r < 4; ++r) a[r][c] *= rinv[c];
-#pragma unroll
-        for (int r = c + 1; r < 4; ++r)
-#pragma unroll
-          for (int q = c + 1; q <= r; ++q) a[r][q] -= a[r][c] * a[q][c];
-      }
-      double m[4][4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-#pragma unroll
-        for (int r = 0; r < c; ++r) m[r][c] = 0.0;
-        m[c][c] = rinv[c];
-#pragma unroll
-        for (int r = c + 1; r < 4; ++r) {
-          double sum = 0.0;
-#pragma unroll
-          for (int q = c; q < r; ++q) sum += a[r][q] * m[q][c];
-          m[r][c] = -sum * rinv[r];
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          dinv[jb][4 * r + c] = m[r][c];
-          if (c > r) a[r][c] = 0.0;
-          double sum = 0.0;  // (m^T m)[r][c]
-#pragma unroll
-          for (int q = 0; q < 4; ++q) sum += m[q][r] * m[q][c];
-          aj[4 * r + c] = sum;
-        }
-    }
-    __syncthreads();  // L_jj^-1, A_jj^-1 and column jb's tiles are published
-    if (wrow > jb && own && bc == jb && br > jb) {
-      // (B) panel tile: L_ij = A_ij L_jj^-T
-      double m[4][4], p[4][4];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) m[e >> 2][e & 3] = dinv[jb][e];
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          double sum = 0.0;
-#pragma unroll
-          for (int q = 0; q <= c; ++q) sum += a[r][q] * m[c][q];
-          p[r][c] = sum;
-        }
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) a[r][c] = p[r][c];
-    } else if (wrow > jb && own && bc > jb) {
-      // (C) trailing tile: A_ik -= (A_ij A_jj^-1) A_kj^T, from column jb's
-      // unscaled tiles (L_ij L_kj^T = A_ij A_jj^-1 A_kj^T), so the panel's
-      // scaling (B) runs beside this update instead of before it
-      double q4[4][4];  // A_ij A_jj^-1
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        double ai[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) ai[q] = pj[br][4 * r + q];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          double sum = 0.0;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) sum += ai[q] * aj[4 * q + c];
-          q4[r][c] = sum;
-        }
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        double ak[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) ak[q] = pj[bc][4 * c + q];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          double sum = 0.0;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) sum += q4[r][q] * ak[q];
-          a[r][c] -= sum;
-        }
-      }
-      // column jb + 1's tiles below the diagonal are now as the next step
-      // needs them
-      if (bc == jb + 1 && br > bc) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) pn[br][e] = a[e >> 2][e & 3];
-      }
-    }
-  }
+  return y;
+}
 
-  double x[4][4];
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const long long b = __builtin_bit_cast(long long, v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)b, l);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(b >> 32), l);
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
+// MFMA operand and accumulator access of one sub-block (slice q = 0..3).
+__device__ __forceinline__ double frag_a(const double* s, int lane, int q) {
+  return s[(4 * q + (lane >> 4)) * kSP + (lane & 15)];  // X[l % 16][4 q + l / 16]
+}
+__device__ __forceinline__ double frag_b(const double* s, int lane, int q) {
+  return s[(lane & 15) * kSP + 4 * q + (lane >> 4)];  // X[4 q + l / 16][l % 16]
+}
+__device__ __forceinline__ f64x4 load_acc(const double* s, int lane) {
+  const double* p = s + (lane & 15) * kSP + (lane >> 4);
+  return f64x4{p[0], p[4], p[8], p[12]};
+}
+__device__ __forceinline__ void store_acc(double* s, int lane, const f64x4& v) {
+  double* p = s + (lane & 15) * kSP + (lane >> 4);
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int e = 0; e < 4; ++e) p[4 * e] = v[e];
+}
+// acc += sgn X Y^T (BT) or sgn X Y
+template <bool BT>
+__device__ __forceinline__ void mma16(f64x4& acc, const double* X, const double* Y, double sgn,
+                                      int lane) {
+  double a[4], b[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) x[r][c] = (own && br == bc && r == c) ? 1.0 : 0.0;
-  for (int ib = 0; ib < ntr; ++ib) {
-    double(*mc)[16] = mcol[ib & 1];
-    double(*xr)[16] = xrow[ib & 1];
-    if (own && br == ib) {
+  for (int q = 0; q < 4; ++q) {
+    a[q] = sgn * frag_a(X, lane, q);
+    b[q] = BT ? frag_a(Y, lane, q) : frag_b(Y, lane, q);
+  }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) xr[bc][e] = x[e >> 2][e & 3];
+  for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a[q], b[q], acc, 0, 0, 0);
+}
+
+// One wave on a 16 x 16 diagonal sub-block `blk` (lower part read).
+// CHOL: blk becomes L (blk = L L^T, zeros above) and inv receives L^-1;
+// a non-positive pivot sets *bad to min(*bad, col0 + column + 1) when that
+// column is below nb. Otherwise blk is lower triangular (unit: its diagonal
+// taken as ones) and inv receives its inverse; blk is not written.
+// Lane (r = l % 16, h = l / 16) holds columns 4 e + h of row r (e = 0..3)
+// of the matrix and of E, the product of the elimination steps so far
+// (unit lower; after the last column E = (unit L)^-1, and L^-1 = diag(1 /
+// l_rr) E). ex: 48 doubles of this wave's LDS (column, E row, 1 / l_cc).
+template <bool CHOL>
+__device__ __forceinline__ void diag16(double* blk, double* inv, double* ex, int lane, bool unit,
+                                       int* bad, int col0, int nb) {
+  double* colb = ex;
+  double* rowb = ex + 16;
+  double* rinvb = ex + 32;
+  const int r = lane & 15, h = lane >> 4;
+  double a[4], E[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int s = 4 * e + h;
+    a[e] = s <= r ? blk[s * kSP + r] : 0.0;
+    if (!CHOL && unit && s == r) a[e] = 1.0;
+    E[e] = s == r ? 1.0 : 0.0;
+  }
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    const int ch = c & 3, ce = c >> 2;
+    const double d = readlane_f64(a[ce], c + 16 * ch);  // the pivot
+    double rinv;
+    if (CHOL) {
+      if (lane == 0 && !(d > 0.0) && col0 + c < nb) *bad = min(*bad, col0 + c + 1);
+      rinv = rsqrt_nr(d);
+    } else {
+      rinv = unit ? 1.0 : rcp_nr(d);
     }
-    if (wrow > ib && own && bc == ib && br > ib) {
+    // column c (scaled to L's for CHOL) and row c of E to the wave
+    if (h == ch) colb[r] = CHOL ? a[ce] * rinv : a[ce];
+    if (r == c) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+      for (int e = 0; e < 4; ++e) rowb[4 * e + h] = E[e];
+    }
+    if (lane == 0) rinvb[c] = rinv;
+    __builtin_amdgcn_wave_barrier();
+    const double lr = colb[r];
+    const double m = lr * rinv;  // the elimination multiplier of row r
+    double cs[4], rk[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          double sum = 0.0;
+    for (int e = 0; e < 4; ++e) {
+      cs[e] = colb[4 * e + h];
+      rk[e] = rowb[4 * e + h];
+    }
+    if (CHOL) {
+      if (h == ch && r >= c) a[ce] = lr;
 #pragma unroll
-          for (int q = c; q < 4; ++q) sum += a[r][q] * dinv[ib][4 * q + c];
-          mc[br][4 * r + c] = sum;
-        }
+      for (int e = 0; e < 4; ++e) {
+        const int s = 4 * e + h;
+        if (s > c && s <= r) a[e] = fma(-lr, cs[e], a[e]);
+      }
+    }
+    if (r > c) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int k = 4 * e + h;
+        if (k <= c) E[e] = fma(-m, rk[e], E[e]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  const double rr = rinvb[r];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int s = 4 * e + h;
+    if (CHOL) blk[s * kSP + r] = s <= r ? a[e] : 0.0;
+    inv[s * kSP + r] = s <= r ? E[e] * rr : 0.0;
+  }
+}
+
+// The block inverse Y = L^-1 in place over the lower sub-block grid G, whose
+// off-diagonal sub-blocks hold L and diagonal ones their inverses: for
+// halves of h = 1, 2, 4 sub-blocks, T = L21 Y11 into scr, then
+// Y21 = -Y22 T over L21.
+__device__ __forceinline__ void block_inverse(double* G, double* scr, int wave, int lane) {
+#pragma unroll
+  for (int h = 1; h < kNS; h *= 2) {
+    const int items = 4 * h;  // (kNS / 2h) pairs x h^2 sub-blocks
+    for (int it = wave; it < items; it += kThreads / 64) {
+      const int pi = it / (h * h), ij = it % (h * h), i = ij / h, j = ij % h, b0 = 2 * h * pi;
+      f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+      for (int k = j; k < h; ++k)
+        mma16<false>(acc, G + sidx(b0 + h + i, b0 + k) * kSB, G + sidx(b0 + k, b0 + j) * kSB, 1.0,
+                     lane);
+      store_acc(scr + it * kSB, lane, acc);
     }
     __syncthreads();
-    if (wrow < ib || !own || bc > ib || br < ib) continue;
-    double xk[4][4];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) xk[e >> 2][e & 3] = xr[bc][e];
-    if (br == ib) {
-      // the final row: L_ib,ib^-1 X_ib
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          double sum = 0.0;
-#pragma unroll
-          for (int q = 0; q <= r; ++q) sum += dinv[ib][4 * r + q] * xk[q][c];
-          x[r][c] = sum;
-        }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        double mr[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) mr[q] = mc[br][4 * r + q];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          double sum = 0.0;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) sum += mr[q] * xk[q][c];
-          x[r][c] -= sum;
-        }
-      }
+    for (int it = wave; it < items; it += kThreads / 64) {
+      const int pi = it / (h * h), ij = it % (h * h), i = ij / h, j = ij % h, b0 = 2 * h * pi;
+      f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+      for (int k = 0; k <= i; ++k)
+        mma16<false>(acc, G + sidx(b0 + h + i, b0 + h + k) * kSB,
+                     scr + (pi * h * h + k * h + j) * kSB, -1.0, lane);
+      store_acc(G + sidx(b0 + h + i, b0 + j) * kSB, lane, acc);
     }
+    __syncthreads();
   }
+}
 
+// Element (i, k) of the 128 x 128 block, i >= k, in the sub-block grid.
+__device__ __forceinline__ double& gel(double* G, int i, int k) {
+  return G[sidx(i >> 4, k >> 4) * kSB + (k & 15) * kSP + (i & 15)];
+}
+
+// The lower triangle of a 128 x 128 block (element (i, k) at
+// X[i * ri + k * ci], the identity past nb) into the sub-block grid: each
+// thread issues all its loads before its first LDS store, so the loads'
+// latency is paid once, not once per element.
+template <typename TT>
+__device__ __forceinline__ void load_lower(double* G, const TT* X, int64_t ri, int64_t ci, int nb,
+                                           int tid) {
+  constexpr int PER = kCholNB * kCholNB / kThreads;
+  double v[PER];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int u = 0; u < PER; ++u) {
+    const int x = u * kThreads + tid, i = x >> 7, k = x & 127;
+    v[u] = (k <= i && i < nb) ? (double)X[i * ri + k * ci] : (i == k ? 1.0 : 0.0);
+  }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int i = 4 * br + r, k = 4 * bc + c;
-      if (own && i < nb && k < nb) {
-        if (k <= i) A[(int64_t)i * lda + k] = a[r][c];
-        Li[(int64_t)i * ldl + k] = k <= i ? x[r][c] : 0.0;
-        // the mirrored tile above the diagonal has no owner: its zeros
-        if (br > bc) Li[(int64_t)k * ldl + i] = 0.0;
-      }
-    }
+  for (int u = 0; u < PER; ++u) {
+    const int x = u * kThreads + tid, i = x >> 7, k = x & 127;
+    if (k <= i) gel(G, i, k) = v[u];
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void chol128_kernel(int nb, double* A, int64_t lda,
+                                                           double* Li, int64_t ldl, int32_t* info,
+                                                           int offset) {
+  __shared__ double G[kNLow * kSB];
+  __shared__ double Dv[kNS * kSB];   // inverses of the diagonal sub-blocks
+  __shared__ double scr[16 * kSB];   // T of the block inverse
+  __shared__ double ex[48];          // diag16's exchange
+  __shared__ int sbad;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (tid == 0) sbad = 0x7fffffff;
+  // the lower triangle, the identity past nb (diag16 reads and writes only
+  // the lower part of a diagonal sub-block)
+  load_lower(G, A, lda, 1, nb, tid);
   __syncthreads();
-  if (t == 0 && sbad != 0x7fffffff && info[0] == 0) info[0] = offset + sbad;
+  for (int p = 0; p < kNS; ++p) {
+    if (wave == 0)
+      diag16<true>(G + sidx(p, p) * kSB, Dv + p * kSB, ex, lane, false, &sbad, 16 * p, nb);
+    __syncthreads();
+    for (int i = p + 1 + wave; i < kNS; i += kThreads / 64) {  // panel
+      f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+      mma16<true>(acc, G + sidx(i, p) * kSB, Dv + p * kSB, 1.0, lane);
+      store_acc(G + sidx(i, p) * kSB, lane, acc);
+    }
+    __syncthreads();
+    const int nt = kNS - 1 - p, items = nt * (nt + 1) / 2;
+    for (int it = wave; it < items; it += kThreads / 64) {  // trailing update
+      int ri = 0;
+      while ((ri + 1) * (ri + 2) / 2 <= it) ++ri;
+      const int i = p + 1 + ri, k = p + 1 + (it - ri * (ri + 1) / 2);
+      f64x4 acc = load_acc(G + sidx(i, k) * kSB, lane);
+      mma16<true>(acc, G + sidx(i, p) * kSB, G + sidx(k, p) * kSB, -1.0, lane);
+      store_acc(G + sidx(i, k) * kSB, lane, acc);
+    }
+    __syncthreads();
+  }
+  // L out (lower triangle of A only), then the diagonal inverses in place
+  for (int x = tid; x < nb * kCholNB; x += kThreads) {
+    const int i = x >> 7, k = x & 127;
+    if (k <= i) A[(int64_t)i * lda + k] = gel(G, i, k);
+  }
+  __syncthreads();
+  for (int x = tid; x < kNS * kSB; x += kThreads) G[sidx(x / kSB, x / kSB) * kSB + x % kSB] = Dv[x];
+  __syncthreads();
+  block_inverse(G, scr, wave, lane);
+  for (int x = tid; x < nb * kCholNB; x += kThreads) {
+    const int i = x >> 7, k = x & 127;
+    if (k < nb) Li[(int64_t)i * ldl + k] = k <= i ? gel(G, i, k) : 0.0;
+  }
+  if (tid == 0 && sbad != 0x7fffffff && info[0] == 0) info[0] = offset + sbad;
+}
+
+// Inverse of diagonal block b of the n x n triangular matrix T: element
+// (i, k) of the lower matrix inverted is T[k0 + i][k0 + k] (lower) or
+// T[k0 + k][k0 + i] (upper: T^T is inverted and the result transposed back),
+// read through the strides (sr, sc) in T's element type. Dinv[b] (128 x 128
+// row-major) receives the inverse, the identity past the matrix.
+template <typename TT>
+__global__ __launch_bounds__(kThreads) void trinv128_kernel(int n, int upper, int unit,
+                                                            const TT* T, int64_t sr, int64_t sc,
+                                                            TT* Dinv) {
+  __shared__ double G[kNLow * kSB];
+  __shared__ double scr[16 * kSB];
+  __shared__ double ex[kThreads / 64][48];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = blockIdx.x, k0 = b * kCholNB, nb = min(kCholNB, n - k0);
+  const int64_t ri = upper ? sc : sr, ci = upper ? sr : sc;  // strides of the lower view
+  load_lower(G, T + (int64_t)k0 * (sr + sc), ri, ci, nb, tid);
+  __syncthreads();
+  // the 8 diagonal sub-blocks' inverses, one wave each, into scr
+  diag16<false>(G + sidx(wave, wave) * kSB, scr + wave * kSB, ex[wave], lane, unit != 0, nullptr,
+                0, 0);
+  __syncthreads();
+  for (int x = tid; x < kNS * kSB; x += kThreads) G[sidx(x / kSB, x / kSB) * kSB + x % kSB] = scr[x];
+  __syncthreads();
+  block_inverse(G, scr, wave, lane);
+  TT* out = Dinv + (int64_t)b * kCholNB * kCholNB;
+  for (int x = tid; x < kCholNB * kCholNB; x += kThreads) {
+    const int i = x >> 7, k = x & 127;
+    // lower: out[i][k] = Y[i][k]; upper: out[i][k] = Y[k][i]
+    const int yi = upper ? k : i, yk = upper ? i : k;
+    out[x] = (TT)(yk <= yi ? gel(G, yi, yk) : 0.0);
+  }
 }
 
 }  // namespace trnblas
@@ -281,7 +339,29 @@ extern "C" int trnblas_hip_chol_block(int64_t nb, double* A, int64_t lda, double
   TRNBLAS_CHECK_ARG(A && Linv && info, "chol_block: NULL pointer");
   TRNBLAS_CHECK_ARG(lda >= nb && ldl >= nb, "chol_block: leading dimension below nb");
   TRNBLAS_CHECK_ARG(offset >= 0 && offset < (1ll << 30), "chol_block: bad offset");
-  hipLaunchKernelGGL(chol_block_kernel, dim3(1), dim3(kCholThreads), 0, (hipStream_t)stream, (int)nb, A,
+  hipLaunchKernelGGL(chol128_kernel, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, (int)nb, A,
                      lda, Linv, ldl, info, (int)offset);
   return check_launch("chol_block");
+}
+
+extern "C" int trnblas_hip_tri_inv_blocks(int dtype, int64_t n, int upper, int unit, const void* T,
+                                          int64_t ldt_r, int64_t ldt_c, void* Dinv, void* stream) {
+  clear_error();
+  TRNBLAS_CHECK_ARG(dtype == TRNBLAS_F32 || dtype == TRNBLAS_F64,
+                    "tri_inv_blocks: dtype %d not supported (f32, f64)", dtype);
+  TRNBLAS_CHECK_ARG(n >= 0 && n < (1ll << 30), "tri_inv_blocks: bad n %lld", (long long)n);
+  if (n == 0) return TRNBLAS_OK;
+  TRNBLAS_CHECK_ARG(T && Dinv, "tri_inv_blocks: NULL pointer");
+  TRNBLAS_CHECK_ARG(ldt_r > 0 && ldt_c > 0 && (ldt_r >= n || ldt_c >= n || n == 1),
+                    "tri_inv_blocks: bad strides");
+  const int nblk = (int)((n + kCholNB - 1) / kCholNB);
+  if (dtype == TRNBLAS_F64)
+    hipLaunchKernelGGL(trinv128_kernel<double>, dim3(nblk), dim3(kThreads), 0, (hipStream_t)stream,
+                       (int)n, upper, unit, static_cast<const double*>(T), ldt_r, ldt_c,
+                       static_cast<double*>(Dinv));
+  else
+    hipLaunchKernelGGL(trinv128_kernel<float>, dim3(nblk), dim3(kThreads), 0, (hipStream_t)stream,
+                       (int)n, upper, unit, static_cast<const float*>(T), ldt_r, ldt_c,
+                       static_cast<float*>(Dinv));
+  return check_launch("tri_inv_blocks");
 }

@@ -19,10 +19,13 @@ import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 _PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("TRNBLAS_HIP_LIB", _PKG / "lib" / "libtrnblas_hip.so"))
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
-F32, BF16, F16 = 0, 1, 2
+F32, BF16, F16, F64 = 0, 1, 2, 3
 DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+# bits of trnblas_hip_dgemm's `tri`
+TRI_A_LOWER, TRI_A_UPPER, TRI_B_LOWER, TRI_B_UPPER = 1, 2, 4, 8
 
 E_ARG, E_LAUNCH, E_NONFINITE, E_WORKSPACE = -1, -2, -3, -4
 
@@ -96,6 +99,28 @@ SIGNATURES = {
     "trnblas_hip_chol_block": (
         _c_int,
         [_c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
+    ),
+    "trnblas_hip_tri_inv_blocks": (
+        _c_int,
+        [_c_int, _c_i64, _c_int, _c_int, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr],
+    ),
+    "trnblas_hip_metric_inv_half_workspace": (_c_size, [_c_i64]),
+    "trnblas_hip_metric_inv_half": (
+        _c_int,
+        [_c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr],
+    ),
+    "trnblas_hip_trsm_workspace": (_c_size, [_c_int, _c_i64, _c_i64]),
+    "trnblas_hip_trsm": (
+        _c_int,
+        [_c_int, _c_i64, _c_i64, _c_int, _c_int, _c_dbl]
+        + [_c_ptr, _c_i64, _c_i64] * 3
+        + [_c_ptr, _c_size, _c_ptr],
+    ),
+    "trnblas_hip_dgemm": (
+        _c_int,
+        [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_dbl]
+        + [_c_ptr, _c_i64, _c_i64] * 2
+        + [_c_dbl, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr],
     ),
 }
 

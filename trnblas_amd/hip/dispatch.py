@@ -522,13 +522,17 @@ def nki_trsm(
     (side "left") or X op(A) = alpha B (side "right"), op(A) = A or A^T.
     Only the `uplo` triangle of A is read; diag "unit" takes its diagonal as
     ones (the reference body, nki/dispatch.py:1707-1738). The reference's
-    device route is a blocked solve whose panels and updates it sends to
-    the host or its fp32 kernels (:1597-1704, Trainium has no fp64); on
-    MI355X a device-resident solve stays on the device in the operands' own
-    precision, float64 included (rocBLAS TRSM through
-    `torch.linalg.solve_triangular`); bf16 / fp16 solve in fp32 and return
-    in B's dtype, as the reference's host route does. Host operands solve on
-    the host. Differentiable in A and B (torch ops throughout)."""
+    device route is a blocked solve, diagonal panels by
+    torch.linalg.solve_triangular and updates by its GEMM kernel
+    (`_nki_trsm_left`, :1740-1799; Trainium has no fp64). On MI355X a
+    device-resident 2-D solve runs the HIP blocked solve (`_trsm_hip`:
+    every 128 x 128 diagonal block inverted at once by
+    trnblas_hip_tri_inv_blocks, then block solves and updates as GEMMs on
+    the fp64 or fp32 MFMA kernels) in the operands' own precision, float64
+    included; bf16 / fp16 solve in fp32 and return in B's dtype, as the
+    reference's host route does. Host operands, complex or batched
+    right-hand sides, and calls that need gradients take torch's
+    `solve_triangular` (differentiable in A and B)."""
     side, uplo, diag = side_flag(side), uplo_flag(uplo), diag_flag(diag)
     trans = trans_flag(trans)
     if A.dim() != 2 or A.shape[0] != A.shape[1]:
@@ -540,6 +544,19 @@ def nki_trsm(
     if not (A.is_floating_point() or A.is_complex()) or not (B.is_floating_point() or B.is_complex()):
         raise NotImplementedError(f"trsm: expected floating point operands; got {A.dtype}, {B.dtype}")
     cdt = _solve_dtype(A, B)
+    if (
+        _use_hip()
+        and A.is_cuda
+        and B.is_cuda
+        and A.device == B.device
+        and B.dim() == 2
+        and cdt in (torch.float32, torch.float64)
+        and not _wants_grad(A, B)
+    ):
+        try:
+            return _trsm_hip(A.to(cdt), B.to(cdt), side, uplo, trans, diag, alpha).to(B.dtype)
+        except Exception as exc:  # noqa: BLE001
+            _kernel_failed(exc)
     mat = A.mT if trans else A  # the uplo triangle of A is the other one of A^T
     upper = (uplo == "upper") != trans
     rhs = B.to(cdt) if alpha == 1.0 else alpha * B.to(cdt)
@@ -549,93 +566,51 @@ def nki_trsm(
     return X.to(B.dtype)
 
 
-_METRIC_LOOKAHEAD = True  # overlap the diagonal-block kernel with the trailing update
+def _trsm_hip(A, B, side, uplo, trans, diag, alpha):
+    """op(A) X = alpha B (left) or X op(A) = alpha B (right) on the device,
+    float32 / float64, through the native blocked solve (trnblas_hip_trsm:
+    the reference's `_nki_trsm_left`, nki/dispatch.py:1740-1799, with its
+    per-block solve_triangular replaced by one launch that inverts every
+    diagonal block). A right solve is the left solve op(A)^T X^T = alpha B^T:
+    the transposed views go to the driver as they are."""
+    from . import kernels
+
+    if side == "left":
+        M, rhs = (A.mT if trans else A), B
+        upper = (uplo == "upper") != trans
+    else:
+        M, rhs = (A if trans else A.mT), B.mT
+        upper = (uplo == "upper") == trans
+    out = torch.empty(B.shape, dtype=B.dtype, device=B.device)
+    kernels.trsm(M, rhs, upper, diag == "unit", alpha, out if side == "left" else out.mT)
+    return out
 
 
 def _metric_inv_half_blocked(J: torch.Tensor) -> torch.Tensor:
-    """X = L^-T of a real SPD J on the ROCm device, in fp64: a right-looking
-    blocked Cholesky whose diagonal blocks (128 wide) are factored and
-    inverted by the HIP kernel `trnblas_hip_chol_block`, whose panels
-    (L_ik = J_ik L_kk^-T) and trailing updates are DGEMMs, then the inverse
-    of L by halves, [[X11, 0], [-X22 L21 X11, X22]], also DGEMMs. Returns
-    float64.
-
-    Look-ahead: after a panel only the next block column is updated on the
-    calling stream, so the next diagonal block (one workgroup) is factored
-    while a second stream applies the rest of the trailing update with the
-    other CUs; the calling stream waits for it before it next writes there."""
+    """X = L^-T of a real SPD J on the ROCm device, in fp64, by the native
+    driver trnblas_hip_metric_inv_half: a right-looking blocked Cholesky
+    (128-wide diagonal blocks factored and inverted by one kernel each,
+    fp64 MFMA GEMM panels and lower-triangle trailing updates, the trailing
+    update on a second stream beside the next diagonal block), then L^-1 by
+    recursive doubling over block halves, one batched GEMM pair per level,
+    and its transpose. Returns float64."""
     from . import kernels
 
-    n = J.shape[0]
-    dev = J.device
-    W = J.to(torch.float64).clone(memory_format=torch.contiguous_format)
-    nb = kernels.CHOL_NB
-    nblk = -(-n // nb)
-    Li = torch.empty(nblk, nb, nb, dtype=torch.float64, device=dev)
-    info = torch.zeros(1, dtype=torch.int32, device=dev)
-    main = torch.cuda.current_stream(dev)
-    side = torch.cuda.Stream(dev) if nblk > 2 and _METRIC_LOOKAHEAD else None
-    rest_done = None  # the side stream's update of W[k1:, k1:] minus the next block column
-    for b in range(nblk):
-        k0, k1 = b * nb, min(n, (b + 1) * nb)
-        Lkk = Li[b, : k1 - k0, : k1 - k0]
-        kernels.chol_block(W[k0:k1, k0:k1], Lkk, info, k0)
-        if k1 == n:
-            break
-        k2 = min(n, k1 + nb)
-        P = W[k1:, k0:k1] @ Lkk.mT  # the panel of L
-        W[k1:, k0:k1] = P
-        if rest_done is not None:
-            main.wait_event(rest_done)  # the next block column is in the side's region
-        # the next block column (lower triangle used; its upper part is scratch)
-        W[k1:, k1:k2].addmm_(P, P[: k2 - k1].mT, alpha=-1.0)
-        rest_done = None
-        if k2 < n:
-            R = P[k2 - k1 :]
-            if side is None:
-                W[k2:, k2:].addmm_(R, R.mT, alpha=-1.0)
-            else:
-                ready = torch.cuda.Event()
-                ready.record(main)
-                side.wait_event(ready)
-                with torch.cuda.stream(side):
-                    W[k2:, k2:].addmm_(R, R.mT, alpha=-1.0)
-                P.record_stream(side)
-                rest_done = torch.cuda.Event()
-                rest_done.record(side)
-    if rest_done is not None:
-        main.wait_event(rest_done)
+    X, info = kernels.metric_inv_half(J.to(torch.float64))
     bad = int(info)  # one small device-to-host read
     if bad != 0:
         raise torch.linalg.LinAlgError(
             f"metric Cholesky failed: leading minor of order {bad} is not positive-definite"
         )
-    X = torch.zeros_like(W)  # L^-1, lower triangular
-
-    def inverse(b0: int, b1: int) -> None:
-        # X over block rows / columns [b0, b1): halves on a block boundary,
-        # X_21 = -X_22 L_21 X_11 (large DGEMMs at the top of the recursion)
-        k0, k1 = b0 * nb, min(n, b1 * nb)
-        if b1 - b0 == 1:
-            X[k0:k1, k0:k1] = Li[b0, : k1 - k0, : k1 - k0]
-            return
-        bm = (b0 + b1) // 2
-        km = bm * nb
-        inverse(b0, bm)
-        inverse(bm, b1)
-        X[km:k1, k0:km] = -(X[km:k1, km:k1] @ (W[km:k1, k0:km] @ X[k0:km, k0:km]))
-
-    if nblk:
-        inverse(0, nblk)
-    return X.mT.contiguous()
+    return X
 
 
 def nki_metric_inv_half(J: torch.Tensor) -> torch.Tensor:
     """Cholesky inverse factor X = L^-T of an SPD metric J = L L^T, so
     X X^T = J^-1 and `A @ X` is the density-fitting metric contraction
     (nki/dispatch.py:1854-1905). On MI355X a real J on the device is factored
-    and inverted there in fp64 (`_metric_inv_half_blocked`: a HIP kernel for
-    the diagonal blocks, DGEMMs around it), where the reference sends device
+    and inverted there in fp64 (`_metric_inv_half_blocked`: the native HIP
+    driver, diagonal-block kernels and fp64 MFMA GEMMs), where the reference sends device
     metrics to host LAPACK or runs torch.linalg.cholesky + trsm in the
     metric's precision; complex metrics and host tensors take torch's
     Cholesky and triangular solve (host LAPACK for host tensors, the

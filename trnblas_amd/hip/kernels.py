@@ -97,11 +97,15 @@ def gemm(
     alpha: float = 1.0,
     beta: float = 0.0,
     C: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """alpha * A @ B + beta * C for device A (M, K), B (K, N) (or batched
     (b, M, K), (b, K, N) with equal or broadcast batch), one launch. Transposed
     views are read in place. Returns a fresh (M, N) / (b, M, N) tensor in
-    A's dtype; C (same shape, or broadcast over the batch) is never written."""
+    A's dtype; C (same shape, or broadcast over the batch) is never written.
+    out (2-D only): an (M, N) view with unit column stride to write instead,
+    which may be C itself (an in-place update; each element of C is read
+    and written by the same thread) but must not overlap A or B."""
     dev = _require_device(A, B, *(() if C is None else (C,)))
     if A.dtype != B.dtype or (C is not None and C.dtype != A.dtype):
         raise TypeError(f"gemm: mixed dtypes {A.dtype}, {B.dtype}")
@@ -115,7 +119,14 @@ def gemm(
             raise ValueError(f"gemm: inner dimensions differ: {tuple(A.shape)} @ {tuple(B.shape)}")
         a, ta, lda = _mat_layout(A)
         b, tb, ldb = _mat_layout(B)
-        D = torch.empty((M, N), dtype=A.dtype, device=dev)
+        if out is None:
+            D, ldd = torch.empty((M, N), dtype=A.dtype, device=dev), N
+        else:
+            if tuple(out.shape) != (M, N) or out.dtype != A.dtype or out.device != dev:
+                raise ValueError(f"gemm: out must be ({M}, {N}) {A.dtype} on {dev}")
+            if M and N and (out.stride(1) != 1 or out.stride(0) < N):
+                raise ValueError("gemm: out needs unit column stride and a row stride >= N")
+            D, ldd = out, max(out.stride(0), N)
         ws = gemm_workspace(dev)
         c, ldc = None, N
         if beta != 0.0 and C is not None:
@@ -126,9 +137,11 @@ def gemm(
         _probed_call(
             "gemm", "trnblas_hip_gemm", code, int(ta), int(tb), M, N, K, float(alpha),
             ptr(a), lda, 0, ptr(b), ldb, 0, float(beta) if c is not None else 0.0,
-            ptr(c), ldc, 0, ptr(D), N, 0, 1, ptr(ws), ws.numel(), stream_of(dev),
+            ptr(c), ldc, 0, ptr(D), ldd, 0, 1, ptr(ws), ws.numel(), stream_of(dev),
         )  # fmt: skip
         return D
+    if out is not None:
+        raise ValueError("gemm: out is supported for 2-D operands only")
     if A.dim() != 3 or B.dim() != 3:
         raise ValueError("gemm: operands must both be 2-D or both 3-D")
     bA, M, K = A.shape
@@ -394,6 +407,170 @@ def mp2_energy_pairs(T_flat, eps_occ_chunk, eps_occ_full, eps_vir) -> torch.Tens
 
 
 # ── metric stage ─────────────────────────────────────────────────────────────
+
+def _dgemm_operand(X: torch.Tensor, is_a: bool):
+    """(tensor, trans, ld, batch stride) of a 3-D fp64 operand for
+    trnblas_hip_dgemm: a row-major or transposed row-major view as is, when
+    its base is 16-byte aligned and its leading dimension, batch stride and
+    contiguous extent are even; otherwise a K-contiguous copy (K is even
+    here: dgemm pads an odd K)."""
+    t, tr, ld, sb = _batched_layout(X)
+    ext = t.shape[1] if tr else t.shape[2]
+    if ptr(t) % 16 == 0 and ld % 2 == 0 and sb % 2 == 0 and ext % 2 == 0:
+        return t, tr, ld, sb
+    c = X.contiguous() if is_a else X.mT.contiguous()  # A (b, M, K); B stored (b, N, K)
+    return c, not is_a, c.shape[2], (0 if c.shape[0] == 1 else c.shape[1] * c.shape[2])
+
+
+def dgemm(
+    A: torch.Tensor,
+    B: torch.Tensor,
+    alpha: float = 1.0,
+    beta: float = 0.0,
+    C: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    lower: bool = False,
+    tri: int = 0,
+) -> torch.Tensor:
+    """fp64 alpha * A @ B + beta * C on the fp64 MFMA (trnblas_hip_dgemm):
+    A (M, K), B (K, N), or batched (b, M, K) @ (b, K, N) (a batch of 1
+    broadcasts). Transposed views are read in place. out: the (M, N) /
+    (b, M, N) tensor to write (unit column stride, row stride >= N), which
+    may be C itself; otherwise a fresh tensor. lower (2-D, M == N): only the
+    elements m >= n are computed and written. tri: _lib.TRI_* bits of
+    triangular operands whose zero blocks the kernel skips (their other
+    triangle must hold zeros)."""
+    dev = _require_device(A, B, *(() if C is None else (C,)), *(() if out is None else (out,)))
+    for X in (A, B) + (() if C is None else (C,)) + (() if out is None else (out,)):
+        if X.dtype != torch.float64:
+            raise TypeError(f"dgemm: float64 operands only, got {X.dtype}")
+    two = A.dim() == 2 and B.dim() == 2
+    if not two and not (A.dim() == 3 and B.dim() == 3):
+        raise ValueError("dgemm: operands must both be 2-D or both 3-D")
+    M, K = A.shape[-2:]
+    K2, N = B.shape[-2:]
+    if K != K2:
+        raise ValueError(f"dgemm: inner dimensions differ: {tuple(A.shape)} @ {tuple(B.shape)}")
+    nb = 1 if two else max(A.shape[0], B.shape[0])
+    if not two and (A.shape[0] not in (1, nb) or B.shape[0] not in (1, nb)):
+        raise ValueError(f"dgemm: batch sizes {A.shape[0]} and {B.shape[0]} do not broadcast")
+    if lower and (not two or M != N):
+        raise ValueError("dgemm: lower needs a square 2-D product")
+    shape = (M, N) if two else (nb, M, N)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.float64, device=dev)
+    if tuple(out.shape) != shape:
+        raise ValueError(f"dgemm: out must be {shape}")
+    o3 = out if out.dim() == 3 else out.unsqueeze(0)
+    if M and N and (o3.stride(2) != 1 or o3.stride(1) < N):
+        raise ValueError("dgemm: out needs unit column stride and a row stride >= N")
+    ldd, sd = max(o3.stride(1), N), (o3.stride(0) if nb > 1 else 0)
+    A3 = A if A.dim() == 3 else A.unsqueeze(0)
+    B3 = B if B.dim() == 3 else B.unsqueeze(0)
+    if K % 2:  # a zero term makes K even (16-byte groups along K)
+        A3 = torch.nn.functional.pad(A3, (0, 1))
+        B3 = torch.nn.functional.pad(B3, (0, 0, 0, 1))
+        K += 1
+    a, ta, lda, sa = _dgemm_operand(A3, True)
+    b, tb, ldb, sb = _dgemm_operand(B3, False)
+    c, ldc, sc = None, N, 0
+    if beta != 0.0 and C is not None:
+        c3 = (C if C.dim() == 3 else C.unsqueeze(0)).expand(nb, M, N)
+        if c3.stride(2) != 1 or c3.stride(1) < N:
+            c3 = c3.contiguous()
+        c, ldc, sc = c3, c3.stride(1), (c3.stride(0) if nb > 1 else 0)
+    _probed_call(
+        "dgemm", "trnblas_hip_dgemm", int(ta), int(tb), M, N, K, float(alpha),
+        ptr(a), lda, sa, ptr(b), ldb, sb, float(beta) if c is not None else 0.0,
+        ptr(c), ldc, sc, ptr(o3), ldd, sd, nb, int(lower), int(tri), stream_of(dev),
+    )  # fmt: skip
+    return out
+
+
+TRI_NB = 128  # block of trnblas_hip_tri_inv_blocks
+
+
+def tri_inv_blocks(T: torch.Tensor, upper: bool, unit: bool = False) -> torch.Tensor:
+    """Inverses of the 128 x 128 diagonal blocks of the triangular (n, n)
+    device matrix T (float32 or float64, any strides; only the `upper` /
+    lower triangle is read, the diagonal taken as ones when unit): a
+    (ceil(n / 128), 128, 128) tensor of T's dtype, block b the inverse of
+    T[128 b:128 b + 128, 128 b:128 b + 128] padded with the identity."""
+    dev = _require_device(T)
+    if T.dim() != 2 or T.shape[0] != T.shape[1]:
+        raise ValueError(f"tri_inv_blocks: T must be square, got {tuple(T.shape)}")
+    codes = {torch.float32: _lib.F32, torch.float64: _lib.F64}
+    if T.dtype not in codes:
+        raise TypeError(f"tri_inv_blocks: float32 / float64 only, got {T.dtype}")
+    n = T.shape[0]
+    nblk = -(-n // TRI_NB)
+    D = torch.empty((nblk, TRI_NB, TRI_NB), dtype=T.dtype, device=dev)
+    if n:
+        sr, sc = T.stride()
+        call(
+            "trnblas_hip_tri_inv_blocks", codes[T.dtype], n, int(bool(upper)), int(bool(unit)),
+            ptr(T), max(sr, 1), max(sc, 1), ptr(D), stream_of(dev),
+        )  # fmt: skip
+    return D
+
+
+def metric_inv_half(J: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(X, info) for the SPD (n, n) float64 device matrix J (lower triangle
+    read): X = L^-T with J = L L^T, exactly upper triangular, from the
+    native driver trnblas_hip_metric_inv_half (blocked Cholesky, block
+    inverse, transpose; one call); info (int32 device tensor of one element)
+    holds the order of the first leading minor that is not positive
+    definite, else 0."""
+    dev = _require_device(J)
+    if J.dtype != torch.float64 or J.dim() != 2 or J.shape[0] != J.shape[1]:
+        raise ValueError("metric_inv_half: J must be a square float64 matrix")
+    n = J.shape[0]
+    X = torch.empty((n, n), dtype=torch.float64, device=dev)
+    info = torch.zeros(1, dtype=torch.int32, device=dev)
+    if n == 0:
+        return X, info
+    if J.stride(1) != 1 or J.stride(0) < n:
+        J = J.contiguous()
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        ws = torch.empty(lib.trnblas_hip_metric_inv_half_workspace(n), dtype=torch.uint8, device=dev)
+        _probed_call(
+            "metric_inv_half", "trnblas_hip_metric_inv_half", n, ptr(J), J.stride(0), ptr(X), n,
+            ptr(info), ptr(ws), ws.numel(), stream_of(dev),
+        )  # fmt: skip
+    return X, info
+
+
+def trsm(T: torch.Tensor, B: torch.Tensor, upper: bool, unit: bool, alpha: float,
+         out: torch.Tensor) -> torch.Tensor:
+    """T X = alpha B for the triangular (n, n) device matrix T (`upper` /
+    lower triangle read; unit: its diagonal taken as ones) and B (n, m),
+    float32 or float64, any strides, into out (n, m, any positive strides,
+    e.g. the transposed view of a right solve's result), through the native
+    driver trnblas_hip_trsm. Returns out."""
+    dev = _require_device(T, B, out)
+    codes = {torch.float32: _lib.F32, torch.float64: _lib.F64}
+    if T.dtype not in codes or B.dtype != T.dtype or out.dtype != T.dtype:
+        raise TypeError(f"trsm: float32 / float64 operands of one dtype, got {T.dtype}, {B.dtype}")
+    n, m = B.shape
+    if tuple(T.shape) != (n, n) or tuple(out.shape) != (n, m):
+        raise ValueError(f"trsm: T {tuple(T.shape)}, B {tuple(B.shape)}, out {tuple(out.shape)}")
+    if n == 0 or m == 0:
+        return out
+    lib = _lib.load()
+    code = codes[T.dtype]
+
+    def st(x):
+        return max(x.stride(0), 1), max(x.stride(1), 1)
+
+    with torch.cuda.device(dev):
+        ws = torch.empty(lib.trnblas_hip_trsm_workspace(code, n, m), dtype=torch.uint8, device=dev)
+        _probed_call(
+            "trsm", "trnblas_hip_trsm", code, n, m, int(bool(upper)), int(bool(unit)), float(alpha),
+            ptr(T), *st(T), ptr(B), *st(B), ptr(out), *st(out), ptr(ws), ws.numel(), stream_of(dev),
+        )  # fmt: skip
+    return out
+
 
 CHOL_NB = 128  # largest diagonal block of trnblas_hip_chol_block
 
