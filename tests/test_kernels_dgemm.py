@@ -85,9 +85,9 @@ def test_dgemm_odd_and_unaligned_operands(dev):
     assert _cw(D, ref, den) <= 1e-13
 
 
-def test_dgemm_lower_and_triangular_operands(dev):
+@pytest.mark.parametrize("n", [300, 2048])  # 32- and 64-wide tiles
+def test_dgemm_lower_and_triangular_operands(dev, n):
     g = torch.Generator().manual_seed(5)
-    n = 300
     A = _mat(g, n, 128, dev)
     C = _mat(g, n, n, dev)
     upper_before = torch.triu(C, 1).clone()

@@ -16,7 +16,7 @@
 //    zeros inside the k range a tile still reads (its diagonal blocks).
 //
 // Layout: a 256-thread workgroup (4 wave64s, 2 x 2) owns a BM x BM tile of D
-// (BM 128, or 64 for launches with fewer 128-tiles than CUs); each wave a
+// (BM 128, or 64 / 32 for launches with fewer 128-tiles than CUs); each wave a
 // BM/2 square as 16 x 16 MFMA blocks with fp64 accumulators. k-tiles of BK
 // values (16 for BM 128, 64 for BM 64: either way 64 MFMAs per wave per
 // k-tile) move by LDS DMA (buffer_load_dwordx4 ... lds) into two LDS stages;
@@ -34,7 +34,8 @@
 //  * M/N-contiguous panel (BK rows k of BM values): group q of row k in slot
 //    q ^ (8 ((k >> 2) & 1)), which puts the rows k and k + 4 that two lane
 //    groups read together on different halves of the banks; a DMA block is
-//    1 (BM 128) or 2 (BM 64) rows. A fragment is four 8-byte column reads.
+//    1 (BM 128), 2 (BM 64) or 4 (BM 32) rows. A fragment is four 8-byte
+//    column reads.
 // Ragged M / N edges read zeros (an offset past the buffer's records);
 // K and each operand's contiguous extent are even (16-byte groups are
 // wholly inside or outside the matrix), checked by the entry point.
@@ -88,10 +89,11 @@ __device__ __forceinline__ void dtri_tile(int t, int& tm, int& tn) {
 
 // A BM x BM output tile, k-tiles of BK values (BK / 2 16-byte groups per
 // K-contiguous row) in two LDS stages. BM 128: BK 16, two workgroups per CU;
-// BM 64 (narrow launches): BK 64, so a k-tile still gives each wave 64 MFMAs
-// to cover the next k-tile's DMA (one workgroup per CU).
+// BM 64 and 32 (launches with fewer tiles than CUs): BK 64, so a k-tile
+// still gives each wave 64 (BM 64) or 16 (BM 32) MFMAs behind the next
+// k-tile's DMA, with one (BM 64) or two (BM 32) workgroups per CU.
 template <int BM, int BK, bool AKC, bool BKC>
-__global__ __launch_bounds__(256, BM == 128 ? 2 : 1) void dgemm_kernel(DgemmArgs g) {
+__global__ __launch_bounds__(256, BM == 64 ? 1 : 2) void dgemm_kernel(DgemmArgs g) {
   constexpr int WT = BM / 2;        // wave tile
   constexpr int F = WT / 16;        // 16 x 16 blocks per wave side
   constexpr int PANEL = BM * BK;    // doubles per operand panel
@@ -352,8 +354,11 @@ extern "C" int trnblas_hip_dgemm(int transA, int transB, int64_t M, int64_t N, i
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
       cus = v;
   }
-  const int64_t t128 = lower ? ((M + 127) / 128) * ((M + 127) / 128 + 1) / 2
-                             : ((M + 127) / 128) * ((N + 127) / 128) * batch;
-  if (t128 >= cus) return dlaunch_layout<128>(g, akc, bkc, (hipStream_t)stream);
-  return dlaunch_layout<64>(g, akc, bkc, (hipStream_t)stream);
+  auto tiles = [&](int64_t bm) {
+    const int64_t tm = (M + bm - 1) / bm, tn = (N + bm - 1) / bm;
+    return lower ? tm * (tm + 1) / 2 : tm * tn * batch;
+  };
+  if (tiles(128) >= cus) return dlaunch_layout<128>(g, akc, bkc, (hipStream_t)stream);
+  if (tiles(64) >= cus) return dlaunch_layout<64>(g, akc, bkc, (hipStream_t)stream);
+  return dlaunch_layout<32>(g, akc, bkc, (hipStream_t)stream);
 }

@@ -32,6 +32,8 @@
 // recursive doubling over halves of 16, 32 and 64,
 // Y21 = -Y22 (L21 Y11), in place over L21, through an LDS scratch for the
 // intermediate product.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace trnblas {
@@ -108,22 +110,52 @@ __device__ __forceinline__ void mma16(f64x4& acc, const double* X, const double*
   for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a[q], b[q], acc, 0, 0, 0);
 }
 
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (N > 0) {
+    static_for<N - 1>(f);
+    f(std::integral_constant<int, N - 1>{});
+  }
+}
+
+// v from lane SRC of the lane's 16-lane row (DPP row_newbcast).
+template <int SRC>
+__device__ __forceinline__ double row_bcast(double v) {
+  const long long b = __builtin_bit_cast(long long, v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)b, 0x150 + SRC, 0xf, 0xf, false);
+  const unsigned hi =
+      (unsigned)__builtin_amdgcn_update_dpp(0, (int)(b >> 32), 0x150 + SRC, 0xf, 0xf, false);
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
 // One wave on a 16 x 16 diagonal sub-block `blk` (lower part read).
 // CHOL: blk becomes L (blk = L L^T, zeros above) and inv receives L^-1;
-// a non-positive pivot sets *bad to min(*bad, col0 + column + 1) when that
-// column is below nb. Otherwise blk is lower triangular (unit: its diagonal
-// taken as ones) and inv receives its inverse; blk is not written.
-// Lane (r = l % 16, h = l / 16) holds columns 4 e + h of row r (e = 0..3)
+// a non-positive (or NaN) pivot sets *bad to min(*bad, col0 + column + 1)
+// when that column is below nb. Otherwise blk is lower triangular (unit:
+// its diagonal taken as ones) and inv receives its inverse; blk is not
+// written.
+// Lane (h = l / 16, r = l % 16) holds columns 4 e + h of row r (e = 0..3)
 // of the matrix and of E, the product of the elimination steps so far
 // (unit lower; after the last column E = (unit L)^-1, and L^-1 = diag(1 /
-// l_rr) E). ex: 48 doubles of this wave's LDS (column, E row, 1 / l_cc).
+// l_rr) E). Per column c: the pivot by readlane; every lane publishes its
+// (scaled) element of column 4 (c / 4) + h through LDS, of which the
+// column-c ones are read back (L[r][c] and L[s][c] for the lane's
+// columns); row c of E comes from lane c of the lane's own 16-lane row
+// (DPP). Updates are unconditional where the arithmetic leaves the final
+// values unchanged (zero multipliers, zero entries of E), so the loop has
+// no branches; the strict upper part of the matrix collects garbage that
+// is never read and is written out as zeros. ex: 80 doubles of this
+// wave's LDS.
 template <bool CHOL>
 __device__ __forceinline__ void diag16(double* blk, double* inv, double* ex, int lane, bool unit,
                                        int* bad, int col0, int nb) {
-  double* colb = ex;
-  double* rowb = ex + 16;
-  double* rinvb = ex + 32;
-  const int r = lane & 15, h = lane >> 4;
+  double* colb = ex;        // colb[16 h + r]: lane (h, r)'s published value
+  double* rinvb = ex + 64;  // 1 / l_cc
+  // (an opaque copy of the lane index: otherwise the per-column lane masks
+  // are computed once, outside the caller's loop, and spill)
+  int ln = lane;
+  asm volatile("" : "+v"(ln));
+  const int r = ln & 15, h = ln >> 4;
   double a[4], E[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -132,51 +164,37 @@ __device__ __forceinline__ void diag16(double* blk, double* inv, double* ex, int
     if (!CHOL && unit && s == r) a[e] = 1.0;
     E[e] = s == r ? 1.0 : 0.0;
   }
-#pragma unroll
-  for (int c = 0; c < 16; ++c) {
-    const int ch = c & 3, ce = c >> 2;
+  static_for<16>([&](auto cI) {
+    constexpr int c = decltype(cI)::value, ch = c & 3, ce = c >> 2;
     const double d = readlane_f64(a[ce], c + 16 * ch);  // the pivot
-    double rinv;
-    if (CHOL) {
-      if (lane == 0 && !(d > 0.0) && col0 + c < nb) *bad = min(*bad, col0 + c + 1);
-      rinv = rsqrt_nr(d);
-    } else {
-      rinv = unit ? 1.0 : rcp_nr(d);
-    }
-    // column c (scaled to L's for CHOL) and row c of E to the wave
-    if (h == ch) colb[r] = CHOL ? a[ce] * rinv : a[ce];
-    if (r == c) {
+    const double rinv = CHOL ? rsqrt_nr(d) : (unit ? 1.0 : rcp_nr(d));
+    colb[16 * h + r] = CHOL ? a[ce] * rinv : a[ce];
+    rinvb[c] = rinv;
+    double ev[4];  // E[c][4 e + h]
 #pragma unroll
-      for (int e = 0; e < 4; ++e) rowb[4 * e + h] = E[e];
-    }
-    if (lane == 0) rinvb[c] = rinv;
+    for (int e = 0; e < 4; ++e) ev[e] = row_bcast<c>(E[e]);
     __builtin_amdgcn_wave_barrier();
-    const double lr = colb[r];
-    const double m = lr * rinv;  // the elimination multiplier of row r
-    double cs[4], rk[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      cs[e] = colb[4 * e + h];
-      rk[e] = rowb[4 * e + h];
-    }
+    const double lr = colb[16 * ch + r];  // L[r][c] (CHOL) / T[r][c]
+    const double m = r > c ? lr * rinv : 0.0;  // the elimination multiplier of row r
     if (CHOL) {
-      if (h == ch && r >= c) a[ce] = lr;
+      double cs[4];  // L[4 e + h][c]
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int s = 4 * e + h;
-        if (s > c && s <= r) a[e] = fma(-lr, cs[e], a[e]);
-      }
-    }
-    if (r > c) {
+      for (int e = ce; e < 4; ++e) cs[e] = colb[16 * ch + 4 * e + h];
+      a[ce] = h == ch ? lr : a[ce];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int k = 4 * e + h;
-        if (k <= c) E[e] = fma(-m, rk[e], E[e]);
-      }
+      for (int e = ce + 1; e < 4; ++e) a[e] = fma(-lr, cs[e], a[e]);
+      a[ce] = h > ch ? fma(-lr, cs[ce], a[ce]) : a[ce];
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) E[e] = fma(-m, ev[e], E[e]);
     __builtin_amdgcn_wave_barrier();
-  }
+  });
   const double rr = rinvb[r];
+  if (CHOL) {  // the first NaN 1 / l_cc is the first pivot that is not positive
+    const bool isbad = ln < 16 && !(rr == rr) && col0 + ln < nb;
+    const unsigned long long msk = __ballot(isbad);
+    if (msk != 0ull && ln == 0) *bad = min(*bad, col0 + (int)__builtin_ctzll(msk) + 1);
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int s = 4 * e + h;
@@ -185,58 +203,116 @@ __device__ __forceinline__ void diag16(double* blk, double* inv, double* ex, int
   }
 }
 
+// acc += sgn sum_{t < n} X_t Y_t (n <= NMAX, wave-uniform) over sub-block
+// pairs given by the offsets xo[t], yo[t] into G / Y buffers: every
+// fragment is read before the first MFMA (offsets past n repeat a valid
+// pair and their MFMAs are skipped), so the LDS reads overlap.
+template <int NMAX>
+__device__ __forceinline__ void mma16_sum(f64x4& acc, const double* X, const int (&xo)[NMAX],
+                                          const double* Y, const int (&yo)[NMAX], int n, double sgn,
+                                          int lane) {
+  double a[NMAX][4], b[NMAX][4];
+#pragma unroll
+  for (int t = 0; t < NMAX; ++t)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      a[t][q] = sgn * frag_a(X + xo[t], lane, q);
+      b[t][q] = frag_b(Y + yo[t], lane, q);
+    }
+#pragma unroll
+  for (int t = 0; t < NMAX; ++t)
+    if (t < n) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a[t][q], b[t][q], acc, 0, 0, 0);
+    }
+}
+
 // The block inverse Y = L^-1 in place over the lower sub-block grid G, whose
 // off-diagonal sub-blocks hold L and diagonal ones their inverses: for
 // halves of h = 1, 2, 4 sub-blocks, T = L21 Y11 into scr, then
 // Y21 = -Y22 T over L21.
 __device__ __forceinline__ void block_inverse(double* G, double* scr, int wave, int lane) {
-#pragma unroll
-  for (int h = 1; h < kNS; h *= 2) {
-    const int items = 4 * h;  // (kNS / 2h) pairs x h^2 sub-blocks
+  static_for<3>([&](auto lI) {
+    constexpr int h = 1 << decltype(lI)::value;
+    constexpr int items = 4 * h;  // (kNS / 2h) pairs x h^2 sub-blocks
     for (int it = wave; it < items; it += kThreads / 64) {
       const int pi = it / (h * h), ij = it % (h * h), i = ij / h, j = ij % h, b0 = 2 * h * pi;
+      int xo[h], yo[h];
+#pragma unroll
+      for (int t = 0; t < h; ++t) {  // k = j + t < h
+        const int k = min(j + t, h - 1);
+        xo[t] = sidx(b0 + h + i, b0 + k) * kSB;
+        yo[t] = sidx(b0 + k, b0 + j) * kSB;
+      }
       f64x4 acc = {0.0, 0.0, 0.0, 0.0};
-      for (int k = j; k < h; ++k)
-        mma16<false>(acc, G + sidx(b0 + h + i, b0 + k) * kSB, G + sidx(b0 + k, b0 + j) * kSB, 1.0,
-                     lane);
+      mma16_sum<h>(acc, G, xo, G, yo, h - j, 1.0, lane);
       store_acc(scr + it * kSB, lane, acc);
     }
     __syncthreads();
     for (int it = wave; it < items; it += kThreads / 64) {
       const int pi = it / (h * h), ij = it % (h * h), i = ij / h, j = ij % h, b0 = 2 * h * pi;
+      int xo[h], yo[h];
+#pragma unroll
+      for (int t = 0; t < h; ++t) {  // k = t <= i
+        const int k = min(t, i);
+        xo[t] = sidx(b0 + h + i, b0 + h + k) * kSB;
+        yo[t] = (pi * h * h + k * h + j) * kSB;
+      }
       f64x4 acc = {0.0, 0.0, 0.0, 0.0};
-      for (int k = 0; k <= i; ++k)
-        mma16<false>(acc, G + sidx(b0 + h + i, b0 + h + k) * kSB,
-                     scr + (pi * h * h + k * h + j) * kSB, -1.0, lane);
+      mma16_sum<h>(acc, G, xo, scr, yo, i + 1, -1.0, lane);
       store_acc(G + sidx(b0 + h + i, b0 + j) * kSB, lane, acc);
     }
     __syncthreads();
-  }
-}
-
-// Element (i, k) of the 128 x 128 block, i >= k, in the sub-block grid.
-__device__ __forceinline__ double& gel(double* G, int i, int k) {
-  return G[sidx(i >> 4, k >> 4) * kSB + (k & 15) * kSP + (i & 15)];
+  });
 }
 
 // The lower triangle of a 128 x 128 block (element (i, k) at
-// X[i * ri + k * ci], the identity past nb) into the sub-block grid: each
-// thread issues all its loads before its first LDS store, so the loads'
-// latency is paid once, not once per element.
+// X[i * ri + k * ci], the identity past nb) into the sub-block grid. Thread
+// t takes column k = t % 128 of rows t / 128 + 4 u (u = 0..31), so its
+// addresses step by a constant and the sub-block of each u is known at
+// compile time; all 32 loads issue before the first LDS store.
 template <typename TT>
 __device__ __forceinline__ void load_lower(double* G, const TT* X, int64_t ri, int64_t ci, int nb,
                                            int tid) {
-  constexpr int PER = kCholNB * kCholNB / kThreads;
+  constexpr int PER = kCholNB * kCholNB / kThreads;  // 32
+  const int k = tid & 127, i0 = tid >> 7;
+  const TT* p = X + i0 * ri + k * ci;
   double v[PER];
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
-    const int x = u * kThreads + tid, i = x >> 7, k = x & 127;
-    v[u] = (k <= i && i < nb) ? (double)X[i * ri + k * ci] : (i == k ? 1.0 : 0.0);
+    const int i = i0 + 4 * u;
+    v[u] = (k <= i && i < nb) ? (double)p[(int64_t)(4 * u) * ri] : (i == k ? 1.0 : 0.0);
   }
+  double* g = G + (k >> 4) * kSB + (k & 15) * kSP + i0;
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
-    const int x = u * kThreads + tid, i = x >> 7, k = x & 127;
-    if (k <= i) gel(G, i, k) = v[u];
+    const int i = i0 + 4 * u;
+    if (k <= i) g[sidx(u >> 2, 0) * kSB + 4 * (u & 3)] = v[u];
+  }
+}
+
+// The lower triangle of the grid out to Z[i * zr + k * zc] for i, k < nb
+// (zeros above the diagonal when `full`, else the strict upper part
+// untouched), in the thread mapping of load_lower.
+template <typename TT>
+__device__ __forceinline__ void store_lower(const double* G, TT* Z, int64_t zr, int64_t zc, int nb,
+                                            bool full, int tid) {
+  constexpr int PER = kCholNB * kCholNB / kThreads;
+  asm volatile("" : "+v"(tid));  // (its masks and addresses computed here, not at kernel entry)
+  const int k = tid & 127, i0 = tid >> 7;
+  const double* g = G + (k >> 4) * kSB + (k & 15) * kSP + i0;
+  double v[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = i0 + 4 * u;
+    v[u] = k <= i ? g[sidx(u >> 2, 0) * kSB + 4 * (u & 3)] : 0.0;
+  }
+  TT* z = Z + (int64_t)i0 * zr + (int64_t)k * zc;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int i = i0 + 4 * u;
+    if (i < nb && k < nb && (full || k <= i)) z[(int64_t)(4 * u) * zr] = (TT)v[u];
   }
 }
 
@@ -246,7 +322,7 @@ __global__ __launch_bounds__(kThreads) void chol128_kernel(int nb, double* A, in
   __shared__ double G[kNLow * kSB];
   __shared__ double Dv[kNS * kSB];   // inverses of the diagonal sub-blocks
   __shared__ double scr[16 * kSB];   // T of the block inverse
-  __shared__ double ex[48];          // diag16's exchange
+  __shared__ double ex[80];          // diag16's exchange
   __shared__ int sbad;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -277,18 +353,12 @@ __global__ __launch_bounds__(kThreads) void chol128_kernel(int nb, double* A, in
     __syncthreads();
   }
   // L out (lower triangle of A only), then the diagonal inverses in place
-  for (int x = tid; x < nb * kCholNB; x += kThreads) {
-    const int i = x >> 7, k = x & 127;
-    if (k <= i) A[(int64_t)i * lda + k] = gel(G, i, k);
-  }
+  store_lower(G, A, lda, (int64_t)1, nb, false, tid);
   __syncthreads();
   for (int x = tid; x < kNS * kSB; x += kThreads) G[sidx(x / kSB, x / kSB) * kSB + x % kSB] = Dv[x];
   __syncthreads();
   block_inverse(G, scr, wave, lane);
-  for (int x = tid; x < nb * kCholNB; x += kThreads) {
-    const int i = x >> 7, k = x & 127;
-    if (k < nb) Li[(int64_t)i * ldl + k] = k <= i ? gel(G, i, k) : 0.0;
-  }
+  store_lower(G, Li, ldl, (int64_t)1, nb, true, tid);
   if (tid == 0 && sbad != 0x7fffffff && info[0] == 0) info[0] = offset + sbad;
 }
 
@@ -303,7 +373,7 @@ __global__ __launch_bounds__(kThreads) void trinv128_kernel(int n, int upper, in
                                                             TT* Dinv) {
   __shared__ double G[kNLow * kSB];
   __shared__ double scr[16 * kSB];
-  __shared__ double ex[kThreads / 64][48];
+  __shared__ double ex[kThreads / 64][80];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = blockIdx.x, k0 = b * kCholNB, nb = min(kCholNB, n - k0);
@@ -317,13 +387,10 @@ __global__ __launch_bounds__(kThreads) void trinv128_kernel(int n, int upper, in
   for (int x = tid; x < kNS * kSB; x += kThreads) G[sidx(x / kSB, x / kSB) * kSB + x % kSB] = scr[x];
   __syncthreads();
   block_inverse(G, scr, wave, lane);
+  // lower: out[i][k] = Y[i][k]; upper: out[k][i] = Y[i][k]
   TT* out = Dinv + (int64_t)b * kCholNB * kCholNB;
-  for (int x = tid; x < kCholNB * kCholNB; x += kThreads) {
-    const int i = x >> 7, k = x & 127;
-    // lower: out[i][k] = Y[i][k]; upper: out[i][k] = Y[k][i]
-    const int yi = upper ? k : i, yk = upper ? i : k;
-    out[x] = (TT)(yk <= yi ? gel(G, yi, yk) : 0.0);
-  }
+  store_lower(G, out, upper ? (int64_t)1 : (int64_t)kCholNB, upper ? (int64_t)kCholNB : (int64_t)1,
+              kCholNB, true, tid);
 }
 
 }  // namespace trnblas
