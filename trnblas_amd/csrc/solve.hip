@@ -12,9 +12,12 @@
 // stream, so block b + 1 is factored while a second stream (per device,
 // default priority) applies the rest of the trailing update (lower
 // triangle only) with the other CUs; the caller's stream waits for it
-// before it next writes there. Then Y = L^-1 by recursive doubling over
-// block halves, Y21 = -Y22 (L21 Y11), one batched GEMM pair per level, and
-// X = Y^T.
+// before it next writes there. Y = L^-1 is built beside the factorisation
+// on a third stream: once block b is factored (its inverse Y_bb written in
+// place by the diagonal kernel), block row b of Y follows from the rows
+// above it, Y[b, :b] = -Y_bb (L[b, :b] Y[:b, :b]), two GEMMs that run
+// while the caller's stream factors the next blocks (the late steps, bound
+// by the one-workgroup diagonal kernel, leave most CUs free). Then X = Y^T.
 #include <mutex>
 
 #include "common.hpp"
@@ -67,14 +70,6 @@ __global__ __launch_bounds__(256) void transpose_kernel(int n, const double* Y, 
   }
 }
 
-// Y's diagonal blocks from the kernel's inverses Li (nblk x 128 x 128)
-__global__ __launch_bounds__(256) void place_diag_kernel(const double* Li, double* Y, int64_t ldy) {
-  const int b = blockIdx.x;
-  const double* src = Li + (int64_t)b * kNB * kNB;
-  double* dst = Y + (int64_t)b * kNB * (ldy + 1);
-  for (int x = threadIdx.x; x < kNB * kNB; x += 256) dst[(int64_t)(x >> 7) * ldy + (x & 127)] = src[x];
-}
-
 static int grid_for(int64_t elems) {
   const int64_t g = (elems + 255) / 256;
   return (int)(g < 4096 ? (g > 0 ? g : 1) : 4096);
@@ -92,8 +87,8 @@ static int fill(double* p, int64_t rows, int64_t cols, int64_t ld, double v, hip
 // from interleaving their use.
 struct SideStream {
   std::mutex mu;
-  hipStream_t side = nullptr;
-  hipEvent_t ready = nullptr, done = nullptr;
+  hipStream_t side = nullptr, inv = nullptr;
+  hipEvent_t ready = nullptr, done = nullptr, factored = nullptr, inverted = nullptr;
 };
 
 static SideStream* side_stream(int& rc) {
@@ -111,24 +106,26 @@ static SideStream* side_stream(int& rc) {
 static int side_init(SideStream* ss) {
   if (ss->side) return TRNBLAS_OK;
   if (hipStreamCreateWithFlags(&ss->side, hipStreamNonBlocking) != hipSuccess ||
+      hipStreamCreateWithFlags(&ss->inv, hipStreamNonBlocking) != hipSuccess ||
       hipEventCreateWithFlags(&ss->ready, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&ss->done, hipEventDisableTiming) != hipSuccess) {
+      hipEventCreateWithFlags(&ss->done, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ss->factored, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ss->inverted, hipEventDisableTiming) != hipSuccess) {
     set_error("metric_inv_half: cannot create the side stream / events");
     return TRNBLAS_E_LAUNCH;
   }
   return TRNBLAS_OK;
 }
 
-static void metric_layout(int64_t n, int64_t& nblk, int64_t& npad, size_t off[5]) {
+static void metric_layout(int64_t n, int64_t& nblk, int64_t& npad, size_t off[4]) {
   nblk = (n + kNB - 1) / kNB;
   npad = nblk * kNB;
-  const size_t sq = (size_t)npad * npad * 8, half = (size_t)(npad / 2) * (npad / 2) * 8;
+  const size_t sq = (size_t)npad * npad * 8;
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
-  off[0] = 0;                                   // W: J, updated in place
-  off[1] = up(off[0] + sq);                     // L: panels of the factor
-  off[2] = up(off[1] + sq);                     // Y: L^-1
-  off[3] = up(off[2] + sq);                     // T: one level's products
-  off[4] = up(off[3] + (half > 0 ? half : 8));  // Li: the diagonal blocks' inverses
+  off[0] = 0;                                // W: J, updated in place
+  off[1] = up(off[0] + sq);                  // L: panels of the factor
+  off[2] = up(off[1] + sq);                  // Y: L^-1 (diagonal blocks from the kernel)
+  off[3] = up(off[2] + sq);                  // T: a block row's product L[b, :b] Y[:b, :b]
 }
 
 #define TRY(x)                        \
@@ -144,9 +141,9 @@ using namespace trnblas;
 extern "C" size_t trnblas_hip_metric_inv_half_workspace(int64_t n) {
   if (n <= 0) return 0;
   int64_t nblk, npad;
-  size_t off[5];
+  size_t off[4];
   metric_layout(n, nblk, npad, off);
-  return off[4] + (size_t)nblk * kNB * kNB * 8;
+  return off[3] + (size_t)kNB * npad * 8;
 }
 
 extern "C" int trnblas_hip_metric_inv_half(int64_t n, const double* J, int64_t ldj, double* X,
@@ -164,42 +161,56 @@ extern "C" int trnblas_hip_metric_inv_half(int64_t n, const double* J, int64_t l
                     "metric_inv_half: workspace must be 256-byte aligned");
   hipStream_t main = (hipStream_t)stream;
   int64_t nblk, npad;
-  size_t off[5];
+  size_t off[4];
   metric_layout(n, nblk, npad, off);
   char* ws = static_cast<char*>(workspace);
   double* W = reinterpret_cast<double*>(ws + off[0]);
   double* L = reinterpret_cast<double*>(ws + off[1]);
   double* Y = reinterpret_cast<double*>(ws + off[2]);
   double* T = reinterpret_cast<double*>(ws + off[3]);
-  double* Li = reinterpret_cast<double*>(ws + off[4]);
   int rc = TRNBLAS_OK;
   SideStream* ss = side_stream(rc);
   if (!ss) return rc;
   std::lock_guard<std::mutex> lock(ss->mu);
-  const bool look = nblk > 2;
-  if (look) TRY(side_init(ss));
+  TRY(side_init(ss));
+  auto wait = [](hipStream_t s, hipEvent_t e) {
+    return hipStreamWaitEvent(s, e, 0) == hipSuccess ? TRNBLAS_OK : TRNBLAS_E_LAUNCH;
+  };
+  auto record = [](hipEvent_t e, hipStream_t s) {
+    return hipEventRecord(e, s) == hipSuccess ? TRNBLAS_OK : TRNBLAS_E_LAUNCH;
+  };
 
-  // W = J zero-padded; Li = 0 (the last block's padding); info = 0
+  // W = J zero-padded; Y = 0 (the last block's padding stays 0); info = 0
   TRY(fill(W, npad, npad, npad, 0.0, main));
   hipLaunchKernelGGL((copy2d_kernel<double, double>), grid2d(n, n), dim3(256), 0, main, n, n, J,
                      ldj, (int64_t)1, W, npad, (int64_t)1, 1.0);
   TRY(check_launch("metric_inv_half(copy)"));
-  TRY(fill(Li, nblk * kNB, kNB, kNB, 0.0, main));
+  TRY(fill(Y, npad, npad, npad, 0.0, main));
   hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, main, info, 0);
   TRY(check_launch("metric_inv_half(info)"));
 
-  bool rest = false;  // the side stream's last trailing update is pending
+  bool rest = false, inv = false;  // the side / inverse stream has work pending
   for (int64_t b = 0; b < nblk; ++b) {
     const int64_t k0 = b * kNB, m = n - k0 < kNB ? n - k0 : kNB;
-    TRY(trnblas_hip_chol_block(m, W + k0 * npad + k0, npad, Li + b * kNB * kNB, kNB, info, k0,
-                               main));
+    double* Ybb = Y + k0 * npad + k0;
+    // L_bb into W (lower triangle), L_bb^-1 = Y_bb straight into Y
+    TRY(trnblas_hip_chol_block(m, W + k0 * npad + k0, npad, Ybb, npad, info, k0, main));
+    if (b > 0) {
+      // block row b of Y: T = L[b, :b] Y[:b, :b], Y[b, :b] = -Y_bb T
+      TRY(record(ss->factored, main));
+      TRY(wait(ss->inv, ss->factored));
+      TRY(trnblas_hip_dgemm(0, 0, kNB, k0, k0, 1.0, L + k0 * npad, npad, 0, Y, npad, 0, 0.0,
+                            nullptr, npad, 0, T, npad, 0, 1, 0, TRNBLAS_TRI_B_LOWER, ss->inv));
+      TRY(trnblas_hip_dgemm(0, 0, kNB, k0, kNB, -1.0, Ybb, npad, 0, T, npad, 0, 0.0, nullptr,
+                            npad, 0, Y + k0 * npad, npad, 0, 1, 0, TRNBLAS_TRI_A_LOWER, ss->inv));
+      inv = true;
+    }
     if (k0 + kNB >= npad) break;
     const int64_t k1 = k0 + kNB, k2 = k1 + kNB, rows = npad - k1;
-    // the panel of L: L[k1:, k0:k1] = W[k1:, k0:k1] Li_b^T
-    TRY(trnblas_hip_dgemm(0, 1, rows, kNB, kNB, 1.0, W + k1 * npad + k0, npad, 0,
-                          Li + b * kNB * kNB, kNB, 0, 0.0, nullptr, npad, 0, L + k1 * npad + k0,
-                          npad, 0, 1, 0, 0, main));
-    if (rest && hipStreamWaitEvent(main, ss->done, 0) != hipSuccess) return TRNBLAS_E_LAUNCH;
+    // the panel of L: L[k1:, k0:k1] = W[k1:, k0:k1] Y_bb^T
+    TRY(trnblas_hip_dgemm(0, 1, rows, kNB, kNB, 1.0, W + k1 * npad + k0, npad, 0, Ybb, npad, 0,
+                          0.0, nullptr, npad, 0, L + k1 * npad + k0, npad, 0, 1, 0, 0, main));
+    if (rest) TRY(wait(main, ss->done));
     rest = false;
     // the next block column: W[k1:, k1:k2] -= P P[:128]^T
     TRY(trnblas_hip_dgemm(0, 1, rows, kNB, kNB, -1.0, L + k1 * npad + k0, npad, 0,
@@ -209,45 +220,18 @@ extern "C" int trnblas_hip_metric_inv_half(int64_t n, const double* J, int64_t l
       const int64_t r2 = npad - k2;
       const double* R = L + k2 * npad + k0;
       double* Wt = W + k2 * npad + k2;
-      hipStream_t s2 = main;
-      if (look) {
-        if (hipEventRecord(ss->ready, main) != hipSuccess ||
-            hipStreamWaitEvent(ss->side, ss->ready, 0) != hipSuccess)
-          return TRNBLAS_E_LAUNCH;
-        s2 = ss->side;
-      }
+      TRY(record(ss->ready, main));
+      TRY(wait(ss->side, ss->ready));
       TRY(trnblas_hip_dgemm(0, 1, r2, r2, kNB, -1.0, R, npad, 0, R, npad, 0, 1.0, Wt, npad, 0, Wt,
-                            npad, 0, 1, 1, 0, s2));
-      if (look) {
-        if (hipEventRecord(ss->done, ss->side) != hipSuccess) return TRNBLAS_E_LAUNCH;
-        rest = true;
-      }
+                            npad, 0, 1, 1, 0, ss->side));
+      TRY(record(ss->done, ss->side));
+      rest = true;
     }
   }
-  if (rest && hipStreamWaitEvent(main, ss->done, 0) != hipSuccess) return TRNBLAS_E_LAUNCH;
-
-  // Y = L^-1: the diagonal blocks, then halves of h blocks
-  TRY(fill(Y, npad, npad, npad, 0.0, main));
-  hipLaunchKernelGGL(place_diag_kernel, dim3((unsigned)nblk), dim3(256), 0, main, Li, Y, npad);
-  TRY(check_launch("metric_inv_half(diag)"));
-  for (int64_t h = 1; h < nblk; h *= 2) {
-    const int64_t s = h * kNB, full = nblk / (2 * h), st = 2 * s * (npad + 1);
-    if (full) {
-      TRY(trnblas_hip_dgemm(0, 0, s, s, s, 1.0, L + s * npad, npad, st, Y, npad, st, 0.0, nullptr,
-                            s, 0, T, s, s * s, full, 0, TRNBLAS_TRI_B_LOWER, main));
-      TRY(trnblas_hip_dgemm(0, 0, s, s, s, -1.0, Y + s * npad + s, npad, st, T, s, s * s, 0.0,
-                            nullptr, npad, 0, Y + s * npad, npad, st, full, 0, TRNBLAS_TRI_A_LOWER,
-                            main));
-    }
-    const int64_t r0 = full * 2 * s;
-    if (npad - r0 > s) {  // a last pair whose second half is shorter
-      const int64_t a = r0 + s, rows = npad - a;
-      TRY(trnblas_hip_dgemm(0, 0, rows, s, s, 1.0, L + a * npad + r0, npad, 0, Y + r0 * npad + r0,
-                            npad, 0, 0.0, nullptr, s, 0, T, s, 0, 1, 0, TRNBLAS_TRI_B_LOWER, main));
-      TRY(trnblas_hip_dgemm(0, 0, rows, s, rows, -1.0, Y + a * npad + a, npad, 0, T, s, 0, 0.0,
-                            nullptr, npad, 0, Y + a * npad + r0, npad, 0, 1, 0, TRNBLAS_TRI_A_LOWER,
-                            main));
-    }
+  if (rest) TRY(wait(main, ss->done));
+  if (inv) {
+    TRY(record(ss->inverted, ss->inv));
+    TRY(wait(main, ss->inverted));
   }
   const unsigned tb = (unsigned)((n + 63) / 64);
   hipLaunchKernelGGL(transpose_kernel, dim3(tb, tb), dim3(256), 0, main, (int)n, Y, npad, X, ldx);
