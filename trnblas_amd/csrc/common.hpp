@@ -27,6 +27,10 @@ void clear_error();
 // After a launch: map hipGetLastError to TRNBLAS_E_LAUNCH.
 int check_launch(const char* what);
 
+// Compute units of the current device, queried once per device (256 if the
+// query fails).
+int device_cus();
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));

@@ -88,12 +88,13 @@ __device__ __forceinline__ void dtri_tile(int t, int& tm, int& tn) {
 }
 
 // A BM x BM output tile, k-tiles of BK values (BK / 2 16-byte groups per
-// K-contiguous row) in two LDS stages. BM 128: BK 16, two workgroups per CU;
-// BM 64 and 32 (launches with fewer tiles than CUs): BK 64, so a k-tile
-// still gives each wave 64 (BM 64) or 16 (BM 32) MFMAs behind the next
-// k-tile's DMA, with one (BM 64) or two (BM 32) workgroups per CU.
+// K-contiguous row) in two LDS stages: 64 KiB for every shape (BM 128: BK 16;
+// BM 64: BK 32; BM 32: BK 64), so two workgroups share a CU, or one shares
+// it with a 90 KiB diagonal-block kernel of a concurrent stream. Each wave
+// has 64 (BM 128), 32 (BM 64) or 16 (BM 32) MFMAs per k-tile behind the
+// next k-tile's DMA.
 template <int BM, int BK, bool AKC, bool BKC>
-__global__ __launch_bounds__(256, BM == 64 ? 1 : 2) void dgemm_kernel(DgemmArgs g) {
+__global__ __launch_bounds__(256, 2) void dgemm_kernel(DgemmArgs g) {
   constexpr int WT = BM / 2;        // wave tile
   constexpr int F = WT / 16;        // 16 x 16 blocks per wave side
   constexpr int PANEL = BM * BK;    // doubles per operand panel
@@ -275,8 +276,8 @@ static int dlaunch(DgemmArgs g, hipStream_t s) {
   g.tiles_m = (g.M + BM - 1) / BM;
   g.tiles_n = (g.N + BM - 1) / BM;
   g.ntiles = g.lower ? g.tiles_m * (g.tiles_m + 1) / 2 : g.tiles_m * g.tiles_n * g.batch;
-  hipLaunchKernelGGL((dgemm_kernel<BM, BM == 128 ? 16 : 64, AKC, BKC>), dim3(g.ntiles), dim3(256),
-                     0, s, g);
+  constexpr int BK = BM == 128 ? 16 : BM == 64 ? 32 : 64;
+  hipLaunchKernelGGL((dgemm_kernel<BM, BK, AKC, BKC>), dim3(g.ntiles), dim3(256), 0, s, g);
   return check_launch("trnblas_hip_dgemm");
 }
 
@@ -347,13 +348,8 @@ extern "C" int trnblas_hip_dgemm(int transA, int transB, int64_t M, int64_t N, i
   g.batch = (int)batch;
   g.lower = lower != 0;
   g.tri = tri;
-  // 128 x 128 tiles when they fill the chip, 64 x 64 for narrow launches
-  int cus = 256, dev = 0;
-  if (hipGetDevice(&dev) == hipSuccess) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      cus = v;
-  }
+  // 128 x 128 tiles when they fill the chip, smaller ones for narrow launches
+  const int cus = device_cus();
   auto tiles = [&](int64_t bm) {
     const int64_t tm = (M + bm - 1) / bm, tn = (N + bm - 1) / bm;
     return lower ? tm * (tm + 1) / 2 : tm * tn * batch;

@@ -839,7 +839,7 @@ struct Cfg {
 constexpr int kTileM = 128, kTileN = 128;
 constexpr size_t kSkSlotBytes = (size_t)kTileM * kTileN * sizeof(float);
 
-static int device_cus() {
+int device_cus() {
   static int cus[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;

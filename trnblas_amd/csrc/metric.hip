@@ -230,40 +230,43 @@ __device__ __forceinline__ void mma16_sum(f64x4& acc, const double* X, const int
 
 // The block inverse Y = L^-1 in place over the lower sub-block grid G, whose
 // off-diagonal sub-blocks hold L and diagonal ones their inverses: for
-// halves of h = 1, 2, 4 sub-blocks, T = L21 Y11 into scr, then
-// Y21 = -Y22 T over L21.
+// halves of h = 1, 2, 4 sub-blocks and each column j of a half, T = L21 Y11
+// (column j) into scr, then Y21 = -Y22 T (column j) over L21. A round
+// handles one column of every pair: 4 sub-blocks of T, so scr holds 4
+// (later rounds read only columns of L21 that earlier rounds left).
 __device__ __forceinline__ void block_inverse(double* G, double* scr, int wave, int lane) {
   static_for<3>([&](auto lI) {
     constexpr int h = 1 << decltype(lI)::value;
-    constexpr int items = 4 * h;  // (kNS / 2h) pairs x h^2 sub-blocks
-    for (int it = wave; it < items; it += kThreads / 64) {
-      const int pi = it / (h * h), ij = it % (h * h), i = ij / h, j = ij % h, b0 = 2 * h * pi;
-      int xo[h], yo[h];
+    for (int j = 0; j < h; ++j) {
+      if (wave < 4) {  // item = (pair pi, row i of the half)
+        const int pi = wave / h, i = wave % h, b0 = 2 * h * pi;
+        int xo[h], yo[h];
 #pragma unroll
-      for (int t = 0; t < h; ++t) {  // k = j + t < h
-        const int k = min(j + t, h - 1);
-        xo[t] = sidx(b0 + h + i, b0 + k) * kSB;
-        yo[t] = sidx(b0 + k, b0 + j) * kSB;
+        for (int t = 0; t < h; ++t) {  // k = j + t < h
+          const int k = min(j + t, h - 1);
+          xo[t] = sidx(b0 + h + i, b0 + k) * kSB;
+          yo[t] = sidx(b0 + k, b0 + j) * kSB;
+        }
+        f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+        mma16_sum<h>(acc, G, xo, G, yo, h - j, 1.0, lane);
+        store_acc(scr + wave * kSB, lane, acc);
       }
-      f64x4 acc = {0.0, 0.0, 0.0, 0.0};
-      mma16_sum<h>(acc, G, xo, G, yo, h - j, 1.0, lane);
-      store_acc(scr + it * kSB, lane, acc);
-    }
-    __syncthreads();
-    for (int it = wave; it < items; it += kThreads / 64) {
-      const int pi = it / (h * h), ij = it % (h * h), i = ij / h, j = ij % h, b0 = 2 * h * pi;
-      int xo[h], yo[h];
+      __syncthreads();
+      if (wave < 4) {
+        const int pi = wave / h, i = wave % h, b0 = 2 * h * pi;
+        int xo[h], yo[h];
 #pragma unroll
-      for (int t = 0; t < h; ++t) {  // k = t <= i
-        const int k = min(t, i);
-        xo[t] = sidx(b0 + h + i, b0 + h + k) * kSB;
-        yo[t] = (pi * h * h + k * h + j) * kSB;
+        for (int t = 0; t < h; ++t) {  // k = t <= i
+          const int k = min(t, i);
+          xo[t] = sidx(b0 + h + i, b0 + h + k) * kSB;
+          yo[t] = (pi * h + k) * kSB;
+        }
+        f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+        mma16_sum<h>(acc, G, xo, scr, yo, i + 1, -1.0, lane);
+        store_acc(G + sidx(b0 + h + i, b0 + j) * kSB, lane, acc);
       }
-      f64x4 acc = {0.0, 0.0, 0.0, 0.0};
-      mma16_sum<h>(acc, G, xo, scr, yo, i + 1, -1.0, lane);
-      store_acc(G + sidx(b0 + h + i, b0 + j) * kSB, lane, acc);
+      __syncthreads();
     }
-    __syncthreads();
   });
 }
 
@@ -297,7 +300,7 @@ __device__ __forceinline__ void load_lower(double* G, const TT* X, int64_t ri, i
 // untouched), in the thread mapping of load_lower.
 template <typename TT>
 __device__ __forceinline__ void store_lower(const double* G, TT* Z, int64_t zr, int64_t zc, int nb,
-                                            bool full, int tid) {
+                                            bool full, int tid, bool skip_diag = false) {
   constexpr int PER = kCholNB * kCholNB / kThreads;
   asm volatile("" : "+v"(tid));  // (its masks and addresses computed here, not at kernel entry)
   const int k = tid & 127, i0 = tid >> 7;
@@ -312,17 +315,22 @@ __device__ __forceinline__ void store_lower(const double* G, TT* Z, int64_t zr, 
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
     const int i = i0 + 4 * u;
-    if (i < nb && k < nb && (full || k <= i)) z[(int64_t)(4 * u) * zr] = (TT)v[u];
+    if (i < nb && k < nb && (full || k <= i) && !(skip_diag && (i >> 4) == (k >> 4)))
+      z[(int64_t)(4 * u) * zr] = (TT)v[u];
   }
 }
 
+// LDS: the sub-block grid (78 KB), one diagonal inverse, the block
+// inverse's scratch and diag16's exchange: 91 KB, so the workgroup shares a
+// CU with a GEMM workgroup (64 KB) of a concurrent stream instead of
+// waiting for a whole free CU.
 __global__ __launch_bounds__(kThreads) void chol128_kernel(int nb, double* A, int64_t lda,
                                                            double* Li, int64_t ldl, int32_t* info,
                                                            int offset) {
   __shared__ double G[kNLow * kSB];
-  __shared__ double Dv[kNS * kSB];   // inverses of the diagonal sub-blocks
-  __shared__ double scr[16 * kSB];   // T of the block inverse
-  __shared__ double ex[80];          // diag16's exchange
+  __shared__ double D1[kSB];        // inverse of the current diagonal sub-block
+  __shared__ double scr[4 * kSB];   // T of the block inverse
+  __shared__ double ex[80];         // diag16's exchange
   __shared__ int sbad;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -332,16 +340,25 @@ __global__ __launch_bounds__(kThreads) void chol128_kernel(int nb, double* A, in
   load_lower(G, A, lda, 1, nb, tid);
   __syncthreads();
   for (int p = 0; p < kNS; ++p) {
-    if (wave == 0)
-      diag16<true>(G + sidx(p, p) * kSB, Dv + p * kSB, ex, lane, false, &sbad, 16 * p, nb);
+    double* Gpp = G + sidx(p, p) * kSB;
+    if (wave == 0) diag16<true>(Gpp, D1, ex, lane, false, &sbad, 16 * p, nb);
     __syncthreads();
     for (int i = p + 1 + wave; i < kNS; i += kThreads / 64) {  // panel
       f64x4 acc = {0.0, 0.0, 0.0, 0.0};
-      mma16<true>(acc, G + sidx(i, p) * kSB, Dv + p * kSB, 1.0, lane);
+      mma16<true>(acc, G + sidx(i, p) * kSB, D1, 1.0, lane);
       store_acc(G + sidx(i, p) * kSB, lane, acc);
     }
     __syncthreads();
     const int nt = kNS - 1 - p, items = nt * (nt + 1) / 2;
+    if (wave == 7) {
+      // L_pp out to A (its lower part), then L_pp^-1 in its place: the
+      // trailing update below does not read the diagonal sub-block
+      for (int e = lane; e < 256; e += 64) {
+        const int r = e >> 4, c = e & 15, i = 16 * p + r, k = 16 * p + c;
+        if (c <= r && i < nb) A[(int64_t)i * lda + k] = Gpp[c * kSP + r];
+      }
+      for (int e = lane; e < kSB; e += 64) Gpp[e] = D1[e];
+    }
     for (int it = wave; it < items; it += kThreads / 64) {  // trailing update
       int ri = 0;
       while ((ri + 1) * (ri + 2) / 2 <= it) ++ri;
@@ -352,10 +369,9 @@ __global__ __launch_bounds__(kThreads) void chol128_kernel(int nb, double* A, in
     }
     __syncthreads();
   }
-  // L out (lower triangle of A only), then the diagonal inverses in place
-  store_lower(G, A, lda, (int64_t)1, nb, false, tid);
-  __syncthreads();
-  for (int x = tid; x < kNS * kSB; x += kThreads) G[sidx(x / kSB, x / kSB) * kSB + x % kSB] = Dv[x];
+  // the off-diagonal sub-blocks of L out (the diagonal ones went out per
+  // step; the diagonal sub-blocks of G now hold their inverses)
+  store_lower(G, A, lda, (int64_t)1, nb, false, tid, true);
   __syncthreads();
   block_inverse(G, scr, wave, lane);
   store_lower(G, Li, ldl, (int64_t)1, nb, true, tid);
@@ -372,7 +388,7 @@ __global__ __launch_bounds__(kThreads) void trinv128_kernel(int n, int upper, in
                                                             const TT* T, int64_t sr, int64_t sc,
                                                             TT* Dinv) {
   __shared__ double G[kNLow * kSB];
-  __shared__ double scr[16 * kSB];
+  __shared__ double scr[4 * kSB];
   __shared__ double ex[kThreads / 64][80];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -380,11 +396,10 @@ __global__ __launch_bounds__(kThreads) void trinv128_kernel(int n, int upper, in
   const int64_t ri = upper ? sc : sr, ci = upper ? sr : sc;  // strides of the lower view
   load_lower(G, T + (int64_t)k0 * (sr + sc), ri, ci, nb, tid);
   __syncthreads();
-  // the 8 diagonal sub-blocks' inverses, one wave each, into scr
-  diag16<false>(G + sidx(wave, wave) * kSB, scr + wave * kSB, ex[wave], lane, unit != 0, nullptr,
-                0, 0);
-  __syncthreads();
-  for (int x = tid; x < kNS * kSB; x += kThreads) G[sidx(x / kSB, x / kSB) * kSB + x % kSB] = scr[x];
+  // the 8 diagonal sub-blocks' inverses, one wave each, in place (diag16
+  // reads the sub-block into registers before it writes the inverse)
+  diag16<false>(G + sidx(wave, wave) * kSB, G + sidx(wave, wave) * kSB, ex[wave], lane, unit != 0,
+                nullptr, 0, 0);
   __syncthreads();
   block_inverse(G, scr, wave, lane);
   // lower: out[i][k] = Y[i][k]; upper: out[k][i] = Y[i][k]
