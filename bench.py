@@ -186,12 +186,14 @@ def run_extras(dev, tb, only=None) -> dict:
         del Xb, Yb
     if only is None or "c3" in only:
         # C3: fused pair energy vs the unfused GPU baseline (hipBLASLt GEMM + torch),
-        # in both kernel arithmetics (bf16x6 is the default)
+        # in the three kernel arithmetics (fp16x3 is the default)
         Bp, eo, ev = df_mp2.config3_inputs(dev)
-        tf = gpu_time_ms(lambda: kernels.pair_energy_sym(Bp, eo, ev, math="bf16x6"), reps=3, warm=1)
+        tf = gpu_time_ms(lambda: kernels.pair_energy_sym(Bp, eo, ev, math="fp16x3"), reps=3, warm=1)
+        tb6 = gpu_time_ms(lambda: kernels.pair_energy_sym(Bp, eo, ev, math="bf16x6"), reps=3, warm=1)
         tf32 = gpu_time_ms(lambda: kernels.pair_energy_sym(Bp, eo, ev, math="fp32"), reps=3, warm=1)
         tu = gpu_time_ms(lambda: dispatch._torch_chunked_pair_energy(Bp, eo, ev), reps=3, warm=1)
-        e_hip = float(kernels.pair_energy_sym(Bp, eo, ev, math="bf16x6"))
+        e_hip = float(kernels.pair_energy_sym(Bp, eo, ev, math="fp16x3"))
+        e_b6 = float(kernels.pair_energy_sym(Bp, eo, ev, math="bf16x6"))
         e_f32 = float(kernels.pair_energy_sym(Bp, eo, ev, math="fp32"))
         e_unf = float(dispatch._torch_chunked_pair_energy(Bp, eo, ev))
         Bd, eod, evd = Bp.double(), eo.double(), ev.double()
@@ -211,16 +213,17 @@ def run_extras(dev, tb, only=None) -> dict:
         probe = LaunchEvents("pair_energy")
         kernels._launch_probe = probe
         for _ in range(3):
-            kernels.pair_energy_sym(Bp, eo, ev, math="bf16x6")
+            kernels.pair_energy_sym(Bp, eo, ev, math="fp16x3")
         kernels._launch_probe = None
         torch.cuda.synchronize()
         t_launch = probe.mean_ms()
         roof = {
-            "kernel": "split_planes_kernel + pair_energy_x3c_kernel (trnblas_hip_pair_energy_bf16x6)",
+            "kernel": "row_exp_kernel + split_planes_kernel<2> + pair_energy_x3c_kernel<2> "
+                      "(trnblas_hip_pair_energy_fp16x3)",
             "bound": "mfma", "launch_ms": t_launch,
-            "achieved": 6 * fl / t_launch / 1e9, "peak": PEAK_BF16_MFMA, "unit": "TFLOP/s (bf16 MFMA)",
-            "frac": 6 * fl / t_launch / 1e9 / PEAK_BF16_MFMA,
-            "achieved_fp32_equiv": fl / t_launch / 1e9, "ceiling_fp32_equiv": PEAK_BF16_MFMA / 6,
+            "achieved": 3 * fl / t_launch / 1e9, "peak": PEAK_BF16_MFMA, "unit": "TFLOP/s (f16 MFMA)",
+            "frac": 3 * fl / t_launch / 1e9 / PEAK_BF16_MFMA,
+            "achieved_fp32_equiv": fl / t_launch / 1e9, "ceiling_fp32_equiv": PEAK_BF16_MFMA / 3,
             "frac_fp32_peak": fl / t_launch / 1e9 / PEAK_FP32_MFMA,
             "algorithmic_flop_per_launch": fl, "traffic": None,
         }  # fmt: skip
@@ -235,11 +238,14 @@ def run_extras(dev, tb, only=None) -> dict:
         cpu_loop_ms = (time.perf_counter() - t0) * 1e3
         del Bh
         out["pair_energy_c3_96_672_2304"] = {
-            "fused_ms": tf, "fused_math": "bf16x6", "unfused_gpu_ms": tu,
+            "fused_ms": tf, "fused_math": "fp16x3", "unfused_gpu_ms": tu,
             "speedup_vs_unfused": tu / tf, "tflops_sym": fl / tf / 1e9,
-            "bf16_mfma_tflops": 6 * fl / tf / 1e9,
-            "frac_bf16_peak": 6 * fl / tf / 1e9 / PEAK_BF16_MFMA,
+            "f16_mfma_tflops": 3 * fl / tf / 1e9,
+            "frac_f16_peak": 3 * fl / tf / 1e9 / PEAK_BF16_MFMA,
             "energy_fp64": e64, "rel_err_fused_vs_fp64": abs(e_hip - e64) / abs(e64),
+            "fused_bf16x6_ms": tb6, "speedup_bf16x6_vs_unfused": tu / tb6,
+            "frac_bf16_peak_bf16x6": 6 * fl / tb6 / 1e9 / PEAK_BF16_MFMA,
+            "rel_err_fused_bf16x6_vs_fp64": abs(e_b6 - e64) / abs(e64),
             "fused_fp32_mfma_ms": tf32, "speedup_fp32_mfma_vs_unfused": tu / tf32,
             "frac_fp32_peak_fp32_mfma": fl / tf32 / 1e9 / PEAK_FP32_MFMA,
             "rel_err_fused_fp32_mfma_vs_fp64": abs(e_f32 - e64) / abs(e64),
@@ -253,14 +259,14 @@ def run_extras(dev, tb, only=None) -> dict:
     if only is None or "c4" in only:
         # C4: the DF-MP2 chain at its real size (nao 1024, nocc 256, nvir 768,
         # naux 4096): two half-transform batched GEMMs into B, then the fused
-        # pair energy (bf16x6); 1.63e14 algorithmic flop (i <= j pair count)
+        # pair energy (fp16x3); 1.63e14 algorithmic flop (i <= j pair count)
         nao, nocc, nvir, naux = 1024, 256, 768, 4096
         eri, Co, Cv, eo4, ev4 = df_mp2.chain_inputs(nao, nocc, nvir, naux, dev, seed=4)
         th = gpu_time_ms(lambda: df_mp2.half_transform(eri, Co, Cv), reps=3, warm=1)
         B4 = df_mp2.half_transform(eri, Co, Cv)
         del eri
-        te = gpu_time_ms(lambda: kernels.pair_energy_sym(B4, eo4, ev4, math="bf16x6"), reps=2, warm=1)
-        e4 = float(kernels.pair_energy_sym(B4, eo4, ev4, math="bf16x6"))
+        te = gpu_time_ms(lambda: kernels.pair_energy_sym(B4, eo4, ev4, math="fp16x3"), reps=2, warm=1)
+        e4 = float(kernels.pair_energy_sym(B4, eo4, ev4, math="fp16x3"))
         fl = df_mp2.chain_flops(nao, nocc, nvir, naux)
         tot = fl["half1"] + fl["half2"] + fl["energy"]
         t_all = th + te
@@ -268,9 +274,9 @@ def run_extras(dev, tb, only=None) -> dict:
             "half_transform_ms": th, "energy_ms": te, "chain_ms": t_all, "energy": e4,
             "flop": tot, "tflops": tot / t_all / 1e9,
             "half_transform_tflops": (fl["half1"] + fl["half2"]) / th / 1e9,
-            "energy_tflops_sym": fl["energy"] / te / 1e9, "energy_math": "bf16x6",
+            "energy_tflops_sym": fl["energy"] / te / 1e9, "energy_math": "fp16x3",
             "frac_fp32_peak": tot / t_all / 1e9 / PEAK_FP32_MFMA,
-            "energy_frac_bf16x6_ceiling": 6 * fl["energy"] / te / 1e9 / PEAK_BF16_MFMA,
+            "energy_frac_f16_peak": 3 * fl["energy"] / te / 1e9 / PEAK_BF16_MFMA,
             "parity": "tests/test_config4_gpu.py: rel <= 1e-6 against the fp64 chain on the device",
         }  # fmt: skip
         log("c4", out["df_mp2_chain_c4_1024_256_768_4096"])

@@ -197,6 +197,35 @@ int trnblas_hip_pair_energy_bf16x6(int64_t nvir, int64_t naux, const float* Bi, 
                                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * DF-MP2 pair energies as trnblas_hip_pair_energy_bf16x6 (same arguments,
+ * pair set, weights, outputs, determinism and row-count rules) with every
+ * fp32 product formed on f16 MFMA (v_mfma_f32_16x16x32_f16, fp32
+ * accumulation) from two fp16 pieces of each operand. Each row (o, a) is
+ * first scaled by 2^e(o, a) so its largest magnitude lies in [2^14, 2^15);
+ * then xs = x 2^e = hi + lo + r (hi = rn_f16(xs), lo = rn_f16(xs - hi),
+ * |r| <= 2^-22 |xs| + 2^-25) and
+ *   xs ys ~= hi_x hi_y + hi_x lo_y + lo_x hi_y,
+ * dropping lo_x lo_y (<= 2^-22 |xs ys|); T_ab = sum 2^-(e(i, a) + e(j, b)) is
+ * formed in fp64. Each T entry carries fp32 accumulation error plus about
+ * 3 2^-22 relative per product (fp32-class accuracy) at 3/16 of the MFMA time
+ * of an fp32 product. workspace must hold
+ * trnblas_hip_pair_energy_fp16x3_workspace(nvir, naux, npairs, ni, nj) bytes
+ * (the pieces plus one int32 exponent per row).
+ *
+ * Replaces the same reference interface as trnblas_hip_pair_energy
+ * (torch.ops.trnblas.pair_energy_sym, trnblas/nki/_native.py:221-239).
+ */
+size_t trnblas_hip_pair_energy_fp16x3_workspace(int64_t nvir, int64_t naux, int64_t npairs,
+                                                int64_t ni, int64_t nj);
+int trnblas_hip_pair_energy_fp16x3(int64_t nvir, int64_t naux, const float* Bi, int64_t ni,
+                                   int64_t ldi_occ, const float* Bj, int64_t nj,
+                                   int64_t ldj_occ, int64_t ld_vir, const float* eps_i,
+                                   const float* eps_j, const float* eps_vir, int64_t nocc,
+                                   int64_t npairs, const int32_t* pair_i, const int32_t* pair_j,
+                                   const double* pair_w, double* out_pairs, double* out_total,
+                                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * trnblas_hip_pair_energy without a workspace argument: same arguments
  * (minus workspace), pair set, weights, outputs, kernels and bits. It
  * allocates nothing: the fp64 partials live in a static device array of

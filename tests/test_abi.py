@@ -61,6 +61,17 @@ def test_argument_errors_are_reported_without_a_gpu():
     rc = lib.trnblas_hip_pair_energy_bf16x6(7, 33, 16, 2, 231, 16, 0, 231, 33, 16, 16, 16, 3,
                                             6, None, None, None, None, 16, 16, 4096, None)
     assert rc == _lib.E_ARG and b"ni >= nocc" in lib.trnblas_hip_last_error()
+    # fp16x3: 2 fp16 pieces per element, then one int32 exponent per
+    # (occupied, padded virtual) row, per operand
+    pieces2 = 96 * 672 * 2 * 2304 * 2
+    exps = -(-(96 * 672 * 4) // 256) * 256
+    assert lib.trnblas_hip_pair_energy_fp16x3_workspace(672, 2304, 4656, 96, 0) == part + pieces2 + exps
+    odd2 = -(-(5 * 8 * 2 * 64 * 2) // 256) * 256
+    exps2 = -(-(5 * 8 * 4) // 256) * 256
+    assert lib.trnblas_hip_pair_energy_fp16x3_workspace(7, 33, 3, 5, 5) == 256 + 2 * odd2 + 2 * exps2
+    rc = lib.trnblas_hip_pair_energy_fp16x3(7, 33, 16, 2, 231, 16, 0, 231, 33, 16, 16, 16, 3,
+                                            6, None, None, None, None, 16, 16, 4096, None)
+    assert rc == _lib.E_ARG and b"ni >= nocc" in lib.trnblas_hip_last_error()
 
 
 def test_syrk_and_triangle_argument_errors_without_a_gpu():

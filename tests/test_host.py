@@ -330,7 +330,7 @@ def test_pair_energy_math_selection(monkeypatch):
     from trnblas_amd.hip import kernels
 
     monkeypatch.delenv("TRNBLAS_PAIR_ENERGY_MATH", raising=False)
-    assert kernels.pair_energy_math() == "bf16x6"
+    assert kernels.pair_energy_math() == "fp16x3"
     monkeypatch.setenv("TRNBLAS_PAIR_ENERGY_MATH", "fp32")
     assert kernels.pair_energy_math() == "fp32"
     assert kernels._check_math(None) == "fp32"
@@ -339,3 +339,5 @@ def test_pair_energy_math_selection(monkeypatch):
     with pytest.raises(ValueError):
         kernels.pair_energy_math()
     assert kernels._PE_ENTRY["bf16x6"] == "trnblas_hip_pair_energy_bf16x6"
+    assert kernels._PE_ENTRY["fp16x3"] == "trnblas_hip_pair_energy_fp16x3"
+    assert kernels._check_math("fp16x3") == "fp16x3"

@@ -10,7 +10,7 @@ from oracle import pair_energy as pe
 
 pytestmark = pytest.mark.gpu
 
-MATHS = ["fp32", "bf16x6"]
+MATHS = ["fp32", "bf16x6", "fp16x3"]
 
 
 def _inputs(nocc, nvir, naux, seed):
@@ -93,12 +93,14 @@ def test_pair_energies_two_operands(dev, math):
     assert torch.allclose(got, want, rtol=1e-6, atol=0)
 
 
-@pytest.mark.parametrize("math", MATHS)
-def test_pair_energy_full_significands(dev, math):
+@pytest.mark.parametrize("math,tol", [("fp32", 2.0**-21), ("bf16x6", 2.0**-21), ("fp16x3", 2.0**-19)])
+def test_pair_energy_full_significands(dev, math, tol):
     # naux = 1, nvir = 1: T = x y exactly, e = T^2 / D. Operands with all 24
     # significand bits set over a wide exponent range: an fp32-class product
-    # is within 2^-22 of x y; a split that lost its lo piece (2^-16) or its mid
-    # piece (2^-8) fails.
+    # is within 2^-22 of x y (bf16x6; a split that lost its lo piece (2^-16)
+    # or its mid piece (2^-8) fails). fp16x3 keeps 22 significand bits per
+    # operand and drops lo_x lo_y: x y within 3 2^-22, so e within 6 2^-22;
+    # without its lo piece it would be off by 2^-11.
     from trnblas_amd.hip import kernels
 
     g = torch.Generator().manual_seed(5)
@@ -116,14 +118,18 @@ def test_pair_energy_full_significands(dev, math):
     got = kernels.pair_energies(Bd, Bd, eo.to(dev), eo.to(dev), ev.to(dev), pi, pj, math=math).cpu()
     want = pe.pair_energies_f64(B, B, eo, eo, ev, pairs)
     rel = ((got - want).abs() / want.abs()).max().item()
-    assert rel <= 2.0**-21, rel
+    assert rel <= tol, rel
 
 
-def test_pair_energy_bf16x6_long_sums_unbiased(dev):
+@pytest.mark.parametrize("math,mean_tol", [("bf16x6", 5e-8), ("fp16x3", 1e-7)])
+def test_pair_energy_split_long_sums_unbiased(dev, math, mean_tol):
     # nvir = 1, naux = 2304, pairs (i, i): T = sum_k x_k^2 > 0 and e = T^2 / D.
     # The recovered T must carry no systematic error: summed slice by slice
     # with fp32 adds its mean relative error is ~1e-10 (std ~1e-7); a long
     # sum chained through the MFMA accumulator comes out ~1.5e-6 low.
+    # fp16x3 drops lo_x lo_y, which for x = y is positive: x^2 comes out low
+    # by lo^2 / x^2, about 2^-22 / 3 times the mean of 1 / m^2 over the
+    # significands m in [1, 2), i.e. ~4e-8.
     from trnblas_amd.hip import kernels
 
     g = torch.Generator().manual_seed(0)
@@ -132,13 +138,13 @@ def test_pair_energy_bf16x6_long_sums_unbiased(dev):
     eo, ev = -torch.ones(n), torch.tensor([0.5])
     idx = torch.arange(n)
     e = kernels.pair_energies(
-        B.to(dev), B.to(dev), eo.to(dev), eo.to(dev), ev.to(dev), idx, idx, math="bf16x6"
+        B.to(dev), B.to(dev), eo.to(dev), eo.to(dev), ev.to(dev), idx, idx, math=math
     ).cpu()
     T = (e * -3.0).sqrt()
     Bd = B.double()[:, 0, :]
     T64 = (Bd * Bd).sum(dim=1)
     rel = (T - T64) / T64
-    assert abs(float(rel.mean())) <= 5e-8, float(rel.mean())
+    assert abs(float(rel.mean())) <= mean_tol, float(rel.mean())
     assert float(rel.abs().max()) <= 2e-6
 
 
@@ -167,8 +173,9 @@ def test_pair_energy_config3_shape_subset(dev, seed, math):
     assert abs(got - want) <= 1e-6 * abs(want), (got, want)
 
 
+@pytest.mark.parametrize("math", ["bf16x6", "fp16x3"])
 @pytest.mark.parametrize("nocc,nvir,naux", [(5, 97, 130), (8, 200, 64), (1, 33, 40)])
-def test_pair_energy_bf16x6_implicit_walk_per_pair(dev, nocc, nvir, naux):
+def test_pair_energy_split_implicit_walk_per_pair(dev, nocc, nvir, naux, math):
     # the implicit walk runs two pairs (i, j), (i, j + 1) per workgroup; its
     # per-pair energies (out_pairs, row-major i <= j) must match the
     # explicit-pair kernel's, pair by pair (odd rows leave a single pair)
@@ -180,13 +187,38 @@ def test_pair_energy_bf16x6_implicit_walk_per_pair(dev, nocc, nvir, naux):
     got = torch.empty(npairs, dtype=torch.float64, device=dev)
     tot = torch.empty((), dtype=torch.float64, device=dev)
     kernels._pe_launch(
-        "bf16x6", dev, nvir, naux, B, nocc, B.stride(0), B, 0, B.stride(0), B.stride(1),
+        math, dev, nvir, naux, B, nocc, B.stride(0), B, 0, B.stride(0), B.stride(1),
         eo, eo, ev, nocc, npairs, None, None, got, tot,
     )  # fmt: skip
     ii, jj = np.triu_indices(nocc)
-    want = kernels.pair_energies(B, B, eo, eo, ev, torch.from_numpy(ii), torch.from_numpy(jj), math="bf16x6")
+    want = kernels.pair_energies(B, B, eo, eo, ev, torch.from_numpy(ii), torch.from_numpy(jj), math=math)
     torch.cuda.synchronize()
     scale = float(want.abs().max()) + 1e-300
     assert float((got - want).abs().max()) <= 1e-12 * scale
     w = torch.where(torch.from_numpy(ii == jj).to(dev), 1.0, 2.0).double()
     assert abs(float(tot) - float((w * want).sum())) <= 1e-12 * abs(float(tot))
+
+
+@pytest.mark.parametrize("math", MATHS)
+def test_pair_energy_wide_dynamic_range(dev, math):
+    # Rows whose scales span e^-8 .. e^8 and elements spanning e^-6 .. e^6
+    # within a row, plus an all-zero row and a row of one nonzero element:
+    # fp16x3's per-row power-of-two scaling must keep every row in fp16's
+    # range (small elements fall into its subnormals), bf16x6 has fp32's
+    # exponent range. Relative 1e-6 against the fp64 closed form.
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(11)
+    nocc, nvir, naux = 4, 150, 200
+    row = torch.exp(4.0 * torch.randn(nocc, nvir, 1, generator=g, dtype=torch.float64))
+    elem = torch.exp(2.0 * torch.randn(nocc, nvir, naux, generator=g, dtype=torch.float64))
+    B = 0.05 * row * elem * torch.randn(nocc, nvir, naux, generator=g, dtype=torch.float64)
+    B[1, 7] = 0.0
+    B[2, 9] = 0.0
+    B[2, 9, 17] = 3.0
+    B = B.float()
+    eo = -0.3 - 1.2 * torch.rand(nocc, generator=g, dtype=torch.float64)
+    ev = 0.1 + 2.9 * torch.rand(nvir, generator=g, dtype=torch.float64)
+    got = float(kernels.pair_energy_sym(B.to(dev), eo.float().to(dev), ev.float().to(dev), math=math))
+    want = pe.pair_energy_f64(B, eo.float(), ev.float())
+    assert abs(got - want) <= 1e-6 * abs(want), (got, want)

@@ -38,8 +38,11 @@ constexpr uint32_t kPeOob = 0x80000000u;
 struct PairArgs {
   int nvir, naux;
   const float* Bi;  // fp32 operands (fp32 kernel)
-  const uint16_t* Pi;  // bf16x6 kernel: bf16 pieces of Bi / Bj (split_planes_kernel)
+  const uint16_t* Pi;  // bf16x6 / fp16x3 kernels: pieces of Bi / Bj (split kernels)
   const uint16_t* Pj;
+  const int32_t* Ei;   // fp16x3: row exponents of Bi / Bj, (occupied row, a) at o * ldE + a
+  const int32_t* Ej;
+  int ldE;
   int ldv;             // piece row length (naux rounded up to 32)
   int rows_i, rows_j;  // occupied rows of Pi / Pj (pair indices beyond give NaN)
   int64_t ldi_occ;
@@ -369,6 +372,104 @@ __device__ __forceinline__ void split_bf16x3(const f32x4& x, i32x2& hi, i32x2& m
   lo = i32x2{(int)l0, (int)l1};
 }
 
+// ── fp16x3: fp32 products from two fp16 pieces on f16 MFMA ──────────────────
+//
+// Each row (o, a) of an operand is scaled by 2^e(o, a) so its largest
+// magnitude lies in [2^14, 2^15); then xs = x 2^e = hi + lo + r with
+// hi = rn_f16(xs), lo = rn_f16(xs - hi) (xs - hi is exact in fp32) and
+// |r| <= 2^-22 |xs| + 2^-25, and
+//   xs ys ~= hi_x hi_y + hi_x lo_y + lo_x hi_y,
+// dropping lo_x lo_y (<= 2^-22 |xs ys|): the two-piece split of Ootomo and
+// Yokota (SGEMM emulation on fp16 tensor cores, 2022) with the scale taken
+// per row instead of the lo piece, so no separate correction accumulator is
+// needed. The row scale keeps every element above the row maximum times
+// 2^-17 inside fp16's normal range; the smaller ones keep an absolute error
+// below 2^-39 of the row maximum. Each fp16 product is exact in fp32, and the
+// kernels sum a slice's products on the MFMA and the slices in fp32 as for
+// bf16x6. T_ab = acc 2^-(e(i, a) + e(j, b)) is formed in fp64. Three products
+// instead of six halve the MFMA work, and two pieces move two thirds of the
+// operand bytes.
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// Arithmetic of the split kernels: NPC pieces per element, the products
+// (piece of A, piece of B) smallest first, and the MFMA on 16-byte fragments.
+template <int NPC>
+struct PeMath;
+template <>
+struct PeMath<3> {  // bf16x6
+  static constexpr int NPROD = 6;
+  static constexpr int ka[6] = {2, 1, 0, 1, 0, 0}, kb[6] = {0, 1, 2, 0, 1, 0};
+  static __device__ __forceinline__ f32x4 mma(i32x4 a, i32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct PeMath<2> {  // fp16x3
+  static constexpr int NPROD = 3;
+  static constexpr int ka[3] = {1, 0, 0}, kb[3] = {0, 1, 0};
+  static __device__ __forceinline__ f32x4 mma(i32x4 a, i32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+// Scale of T_ab from the row exponents (1 for bf16x6, which is unscaled).
+template <int NPC>
+__device__ __forceinline__ double pe_scale(const PairArgs& g, const int32_t* Ea, int oa, int a,
+                                           const int32_t* Eb, int ob, int b) {
+  if constexpr (NPC == 2)
+    return ldexp(1.0, -(Ea[(int64_t)oa * g.ldE + a] + Eb[(int64_t)ob * g.ldE + b]));
+  else
+    return 1.0;
+}
+
+// Row exponents of the fp16x3 split: e(o, a) = 15 - E for the row's largest
+// magnitude m = f 2^E, f in [0.5, 1), so m 2^e lies in [2^14, 2^15); 0 for
+// zero or non-finite rows and for the padding row (a = nvir) of an odd nvir.
+// One wave per row (o, a) of the padded 2 ceil(nvir / 2) rows per occupied
+// index, at E[o * nv2 + a].
+__global__ __launch_bounds__(256) void row_exp_kernel(int nvir, int naux, int nrows,
+                                                      const float* X, int64_t ld_occ,
+                                                      int64_t ld_vir, int32_t* E) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= nrows) return;
+  const int nv2 = (nvir + 1) & ~1, o = row / nv2, a = row - o * nv2;
+  float m = 0.0f;
+  if (a < nvir) {
+    const float* src = X + (int64_t)o * ld_occ + (int64_t)a * ld_vir;
+    for (int k = lane; k < naux; k += 64) m = fmaxf(m, fabsf(src[k]));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if (lane == 0) {
+    int e = 0;
+    if (m > 0.0f && m <= 3.402823466e38f) {
+      int ex;
+      frexpf(m, &ex);
+      e = 15 - ex;
+    }
+    E[row] = e;
+  }
+}
+
+__device__ __forceinline__ void split_f16x2(const f32x4& x, int e, i32x2& hi, i32x2& lo) {
+  _Float16 h[4], l[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const float xs = ldexpf(x[u], e);
+    h[u] = (_Float16)xs;
+    l[u] = (_Float16)(xs - (float)h[u]);
+  }
+  auto pk = [](_Float16 a, _Float16 b) {
+    return (int)((uint32_t)__builtin_bit_cast(uint16_t, a) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16));
+  };
+  hi = i32x2{pk(h[0], h[1]), pk(h[2], h[3])};
+  lo = i32x2{pk(l[0], l[1]), pk(l[2], l[3])};
+}
+
 constexpr int kX3S = 96, kX3BK = 32;
 
 // LDS slot of 16-byte group `grp` of panel row `r` (rows of 64 bytes): the
@@ -377,21 +478,23 @@ constexpr int kX3S = 96, kX3BK = 32;
 // conflict free without padding.
 __device__ __forceinline__ int x3_slot(int r, int grp) { return grp ^ (((r >> 1) ^ (r >> 2)) & 3); }
 
-// fp32 operand X (n, nvir, naux), strides (ld_occ, ld_vir, 1), as its three
-// bf16 pieces p (0 hi, 1 mid, 2 lo) in 32-wide k slices s, rows taken in
-// pairs: element (o, a, p, k), a = 2 m + d, k = 32 s + c, at
-//   ((((o * nvp + m) * nk + s) * 3 + p) * 2 + d) * 32 + c,   nvp = ceil(nvir / 2),
+// fp32 operand X (n, nvir, naux), strides (ld_occ, ld_vir, 1), as its NPC
+// pieces p (bf16x6: 0 hi, 1 mid, 2 lo; fp16x3: 0 hi, 1 lo of the row-scaled
+// value, exponents E from row_exp_kernel) in 32-wide k slices s, rows taken
+// in pairs: element (o, a, p, k), a = 2 m + d, k = 32 s + c, at
+//   ((((o * nvp + m) * nk + s) * NPC + p) * 2 + d) * 32 + c,   nvp = ceil(nvir / 2),
 // nk = ldv / 32. The 64 bytes of one row's slice of one piece share a
-// 128-byte line with the other row of its pair, and the three pieces of a
-// row pair's slice are 384 contiguous bytes, so a wave's 16-row load reads
+// 128-byte line with the other row of its pair, and the pieces of a row
+// pair's slice are NPC x 128 contiguous bytes, so a wave's 16-row load reads
 // 8 whole lines (half lines would cost the address path twice as much).
 // Columns [naux, ldv) are zero, and so is the second row of the last pair
 // of an odd nvir. One thread per 8 consecutive k of a row (rows of the
 // padded 2 ceil(nvir / 2)); `total` = n * 2 ceil(nvir / 2) * ldv / 8 threads.
-template <bool VEC>
+template <int NPC, bool VEC>
 __global__ __launch_bounds__(256) void split_planes_kernel(int nvir, int naux, int ldv, int total,
                                                           const float* X, int64_t ld_occ,
-                                                          int64_t ld_vir, uint16_t* P) {
+                                                          int64_t ld_vir, const int32_t* E,
+                                                          uint16_t* P) {
   const int idx = blockIdx.x * 256 + threadIdx.x;
   if (idx >= total) return;
   const int gpr = ldv >> 3, nv2 = (nvir + 1) & ~1;
@@ -411,15 +514,24 @@ __global__ __launch_bounds__(256) void split_planes_kernel(int nvir, int naux, i
       x1[e] = k0 + 4 + e < naux ? src[4 + e] : 0.0f;
     }
   }
-  i32x2 h0, m0, l0, h1, m1, l1;
-  split_bf16x3(x0, h0, m0, l0);
-  split_bf16x3(x1, h1, m1, l1);
   const int nvp = (nvir + 1) >> 1, nk = ldv >> 5;
-  uint16_t* dst = P + ((((int64_t)o * nvp + (a >> 1)) * nk + (k0 >> 5)) * 3 * 2 + (a & 1)) * 32 +
+  uint16_t* dst = P + ((((int64_t)o * nvp + (a >> 1)) * nk + (k0 >> 5)) * NPC * 2 + (a & 1)) * 32 +
                   (k0 & 31);
-  *reinterpret_cast<i32x4*>(dst) = i32x4{h0[0], h0[1], h1[0], h1[1]};
-  *reinterpret_cast<i32x4*>(dst + 64) = i32x4{m0[0], m0[1], m1[0], m1[1]};
-  *reinterpret_cast<i32x4*>(dst + 128) = i32x4{l0[0], l0[1], l1[0], l1[1]};
+  if constexpr (NPC == 3) {
+    i32x2 h0, m0, l0, h1, m1, l1;
+    split_bf16x3(x0, h0, m0, l0);
+    split_bf16x3(x1, h1, m1, l1);
+    *reinterpret_cast<i32x4*>(dst) = i32x4{h0[0], h0[1], h1[0], h1[1]};
+    *reinterpret_cast<i32x4*>(dst + 64) = i32x4{m0[0], m0[1], m1[0], m1[1]};
+    *reinterpret_cast<i32x4*>(dst + 128) = i32x4{l0[0], l0[1], l1[0], l1[1]};
+  } else {
+    const int e = E[row];
+    i32x2 h0, l0, h1, l1;
+    split_f16x2(x0, e, h0, l0);
+    split_f16x2(x1, e, h1, l1);
+    *reinterpret_cast<i32x4*>(dst) = i32x4{h0[0], h0[1], h1[0], h1[1]};
+    *reinterpret_cast<i32x4*>(dst + 64) = i32x4{l0[0], l0[1], l1[0], l1[1]};
+  }
 }
 
 // Work item = (pair, virtual tile pair A <= B) as in pair_energy_kernel, 96 x 96
@@ -428,18 +540,22 @@ __global__ __launch_bounds__(256) void split_planes_kernel(int nvir, int naux, i
 // pipeline: X = B_i[A] B_j[B]^T, then X' = B_j[A] B_i[B]^T (both held in
 // registers); diagonal items run the first pass only (B = A). The operands
 // come pre-split (split_planes_kernel), so a k-step spends no VALU on the
-// split. A stage is one 32-wide k slice of the 3 pieces x 2 panels of the
-// running pass (36 KiB); LDS holds two stages (72 KiB, two workgroups per
-// CU) and two register sets hold the next two slices in flight: slice t is
-// multiplied from LDS while slices t + 1 and t + 2 load, and slice t + 1
-// goes to LDS at the end of step t. The MFMA partial of each block spans two
-// slices (12 products) before it joins the running sum by an fp32 add.
+// split. A stage is one 32-wide k slice of the NPC pieces x 2 panels of the
+// running pass (36 KiB for bf16x6, 24 KiB for fp16x3); LDS holds two stages
+// (the epilogue's 72 KiB, two workgroups per CU) and two register sets hold
+// the next two slices in flight: slice t is multiplied from LDS while slices
+// t + 1 and t + 2 load, and slice t + 1 goes to LDS at the end of step t.
+// The MFMA partial of each block spans two slices (2 NPROD products) before
+// it joins the running sum by an fp32 add.
+template <int NPC>
 __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
+  using M = PeMath<NPC>;
   constexpr int S = kX3S, BK = kX3BK;
-  constexpr int STAGE = 6 * S * BK;  // bf16 elements: 3 pieces x 2 panels
-  static_assert(STAGE * 2 == 36 * 1024 && S == 96 && BK == 32, "9 KiB per wave per stage");
-  static_assert(2 * STAGE * 2 >= 2 * S * S * 4, "epilogue fits in the stage buffers");
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+  constexpr int STAGE = 2 * NPC * S * BK;  // 16-bit elements: NPC pieces x 2 panels
+  constexpr int NU = NPC * 3;              // 1 KiB loads per wave per stage
+  static_assert(STAGE * 2 == NPC * 12 * 1024 && S == 96 && BK == 32, "3 KiB per piece per wave");
+  constexpr int LDS_ELEMS = 2 * STAGE > 2 * S * S * 2 ? 2 * STAGE : 2 * S * S * 2;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];  // stages / epilogue
   __shared__ double red[4];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -456,7 +572,7 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
   const bool diag = TA == TB;
   const int a0 = TA * S, b0 = TB * S;
   const int nvir = g.nvir, ldv = g.ldv;
-  const int64_t ostride = (int64_t)((nvir + 1) >> 1) * 6 * ldv;  // pieces of one occupied row
+  const int64_t ostride = (int64_t)((nvir + 1) >> 1) * 2 * NPC * ldv;  // one occupied row
   const uint16_t* Xi = g.Pi + i * ostride;
   const uint16_t* Xj = g.Pj + j * ostride;
   const int nk = ldv / BK;  // even: ldv is a multiple of 2 BK
@@ -464,47 +580,48 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
 
   // LDS stage layout [side][piece][row][BK], side 0 the A side (rows a0:
   // B_i in pass 0, B_j in pass 1), side 1 the B side (rows b0: B_j, then
-  // B_i). Waves 2 s and 2 s + 1 fill side s, 18 row blocks of 16 rows x 64
+  // B_i). Waves 2 s and 2 s + 1 fill side s, 6 NPC row blocks of 16 rows x 64
   // bytes (one 16-byte load per lane each), block e = piece * 6 + blk at
   // stage offset e KiB; wave h = w >> 1 of the side takes e = h + 2 u. Lane
   // l carries LDS slot l % 4 of row 16 blk + l / 4, i.e. the global 16-byte
   // group x3_slot(row, l % 4), and stores it lane-linearly; lanes 8 v ..
   // 8 v + 7 read one 128-byte line (a row pair of split_planes_kernel's
   // layout). The lane's byte offset from the panel's first row pair is
-  // fixed; the slice offset (384 bytes per slice) goes into soffset and the
+  // fixed; the slice offset (NPC x 128 bytes per slice) goes into soffset and the
   // panel (operand, rows) into the buffer resource, one per pass. Rows past
   // nvir read as zeros.
   const int side = w & 1, h = w >> 1;
   const int rbase = side ? b0 : a0;
   const int lr = lane >> 2;
-  uint32_t voff[9];
+  uint32_t voff[NU];
 #pragma unroll
-  for (int u = 0; u < 9; ++u) {
+  for (int u = 0; u < NU; ++u) {
     const int e = h + 2 * u, pc = e / 6, r = 16 * (e - 6 * pc) + lr;
-    voff[u] = r < nvir - rbase ? (uint32_t)(((r >> 1) * nk * 192 + pc * 64 + (r & 1) * 32 +
+    voff[u] = r < nvir - rbase ? (uint32_t)(((r >> 1) * nk * (NPC * 64) + pc * 64 + (r & 1) * 32 +
                                              8 * x3_slot(r, lane & 3)) *
                                             2)
                                : kPeOob;
   }
-  const int64_t prow = (int64_t)(rbase >> 1) * nk * 192;  // rbase is even
+  const int64_t prow = (int64_t)(rbase >> 1) * nk * (NPC * 64);  // rbase is even
   const __amdgpu_buffer_rsrc_t rs0 = pe_rsrc((side ? Xj : Xi) + prow);
   const __amdgpu_buffer_rsrc_t rs1 = pe_rsrc((side ? Xi : Xj) + prow);
   // Past the last slice the loads still issue (every step issues the same
-  // 9, which keeps the compiler's wait counts exact), re-reading the last
+  // NU, which keeps the compiler's wait counts exact), re-reading the last
   // slice (L2-resident); their data is never stored.
-  i32x4 stg[2][9];  // slice t in set t & 1 between its load and its store
-  auto load = [&](int t, i32x4(&set)[9]) {
+  i32x4 stg[2][NU];  // slice t in set t & 1 between its load and its store
+  auto load = [&](int t, i32x4(&set)[NU]) {
     if (t >= nsteps) t = nsteps - 1;
     const bool pass1 = t >= nk;
     const int sl = pass1 ? t - nk : t;
     const __amdgpu_buffer_rsrc_t rs = pass1 ? rs1 : rs0;
 #pragma unroll
-    for (int u = 0; u < 9; ++u) set[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[u], sl * 384, 0);
+    for (int u = 0; u < NU; ++u)
+      set[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[u], sl * NPC * 128, 0);
   };
-  auto store = [&](const i32x4(&set)[9], int buf) {
+  auto store = [&](const i32x4(&set)[NU], int buf) {
     uint16_t* dst = lds + buf * STAGE + side * (STAGE / 2) + h * 512 + lane * 8;
 #pragma unroll
-    for (int u = 0; u < 9; ++u) *reinterpret_cast<i32x4*>(dst + u * 1024) = set[u];
+    for (int u = 0; u < NU; ++u) *reinterpret_cast<i32x4*>(dst + u * 1024) = set[u];
   };
 
   // The fragment row of a lane is row0 + 16 blk + (lane & 15) with row0 a
@@ -520,7 +637,7 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
   // Step t (global over both passes; P = t & 1 is static): slice t is in LDS
   // buffer P (the barrier publishes it and retires every read of buffer
   // 1 - P), set P is free (its slice t went to LDS in step t - 1) and takes
-  // slice t + 2, slice t is multiplied (the six products of each block,
+  // slice t + 2, slice t is multiplied (the NPROD products of each block,
   // smallest first, into its partial, started at zero when FIRST), then set
   // 1 - P (slice t + 1) goes to buffer 1 - P.
   auto step = [&](auto P_, auto FIRST_, int t) {
@@ -530,29 +647,27 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
     load(t + 2, stg[P]);
     const uint16_t* buf = lds + P * STAGE;
     auto frag = [&](int pc, int sd, int r) {
-      return *reinterpret_cast<const bf16x8*>(buf + ((sd * 3 + pc) * S + r) * BK + fslot);
+      return *reinterpret_cast<const i32x4*>(buf + ((sd * NPC + pc) * S + r) * BK + fslot);
     };
-    bf16x8 fa[3][3];
+    i32x4 fa[3][NPC];
 #pragma unroll
     for (int rb = 0; rb < 3; ++rb)
 #pragma unroll
-      for (int pc = 0; pc < 3; ++pc) fa[rb][pc] = frag(pc, 0, ar0 + 16 * rb + (lane & 15));
+      for (int pc = 0; pc < NPC; ++pc) fa[rb][pc] = frag(pc, 0, ar0 + 16 * rb + (lane & 15));
 #pragma unroll
     for (int cb = 0; cb < 3; ++cb) {
-      bf16x8 fb[3];
+      i32x4 fb[NPC];
 #pragma unroll
-      for (int pc = 0; pc < 3; ++pc) fb[pc] = frag(pc, 1, br0 + 16 * cb + (lane & 15));
+      for (int pc = 0; pc < NPC; ++pc) fb[pc] = frag(pc, 1, br0 + 16 * cb + (lane & 15));
 #pragma unroll
       for (int rb = 0; rb < 3; ++rb)
-        part[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            fa[rb][2], fb[0], FIRST ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb], 0, 0, 0);
+        part[rb][cb] = M::mma(fa[rb][M::ka[0]], fb[M::kb[0]],
+                              FIRST ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb]);
 #pragma unroll
-      for (int e = 1; e < 6; ++e) {
-        constexpr int ka[6] = {2, 1, 0, 1, 0, 0}, kb[6] = {0, 1, 2, 0, 1, 0};
+      for (int e = 1; e < M::NPROD; ++e) {
 #pragma unroll
         for (int rb = 0; rb < 3; ++rb)
-          part[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[rb][ka[e]], fb[kb[e]],
-                                                                 part[rb][cb], 0, 0, 0);
+          part[rb][cb] = M::mma(fa[rb][M::ka[e]], fb[M::kb[e]], part[rb][cb]);
       }
     }
     if (t + 1 < nsteps) store(stg[1 - P], 1 - P);
@@ -607,8 +722,11 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
   for (int e = 0; e < S * S / 256; ++e) {
     const int idx = tid + 256 * e, a = idx / S, b = idx - a * S;
     if (a0 + a < nvir && b0 + b < nvir) {
-      const double x = xs[a * ldx + b];
-      const double xp = diag ? xs[b * ldx + a] : xs[S * S + a * S + b];
+      // X = B_i[A] B_j[B]^T, X' = B_j[A] B_i[B]^T (diagonal: X' = X^T)
+      const double x = xs[a * ldx + b] * pe_scale<NPC>(g, g.Ei, i, a0 + a, g.Ej, j, b0 + b);
+      const double xp = diag ? xs[b * ldx + a] * pe_scale<NPC>(g, g.Ei, i, a0 + b, g.Ej, j, a0 + a)
+                             : xs[S * S + a * S + b] *
+                                   pe_scale<NPC>(g, g.Ej, j, a0 + a, g.Ei, i, b0 + b);
       const double d = eo - (double)g.eps_vir[a0 + a] - (double)g.eps_vir[b0 + b];
       sum += (diag ? x * (2.0 * x - xp) : 2.0 * (x * x + xp * xp - x * xp)) / d;
     }
@@ -646,7 +764,7 @@ __device__ __forceinline__ void couple_of(int c, int n, int& i, int& j0) {
 
 // The implicit walk two pairs at a time: work item = (couple (i, j0, j1),
 // tile pair A <= B). Both pairs share B_i, so a k-step stages three 96-row
-// panels (54 KiB) for two 96 x 96 outputs where two single-pair workgroups
+// panels (54 KiB bf16x6, 36 KiB fp16x3) for two 96 x 96 outputs where two single-pair workgroups
 // stage four: a quarter fewer operand bytes per product, which is what bounds
 // pair_energy_x3_kernel. 8 waves, one workgroup per CU: waves 4 g .. 4 g + 3
 // compute pair g of the couple, each the 48 x 48 quadrant (w & 1, w >> 1) as
@@ -654,15 +772,18 @@ __device__ __forceinline__ void couple_of(int c, int n, int& i, int& j0) {
 // partials and two-deep register pipeline. Stage slots: 0 = the shared panel
 // (B_i[A] in pass 0, B_i[B] in pass 1), 1 + g = pair g's (B_jg[B], then
 // B_jg[A]); a single-pair couple runs pair 0 twice and drops the copy.
+template <int NPC>
 __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
+  using M = PeMath<NPC>;
   constexpr int S = kX3S, BK = kX3BK;
-  constexpr int SLOT = 3 * S * BK;  // bf16 elements of one panel slice, 3 pieces (9216)
+  constexpr int SLOT = NPC * S * BK;  // 16-bit elements of one panel slice, NPC pieces
   constexpr int STAGE = 3 * SLOT;
-  constexpr int NQ = STAGE * 2 / 1024;  // 1 KiB load instructions per stage (54)
-  constexpr int NL = (NQ + 7) / 8;      // per wave (7; the 2 spare ones re-load, unstored)
-  static_assert(NQ == 54 && S == 96 && BK == 32, "stage split");
-  static_assert(2 * STAGE * 2 >= 2 * S * (S + 1) * 4, "diagonal epilogue fits");
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
+  constexpr int NQ = STAGE * 2 / 1024;  // 1 KiB load instructions per stage (18 NPC)
+  constexpr int NL = (NQ + 7) / 8;      // per wave (the spare ones re-load, unstored)
+  constexpr int BPS = NPC * 6;          // load blocks per slot
+  static_assert(NQ == 18 * NPC && S == 96 && BK == 32, "stage split");
+  constexpr int LDS_ELEMS = 2 * STAGE > S * (S + 1) * 4 ? 2 * STAGE : S * (S + 1) * 4;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];  // stages / diagonal epilogue
   __shared__ double red[8];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -681,9 +802,9 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
   const int nvir = g.nvir, ldv = g.ldv;
   const int nk = ldv / BK;  // even
   const int nsteps = diag ? nk : 2 * nk;
-  const int64_t ostride = (int64_t)((nvir + 1) >> 1) * 6 * ldv;
+  const int64_t ostride = (int64_t)((nvir + 1) >> 1) * 2 * NPC * ldv;
 
-  // Load instruction qq = slot * 18 + piece * 6 + blk (rows 16 blk ..
+  // Load instruction qq = slot * 6 NPC + piece * 6 + blk (rows 16 blk ..
   // 16 blk + 15 of that slot's panel) fills stage offset qq KiB; wave w
   // issues qq = w + 8 u. The lane offsets are those of pair_energy_x3_kernel
   // (row-pair layout, one 128-byte line per 8 lanes) and do not depend on
@@ -694,13 +815,15 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
 #pragma unroll
   for (int u = 0; u < NL; ++u) {
     const int qq = w + 8 * u < NQ ? w + 8 * u : w + 8 * u - 8;
-    const int e = qq % 18, pc = e / 6, r = 16 * (e - 6 * pc) + lr;
-    voff[u] = (uint32_t)(((r >> 1) * nk * 192 + pc * 64 + (r & 1) * 32 + 8 * x3_slot(r, lane & 3)) * 2);
+    const int e = qq % BPS, pc = e / 6, r = 16 * (e - 6 * pc) + lr;
+    voff[u] = (uint32_t)(((r >> 1) * nk * (NPC * 64) + pc * 64 + (r & 1) * 32 +
+                          8 * x3_slot(r, lane & 3)) * 2);
   }
   // Panel (slot sl, pass ps): operand rows from rbase; its resource spans the
   // valid row pairs only. Wave-uniform scalars, computed per load.
   const int pairsA = min((nvir - a0 + 1) >> 1, S / 2), pairsB = min((nvir - b0 + 1) >> 1, S / 2);
-  const int64_t rowA = (int64_t)(a0 >> 1) * nk * 192, rowB = (int64_t)(b0 >> 1) * nk * 192;
+  const int64_t rowA = (int64_t)(a0 >> 1) * nk * (NPC * 64),
+                rowB = (int64_t)(b0 >> 1) * nk * (NPC * 64);
   i32x4 stg[2][NL];
   auto load = [&](int t, i32x4(&set)[NL]) __attribute__((always_inline)) {
     if (t >= nsteps) t = nsteps - 1;  // keeps every step at NL loads (exact wait counts)
@@ -708,16 +831,16 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
 #pragma unroll
     for (int u = 0; u < NL; ++u) {
       const int qq = w + 8 * u < NQ ? w + 8 * u : w + 8 * u - 8;
-      const int sl = qq / 18;
+      const int sl = qq / BPS;
       const bool onA = (sl == 0) == (ps == 0);  // the panel's rows are the A tile's
       // operand row i, j0 or j1 by arithmetic (a select chain becomes a table in memory)
       const int o = i + (sl > 0) * (j0 - i) + (sl > 1) * (j1 - j0);
       const uint16_t* base = g.Pi + o * ostride + (onA ? rowA : rowB);
       const uint32_t v = voff[u];
-      const int soff = sl0 * 384;
+      const int soff = sl0 * NPC * 128;
       set[u] = __builtin_amdgcn_raw_buffer_load_b128(
           __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0,
-                                            (onA ? pairsA : pairsB) * nk * 384, 0x00020000),
+                                            (onA ? pairsA : pairsB) * nk * NPC * 128, 0x00020000),
           v, soff, 0);
     }
   };
@@ -745,18 +868,17 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
     const uint16_t* bufA = lds + P * STAGE + (ps ? 1 + gp : 0) * SLOT;
     const uint16_t* bufB = lds + P * STAGE + (ps ? 0 : 1 + gp) * SLOT;
     auto frag = [&](const uint16_t* b, int pc, int r) __attribute__((always_inline)) {
-      return *reinterpret_cast<const bf16x8*>(b + (pc * S + r) * BK + fslot);
+      return *reinterpret_cast<const i32x4*>(b + (pc * S + r) * BK + fslot);
     };
-    constexpr int ka[6] = {2, 1, 0, 1, 0, 0}, kb[6] = {0, 1, 2, 0, 1, 0};
-    bf16x8 fa[3][3];
-    // Blocks (rb, cb) in the order cb-major; before a block's six MFMAs
+    i32x4 fa[3][NPC];
+    // Blocks (rb, cb) in the order cb-major; before a block's NPROD MFMAs
     // the fragments the next block adds (A rows of rb + 1 in column block
     // 0, B columns of cb + 1 at rb = 2) are read, and scheduling barriers
     // keep that order: the LDS reads of a step are spread over its MFMAs
     // instead of all preceding them (C3: 55.5 against 56.4 ms).
-    bf16x8 fb[3][3];
+    i32x4 fb[3][NPC];
 #pragma unroll
-    for (int pc = 0; pc < 3; ++pc) {
+    for (int pc = 0; pc < NPC; ++pc) {
       fb[0][pc] = frag(bufB, pc, br0 + (lane & 15));
       fa[0][pc] = frag(bufA, pc, ar0 + (lane & 15));
     }
@@ -766,20 +888,19 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
       for (int rb = 0; rb < 3; ++rb) {
         if (cb == 0 && rb < 2) {
 #pragma unroll
-          for (int pc = 0; pc < 3; ++pc)
+          for (int pc = 0; pc < NPC; ++pc)
             fa[rb + 1][pc] = frag(bufA, pc, ar0 + 16 * (rb + 1) + (lane & 15));
         } else if (rb == 2 && cb < 2) {
 #pragma unroll
-          for (int pc = 0; pc < 3; ++pc)
+          for (int pc = 0; pc < NPC; ++pc)
             fb[cb + 1][pc] = frag(bufB, pc, br0 + 16 * (cb + 1) + (lane & 15));
         }
         __builtin_amdgcn_sched_barrier(0);
-        part[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            fa[rb][2], fb[cb][0], FIRST ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb], 0, 0, 0);
+        part[rb][cb] = M::mma(fa[rb][M::ka[0]], fb[cb][M::kb[0]],
+                              FIRST ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb]);
 #pragma unroll
-        for (int e = 1; e < 6; ++e)
-          part[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[rb][ka[e]], fb[cb][kb[e]],
-                                                                 part[rb][cb], 0, 0, 0);
+        for (int e = 1; e < M::NPROD; ++e)
+          part[rb][cb] = M::mma(fa[rb][M::ka[e]], fb[cb][M::kb[e]], part[rb][cb]);
         __builtin_amdgcn_sched_barrier(0);
       }
     if (t + 1 < nsteps) store(stg[1 - P], 1 - P);
@@ -823,7 +944,9 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
         for (int r = 0; r < 4; ++r) {
           const int a = a0 + ar0 + 16 * rb + 4 * (lane >> 4) + r;
           if (a < nvir && b < nvir) {
-            const double x = accX[rb][cb][r], xp = accP[rb][cb][r];
+            // X = B_i[A] B_jg[B]^T, X' = B_jg[A] B_i[B]^T
+            const double x = accX[rb][cb][r] * pe_scale<NPC>(g, g.Ei, i, a, g.Ei, jg, b);
+            const double xp = accP[rb][cb][r] * pe_scale<NPC>(g, g.Ei, jg, a, g.Ei, i, b);
             sum += 2.0 * (x * x + xp * xp - x * xp) / (eo - (double)g.eps_vir[a] - eb);
           }
         }
@@ -846,7 +969,8 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
     for (int e = 0; e < S * S / 256; ++e) {
       const int idx = lt + 256 * e, a = idx / S, b = idx - a * S;
       if (a0 + a < nvir && a0 + b < nvir) {
-        const double x = xs[a * (S + 1) + b], xt = xs[b * (S + 1) + a];
+        const double x = xs[a * (S + 1) + b] * pe_scale<NPC>(g, g.Ei, i, a0 + a, g.Ei, jg, a0 + b);
+        const double xt = xs[b * (S + 1) + a] * pe_scale<NPC>(g, g.Ei, i, a0 + b, g.Ei, jg, a0 + a);
         sum += x * (2.0 * x - xt) /
                (eo - (double)g.eps_vir[a0 + a] - (double)g.eps_vir[a0 + b]);
       }
@@ -921,43 +1045,76 @@ extern "C" size_t trnblas_hip_pair_energy_workspace(int64_t nvir, int64_t npairs
   return (size_t)(npairs * pe_nq(nvir) + npairs) * sizeof(double);
 }
 
-// bf16x6 workspace: the partials of the fp32 layout, then the bf16 pieces of
-// Bi (ni x ceil(nvir / 2) row pairs of 6 x ldv), then those of Bj (nj x
-// ceil(nvir / 2); none when nj == 0, where Bj shares Bi's pieces), each
-// region 256-byte aligned.
+// Split workspaces (bf16x6: NPC = 3; fp16x3: NPC = 2): the partials of the
+// fp32 layout, then the pieces of Bi (ni x ceil(nvir / 2) row pairs of
+// 2 NPC x ldv), then those of Bj (nj x ceil(nvir / 2); none when nj == 0,
+// where Bj shares Bi's pieces); fp16x3 adds the int32 row exponents of Bi
+// (ni x 2 ceil(nvir / 2)), then of Bj. Each region is 256-byte aligned.
 static int64_t x3_ldv(int64_t naux) { return (naux + 2 * kX3BK - 1) / (2 * kX3BK) * (2 * kX3BK); }
 static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
-static size_t x3_planes_bytes(int64_t n, int64_t nvir, int64_t naux) {
-  return al256((size_t)(6 * n * ((nvir + 1) / 2) * x3_ldv(naux)) * sizeof(uint16_t));
+static size_t x3_planes_bytes(int npc, int64_t n, int64_t nvir, int64_t naux) {
+  return al256((size_t)(2 * npc * n * ((nvir + 1) / 2) * x3_ldv(naux)) * sizeof(uint16_t));
+}
+static size_t h3_exps_bytes(int64_t n, int64_t nvir) {
+  return al256((size_t)(n * ((nvir + 1) & ~1ll)) * sizeof(int32_t));
+}
+static size_t split_workspace(int npc, int64_t nvir, int64_t naux, int64_t npairs, int64_t ni,
+                              int64_t nj) {
+  if (nvir <= 0 || npairs <= 0 || naux < 0 || ni < 0 || nj < 0) return 0;
+  size_t b = al256(trnblas_hip_pair_energy_workspace(nvir, npairs)) +
+             x3_planes_bytes(npc, ni, nvir, naux) + x3_planes_bytes(npc, nj, nvir, naux);
+  if (npc == 2) b += h3_exps_bytes(ni, nvir) + h3_exps_bytes(nj, nvir);
+  return b;
 }
 
 extern "C" size_t trnblas_hip_pair_energy_bf16x6_workspace(int64_t nvir, int64_t naux,
                                                            int64_t npairs, int64_t ni,
                                                            int64_t nj) {
-  if (nvir <= 0 || npairs <= 0 || naux < 0 || ni < 0 || nj < 0) return 0;
-  return al256(trnblas_hip_pair_energy_workspace(nvir, npairs)) +
-         x3_planes_bytes(ni, nvir, naux) + x3_planes_bytes(nj, nvir, naux);
+  return split_workspace(3, nvir, naux, npairs, ni, nj);
 }
 
-// Split n x nvir rows (o, a) of X into the pieces at P (split_planes_kernel).
+extern "C" size_t trnblas_hip_pair_energy_fp16x3_workspace(int64_t nvir, int64_t naux,
+                                                           int64_t npairs, int64_t ni,
+                                                           int64_t nj) {
+  return split_workspace(2, nvir, naux, npairs, ni, nj);
+}
+
+// Split n x nvir rows (o, a) of X into the pieces at P (split_planes_kernel;
+// fp16x3: the row exponents into E first, row_exp_kernel).
+template <int NPC>
 static void x3_split(const float* X, int64_t n, int64_t ld_occ, int64_t ld_vir, int nvir,
-                     int naux, int ldv, uint16_t* P, hipStream_t s) {
+                     int naux, int ldv, uint16_t* P, int32_t* E, hipStream_t s) {
   const int64_t threads = n * ((nvir + 1) & ~1) * (ldv / 8);
   if (threads == 0) return;
+  if (NPC == 2) {
+    const int64_t rows = n * ((nvir + 1) & ~1);
+    hipLaunchKernelGGL(row_exp_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, nvir,
+                       naux, (int)rows, X, ld_occ, ld_vir, E);
+  }
   const unsigned blocks = (unsigned)((threads + 255) / 256);
   const bool vec = (reinterpret_cast<uintptr_t>(X) & 15) == 0 && ld_occ % 4 == 0 &&
                    ld_vir % 4 == 0;
   if (vec)
-    hipLaunchKernelGGL(split_planes_kernel<true>, dim3(blocks), dim3(256), 0, s, nvir, naux, ldv,
-                       (int)threads, X, ld_occ, ld_vir, P);
+    hipLaunchKernelGGL((split_planes_kernel<NPC, true>), dim3(blocks), dim3(256), 0, s, nvir, naux,
+                       ldv, (int)threads, X, ld_occ, ld_vir, (const int32_t*)E, P);
   else
-    hipLaunchKernelGGL(split_planes_kernel<false>, dim3(blocks), dim3(256), 0, s, nvir, naux, ldv,
-                       (int)threads, X, ld_occ, ld_vir, P);
+    hipLaunchKernelGGL((split_planes_kernel<NPC, false>), dim3(blocks), dim3(256), 0, s, nvir,
+                       naux, ldv, (int)threads, X, ld_occ, ld_vir, (const int32_t*)E, P);
 }
 
-// Shared driver of the fp32 and bf16x6 pair-energy entry points: argument
-// checks, the fused kernel, then the per-pair and total reductions.
-static int pair_energy_run(bool x3, const char* name, int64_t nvir, int64_t naux, const float* Bi,
+template <int NPC>
+static void split_launch(const PairArgs& g, bool implicit, int64_t citems, int64_t items,
+                         hipStream_t s) {
+  if (implicit)
+    hipLaunchKernelGGL(pair_energy_x3c_kernel<NPC>, dim3((unsigned)citems), dim3(512), 0, s, g);
+  else
+    hipLaunchKernelGGL(pair_energy_x3_kernel<NPC>, dim3((unsigned)items), dim3(256), 0, s, g);
+}
+
+// Shared driver of the fp32 (npc 0), bf16x6 (npc 3) and fp16x3 (npc 2)
+// pair-energy entry points: argument checks, the split, the fused kernel,
+// then the per-pair and total reductions.
+static int pair_energy_run(int npc, const char* name, int64_t nvir, int64_t naux, const float* Bi,
                            int64_t ni, int64_t ldi_occ, const float* Bj, int64_t nj,
                            int64_t ldj_occ, int64_t ld_vir, const float* eps_i, const float* eps_j,
                            const float* eps_vir, int64_t nocc, int64_t npairs,
@@ -989,6 +1146,7 @@ static int pair_energy_run(bool x3, const char* name, int64_t nvir, int64_t naux
   const int64_t nq = pe_nq(nvir);
   const int64_t items = npairs * nq;
   TRNBLAS_CHECK_ARG(items < (1ll << 31), "%s: too many work items", name);
+  const bool x3 = npc != 0;
   if (x3) {
     TRNBLAS_CHECK_ARG(ni >= 0 && nj >= 0 && ni < (1 << 30) && nj < (1 << 30),
                       "%s: bad row count", name);
@@ -996,12 +1154,12 @@ static int pair_energy_run(bool x3, const char* name, int64_t nvir, int64_t naux
                       "%s: the implicit walk needs ni >= nocc and nj == 0", name);
     TRNBLAS_CHECK_ARG(nj > 0 || (Bj == Bi && ldj_occ == ldi_occ),
                       "%s: nj == 0 shares Bi's pieces and needs Bj == Bi", name);
-    TRNBLAS_CHECK_ARG((int64_t)kX3S * 3 * x3_ldv(naux) * 2 < 0x7fffff00ll,
+    TRNBLAS_CHECK_ARG((int64_t)kX3S * npc * x3_ldv(naux) * 2 < 0x7fffff00ll,
                       "%s: naux too large for 32-bit panel offsets", name);
     TRNBLAS_CHECK_ARG((ni > nj ? ni : nj) * (nvir + 1) * (x3_ldv(naux) / 8) < (1ll << 31),
                       "%s: operands too large for one split launch", name);
   }
-  const size_t need = x3 ? trnblas_hip_pair_energy_bf16x6_workspace(nvir, naux, npairs, ni, nj)
+  const size_t need = x3 ? split_workspace(npc, nvir, naux, npairs, ni, nj)
                          : trnblas_hip_pair_energy_workspace(nvir, npairs);
   if (workspace == nullptr || workspace_bytes < need) {
     set_error("%s: workspace of %zu bytes needed, %zu given", name, need, workspace_bytes);
@@ -1034,25 +1192,37 @@ static int pair_energy_run(bool x3, const char* name, int64_t nvir, int64_t naux
     const int ldv = (int)x3_ldv(naux);
     char* pieces =
         static_cast<char*>(workspace) + al256(trnblas_hip_pair_energy_workspace(nvir, npairs));
+    const size_t pbi = x3_planes_bytes(npc, ni, nvir, naux), pbj = x3_planes_bytes(npc, nj, nvir, naux);
     uint16_t* Pi = reinterpret_cast<uint16_t*>(pieces);
-    uint16_t* Pj = nj ? reinterpret_cast<uint16_t*>(pieces + x3_planes_bytes(ni, nvir, naux)) : Pi;
+    uint16_t* Pj = nj ? reinterpret_cast<uint16_t*>(pieces + pbi) : Pi;
+    int32_t* Ei = npc == 2 ? reinterpret_cast<int32_t*>(pieces + pbi + pbj) : nullptr;
+    int32_t* Ej = npc == 2 && nj ? reinterpret_cast<int32_t*>(pieces + pbi + pbj +
+                                                             h3_exps_bytes(ni, nvir))
+                                 : Ei;
     g.Pi = Pi;
     g.Pj = Pj;
+    g.Ei = Ei;
+    g.Ej = Ej;
+    g.ldE = (int)((nvir + 1) & ~1ll);
     g.ldv = ldv;
     g.rows_i = (int)ni;
     g.rows_j = (int)(nj ? nj : ni);
-    x3_split(Bi, ni, ldi_occ, ld_vir, (int)nvir, (int)naux, ldv, Pi, s);
-    if (nj) x3_split(Bj, nj, ldj_occ, ld_vir, (int)nvir, (int)naux, ldv, Pj, s);
+    const int64_t citems = pair_i == nullptr ? pe_couples(nocc) * nq : 0;
+    TRNBLAS_CHECK_ARG(citems < (1ll << 31), "%s: too many work items", name);
+    if (npc == 3) {
+      x3_split<3>(Bi, ni, ldi_occ, ld_vir, (int)nvir, (int)naux, ldv, Pi, nullptr, s);
+      if (nj) x3_split<3>(Bj, nj, ldj_occ, ld_vir, (int)nvir, (int)naux, ldv, Pj, nullptr, s);
+    } else {
+      x3_split<2>(Bi, ni, ldi_occ, ld_vir, (int)nvir, (int)naux, ldv, Pi, Ei, s);
+      if (nj) x3_split<2>(Bj, nj, ldj_occ, ld_vir, (int)nvir, (int)naux, ldv, Pj, Ej, s);
+    }
     int rc = check_launch(name);
     if (rc) return rc;
-    if (pair_i == nullptr) {
-      // the implicit walk: two pairs sharing B_i per workgroup
-      const int64_t citems = pe_couples(nocc) * nq;
-      TRNBLAS_CHECK_ARG(citems < (1ll << 31), "%s: too many work items", name);
-      hipLaunchKernelGGL(pair_energy_x3c_kernel, dim3((unsigned)citems), dim3(512), 0, s, g);
-    } else {
-      hipLaunchKernelGGL(pair_energy_x3_kernel, dim3((unsigned)items), dim3(256), 0, s, g);
-    }
+    // the implicit walk: two pairs sharing B_i per workgroup
+    if (npc == 3)
+      split_launch<3>(g, pair_i == nullptr, citems, items, s);
+    else
+      split_launch<2>(g, pair_i == nullptr, citems, items, s);
   } else {
     constexpr int NT = kPeS / 32 * 64;
     if (vec)
@@ -1085,7 +1255,7 @@ extern "C" int trnblas_hip_pair_energy(int64_t nvir, int64_t naux, const float* 
                                        double* out_total, void* workspace,
                                        size_t workspace_bytes, void* stream) {
   clear_error();
-  return pair_energy_run(false, "pair_energy", nvir, naux, Bi, 0, ldi_occ, Bj, 0, ldj_occ, ld_vir,
+  return pair_energy_run(0, "pair_energy", nvir, naux, Bi, 0, ldi_occ, Bj, 0, ldj_occ, ld_vir,
                          eps_i, eps_j, eps_vir, nocc, npairs, pair_i, pair_j, pair_w,
                          out_pairs, out_total, workspace, workspace_bytes, (hipStream_t)stream);
 }
@@ -1101,7 +1271,23 @@ extern "C" int trnblas_hip_pair_energy_bf16x6(int64_t nvir, int64_t naux, const 
                                               double* out_total, void* workspace,
                                               size_t workspace_bytes, void* stream) {
   clear_error();
-  return pair_energy_run(true, "pair_energy_bf16x6", nvir, naux, Bi, ni, ldi_occ, Bj, nj, ldj_occ,
+  return pair_energy_run(3, "pair_energy_bf16x6", nvir, naux, Bi, ni, ldi_occ, Bj, nj, ldj_occ,
+                         ld_vir, eps_i, eps_j, eps_vir, nocc, npairs, pair_i, pair_j, pair_w,
+                         out_pairs, out_total, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int trnblas_hip_pair_energy_fp16x3(int64_t nvir, int64_t naux, const float* Bi,
+                                              int64_t ni, int64_t ldi_occ, const float* Bj,
+                                              int64_t nj, int64_t ldj_occ,
+                                              int64_t ld_vir, const float* eps_i,
+                                              const float* eps_j, const float* eps_vir,
+                                              int64_t nocc, int64_t npairs,
+                                              const int32_t* pair_i, const int32_t* pair_j,
+                                              const double* pair_w, double* out_pairs,
+                                              double* out_total, void* workspace,
+                                              size_t workspace_bytes, void* stream) {
+  clear_error();
+  return pair_energy_run(2, "pair_energy_fp16x3", nvir, naux, Bi, ni, ldi_occ, Bj, nj, ldj_occ,
                          ld_vir, eps_i, eps_j, eps_vir, nocc, npairs, pair_i, pair_j, pair_w,
                          out_pairs, out_total, workspace, workspace_bytes, (hipStream_t)stream);
 }
@@ -1172,7 +1358,7 @@ extern "C" int trnblas_hip_pair_energy_noalloc(int64_t nvir, int64_t naux, const
   void* ws = nullptr;
   const int rc = scratch_address(name, &ws);
   if (rc) return rc;
-  return pair_energy_run(false, name, nvir, naux, Bi, 0, ldi_occ, Bj, 0, ldj_occ, ld_vir, eps_i,
+  return pair_energy_run(0, name, nvir, naux, Bi, 0, ldi_occ, Bj, 0, ldj_occ, ld_vir, eps_i,
                          eps_j, eps_vir, nocc, npairs, pair_i, pair_j, pair_w, out_pairs,
                          out_total, ws, kPeScratchBytes, (hipStream_t)stream);
 }

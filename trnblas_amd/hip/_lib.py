@@ -19,7 +19,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 _PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("TRNBLAS_HIP_LIB", _PKG / "lib" / "libtrnblas_hip.so"))
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 F32, BF16, F16, F64 = 0, 1, 2, 3
 DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
@@ -66,6 +66,13 @@ SIGNATURES = {
     ),
     "trnblas_hip_pair_energy_bf16x6_workspace": (_c_size, [_c_i64] * 5),
     "trnblas_hip_pair_energy_bf16x6": (
+        _c_int,
+        [_c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64]
+        + [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_ptr, _c_size, _c_ptr],
+    ),
+    "trnblas_hip_pair_energy_fp16x3_workspace": (_c_size, [_c_i64] * 5),
+    "trnblas_hip_pair_energy_fp16x3": (
         _c_int,
         [_c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64]
         + [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr]

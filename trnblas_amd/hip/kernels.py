@@ -282,18 +282,23 @@ def _pe_operand(X: torch.Tensor) -> torch.Tensor:
     return X
 
 
-PAIR_ENERGY_MATH = ("fp32", "bf16x6")
+PAIR_ENERGY_MATH = ("fp32", "bf16x6", "fp16x3")
 
 
-_PE_ENTRY = {"fp32": "trnblas_hip_pair_energy", "bf16x6": "trnblas_hip_pair_energy_bf16x6"}
+_PE_ENTRY = {
+    "fp32": "trnblas_hip_pair_energy",
+    "bf16x6": "trnblas_hip_pair_energy_bf16x6",
+    "fp16x3": "trnblas_hip_pair_energy_fp16x3",
+}
 
 
 def pair_energy_math() -> str:
     """Arithmetic of the fused pair-energy kernel: TRNBLAS_PAIR_ENERGY_MATH =
-    "bf16x6" (default: bf16 MFMA on three-piece splits, fp32 slice sums; the
-    faster and, measured against fp64, the more accurate) or "fp32" (fp32
-    MFMA)."""
-    return _check_math(os.environ.get("TRNBLAS_PAIR_ENERGY_MATH", "bf16x6").strip().lower())
+    "fp16x3" (default: f16 MFMA on two-piece splits of row-scaled operands,
+    three products, fp32 slice sums; the fastest, with fp32 MFMA's accuracy
+    against fp64), "bf16x6" (bf16 MFMA on three-piece splits, six products;
+    the most accurate) or "fp32" (fp32 MFMA)."""
+    return _check_math(os.environ.get("TRNBLAS_PAIR_ENERGY_MATH", "fp16x3").strip().lower())
 
 
 def _check_math(math: str | None) -> str:
@@ -308,8 +313,10 @@ def pair_energy_sym(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tenso
     """E = sum_{i,j} e_ij over all ordered pairs, evaluated as the i <= j walk
     (weights 1 / 2) in one launch. B (nocc, nvir, naux) fp32 on the GPU.
     math: "fp32" (fp32 MFMA), "bf16x6" (each fp32 operand split into three
-    bf16 pieces by a first pass; six bf16 MFMA products per fp32 product) or
-    None (pair_energy_math()). Returns a 0-d float64 device tensor."""
+    bf16 pieces by a first pass; six bf16 MFMA products per fp32 product),
+    "fp16x3" (each row scaled by a power of two and split into two fp16
+    pieces; three f16 MFMA products per fp32 product) or None
+    (pair_energy_math()). Returns a 0-d float64 device tensor."""
     dev = _require_device(B, eps_occ, eps_vir)
     math = _check_math(math)
     B = _pe_operand(B)
@@ -329,10 +336,10 @@ def pair_energy_sym(B: torch.Tensor, eps_occ: torch.Tensor, eps_vir: torch.Tenso
 def _pe_launch(math, dev, nvir, naux, Bi, ni, ldi, Bj, nj, ldj, ld_vir, ei, ej, ev, nocc, npairs,
                pi, pj, out_pairs, out_total, probed=False):
     """One pair-energy launch with its workspace. ni / nj: rows of Bi / Bj
-    (nj == 0: Bj is Bi), used by the bf16x6 entry point for its planes."""
+    (nj == 0: Bj is Bi), used by the split entry points for their planes."""
     lib = _lib.load()
-    if math == "bf16x6":
-        ws = lib.trnblas_hip_pair_energy_bf16x6_workspace(nvir, naux, npairs, ni, nj)
+    if math in ("bf16x6", "fp16x3"):
+        ws = getattr(lib, _PE_ENTRY[math] + "_workspace")(nvir, naux, npairs, ni, nj)
         head = (nvir, naux, ptr(Bi), ni, ldi, ptr(Bj), nj, ldj, ld_vir)
     else:
         ws = lib.trnblas_hip_pair_energy_workspace(nvir, npairs)
