@@ -863,13 +863,37 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
     constexpr int P = decltype(P_)::value;
     constexpr bool FIRST = decltype(FIRST_)::value;
     __syncthreads();
-    load(t + 2, stg[P]);
     const int ps = t >= nk ? 1 : 0;
     const uint16_t* bufA = lds + P * STAGE + (ps ? 1 + gp : 0) * SLOT;
     const uint16_t* bufB = lds + P * STAGE + (ps ? 0 : 1 + gp) * SLOT;
     auto frag = [&](const uint16_t* b, int pc, int r) __attribute__((always_inline)) {
       return *reinterpret_cast<const i32x4*>(b + (pc * S + r) * BK + fslot);
     };
+    if constexpr (NPC == 2) {
+      // fp16x3: three MFMAs per block are too few to hide a block's reads
+      // behind the block before; all twelve fragments are read first, then
+      // the next slices' loads issue, then the 27 MFMAs
+      i32x4 fa[3][2], fb[3][2];
+#pragma unroll
+      for (int u = 0; u < 3; ++u)
+#pragma unroll
+        for (int pc = 0; pc < 2; ++pc) {
+          fa[u][pc] = frag(bufA, pc, ar0 + 16 * u + (lane & 15));
+          fb[u][pc] = frag(bufB, pc, br0 + 16 * u + (lane & 15));
+        }
+      load(t + 2, stg[P]);
+#pragma unroll
+      for (int e = 0; e < M::NPROD; ++e)
+#pragma unroll
+        for (int cb = 0; cb < 3; ++cb)
+#pragma unroll
+          for (int rb = 0; rb < 3; ++rb)
+            part[rb][cb] = M::mma(fa[rb][M::ka[e]], fb[cb][M::kb[e]],
+                                  FIRST && e == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb]);
+      if (t + 1 < nsteps) store(stg[1 - P], 1 - P);
+      return;
+    }
+    load(t + 2, stg[P]);
     i32x4 fa[3][NPC];
     // Blocks (rb, cb) in the order cb-major; before a block's NPROD MFMAs
     // the fragments the next block adds (A rows of rb + 1 in column block
