@@ -616,7 +616,8 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
     const __amdgpu_buffer_rsrc_t rs = pass1 ? rs1 : rs0;
 #pragma unroll
     for (int u = 0; u < NU; ++u)
-      set[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[u], sl * NPC * 128, 0);
+      set[u] = __builtin_amdgcn_raw_buffer_load_b128(
+          rs, voff[u], __builtin_amdgcn_readfirstlane(sl * NPC * 128), 0);
   };
   auto store = [&](const i32x4(&set)[NU], int buf) {
     uint16_t* dst = lds + buf * STAGE + side * (STAGE / 2) + h * 512 + lane * 8;
@@ -837,7 +838,9 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
       const int o = i + (sl > 0) * (j0 - i) + (sl > 1) * (j1 - j0);
       const uint16_t* base = g.Pi + o * ostride + (onA ? rowA : rowB);
       const uint32_t v = voff[u];
-      const int soff = sl0 * NPC * 128;
+      // (readfirstlane: an offset the compiler keeps in a VGPR after a select
+      // wraps the load in a loop over the lanes' distinct values)
+      const int soff = __builtin_amdgcn_readfirstlane(sl0 * NPC * 128);
       set[u] = __builtin_amdgcn_raw_buffer_load_b128(
           __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0,
                                             (onA ? pairsA : pairsB) * nk * NPC * 128, 0x00020000),
