@@ -762,8 +762,11 @@ def _torch_chunked_pair_energy(B, eps_occ, eps_vir, mem_budget_bytes: int = 1_50
 # off the tile diagonal) form the whole critical path, or where nvir is far
 # below the 96-row tile; the unfused path costs a ~0.115 ms floor plus its
 # ordered-pair GEMM (~100 TFLOP/s) and six fp32 passes over T (~3 TB/s).
-# The model below picks the faster route in 87 of the 90 cases (mean loss
-# 0.7 %); at C3 / C4 it keeps the fused kernel by a wide margin.
+# The model below picks the faster route in 88 of the 90 cases with the
+# default fp16x3 arithmetic (mean loss 0.02 %; 87 of 90 with bf16x6): on these
+# shapes one item's k-step takes about as long in either arithmetic, the
+# step being latency-bound when few items share the chip. At C3 / C4 it
+# keeps the fused kernel by a wide margin.
 _PE_STEP_MS = 1.9e-3
 _PE_FUSED_FLOOR_MS = 0.02
 _PE_UNFUSED_FLOOR_MS = 0.115
