@@ -146,10 +146,16 @@ def run_extras(dev, tb, only=None) -> dict:
         cpu_ms = (time.perf_counter() - t0) * 1e3
         den = Ah.double().abs().T @ Bh.double().abs() + 0.5 * Ch.double().abs()
         err = float(((D.cpu().double() - cpu.double()) / den).abs().max())
+        # hipBLASLt through torch on the same operands (A^T as a view)
+        tl = gpu_time_ms(lambda: torch.addmm(C, A.mT, B, beta=0.5), reps=20, warm=20)
+        Dl = torch.addmm(C, A.mT, B, beta=0.5)
+        err_l = float(((Dl.cpu().double() - cpu.double()) / den).abs().max())
         fl = 2 * 2048**3
         out["c1_gemm_2048_transA"] = {
             "ms": t, "tflops": fl / t / 1e9, "frac_fp32_peak": fl / t / 1e9 / PEAK_FP32_MFMA,
             "cw_err_vs_cpu_path": err, "gate": 1e-6, "cpu_ms": cpu_ms, "cpu_threads": torch.get_num_threads(),
+            "route": dispatch._gemm_route(A.mT, B), "torch_hipblaslt_ms": tl,
+            "torch_hipblaslt_tflops": fl / tl / 1e9, "torch_hipblaslt_cw_err_vs_cpu_path": err_l,
         }  # fmt: skip
         log("c1", out["c1_gemm_2048_transA"])
     if only is None or "gemm8192" in only:
