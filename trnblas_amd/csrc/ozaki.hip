@@ -310,7 +310,12 @@ struct OzArgs {
   int tiles_m, tiles_n;
   int flush;      // fast mode: k-steps between int32 -> fp64 flushes of the diagonals
   int64_t hl_rs, hl_cs, hl_lo;  // oz_exact_kernel: (hi, lo) output strides (floats)
+  int fuse;                     // oz_exact_kernel: combine into C in the epilogue
 };
+
+// The fp64 recombination of one exact-mode element (ozaki.py:418-455,
+// `combine`): ((double) hi + (double) lo) 2^(eA + off) 2^eB.
+__device__ __forceinline__ double oz_combine(float hi, float lo, int ea_raw, int eb, int k);
 
 __device__ __forceinline__ void two_sum32(float& hi, float& lo, float p) {
 #pragma clang fp contract(off)
@@ -979,11 +984,29 @@ __global__ __launch_bounds__(256, 2) void oz_exact_kernel(OzArgs g) {
       d = nd, sp = ns, ks = nk;
     }
 
-    // Epilogue: the raw (hi, lo) pairs (lane l of a 32x32 block: column
-    // l % 32, rows 8 (r/4) + 4 (l/32) + r % 4), into two planes (the hilo
-    // surface) or as the two words of C's own 8 bytes per element (the fp64
-    // recombination is then oz_combine_kernel, which reads them in place).
+    // Epilogue (lane l of a 32x32 block: column l % 32, rows 8 (r/4) +
+    // 4 (l/32) + r % 4): the fp64 recombination into C (gemm_fp64), or the
+    // raw (hi, lo) pairs into two planes (the hilo surface).
     asm volatile("" : "+v"(lane));
+    if (g.fuse) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = n0 + wn0 + j * 32 + (lane & 31);
+          const int mb = m0 + wm0 + i * 32 + (lane >> 5) * 4;
+          if (n >= g.N) continue;
+          const int eb = g.eB[n];
+          double* cb = g.C + (int64_t)mb * g.ldc_m + (int64_t)n * g.ldc_n;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int dm = (r >> 2) * 8 + (r & 3);
+            if (mb + dm >= g.M) continue;
+            cb[dm * g.ldc_m] = oz_combine(hi[i][j][r], lo[i][j][r], g.eA[mb + dm], eb, k);
+          }
+        }
+      return;
+    }
     // (one base address per 32 x 32 block; the row offsets are uniform)
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -1006,30 +1029,12 @@ __global__ __launch_bounds__(256, 2) void oz_exact_kernel(OzArgs g) {
   }
 }
 
-// The fp64 recombination of the exact mode (ozaki.py:418-455, `combine`):
-// C[m][n] = ((double) hi + (double) lo) 2^(eA[m] + eB[n] + off), reading the
-// float2 (hi, lo) that oz_exact_kernel left in C's own 8 bytes and writing
-// the fp64 value in its place. One element per thread.
-__global__ __launch_bounds__(256) void oz_combine_kernel(int M, int N, int k, const int32_t* eA,
-                                                         const int32_t* eB, double* C,
-                                                         int64_t ldc_m, int64_t ldc_n) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)M * N) return;
-  // consecutive threads along C's contiguous dimension
-  const bool n_fast = ldc_n == 1;
-  const int m = n_fast ? (int)(idx / N) : (int)(idx % M);
-  const int n = n_fast ? (int)(idx % N) : (int)(idx / M);
-  double* dst = C + (int64_t)m * ldc_m + (int64_t)n * ldc_n;
-  const float2 hl = *reinterpret_cast<const float2*>(dst);
+__device__ __forceinline__ double oz_combine(float hi, float lo, int ea_raw, int eb, int k) {
   const int off = -2 * (kSliceBits - 1) - kSliceBits * (k - 1);
-  const int ea = eA[m] + off, eb = eB[n];
-  const double v = (double)hl.x + (double)hl.y;
-  double c;
-  if (ea < 900 && ea > -900 && eb < 900 && eb > -900)
-    c = (v * pow2(ea)) * pow2(eb);
-  else
-    c = ldexp(v, ea + eb);
-  *dst = c;
+  const int ea = ea_raw + off;
+  const double v = (double)hi + (double)lo;
+  if (ea < 900 && ea > -900 && eb < 900 && eb > -900) return (v * pow2(ea)) * pow2(eb);
+  return ldexp(v, ea + eb);
 }
 
 constexpr int kOzBM = 128, kOzBN = 128, kOzBK = 64;
@@ -1041,25 +1046,16 @@ static int oz_launch(OzArgs& g, int out, hipStream_t s) {
   TRNBLAS_CHECK_ARG(nt < (1ll << 31), "ozaki: too many tiles");
   if (g.kb == g.Kp) {
     // one K block (K up to ~2^16): the streamed kernel (C5: 22.7 ms against
-    // 63.8 ms for oz_gemm_kernel, bit-equal), then (into C) the fp64 combine
-    if (out == 0) {
-      g.hilo = reinterpret_cast<float*>(g.C);
-      g.hl_rs = 2 * g.ldc_m;
-      g.hl_cs = 2 * g.ldc_n;
-      g.hl_lo = 1;
-    } else {
+    // 63.8 ms for oz_gemm_kernel, bit-equal), with the fp64 combine in its
+    // epilogue (mode 0) or the (hi, lo) planes out (mode 1)
+    g.fuse = out == 0;
+    if (out != 0) {
       g.hl_rs = g.ldh;
       g.hl_cs = 1;
       g.hl_lo = (int64_t)g.M * g.ldh;
     }
     hipLaunchKernelGGL(oz_exact_kernel, dim3((unsigned)nt), dim3(256), 0, s, g);
-    int rc = check_launch("ozaki_gemm");
-    if (rc || out != 0) return rc;
-    const int64_t n = (int64_t)g.M * g.N;
-    TRNBLAS_CHECK_ARG((n + 255) / 256 < (1ll << 31), "ozaki: too many elements");
-    hipLaunchKernelGGL(oz_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g.M,
-                       g.N, g.k, g.eA, g.eB, g.C, g.ldc_m, g.ldc_n);
-    return check_launch("ozaki_gemm(combine)");
+    return check_launch("ozaki_gemm");
   }
   if (out == 0)
     hipLaunchKernelGGL((oz_gemm_kernel<kOzBM, kOzBN, kOzBK, 0>), dim3((unsigned)nt), dim3(256),
