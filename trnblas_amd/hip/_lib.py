@@ -212,5 +212,27 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 def stream_of(device: torch.device) -> int:
-    """hipStream_t of torch's current stream on `device`, as an int."""
-    return torch.cuda.current_stream(device).cuda_stream
+    """hipStream_t of torch's current stream on `device`, as an int (the raw
+    lookup: torch.cuda.current_stream builds a Stream object per call, a few
+    microseconds on every launch)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
+
+
+def broadcast_shapes(a, b) -> tuple:
+    """torch.broadcast_shapes for two shapes, in plain Python (torch's goes
+    through its symbolic-shape machinery, ~10 us per call on the launch
+    path); the same RuntimeError on shapes that do not broadcast."""
+    a, b = tuple(a), tuple(b)
+    n = max(len(a), len(b))
+    a = (1,) * (n - len(a)) + a
+    b = (1,) * (n - len(b)) + b
+    out = []
+    for x, y in zip(a, b):
+        if x == y or y == 1:
+            out.append(x)
+        elif x == 1:
+            out.append(y)
+        else:
+            raise RuntimeError(f"shapes {a} and {b} are not broadcastable")
+    return tuple(out)

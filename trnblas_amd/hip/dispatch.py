@@ -305,7 +305,7 @@ def _aten_gemm_wins(a_shape, b_shape, dtype: torch.dtype, contiguous: bool, op: 
     if op == "syrk" or dtype not in (torch.bfloat16, torch.float16):
         return False
     M, K, N = a_shape[-2], a_shape[-1], b_shape[-1]
-    nb = math.prod(torch.broadcast_shapes(tuple(a_shape[:-2]), tuple(b_shape[:-2])))
+    nb = math.prod(_lib.broadcast_shapes(tuple(a_shape[:-2]), tuple(b_shape[:-2])))
     if nb > 1 and not contiguous:
         return False
     return nb * M * N >= _ATEN_16BIT_MIN_MN and K >= _ATEN_16BIT_MIN_K
@@ -379,7 +379,7 @@ def _fused_epilogue_ok(C, beta, shape, dtype, device) -> bool:
     return (
         C.dtype == dtype
         and C.device == device
-        and torch.broadcast_shapes(tuple(shape), tuple(C.shape)) == tuple(shape)
+        and _lib.broadcast_shapes(tuple(shape), tuple(C.shape)) == tuple(shape)
     )
 
 
@@ -415,7 +415,7 @@ def hip_gemm(A, B, alpha=1.0, beta=0.0, C=None) -> torch.Tensor:
 def _flatten_batch(A, B):
     """A (..., M, K), B (..., K, N) -> 3-D operands with one broadcast batch
     dim (views when possible), and the broadcast batch shape."""
-    batch = torch.broadcast_shapes(A.shape[:-2], B.shape[:-2])
+    batch = _lib.broadcast_shapes(A.shape[:-2], B.shape[:-2])
     nb = math.prod(batch)
 
     def as3(X):
@@ -455,7 +455,7 @@ def nki_batched_gemm(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     """torch.matmul batch semantics (dispatch.py:1384-1427) in one launch."""
     if A.dim() < 2 or B.dim() < 2:
         return torch.matmul(A, B)
-    batch = torch.broadcast_shapes(A.shape[:-2], B.shape[:-2])
+    batch = _lib.broadcast_shapes(A.shape[:-2], B.shape[:-2])
     if math.prod(batch) == 0:
         return torch.matmul(A, B)
     route = _gemm_route(A, B, op="batched_gemm")
@@ -477,7 +477,7 @@ def gemm_scaled(alpha, a, b, beta, C):
     the route is a kernel route (level3.gemm / batched_gemm)."""
     if a.dim() < 2 or b.dim() < 2:
         return _torch_scale_add(torch.matmul(a, b), alpha, beta, C)
-    batch = torch.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    batch = _lib.broadcast_shapes(a.shape[:-2], b.shape[:-2])
     route = _gemm_route(a, b, op="gemm" if a.dim() == 2 and b.dim() == 2 else "batched_gemm")
     if route not in ("hip", "upload") or math.prod(batch) == 0 or len(batch) > 1:
         if route in ("hip", "upload") and len(batch) > 1:

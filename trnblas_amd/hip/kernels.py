@@ -39,7 +39,7 @@ def gemm_workspace(dev: torch.device) -> torch.Tensor:
     launches on one stream are ordered, launches on two streams may overlap,
     so each stream has its own)."""
     key = (dev.index if dev.index is not None else torch.cuda.current_device())
-    stream = torch.cuda.current_stream(key).cuda_stream
+    stream = torch._C._cuda_getCurrentRawStream(key)
     ws = _gemm_ws.get((key, stream))
     if ws is None:
         with torch.cuda.device(key):

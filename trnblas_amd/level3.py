@@ -26,6 +26,7 @@ import torch
 
 from ._flags import diag_flag, side_flag, trans_flag, uplo_flag
 from .hip import dispatch as _d
+from .hip._lib import broadcast_shapes as _broadcast_shapes
 
 
 def _owned_inplace_ok(result: torch.Tensor) -> bool:
@@ -45,7 +46,7 @@ def _scale_add(result: torch.Tensor, alpha: float, beta: float, C) -> torch.Tens
         inplace = (
             C.dtype == result.dtype
             and C.device == result.device
-            and torch.broadcast_shapes(result.shape, C.shape) == result.shape
+            and _broadcast_shapes(result.shape, C.shape) == tuple(result.shape)
         )
     if not inplace:
         result = alpha * result
