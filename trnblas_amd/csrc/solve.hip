@@ -88,7 +88,7 @@ static int fill(double* p, int64_t rows, int64_t cols, int64_t ld, double v, hip
 struct SideStream {
   std::mutex mu;
   hipStream_t side = nullptr, inv = nullptr;
-  hipEvent_t ready = nullptr, done = nullptr, factored = nullptr, inverted = nullptr;
+  hipEvent_t ready = nullptr, done = nullptr, inverted = nullptr;
 };
 
 static SideStream* side_stream(int& rc) {
@@ -109,7 +109,6 @@ static int side_init(SideStream* ss) {
       hipStreamCreateWithFlags(&ss->inv, hipStreamNonBlocking) != hipSuccess ||
       hipEventCreateWithFlags(&ss->ready, hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ss->done, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&ss->factored, hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ss->inverted, hipEventDisableTiming) != hipSuccess) {
     set_error("metric_inv_half: cannot create the side stream / events");
     return TRNBLAS_E_LAUNCH;
@@ -195,17 +194,24 @@ extern "C" int trnblas_hip_metric_inv_half(int64_t n, const double* J, int64_t l
     double* Ybb = Y + k0 * npad + k0;
     // L_bb into W (lower triangle), L_bb^-1 = Y_bb straight into Y
     TRY(trnblas_hip_chol_block(m, W + k0 * npad + k0, npad, Ybb, npad, info, k0, main));
-    if (b > 0) {
-      // block row b of Y: T = L[b, :b] Y[:b, :b], Y[b, :b] = -Y_bb T
-      TRY(record(ss->factored, main));
-      TRY(wait(ss->inv, ss->factored));
+    // block row b of Y: T = L[b, :b] Y[:b, :b], Y[b, :b] = -Y_bb T, on the
+    // inverse stream once `ready` (recorded after this step's GEMMs on the
+    // caller's stream, or right here in the last step) follows Y_bb
+    auto inv_row = [&]() -> int {
+      if (b == 0) return TRNBLAS_OK;
+      TRY(wait(ss->inv, ss->ready));
       TRY(trnblas_hip_dgemm(0, 0, kNB, k0, k0, 1.0, L + k0 * npad, npad, 0, Y, npad, 0, 0.0,
                             nullptr, npad, 0, T, npad, 0, 1, 0, TRNBLAS_TRI_B_LOWER, ss->inv));
       TRY(trnblas_hip_dgemm(0, 0, kNB, k0, kNB, -1.0, Ybb, npad, 0, T, npad, 0, 0.0, nullptr,
                             npad, 0, Y + k0 * npad, npad, 0, 1, 0, TRNBLAS_TRI_A_LOWER, ss->inv));
       inv = true;
+      return TRNBLAS_OK;
+    };
+    if (k0 + kNB >= npad) {
+      if (b > 0) TRY(record(ss->ready, main));
+      TRY(inv_row());
+      break;
     }
-    if (k0 + kNB >= npad) break;
     const int64_t k1 = k0 + kNB, k2 = k1 + kNB, rows = npad - k1;
     // the panel of L: L[k1:, k0:k1] = W[k1:, k0:k1] Y_bb^T
     TRY(trnblas_hip_dgemm(0, 1, rows, kNB, kNB, 1.0, W + k1 * npad + k0, npad, 0, Ybb, npad, 0,
@@ -216,11 +222,14 @@ extern "C" int trnblas_hip_metric_inv_half(int64_t n, const double* J, int64_t l
     TRY(trnblas_hip_dgemm(0, 1, rows, kNB, kNB, -1.0, L + k1 * npad + k0, npad, 0,
                           L + k1 * npad + k0, npad, 0, 1.0, W + k1 * npad + k1, npad, 0,
                           W + k1 * npad + k1, npad, 0, 1, 0, 0, main));
+    // one event for both: the side stream's trailing update and the
+    // inverse stream's block row (one record per step fewer on the host)
+    if (k2 < npad || b > 0) TRY(record(ss->ready, main));
+    TRY(inv_row());
     if (k2 < npad) {
       const int64_t r2 = npad - k2;
       const double* R = L + k2 * npad + k0;
       double* Wt = W + k2 * npad + k2;
-      TRY(record(ss->ready, main));
       TRY(wait(ss->side, ss->ready));
       TRY(trnblas_hip_dgemm(0, 1, r2, r2, kNB, -1.0, R, npad, 0, R, npad, 0, 1.0, Wt, npad, 0, Wt,
                             npad, 0, 1, 1, 0, ss->side));
