@@ -89,6 +89,28 @@ def test_gemm_same_sign_long_k(dev):
     assert _cw(S, As @ As.T, As @ As.T) <= 1e-6
 
 
+@pytest.mark.parametrize("n,k", [(1030, 260), (1030, 1000), (1024, 2500), (768, 4096)])
+@pytest.mark.parametrize("trans", [False, True])
+def test_syrk_same_sign_short_k(dev, n, k, trans):
+    # U(0, 1) operands with K of a few hundred to a few thousand: one
+    # accumulation chain carries most of each sum (with 256-long chains the
+    # largest error over a 1030^2 SYRK at K = 260 was 1.05e-6). Gate: 1e-6
+    # against fp64 and against the reference's CPU path; the output covers
+    # ~1M elements, so the gate holds at the tail, not only on average.
+    g = torch.Generator().manual_seed(n + k + int(trans))
+    A = torch.rand((k, n) if trans else (n, k), generator=g)
+    S = tb.syrk(1.0, A.to(dev), trans=trans, uplo="lower").cpu()
+    op = (A.T if trans else A).double()
+    ref, den = op @ op.T, op @ op.T
+    assert _cw(S, ref, den) <= 1e-6
+    cpu = blas.syrk_cpu(1.0, A, trans=trans, uplo="lower").double()
+    # the CPU path's own error against fp64 (its transposed reads can be
+    # less accurate than the gate) bounds how far the two may differ
+    assert _cw(S, cpu, den) <= 1e-6 + _cw(cpu.float(), ref, den)
+    G = tb.gemm(1.0, op.float().to(dev), op.T.contiguous().float().to(dev)).cpu()
+    assert _cw(G, ref, den) <= 1e-6
+
+
 # ── GEMM semantics and edge cases ────────────────────────────────────────────
 
 

@@ -108,11 +108,17 @@ __device__ __forceinline__ i32x4 load_group(__amdgpu_buffer_rsrc_t rs, uint32_t 
 // fp32 sum with a VALU add (fold_span). One chain over all of K rounds the
 // running sum at every step: a sum of 8192 same-sign products (a SYRK
 // diagonal) came out 5.3e-6 off. With chains of L values folded into the sum
-// the error is that of L chain steps plus K / L folds; L near 2 sqrt(K)
-// balances them, and at K = 8192 the result stays near 3e-7, the error of
-// the host's blocked fp32 matmul. (A multiple of every k-tile, 128 k.)
-static inline int chain_length(int64_t K) {
-  return K < 16384 ? 256 : K < 65536 ? 512 : 1024;
+// the error is that of one L-long chain (averaged over the K / L chains)
+// plus that of K / L folds. Measured on the MI355X, largest componentwise
+// error over the whole output with U(0, 1) operands, L = 64 / 128 / 256:
+// SYRK 1030 x 260 (one chain dominates) 3.5e-7 / 5.7e-7 / 1.05e-6; SYRK
+// 4096 x 8192 (the folds dominate) 7.8e-7 / 6.2e-7 / 4.5e-7; C2a (N(0, 1))
+// 6.1e-7 / 4.2e-7 / 3.6e-7, at 1.094 / 1.057 / 1.046 ms. Hence L grows with
+// K. 16-bit operands keep L >= 128 (two of their 64-wide k-tiles: the DMA
+// kernel folds after an even number of k-tiles).
+static inline int chain_length(int64_t K, int elem_bytes) {
+  const int L = K <= 1024 ? 64 : K <= 4096 ? 128 : K < 16384 ? 256 : K < 65536 ? 512 : 1024;
+  return elem_bytes == 2 && L < 128 ? 128 : L;
 }
 
 __device__ __forceinline__ void fold_span(f32x16& sum, f32x16& acc) {
@@ -888,7 +894,7 @@ static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   constexpr bool DMA = VEC;  // aligned operands: gemm_dma_kernel
   constexpr int BK = DMA ? 128 / (int)sizeof(T) : C::template bk<VEC>();
   g.nk = (g.K + BK - 1) / BK;
-  g.span = chain_length(g.K) / BK;  // even for every k-tile (32, 64)
+  g.span = chain_length(g.K, (int)sizeof(T)) / BK;  // even for the DMA kernel's k-tiles
   void (*kern)(GemmArgs);
   if constexpr (DMA)
     kern = gemm_dma_kernel<T, AKC, BKC, SYRK>;
