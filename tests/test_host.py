@@ -341,3 +341,58 @@ def test_pair_energy_math_selection(monkeypatch):
     assert kernels._PE_ENTRY["bf16x6"] == "trnblas_hip_pair_energy_bf16x6"
     assert kernels._PE_ENTRY["fp16x3"] == "trnblas_hip_pair_energy_fp16x3"
     assert kernels._check_math("fp16x3") == "fp16x3"
+
+
+# ── autotune (measured kernel-vs-hipBLASLt route, cached per shape bucket) ───
+
+
+def test_autotune_bucket_key():
+    from trnblas_amd.hip import dispatch as d
+
+    k = d._autotune_key((1000, 300), (300, 70), torch.bfloat16, False, False, True)
+    assert k == "bfloat16,001,1,1024,512,128"  # power-of-two ceilings of batch, M, K, N
+    # shapes within one bucket share the key, the next power of two does not
+    assert d._autotune_key((600, 257), (257, 65), torch.bfloat16, False, False, True) == k
+    assert d._autotune_key((1025, 300), (300, 70), torch.bfloat16, False, False, True) != k
+    # batch broadcast, layout and dtype are part of the key
+    kb = d._autotune_key((3, 1, 64, 64), (5, 64, 64), torch.float16, False, True, False)
+    assert kb == "float16,010,16,64,64,64"
+
+
+def test_autotune_cache_round_trip(monkeypatch, tmp_path):
+    from trnblas_amd.hip import dispatch as d
+
+    path = tmp_path / "sub" / "cache.json"
+    monkeypatch.setattr(d, "_AUTOTUNE_CACHE_FILE", str(path))
+    monkeypatch.setattr(d, "_autotune_mem", {"bfloat16,001,1,1024,512,128": "aten"})
+    monkeypatch.setattr(d, "_autotune_loaded", True)
+    d._save_autotune_cache()  # creates the directory
+    monkeypatch.setattr(d, "_autotune_mem", {})
+    monkeypatch.setattr(d, "_autotune_loaded", False)
+    d._load_autotune_cache()
+    assert d._autotune_mem == {"bfloat16,001,1,1024,512,128": "aten"}
+    # unknown route names and unreadable files are ignored
+    path.write_text('{"a": "hip", "b": "cuda"}')
+    monkeypatch.setattr(d, "_autotune_loaded", False)
+    d._load_autotune_cache()
+    assert d._autotune_mem == {"a": "hip"}
+    path.write_text("not json")
+    monkeypatch.setattr(d, "_autotune_loaded", False)
+    d._load_autotune_cache()
+    assert d._autotune_mem == {}
+
+
+def test_autotune_flag_and_inadmissible_operands(monkeypatch):
+    from trnblas_amd.hip import dispatch as d
+
+    monkeypatch.setattr(d, "_AUTOTUNE", False)
+    tb.set_autotune(True)
+    assert tb.get_autotune() is True
+    tb.set_autotune(False)
+    assert tb.get_autotune() is False
+    # fp32, SYRK and mixed-rank operands are never timed: the static rule decides
+    a = torch.empty(64, 64)
+    assert d._autotune_gemm_route(a, a, "gemm") is None
+    h = a.bfloat16()
+    assert d._autotune_gemm_route(h, h, "syrk") is None
+    assert d._autotune_gemm_route(h.expand(2, 64, 64), h, "batched_gemm") is None

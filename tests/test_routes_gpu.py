@@ -118,3 +118,39 @@ def test_pair_energy_route_small_shape_takes_unfused(dev):
     # and the fused kernel on the same inputs agrees
     got = float(kernels.pair_energy_sym(Bd, eod, evd))
     assert abs(got - want) <= 1e-6 * abs(want)
+
+
+def test_autotune_measures_once_per_bucket(dev, monkeypatch, tmp_path):
+    # with autotune on, the first 16-bit device GEMM of a shape bucket times
+    # the kernel and hipBLASLt and routes by the result; later calls of the
+    # bucket reuse it (also from the cache file), fp32 is never timed
+    path = tmp_path / "autotune.json"
+    monkeypatch.setattr(d, "_AUTOTUNE_CACHE_FILE", str(path))
+    monkeypatch.setattr(d, "_autotune_mem", {})
+    monkeypatch.setattr(d, "_autotune_loaded", False)
+    monkeypatch.setattr(d, "_autotune_measured", 0)
+    monkeypatch.setattr(d, "_AUTOTUNE", True)
+    g = torch.Generator(device=dev).manual_seed(31)
+    A = torch.randn(2048, 1024, device=dev, generator=g).bfloat16()
+    B = torch.randn(1024, 1536, device=dev, generator=g).bfloat16()
+    route = d._gemm_route(A, B)
+    assert route in ("hip", "aten") and d._autotune_measured == 1
+    key = d._autotune_key(A.shape, B.shape, A.dtype, False, False, True)
+    assert d._autotune_mem[key] == route
+    import json
+
+    assert json.loads(path.read_text())[key] == route
+    with _Launches() as seen:
+        D = tb.gemm(1.0, A, B)
+    assert ("gemm" in seen.names) == (route == "hip")
+    ref = A.double() @ B.double()
+    den = A.double().abs() @ B.double().abs()
+    assert _cw(D, ref, den) <= 2.0**-8
+    # a shape of the same bucket, and a fresh process state reading the file
+    A2, B2 = A[:1500, :1000].contiguous(), B[:1000, :1100].contiguous()
+    assert d._gemm_route(A2, B2) == route and d._autotune_measured == 1
+    monkeypatch.setattr(d, "_autotune_mem", {})
+    monkeypatch.setattr(d, "_autotune_loaded", False)
+    assert d._gemm_route(A, B) == route and d._autotune_measured == 1
+    # fp32 stays on the kernel without a measurement
+    assert d._gemm_route(A.float(), B.float()) == "hip" and d._autotune_measured == 1

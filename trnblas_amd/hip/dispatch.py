@@ -25,6 +25,7 @@ fallback-with-warning / REQUIRE switch (:35, :54-80). What changes:
 
 from __future__ import annotations
 
+import json
 import math
 import os
 import warnings
@@ -116,8 +117,11 @@ _AUTOTUNE = _env_flag("TRNBLAS_AUTOTUNE")
 
 
 def set_autotune(enabled: bool) -> None:
-    """Kept for API compatibility (trnblas.set_autotune): the HIP kernels
-    choose their tiles statically, so this only records the flag."""
+    """Measure, per shape bucket, which device GEMM implementation is faster
+    and route by the measurement (trnblas.set_autotune; the reference's sweep
+    over its own tile configurations, nki/dispatch.py:1224-1241, :2255-2325).
+    The candidates here are the HIP kernel and hipBLASLt (torch.matmul) for
+    16-bit operands; results persist in $TRNBLAS_AUTOTUNE_CACHE."""
     global _AUTOTUNE
     _AUTOTUNE = bool(enabled)
 
@@ -311,6 +315,119 @@ def _aten_gemm_wins(a_shape, b_shape, dtype: torch.dtype, contiguous: bool, op: 
     return nb * M * N >= _ATEN_16BIT_MIN_MN and K >= _ATEN_16BIT_MIN_K
 
 
+# ── autotune: measured kernel-vs-hipBLASLt choice per shape bucket ───────────
+#
+# The reference times each of its tile configurations on the first call of a
+# shape bucket and keeps the winner in a JSON file
+# (nki/dispatch.py:1224-1241, :2249-2325). Here the candidates are the HIP
+# kernel and hipBLASLt for 16-bit device GEMMs (fp32 stays on the kernel for
+# accuracy, SYRK on the kernel because it computes only the triangle): on the
+# first call of a bucket both run on the caller's operands (one warm-up and
+# three timed calls each, HIP events on the current stream, best of three)
+# and the faster one serves every later call of that bucket.
+
+_AUTOTUNE_CACHE_FILE = os.environ.get(
+    "TRNBLAS_AUTOTUNE_CACHE", os.path.join("/var/tmp", "trnblas-amd-autotune", "cache.json")
+)
+_autotune_mem: dict[str, str] = {}
+_autotune_loaded = False
+_autotune_measured = 0  # buckets timed by this process (tests read it)
+
+
+def _ceil_pow2(n: int) -> int:
+    p = 1
+    while p < n:
+        p <<= 1
+    return p
+
+
+def _autotune_key(a_shape, b_shape, dtype: torch.dtype, ta: bool, tb: bool, contiguous: bool) -> str:
+    """Shape bucket: dtype, operand layouts and the power-of-two ceilings of
+    batch, M, K, N (the reference's `_autotune_bucket` on M, K, N)."""
+    M, K, N = a_shape[-2], a_shape[-1], b_shape[-1]
+    nb = math.prod(_lib.broadcast_shapes(tuple(a_shape[:-2]), tuple(b_shape[:-2])))
+    name = str(dtype).replace("torch.", "")
+    dims = ",".join(str(_ceil_pow2(max(1, x))) for x in (nb, M, K, N))
+    return f"{name},{int(ta)}{int(tb)}{int(contiguous)},{dims}"
+
+
+def _load_autotune_cache() -> None:
+    global _autotune_mem, _autotune_loaded
+    if _autotune_loaded:
+        return
+    _autotune_loaded = True
+    try:
+        with open(_AUTOTUNE_CACHE_FILE) as f:
+            raw = json.load(f)
+        _autotune_mem = {str(k): str(v) for k, v in raw.items() if v in ("hip", "aten")}
+    except (OSError, ValueError, AttributeError):
+        _autotune_mem = {}
+
+
+def _save_autotune_cache() -> None:
+    try:
+        d = os.path.dirname(_AUTOTUNE_CACHE_FILE)
+        if d:
+            os.makedirs(d, exist_ok=True)
+        tmp = f"{_AUTOTUNE_CACHE_FILE}.{os.getpid()}.tmp"
+        with open(tmp, "w") as f:
+            json.dump(_autotune_mem, f, indent=0, sort_keys=True)
+        os.replace(tmp, _AUTOTUNE_CACHE_FILE)
+    except OSError:
+        pass  # an unwritable cache only costs a re-measurement next process
+
+
+def _time_device_call(fn, reps: int = 3) -> float:
+    """Best of `reps` timed calls (ms, HIP events on the current stream)
+    after one warm-up call."""
+    fn()
+    best = float("inf")
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        e1.synchronize()
+        best = min(best, e0.elapsed_time(e1))
+    return best
+
+
+def _autotune_gemm_route(a: torch.Tensor, b: torch.Tensor, op: str) -> str | None:
+    """'hip' or 'aten' for device operands a, b by measurement (cached per
+    bucket), or None where only one candidate is admissible (the static rule
+    decides)."""
+    global _autotune_measured
+    if op == "syrk" or a.dtype not in (torch.bfloat16, torch.float16) or a.dim() != b.dim():
+        return None
+    contiguous = a.is_contiguous() and b.is_contiguous()
+    if a.dim() > 2 and not contiguous:
+        return None  # a transposed right operand of a 16-bit bmm stays off hipBLASLt
+    ta = a.dim() == 2 and a.stride(-2) == 1 and a.shape[-2] > 1
+    tb = b.dim() == 2 and b.stride(-2) == 1 and b.shape[-2] > 1
+    key = _autotune_key(a.shape, b.shape, a.dtype, ta, tb, contiguous)
+    _load_autotune_cache()
+    hit = _autotune_mem.get(key)
+    if hit is not None:
+        return hit
+    from . import kernels
+
+    try:
+        if a.dim() == 2:
+            t_hip = _time_device_call(lambda: kernels.gemm(a, b))
+        else:
+            a3, b3, _ = _flatten_batch(a, b)
+            t_hip = _time_device_call(lambda: kernels.gemm(a3, b3))
+    except Exception as exc:  # noqa: BLE001
+        _kernel_failed(exc)  # raises under TRNBLAS_REQUIRE_HIP
+        return "aten"  # not cached: the kernel is retried in the next process
+    t_aten = _time_device_call(lambda: torch.matmul(a, b))
+    choice = "aten" if t_aten < t_hip else "hip"
+    _autotune_mem[key] = choice
+    _autotune_measured += 1
+    _save_autotune_cache()
+    return choice
+
+
 def _gemm_route(*tensors, op: str = "gemm", macs: float | None = None, nbytes: int | None = None):
     """'torch', 'hip', 'host', 'upload' or 'aten' for a GEMM-family call."""
     if not _use_hip() or _mixed_dtypes(*tensors) or _wants_grad(*tensors):
@@ -324,6 +441,9 @@ def _gemm_route(*tensors, op: str = "gemm", macs: float | None = None, nbytes: i
             return "aten"
         if policy == "auto" and _backend == "auto" and len(tensors) >= 2:
             a, b = tensors[0], tensors[1]
+            tuned = _autotune_gemm_route(a, b, op) if _AUTOTUNE else None
+            if tuned is not None:
+                return tuned
             if _aten_gemm_wins(a.shape, b.shape, a.dtype, a.is_contiguous() and b.is_contiguous(), op):
                 return "aten"
         return "hip"
