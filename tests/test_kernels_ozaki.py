@@ -112,12 +112,14 @@ def test_split_interleaved_layout(dev, per, k):
     "M,K,N,k",
     [(64, 64, 64, 8), (130, 4100, 7, 8), (200, 9000, 31, 8), (300, 257, 520, 8), (1, 1, 1, 8),
      (65, 129, 63, 8), (200, 9000, 31, 1), (130, 4100, 70, 3), (300, 257, 520, 9),
-     (200, 9000, 31, 10), (65, 129, 63, 11), (130, 4100, 70, 12), (33, 50000, 20, 12)],
+     (200, 9000, 31, 10), (65, 129, 63, 10), (130, 4100, 70, 10), (33, 60000, 20, 10),
+     (65, 129, 63, 11), (130, 4100, 70, 12), (33, 50000, 20, 12)],
 )
 def test_fast_gemm_interleaved_equals_plain(dev, M, K, N, k):
     # same digits, same int32 diagonal sums, same fp64 recombination order:
     # the interleaved-digit kernel must match the plain-layout one bit for bit
-    # (K = 50000 at k = 12 crosses the int32 flush of the diagonals)
+    # (K = 50000 at k = 12 and K = 60000 at k = 10 cross the int32 flush of the
+    # diagonals; k = 10 runs its own two-workgroups-per-CU layout)
     from trnblas_amd.hip import kernels
 
     A, B = inputs(M, K, N, seed=M + 3 * N + k)

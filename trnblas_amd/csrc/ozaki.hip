@@ -689,6 +689,27 @@ __global__ __launch_bounds__(256, NB == 1 ? 2 : 1) void oz_fast_kernel(OzArgs g)
   if (nsteps == 0) flush(true);
 }
 
+// One 16-byte-per-lane LDS DMA (buffer_load_dwordx4 ... lds) issued by
+// inline asm, so the compiler does not see it: it then places no wait for it
+// before LDS reads of the other stage, and the kernel waits for it itself
+// (`s_waitcnt vmcnt` before the barrier that publishes the stage). Lane l's
+// 16 bytes at voff + soff of the resource land at lds + 16 l.
+__device__ __forceinline__ void oz_dma16_asm(const void* base, const void* lds, uint32_t voff,
+                                             int soff) {
+  const uint64_t b = (uint64_t)base;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(b >> 32) & 0xffffu));
+  r[2] = 0x7ffffff0;
+  r[3] = 0x00020000;
+  const int m = __builtin_amdgcn_readfirstlane(
+      (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(m), "v"(voff), "s"(r), "s"(soff)
+               : "memory", "m0");
+}
+
 // Fast mode on interleaved digits of any slice count KS (1..12): row r's
 // 32-wide K chunk kc holds the KS slices' 32 bytes side by side at
 // r * ld + kc * 32 KS + s * 32 (trnblas_hip_ozaki_split, per_row bit 1), so
@@ -711,13 +732,25 @@ __global__ __launch_bounds__(256, NB == 1 ? 2 : 1) void oz_fast_kernel(OzArgs g)
 // block b fills slot q = 64 b + l, i.e. group q % (2 KS + 1) of row
 // q / (2 KS + 1); pad slots and rows outside the matrix read zeros without a
 // memory access.
+//
+// KS = 10 (the slice count at which C5's wide-range data reaches host-fp64
+// accuracy) is laid out to keep two workgroups per CU ("LZ"): rows of 2 KS =
+// 20 groups with no pad, group j of row r in slot j ^ ((r >> 2) & 3) (the
+// 16 rows of a fragment read: 4 (r % 4) + the XOR term covers 16 distinct
+// bank groups), so a stage is 40 KiB and two workgroups fit the 160 KiB of
+// LDS; and B's fragments are read one slice ahead of their MFMAs instead of
+// all at once (accumulators 160 + A fragments 40 + B 8 VGPRs fit the 256 of
+// two waves per SIMD). Those reads follow the next step's DMA, so that DMA
+// is issued by inline asm (oz_dma16_asm) and waited for explicitly.
 template <int KS>
-__global__ __launch_bounds__(256, KS <= 9 ? 2 : 1) void oz_fast_ilk_kernel(OzArgs g) {
+__global__ __launch_bounds__(256, KS <= 10 ? 2 : 1) void oz_fast_ilk_kernel(OzArgs g) {
   constexpr int T = 64, W = 4;
-  constexpr int RG = 2 * KS, PG = RG + 1;  // groups of a row's step, LDS pitch in groups
+  constexpr bool LZ = KS == 10;
+  constexpr int RG = 2 * KS, PG = LZ ? RG : RG + 1;  // groups of a row's step, LDS pitch
   constexpr int NIP = (T * PG + 63) / 64;  // 1 KiB DMA blocks per panel
   constexpr int OPA = NIP * 1024, STAGE = 2 * OPA;
   constexpr int PER = (NIP + W - 1) / W;   // blocks per wave, panel and step
+  static_assert(!LZ || (RG % 4 == 0 && T * PG % 64 == 0), "LZ layout: 4-group XOR, whole blocks");
   __shared__ __attribute__((aligned(16))) int8_t lds[2 * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -733,7 +766,8 @@ __global__ __launch_bounds__(256, KS <= 9 ? 2 : 1) void oz_fast_ilk_kernel(OzArg
   uint32_t voffA[PER], voffB[PER];
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
-    const int q = 64 * (w + u * W) + lane, r = q / PG, j = q % PG;
+    const int q = 64 * (w + u * W) + lane, r = q / PG;
+    const int j = LZ ? (q % PG) ^ ((r >> 2) & 3) : q % PG;  // the group slot q holds
     const bool in = j < RG && r < T;
     voffA[u] = (in && m0 + r < g.M) ? (uint32_t)(r * g.lda + 16 * j) : kOzOob;
     voffB[u] = (in && n0 + r < g.N) ? (uint32_t)(r * g.ldb + 16 * j) : kOzOob;
@@ -747,21 +781,31 @@ __global__ __launch_bounds__(256, KS <= 9 ? 2 : 1) void oz_fast_ilk_kernel(OzArg
       if (NIP % W != 0 && u + 1 == PER && w + u * W >= NIP) break;
       int8_t* dst = lds + buf * STAGE + (w + u * W) * 1024;
       const uint32_t va = voffA[u], vb = voffB[u];
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(oz_rsrc(baseA),
-                                               (__attribute__((address_space(3))) void*)dst, 16,
-                                               va, soff, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(oz_rsrc(baseB),
-                                               (__attribute__((address_space(3))) void*)(dst + OPA),
-                                               16, vb, soff, 0, 0);
+      if constexpr (LZ) {
+        oz_dma16_asm(baseA, dst, va, soff);
+        oz_dma16_asm(baseB, dst + OPA, vb, soff);
+      } else {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(oz_rsrc(baseA),
+                                                 (__attribute__((address_space(3))) void*)dst, 16,
+                                                 va, soff, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            oz_rsrc(baseB), (__attribute__((address_space(3))) void*)(dst + OPA), 16, vb, soff, 0,
+            0);
+      }
     }
   };
 
   // Wave w: rows 32 (w & 1), columns 32 (w >> 1) of the tile. Lane l reads
   // row l % 32 of its block, bytes 16 (l / 32) .. +15 of each slice's 32.
+  // LZ: group 2 s + h sits in slot (2 s + h) ^ x, x = (row >> 2) & 3, i.e.
+  // at 32 (s ^ (x >> 1)) + 16 (h ^ (x & 1)): s + x/2 for even s, s - x/2 for
+  // odd s (two per-lane bases, the slice offset an immediate).
   const int wm = w & 1, wn = w >> 1;
   const int h = lane >> 5;
-  const int rowA = (32 * wm + (lane & 31)) * 16 * PG + 16 * h;
-  const int rowB = OPA + (32 * wn + (lane & 31)) * 16 * PG + 16 * h;
+  const int x = LZ ? ((lane & 31) >> 2) & 3 : 0;
+  const int hx = 16 * (h ^ (x & 1)), x1 = 32 * (x >> 1);
+  const int rowA = (32 * wm + (lane & 31)) * 16 * PG + hx;
+  const int rowB = OPA + (32 * wn + (lane & 31)) * 16 * PG + hx;
   i32x16 acc[KS];
 #pragma unroll
   for (int d = 0; d < KS; ++d)
@@ -800,11 +844,16 @@ __global__ __launch_bounds__(256, KS <= 9 ? 2 : 1) void oz_fast_ilk_kernel(OzArg
     }
   };
 
+  // the fragment of slice s2 from the A (base rowA) or B (rowB) panel
+  auto frag = [&](const int8_t* buf, int row, int s2) __attribute__((always_inline)) {
+    const int o = LZ ? ((s2 & 1) ? row - x1 : row + x1) : row;
+    return *reinterpret_cast<const i32x4*>(buf + o + 32 * s2);
+  };
   auto read = [&](const int8_t* buf, i32x4 (&fa)[KS], i32x4 (&fb)[KS]) __attribute__((always_inline)) {
 #pragma unroll
     for (int s2 = 0; s2 < KS; ++s2) {
-      fa[s2] = *reinterpret_cast<const i32x4*>(buf + rowA + 32 * s2);
-      fb[s2] = *reinterpret_cast<const i32x4*>(buf + rowB + 32 * s2);
+      fa[s2] = frag(buf, rowA, s2);
+      fb[s2] = frag(buf, rowB, s2);
     }
   };
   auto mfmas = [&](const i32x4 (&fa)[KS], const i32x4 (&fb)[KS]) __attribute__((always_inline)) {
@@ -821,12 +870,34 @@ __global__ __launch_bounds__(256, KS <= 9 ? 2 : 1) void oz_fast_ilk_kernel(OzArg
     load(s0, 0);
     for (int s = s0; s < s1; ++s) {
       const int cur = (s - s0) & 1;
-      __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA of step s has landed
-      __syncthreads();                // every wave's has; stage cur ^ 1 is free
-      i32x4 fa[KS], fb[KS];
-      read(lds + cur * STAGE, fa, fb);
-      if (s + 1 < s1) load(s + 1, cur ^ 1);
-      mfmas(fa, fb);
+      const int8_t* buf = lds + cur * STAGE;
+      if constexpr (LZ) {
+        // this wave's DMA of step s has landed, then every wave's has (and
+        // every wave is done reading stage cur ^ 1)
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        i32x4 fa[KS];
+#pragma unroll
+        for (int s2 = 0; s2 < KS; ++s2) fa[s2] = frag(buf, rowA, s2);
+        i32x4 fb = frag(buf, rowB, 0);
+        if (s + 1 < s1) load(s + 1, cur ^ 1);
+#pragma unroll
+        for (int tt = 0; tt < KS; ++tt) {
+          i32x4 fn = fb;
+          if (tt + 1 < KS) fn = frag(buf, rowB, tt + 1);
+#pragma unroll
+          for (int s2 = 0; s2 < KS - tt; ++s2)
+            acc[s2 + tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s2], fb, acc[s2 + tt], 0, 0, 0);
+          fb = fn;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA of step s has landed
+        __syncthreads();                // every wave's has; stage cur ^ 1 is free
+        i32x4 fa[KS], fb[KS];
+        read(buf, fa, fb);
+        if (s + 1 < s1) load(s + 1, cur ^ 1);
+        mfmas(fa, fb);
+      }
     }
     flush(s0 == 0);
   }
