@@ -704,10 +704,15 @@ __device__ __forceinline__ void oz_dma16_asm(const void* base, const void* lds, 
   r[3] = 0x00020000;
   const int m = __builtin_amdgcn_readfirstlane(
       (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(m), "v"(voff), "s"(r), "s"(soff)
-               : "memory", "m0");
+  // m0 (the LDS address of the DMA) is saved and restored around the load,
+  // so the statement leaves every register the compiler may use as it was
+  int saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(m), "v"(voff), "s"(r), "s"(soff)
+      : "memory");
 }
 
 // Fast mode on interleaved digits of any slice count KS (1..12): row r's
