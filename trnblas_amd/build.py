@@ -6,6 +6,7 @@ exports the C ABI of `include/trnblas_hip.h`; Python loads it with ctypes
 (`trnblas_amd/hip/_lib.py`). No CUDA, no HIP/CUDA dual paths.
 
     python -m trnblas_amd.build          # or trnblas_amd.build.build()
+    python -m trnblas_amd.build --asan   # host-side ASan build, lib/asan/
 """
 
 from __future__ import annotations
@@ -54,18 +55,28 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
+# Host-side AddressSanitizer (the C-ABI argument checks, error paths and
+# drivers; device code is built as usual): each -fsanitize applies to the host
+# pass only.
+ASAN_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer", "-g"]
+
+
+def build(verbose: bool = False, jobs: int | None = None, asan: bool = False) -> Path:
     """Compile every HIP source for gfx950 and link the shared library.
-    Always rebuilds (this is the build check). Returns the library path."""
-    LIBDIR.mkdir(exist_ok=True)
-    objdir = LIBDIR / "obj"
+    Always rebuilds (this is the build check). Returns the library path.
+    asan: a host-ASan build into lib/asan/ instead (load it with
+    TRNBLAS_HIP_LIB and the clang ASan runtime preloaded)."""
+    libdir = LIBDIR / "asan" if asan else LIBDIR
+    libdir.mkdir(parents=True, exist_ok=True)
+    objdir = libdir / "obj"
     objdir.mkdir(exist_ok=True)
     cc = hipcc()
     srcs = sources()
+    extra = ASAN_FLAGS if asan else []
 
     def compile_one(src: Path) -> Path:
         obj = objdir / (src.stem + ".o")
-        cmd = [cc, *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = [cc, *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True)
@@ -76,9 +87,10 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     n = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(n) as ex:
         objs = list(ex.map(compile_one, srcs))
-    out = LIBDIR / LIBNAME
-    tmp = LIBDIR / (LIBNAME + ".tmp")
-    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    out = libdir / LIBNAME
+    tmp = libdir / (LIBNAME + ".tmp")
+    link_extra = ["-Xarch_host", "-fsanitize=address"] if asan else []
+    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *link_extra, "-o", str(tmp), *map(str, objs)]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -89,5 +101,5 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
+    path = build(verbose="-v" in sys.argv, asan="--asan" in sys.argv)
     print(path)
