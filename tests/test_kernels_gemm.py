@@ -379,3 +379,29 @@ def test_syrk_16bit_trans_aligned(dev, dtype, tol):
     ref = Ad @ Ad.T + 0.5 * Cs
     den = Ad.abs() @ Ad.abs().T + 0.5 * Cs.abs()
     assert ((D.double() - ref).abs() / den).max().item() <= tol
+
+
+@pytest.mark.parametrize(
+    "batch,M,N,K",
+    [(1, 2048, 2048, 512), (1, 1900, 2100, 1000), (1, 2000, 1930, 700), (2, 1024, 2048, 768),
+     (1, 2048, 2048, 2048)],
+)
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_gemm_narrow_tiles(dev, batch, M, N, K, ta, tb):
+    # launches whose 128 x 128 tiles fill at most one slot per CU of the
+    # MI355X's 256 CUs and whose 128 x 64 tiles fill 90-100 % of two run the
+    # 128 x 64 kernel (whole tiles, no stream-K pass): every layout, ragged
+    # edges, a batch, alpha / beta, at the 1e-6 gate
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(M + N + K + 2 * ta + tb)
+    A = torch.randn(batch, K, M, generator=g).transpose(1, 2) if ta else torch.randn(batch, M, K, generator=g)
+    B = torch.randn(batch, N, K, generator=g).transpose(1, 2) if tb else torch.randn(batch, K, N, generator=g)
+    C = torch.randn(batch, M, N, generator=g)
+    if batch == 1:
+        D = kernels.gemm(A[0].to(dev), B[0].to(dev), 1.5, -0.5, C[0].to(dev)).unsqueeze(0)
+    else:
+        D = kernels.gemm(A.to(dev), B.to(dev), 1.5, -0.5, C.to(dev))
+    torch.cuda.synchronize()
+    err = max(_cw_err(D[b].cpu(), A[b], B[b], 1.5, -0.5, C[b]) for b in range(batch))
+    assert err <= 1e-6, err

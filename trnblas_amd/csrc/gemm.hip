@@ -564,16 +564,26 @@ __device__ __forceinline__ s16x4 lds_tr16(const void* p) {
 // row's bytes exactly once. Ragged edges: a group outside the matrix gets
 // an offset past the buffer's records and reads as zeros (VEC operands:
 // every 16-byte group is wholly inside or outside).
-template <typename T, bool AKC, bool BKC, bool SYRK>
+//
+// BN = 64 (fp32 GEMM only): 128 x 64 tiles, waves of 64 x 32 (one MFMA block
+// column), a 64-row B panel (8 DMA blocks, two per wave; M/N-contiguous rows
+// of 64 values keep the same swizzle). For a launch whose 128 x 128 tiles
+// would fill at most one workgroup slot per CU (the stream-K split of every
+// tile plus a fixup pass), 128 x 64 tiles fill two slots per CU with whole
+// tiles instead (launch_narrow).
+template <typename T, bool AKC, bool BKC, bool SYRK, int BN = 128>
 __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
   constexpr int EV = 16 / sizeof(T);  // values per 16-byte group
-  constexpr int BM = 128, BN = 128, BK = 128 / sizeof(T), WM = 64, WN = 64, FM = 2, FN = 2;
+  constexpr int BM = 128, BK = 128 / sizeof(T), WM = 64, WN = BN / 2, FM = 2, FN = WN / 32;
+  static_assert(BN == 128 || (BN == 64 && !SYRK), "tile shapes: 128 x 128, or 128 x 64 for GEMM");
   constexpr int CH = 2 * EV;          // k per fragment chunk (both lane halves)
-  constexpr int PANEL = 128 * BK;     // values of one operand panel (16 KiB)
-  constexpr int MG = 128 / EV;        // 16-byte groups in an M/N-contiguous row
+  constexpr int PANEL = 128 * BK;     // values of the A panel (16 KiB)
+  constexpr int BPANEL = BN * BK;     // values of the B panel
+  constexpr int MGA = 128 / EV, MGB = BN / EV;  // 16-byte groups in an M/N-contiguous row
+  constexpr int NBW = BPANEL * (int)sizeof(T) / 4096;  // B DMA blocks per wave (4 or 2)
   constexpr int MSW = 2 * sizeof(T);  // M/N swizzle (groups)
-  __shared__ __attribute__((aligned(16))) T st0[2 * PANEL];
-  __shared__ __attribute__((aligned(16))) T st1[2 * PANEL];
+  __shared__ __attribute__((aligned(16))) T st0[PANEL + BPANEL];
+  __shared__ __attribute__((aligned(16))) T st1[PANEL + BPANEL];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -600,36 +610,38 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
       // rows / columns of the matrix left from the panel's corner
       const int ra = AKC ? M - m0 : K - k0, ca = AKC ? K - k0 : M - m0;
       const int rb = BKC ? N - n0 : K - k0, cb = BKC ? K - k0 : N - n0;
-      // wave w fills blocks 4 w .. 4 w + 3 of each panel. KC block b: row
-      // 8 b + l / 8, global group (l % 8) ^ swizzle; MN block b: row
-      // (64 / MG) b + l / MG, global group (l % MG) ^ swizzle.
-      auto geo = [&](bool kc, int u, int& row, int& grp) __attribute__((always_inline)) {
-        const int b = 4 * wave + u;
+      // wave w fills blocks nb w .. nb w + nb - 1 of a panel (nb = 4 for A,
+      // NBW for B). KC block b: row 8 b + l / 8, global group (l % 8) ^
+      // swizzle; MN block b (rows of mg groups): row (64 / mg) b + l / mg,
+      // global group (l % mg) ^ swizzle.
+      auto geo = [&](bool kc, int mg, int nb, int u, int& row, int& grp)
+                     __attribute__((always_inline)) {
+        const int b = nb * wave + u;
         if (kc) {
           row = 8 * b + (lane >> 3);
           grp = (lane & 7) ^ ((row >> 1) & 7);
         } else {
-          row = (64 / MG) * b + lane / MG;
-          grp = (lane % MG) ^ (MSW * ((row / EV) & 1));
+          row = (64 / mg) * b + lane / mg;
+          grp = (lane % mg) ^ (MSW * ((row / EV) & 1));
         }
       };
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         int rw, gp;
-        geo(AKC, u, rw, gp);
+        geo(AKC, MGA, 4, u, rw, gp);
         const bool oka = rw < ra && EV * gp < ca;
         const uint32_t va =
             oka ? (uint32_t)((int64_t)rw * g.lda * (int64_t)sizeof(T) + 16 * gp) : kOob;
         lds_dma16(pa, st + (4 * wave + u) * (1024 / sizeof(T)), va);
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < NBW; ++u) {
         int rw, gp;
-        geo(BKC, u, rw, gp);
+        geo(BKC, MGB, NBW, u, rw, gp);
         const bool okb = rw < rb && EV * gp < cb;
         const uint32_t vb =
             okb ? (uint32_t)((int64_t)rw * g.ldb * (int64_t)sizeof(T) + 16 * gp) : kOob;
-        lds_dma16(pb, st + PANEL + (4 * wave + u) * (1024 / sizeof(T)), vb);
+        lds_dma16(pb, st + PANEL + (NBW * wave + u) * (1024 / sizeof(T)), vb);
       }
     };
 
@@ -649,8 +661,9 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
 
     // Fragment of the lane's row r (32 rows per MFMA block) at k offset kk
     // (EV consecutive k, kk a multiple of EV): one 16-byte read from a
-    // K-contiguous panel, EV column reads from an M/N-contiguous one.
-    auto frag = [&](const T* p, bool kc, int r, int kk) __attribute__((always_inline)) {
+    // K-contiguous panel, EV column reads from an M/N-contiguous one (rows
+    // of W values: the panel's width).
+    auto frag = [&](const T* p, bool kc, int r, int kk, int W) __attribute__((always_inline)) {
       if (kc)
         return *reinterpret_cast<const i32x4*>(p + r * BK + EV * ((kk / EV) ^ ((r >> 1) & 7)));
       if constexpr (sizeof(T) == 2) {
@@ -661,13 +674,13 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
         const int i = lane & 15;
         const int c0 = r - i + 4 * (i & 3);
         const int k1 = kk + (i >> 2);
-        const T* s0 = p + k1 * 128 + EV * ((c0 / EV) ^ (MSW * ((kk / EV) & 1))) + (c0 & 4);
+        const T* s0 = p + k1 * W + EV * ((c0 / EV) ^ (MSW * ((kk / EV) & 1))) + (c0 & 4);
         union {
           s16x4 h[2];
           i32x4 v;
         } u;
         u.h[0] = lds_tr16(s0);
-        u.h[1] = lds_tr16(s0 + 4 * 128);
+        u.h[1] = lds_tr16(s0 + 4 * W);
         return u.v;
       }
       const T* q = p + EV * ((r / EV) ^ (MSW * ((kk / EV) & 1))) + (r % EV);
@@ -676,7 +689,7 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
         T e[EV];
       } u;
 #pragma unroll
-      for (int e = 0; e < EV; ++e) u.e[e] = q[(kk + e) * 128];
+      for (int e = 0; e < EV; ++e) u.e[e] = q[(kk + e) * W];
       return u.v;
     };
     // One k-tile from stage `cur`: every fragment of the k-tile is read into
@@ -700,10 +713,11 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
         for (int c = 0; c < BK / CH; ++c) {
           const int kk = c * CH + (lane >> 5) * EV;
 #pragma unroll
-          for (int i = 0; i < FM; ++i) fa[c][i] = frag(cur, AKC, wm0 + i * 32 + (lane & 31), kk);
+          for (int i = 0; i < FM; ++i)
+            fa[c][i] = frag(cur, AKC, wm0 + i * 32 + (lane & 31), kk, 128);
 #pragma unroll
           for (int j = 0; j < FN; ++j)
-            fb[c][j] = frag(cur + PANEL, BKC, wn0 + j * 32 + (lane & 31), kk);
+            fb[c][j] = frag(cur + PANEL, BKC, wn0 + j * 32 + (lane & 31), kk, BN);
         }
       }
       if (next >= 0) dma(oth, next);
@@ -780,7 +794,7 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
 template <typename T, int BM, int BN, bool SYRK>
 __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs g) {
   constexpr int MAXC = 64;  // contributors per tile (choose_sk keeps to it)
-  constexpr int ROWS = 8;
+  constexpr int ROWS = 1024 / BN;
   static_assert(ROWS * BN / 4 == 256, "one float4 per thread");
   __shared__ int64_t src[MAXC];
   __shared__ int ncontrib;
@@ -888,6 +902,37 @@ static int choose_sk(GemmArgs& g, int occupancy, size_t ws_bytes) {
   return (int)groups;
 }
 
+// 128 x 64 tiles pay where 128 x 128 tiles fill at most one workgroup slot
+// per CU (every tile would be split by stream-K and summed by the fixup
+// pass) and 128 x 64 tiles fill 90-100 % of the two slots per CU in one
+// round of whole tiles, with k-iterations enough (16) to amortise the
+// epilogue. Measured (fp32, against the stream-K split of 128 x 128 tiles):
+// 2048^2 x 512 102.6 against 74.8 TFLOP/s, 1900 x 2100 x 1000 107.4 against
+// 79.2, 4096 x 1024 x 2048 123.7 against 115.5, 2048^3 A^T B + 0.5 C (C1)
+// 148.5 against 151.9 us.
+static bool narrow_tiles_pay(const GemmArgs& g) {
+  const int64_t cus = device_cus();
+  if (g.ntiles > cus || g.nk < 16) return false;
+  const int64_t n64 = (int64_t)g.tiles_m * ((g.N + 63) / 64) * g.batch;
+  return n64 <= 2 * cus && 10 * n64 >= 9 * 2 * cus;
+}
+
+constexpr size_t kNarrowLdsPad = 16384;
+
+template <bool AKC, bool BKC>
+static int launch_narrow(GemmArgs g, hipStream_t s) {
+  g.tiles_n = (g.N + 63) / 64;
+  g.ntiles = g.tiles_m * g.tiles_n * g.batch;
+  g.sk_groups = 0;
+  g.dp_tiles = 0;
+  // 48 KiB of LDS and ~150 VGPRs would let three workgroups share a CU, so
+  // a one-round grid of 2 per CU could land 3 + 1 on some CUs; 16 KiB of
+  // unused dynamic LDS caps it at two (64 KiB each)
+  hipLaunchKernelGGL((gemm_dma_kernel<float, AKC, BKC, false, 64>), dim3(g.ntiles), dim3(256),
+                     kNarrowLdsPad, s, g);
+  return check_launch("trnblas_hip_gemm");
+}
+
 template <typename T, bool AKC, bool BKC, bool VEC, bool SYRK>
 static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   using C = Cfg<T>;
@@ -895,6 +940,9 @@ static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   constexpr int BK = DMA ? 128 / (int)sizeof(T) : C::template bk<VEC>();
   g.nk = (g.K + BK - 1) / BK;
   g.span = chain_length(g.K, (int)sizeof(T)) / BK;  // even for the DMA kernel's k-tiles
+  if constexpr (DMA && sizeof(T) == 4 && !SYRK) {
+    if (narrow_tiles_pay(g)) return launch_narrow<AKC, BKC>(g, s);
+  }
   void (*kern)(GemmArgs);
   if constexpr (DMA)
     kern = gemm_dma_kernel<T, AKC, BKC, SYRK>;
