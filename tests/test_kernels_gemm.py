@@ -384,14 +384,16 @@ def test_syrk_16bit_trans_aligned(dev, dtype, tol):
 @pytest.mark.parametrize(
     "batch,M,N,K",
     [(1, 2048, 2048, 512), (1, 1900, 2100, 1000), (1, 2000, 1930, 700), (2, 1024, 2048, 768),
-     (1, 2048, 2048, 2048)],
+     (1, 2048, 2048, 2048), (1, 1024, 1024, 1024), (1, 512, 512, 8192), (1, 1280, 1272, 1280),
+     (3, 256, 520, 2048), (1, 96, 200, 30000)],
 )
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
 def test_gemm_narrow_tiles(dev, batch, M, N, K, ta, tb):
     # launches whose 128 x 128 tiles fill at most one slot per CU of the
-    # MI355X's 256 CUs and whose 128 x 64 tiles fill 90-100 % of two run the
-    # 128 x 64 kernel (whole tiles, no stream-K pass): every layout, ragged
-    # edges, a batch, alpha / beta, at the 1e-6 gate
+    # MI355X's 256 CUs run the 128 x 64 kernel: whole tiles where they fill
+    # one round of two slots per CU, else split by stream-K over 128 x 64
+    # tiles (up to the fixup's 64 contributors at K = 30000): every layout,
+    # ragged edges, a batch, alpha / beta, at the 1e-6 gate
     from trnblas_amd.hip import kernels
 
     g = torch.Generator().manual_seed(M + N + K + 2 * ta + tb)

@@ -567,10 +567,8 @@ __device__ __forceinline__ s16x4 lds_tr16(const void* p) {
 //
 // BN = 64 (fp32 GEMM only): 128 x 64 tiles, waves of 64 x 32 (one MFMA block
 // column), a 64-row B panel (8 DMA blocks, two per wave; M/N-contiguous rows
-// of 64 values keep the same swizzle). For a launch whose 128 x 128 tiles
-// would fill at most one workgroup slot per CU (the stream-K split of every
-// tile plus a fixup pass), 128 x 64 tiles fill two slots per CU with whole
-// tiles instead (launch_narrow).
+// of 64 values keep the same swizzle), for launches whose 128 x 128 tiles
+// would fill at most one workgroup slot per CU (launch_narrow).
 template <typename T, bool AKC, bool BKC, bool SYRK, int BN = 128>
 __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
   constexpr int EV = 16 / sizeof(T);  // values per 16-byte group
@@ -903,34 +901,38 @@ static int choose_sk(GemmArgs& g, int occupancy, size_t ws_bytes) {
 }
 
 // 128 x 64 tiles pay where 128 x 128 tiles fill at most one workgroup slot
-// per CU (every tile would be split by stream-K and summed by the fixup
-// pass) and 128 x 64 tiles fill 90-100 % of the two slots per CU in one
-// round of whole tiles, with k-iterations enough (16) to amortise the
-// epilogue. Measured (fp32, against the stream-K split of 128 x 128 tiles):
-// 2048^2 x 512 102.6 against 74.8 TFLOP/s, 1900 x 2100 x 1000 107.4 against
-// 79.2, 4096 x 1024 x 2048 123.7 against 115.5, 2048^3 A^T B + 0.5 C (C1)
-// 148.5 against 151.9 us.
+// per CU (k-iterations >= 16): twice the tiles for the same grid, so a
+// one-round grid of 128 x 128 tiles split by stream-K becomes whole 128 x 64
+// tiles (no partials, no fixup launch), and a smaller one is split into half
+// as many pieces per tile, with half the partial-tile bytes. Measured (fp32,
+// microseconds, against the stream-K split of 128 x 128 tiles): 512^3 14.5 /
+// 19.3, 1024^3 31.1 / 35.0, 1280^3 53.2 / 62.1, 512^2 x 8192 49.0 / 54.8,
+// 2048^2 x 512 (102.6 / 74.8 TFLOP/s), 1900 x 2100 x 1000 (107.4 / 79.2
+// TFLOP/s), C1 (2048^3 A^T B + 0.5 C) 148.5 / 151.9; 1536^2 x 2048 and
+// 256^2 x 16384 unchanged.
 static bool narrow_tiles_pay(const GemmArgs& g) {
-  const int64_t cus = device_cus();
-  if (g.ntiles > cus || g.nk < 16) return false;
-  const int64_t n64 = (int64_t)g.tiles_m * ((g.N + 63) / 64) * g.batch;
-  return n64 <= 2 * cus && 10 * n64 >= 9 * 2 * cus;
+  return g.ntiles <= device_cus() && g.nk >= 16;
 }
 
 constexpr size_t kNarrowLdsPad = 16384;
+static int choose_sk(GemmArgs& g, int occupancy, size_t ws_bytes);
 
 template <bool AKC, bool BKC>
-static int launch_narrow(GemmArgs g, hipStream_t s) {
+static int launch_narrow(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   g.tiles_n = (g.N + 63) / 64;
   g.ntiles = g.tiles_m * g.tiles_n * g.batch;
-  g.sk_groups = 0;
-  g.dp_tiles = 0;
   // 48 KiB of LDS and ~150 VGPRs would let three workgroups share a CU, so
   // a one-round grid of 2 per CU could land 3 + 1 on some CUs; 16 KiB of
   // unused dynamic LDS caps it at two (64 KiB each)
-  hipLaunchKernelGGL((gemm_dma_kernel<float, AKC, BKC, false, 64>), dim3(g.ntiles), dim3(256),
+  g.sk_groups = choose_sk(g, 2, ws_bytes);  // (its slot check assumes 64 KiB partials: 32 here)
+  const int grid = g.sk_groups ? g.sk_groups : g.ntiles;
+  hipLaunchKernelGGL((gemm_dma_kernel<float, AKC, BKC, false, 64>), dim3(grid), dim3(256),
                      kNarrowLdsPad, s, g);
-  return check_launch("trnblas_hip_gemm");
+  int rc = check_launch("trnblas_hip_gemm");
+  if (rc || !g.sk_groups) return rc;
+  hipLaunchKernelGGL((gemm_fixup_kernel<float, 128, 64, false>),
+                     dim3(g.ntiles - g.dp_tiles, 128 / 16), dim3(256), 0, s, g);
+  return check_launch("trnblas_hip_gemm(fixup)");
 }
 
 template <typename T, bool AKC, bool BKC, bool VEC, bool SYRK>
@@ -941,7 +943,7 @@ static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   g.nk = (g.K + BK - 1) / BK;
   g.span = chain_length(g.K, (int)sizeof(T)) / BK;  // even for the DMA kernel's k-tiles
   if constexpr (DMA && sizeof(T) == 4 && !SYRK) {
-    if (narrow_tiles_pay(g)) return launch_narrow<AKC, BKC>(g, s);
+    if (narrow_tiles_pay(g)) return launch_narrow<AKC, BKC>(g, ws_bytes, s);
   }
   void (*kern)(GemmArgs);
   if constexpr (DMA)
