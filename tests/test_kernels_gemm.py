@@ -407,3 +407,22 @@ def test_gemm_narrow_tiles(dev, batch, M, N, K, ta, tb):
     torch.cuda.synchronize()
     err = max(_cw_err(D[b].cpu(), A[b], B[b], 1.5, -0.5, C[b]) for b in range(batch))
     assert err <= 1e-6, err
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2.0**-8), (torch.float16, 2.0**-10)])
+@pytest.mark.parametrize("M,N,K", [(1024, 1024, 4096), (1280, 1272, 1280), (512, 520, 8192), (2048, 2048, 2048)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_gemm_16bit_narrow_tiles(dev, dtype, tol, M, N, K, ta, tb):
+    # 16-bit launches with at most one 128 x 128 tile per CU and >= 20
+    # 64-wide k-tiles run the 128 x 64 kernel (stream-K where the grid is
+    # small); every layout, a ragged edge, against fp64 of the rounded inputs
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(M + N + K + 2 * ta + tb)
+    A = (torch.randn(K, M, generator=g).T if ta else torch.randn(M, K, generator=g)).to(dtype)
+    B = (torch.randn(N, K, generator=g).T if tb else torch.randn(K, N, generator=g)).to(dtype)
+    C = torch.randn(M, N, generator=g).to(dtype)
+    D = kernels.gemm(A.to(dev), B.to(dev), 1.0, 0.5, C.to(dev)).cpu()
+    ref = A.double() @ B.double() + 0.5 * C.double()
+    den = A.double().abs() @ B.double().abs() + 0.5 * C.double().abs()
+    assert ((D.double() - ref).abs() / den).max().item() <= tol

@@ -565,7 +565,7 @@ __device__ __forceinline__ s16x4 lds_tr16(const void* p) {
 // an offset past the buffer's records and reads as zeros (VEC operands:
 // every 16-byte group is wholly inside or outside).
 //
-// BN = 64 (fp32 GEMM only): 128 x 64 tiles, waves of 64 x 32 (one MFMA block
+// BN = 64 (GEMM only): 128 x 64 tiles, waves of 64 x 32 (one MFMA block
 // column), a 64-row B panel (8 DMA blocks, two per wave; M/N-contiguous rows
 // of 64 values keep the same swizzle), for launches whose 128 x 128 tiles
 // would fill at most one workgroup slot per CU (launch_narrow).
@@ -909,15 +909,17 @@ static int choose_sk(GemmArgs& g, int occupancy, size_t ws_bytes) {
 // 19.3, 1024^3 31.1 / 35.0, 1280^3 53.2 / 62.1, 512^2 x 8192 49.0 / 54.8,
 // 2048^2 x 512 (102.6 / 74.8 TFLOP/s), 1900 x 2100 x 1000 (107.4 / 79.2
 // TFLOP/s), C1 (2048^3 A^T B + 0.5 C) 148.5 / 151.9; 1536^2 x 2048 and
-// 256^2 x 16384 unchanged.
-static bool narrow_tiles_pay(const GemmArgs& g) {
-  return g.ntiles <= device_cus() && g.nk >= 16;
+// 256^2 x 16384 unchanged. bf16 / fp16 (64-wide k-tiles): 2048^3 28.1 / 38.1,
+// 1280^3 22.9 / 26.5, 1024^2 x 4096 24.6 / 27.9, 512^2 x 8192 25.5 / 29.7;
+// at 1024^3 (16 k-tiles) 20.9 / 20.1, hence 20 k-tiles at least there.
+static bool narrow_tiles_pay(const GemmArgs& g, int elem_bytes) {
+  return g.ntiles <= device_cus() && g.nk >= (elem_bytes == 4 ? 16 : 20);
 }
 
 constexpr size_t kNarrowLdsPad = 16384;
 static int choose_sk(GemmArgs& g, int occupancy, size_t ws_bytes);
 
-template <bool AKC, bool BKC>
+template <typename T, bool AKC, bool BKC>
 static int launch_narrow(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   g.tiles_n = (g.N + 63) / 64;
   g.ntiles = g.tiles_m * g.tiles_n * g.batch;
@@ -926,11 +928,11 @@ static int launch_narrow(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   // unused dynamic LDS caps it at two (64 KiB each)
   g.sk_groups = choose_sk(g, 2, ws_bytes);  // (its slot check assumes 64 KiB partials: 32 here)
   const int grid = g.sk_groups ? g.sk_groups : g.ntiles;
-  hipLaunchKernelGGL((gemm_dma_kernel<float, AKC, BKC, false, 64>), dim3(grid), dim3(256),
+  hipLaunchKernelGGL((gemm_dma_kernel<T, AKC, BKC, false, 64>), dim3(grid), dim3(256),
                      kNarrowLdsPad, s, g);
   int rc = check_launch("trnblas_hip_gemm");
   if (rc || !g.sk_groups) return rc;
-  hipLaunchKernelGGL((gemm_fixup_kernel<float, 128, 64, false>),
+  hipLaunchKernelGGL((gemm_fixup_kernel<T, 128, 64, false>),
                      dim3(g.ntiles - g.dp_tiles, 128 / 16), dim3(256), 0, s, g);
   return check_launch("trnblas_hip_gemm(fixup)");
 }
@@ -942,8 +944,8 @@ static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   constexpr int BK = DMA ? 128 / (int)sizeof(T) : C::template bk<VEC>();
   g.nk = (g.K + BK - 1) / BK;
   g.span = chain_length(g.K, (int)sizeof(T)) / BK;  // even for the DMA kernel's k-tiles
-  if constexpr (DMA && sizeof(T) == 4 && !SYRK) {
-    if (narrow_tiles_pay(g)) return launch_narrow<AKC, BKC>(g, ws_bytes, s);
+  if constexpr (DMA && !SYRK) {
+    if (narrow_tiles_pay(g, (int)sizeof(T))) return launch_narrow<T, AKC, BKC>(g, ws_bytes, s);
   }
   void (*kern)(GemmArgs);
   if constexpr (DMA)
