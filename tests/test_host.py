@@ -396,3 +396,43 @@ def test_autotune_flag_and_inadmissible_operands(monkeypatch):
     h = a.bfloat16()
     assert d._autotune_gemm_route(h, h, "syrk") is None
     assert d._autotune_gemm_route(h.expand(2, 64, 64), h, "batched_gemm") is None
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K,shift", [(37, 53, 71, False), (16, 24, 32, True), (5, 8, 3, False), (64, 64, 64, False)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_packed_operands_are_dma_ready_and_exact(monkeypatch, dtype, M, N, K, shift, ta, tb):
+    # the host side of operand packing, on CPU tensors: the C-ABI arguments
+    # it returns describe 16-byte-ready operands (every check the library's
+    # DMA gate makes) which, read as the kernel reads them, are the original
+    # operands with zero columns of A and zero rows of B appended along K
+    from trnblas_amd.hip import kernels as k
+
+    monkeypatch.setattr(k, "PACK_MIN_MACS", {4: 0, 2: 0})
+    g = torch.Generator().manual_seed(M + N + K + 2 * ta + tb)
+    A = torch.randn(K, M, generator=g).T if ta else torch.randn(M, K, generator=g)
+    B = torch.randn(N, K, generator=g).T if tb else torch.randn(K, N, generator=g)
+    A, B = A.to(dtype), B.to(dtype)
+    if shift:
+        buf = torch.empty(A.numel() + 1, dtype=dtype)
+        A = buf[1:].view(M, K).copy_(A)
+    a, ta2, lda = k._mat_layout(A)
+    b, tb2, ldb = k._mat_layout(B)
+    a, ta2, lda, _, b, tb2, ldb, _, kp = k._packed_operands(A, B, a, ta2, lda, 0, b, tb2, ldb, 0, M, N, K, 1)
+    ev = 16 // A.element_size()
+    assert kp % ev == 0 and kp >= K
+    assert k._dma_ready(a, lda, 0, M if ta2 else kp, ev) and k._dma_ready(b, ldb, 0, kp if tb2 else N, ev)
+    A2 = torch.as_strided(a, (M, kp), (1, lda) if ta2 else (lda, 1))
+    B2 = torch.as_strided(b, (kp, N), (1, ldb) if tb2 else (ldb, 1))
+    assert torch.equal(A2[:, :K], A) and torch.equal(B2[:K], B)
+    assert not A2[:, K:].any() and not B2[K:].any()
+    if not (K % ev or shift or (ta and M % ev) or (not tb and N % ev)):
+        assert a is A or a.data_ptr() == A.data_ptr()  # ready operands are not copied
+
+
+def test_packed_operands_below_threshold_untouched():
+    from trnblas_amd.hip import kernels as k
+
+    A, B = torch.randn(37, 71), torch.randn(71, 53)
+    out = k._packed_operands(A, B, A, False, 71, 0, B, False, 53, 0, 37, 53, 71, 1)
+    assert out[0] is A and out[4] is B and out[8] == 71

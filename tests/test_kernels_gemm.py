@@ -426,3 +426,94 @@ def test_gemm_16bit_narrow_tiles(dev, dtype, tol, M, N, K, ta, tb):
     ref = A.double() @ B.double() + 0.5 * C.double()
     den = A.double().abs() @ B.double().abs() + 0.5 * C.double().abs()
     assert ((D.double() - ref).abs() / den).max().item() <= tol
+
+
+def _misaligned(X, dev):
+    # X on the device one element past a 16-byte boundary (same values)
+    buf = torch.empty(X.numel() + 1, dtype=X.dtype, device=dev)
+    Y = buf[1:].view(X.shape)
+    Y.copy_(X.to(dev))
+    return Y
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-6), (torch.bfloat16, 2.0**-8)])
+@pytest.mark.parametrize(
+    "batch,bb,M,N,K,shift",
+    [(1, 1, 37, 53, 71, False), (1, 1, 130, 257, 1001, False), (1, 1, 1, 5, 3, False),
+     (1, 1, 200, 64, 3, False), (1, 1, 128, 128, 128, True), (1, 1, 129, 130, 517, True),
+     (3, 1, 65, 70, 33, False), (4, 4, 96, 33, 250, False)],
+)
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_gemm_packed_operands(dev, monkeypatch, dtype, tol, batch, bb, M, N, K, shift, ta, tb):
+    # operands the DMA kernel cannot read in place (ragged contiguous
+    # extents, K not a multiple of 16 bytes, a base one element off a
+    # 16-byte boundary) packed into zero-padded K-contiguous buffers at
+    # every size (threshold 0): every layout, a batch (B broadcast or not),
+    # alpha / beta, against fp64 at the north-star gate
+    from trnblas_amd.hip import kernels
+
+    monkeypatch.setattr(kernels, "PACK_MIN_MACS", {4: 0, 2: 0})
+    packs = []
+    orig = kernels._pack_k
+    monkeypatch.setattr(kernels, "_pack_k", lambda X, kp: packs.append(kp) or orig(X, kp))
+    g = torch.Generator().manual_seed(M + 3 * N + 7 * K + batch + 2 * ta + tb)
+    A = torch.randn(batch, K, M, generator=g).transpose(1, 2) if ta else torch.randn(batch, M, K, generator=g)
+    B = torch.randn(bb, N, K, generator=g).transpose(1, 2) if tb else torch.randn(bb, K, N, generator=g)
+    A, B = A.to(dtype), B.to(dtype)
+    C = torch.randn(batch, M, N, generator=g).to(dtype)
+    if batch == 1:
+        Ad, Bd = A[0].to(dev), B[0].to(dev)
+        if shift:
+            Ad = _misaligned(A[0].mT.contiguous(), dev).mT if ta else _misaligned(A[0], dev)
+        D = kernels.gemm(Ad, Bd, 1.5, -0.5, C[0].to(dev)).unsqueeze(0).cpu()
+    else:
+        D = kernels.gemm(A.to(dev), B.to(dev), 1.5, -0.5, C.to(dev)).cpu()
+    ev = 16 // A.element_size()
+    # an operand is packed exactly when it is not DMA-ready in place
+    assert bool(packs) == bool(shift or (M if ta else K) % ev or (K if tb else N) % ev)
+    for b in range(batch):
+        Ab, Bb = A[b].double(), B[min(b, bb - 1)].double()
+        ref = 1.5 * (Ab @ Bb) - 0.5 * C[b].double()
+        den = 1.5 * (Ab.abs() @ Bb.abs()) + 0.5 * C[b].double().abs()
+        den = torch.where(den > 0, den, torch.ones_like(den))
+        assert ((D[b].double() - ref).abs() / den).max().item() <= tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-6), (torch.bfloat16, 2.0**-8)])
+@pytest.mark.parametrize("M,N,K,ta,tb", [(1537, 1539, 1541, False, False), (2047, 1025, 1027, True, True),
+                                         (1023, 2049, 1031, False, True)])
+def test_gemm_unaligned_large(dev, dtype, tol, M, N, K, ta, tb):
+    # products above the packing threshold with odd extents take the DMA
+    # kernel on packed operands (at the default threshold)
+    from trnblas_amd.hip import kernels
+
+    assert M * N * K >= kernels.PACK_MIN_MACS[4]
+    g = torch.Generator().manual_seed(M + N + K)
+    A = (torch.randn(K, M, generator=g).T if ta else torch.randn(M, K, generator=g)).to(dtype)
+    B = (torch.randn(N, K, generator=g).T if tb else torch.randn(K, N, generator=g)).to(dtype)
+    C = torch.randn(M, N, generator=g).to(dtype)
+    D = kernels.gemm(A.to(dev), B.to(dev), 1.0, 0.5, C.to(dev)).cpu()
+    ref = A.double() @ B.double() + 0.5 * C.double()
+    den = A.double().abs() @ B.double().abs() + 0.5 * C.double().abs()
+    assert ((D.double() - ref).abs() / den).max().item() <= tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-6), (torch.bfloat16, 2.0**-8)])
+@pytest.mark.parametrize("n,k", [(130, 1001), (257, 33), (1, 3), (2047, 1027)])
+@pytest.mark.parametrize("trans", [False, True])
+def test_syrk_packed_operand(dev, monkeypatch, dtype, tol, n, k, trans):
+    # SYRK on an operand packed K-contiguous with k padded (threshold 0)
+    from trnblas_amd.hip import kernels
+
+    monkeypatch.setattr(kernels, "PACK_MIN_MACS", {4: 0, 2: 0})
+    g = torch.Generator().manual_seed(n + k + trans)
+    A = torch.randn((k, n) if trans else (n, k), generator=g).to(dtype)
+    X = torch.randn(n, n, generator=g).to(dtype)
+    D = kernels.syrk(A.to(dev), 1.0, 0.5, X.to(dev), trans=trans, uplo="lower").cpu()
+    assert torch.equal(D, D.T)
+    opA = (A.T if trans else A).double()
+    Xd = X.double()
+    Cs = torch.tril(Xd) + torch.tril(Xd, -1).T
+    ref = opA @ opA.T + 0.5 * Cs
+    den = opA.abs() @ opA.abs().T + 0.5 * Cs.abs()
+    assert ((D.double() - ref).abs() / den).max().item() <= tol

@@ -91,6 +91,70 @@ def _batched_layout(X: torch.Tensor):
     return X, False, max(c, 1), r * c
 
 
+# The GEMM / SYRK launcher moves operand panels by LDS DMA only when every
+# 16-byte group of an operand lies wholly inside or outside the matrix: a
+# 16-byte aligned base, and a leading dimension, batch stride and contiguous
+# extent that are multiples of 16 bytes. Other operands run on the
+# register-staged kernel: on the MI355X 74 TFLOP/s fp32 at 4095^3 and 8191^3
+# (DMA kernel: 119 and 132 after packing) and 81 TFLOP/s bf16 at 4095^3
+# (566 after packing). From PACK_MIN_MACS multiply-adds per launch on (by
+# element size), such operands are first copied into fresh K-contiguous
+# buffers whose rows are padded with zeros to a multiple of 16 bytes (zero
+# products add nothing to any sum; the reference pads its kernel operands
+# the same way, nki/dispatch.py:2344-2368) and the product takes the DMA
+# kernel. Below it the copies' launches cost more than they save (fp32
+# 1023^3: 54 us in place, 67 us packed; 1535^3: 132 and 120 us; bf16 767^3:
+# 38 and 47 us, 1535^3: 120 and 67 us).
+PACK_MIN_MACS = {4: 1 << 31, 2: 1 << 30}
+
+
+def _dma_ready(t: torch.Tensor, ld: int, stride: int, ext: int, ev: int) -> bool:
+    return t.data_ptr() % 16 == 0 and ld % ev == 0 and stride % ev == 0 and ext % ev == 0
+
+
+def _pack_k(X: torch.Tensor, kp: int) -> torch.Tensor:
+    """X (..., R, K) copied into a fresh row-major (..., R, kp) buffer whose
+    columns K .. kp - 1 are zero."""
+    k = X.shape[-1]
+    P = torch.empty((*X.shape[:-1], kp), dtype=X.dtype, device=X.device)
+    P[..., :k].copy_(X)
+    if kp > k:
+        P[..., k:].zero_()
+    return P
+
+
+def _packed_operands(A, B, a, ta, lda, sa, b, tb, ldb, sb, M, N, K, nb):
+    """The C-ABI operand arguments of A (M, K) and B (K, N) (3-D: batched,
+    batch 1 broadcast): (a, ta, lda, sa, b, tb, ldb, sb, K) as laid out, or
+    with the operands the DMA kernel cannot read packed K-contiguous (and K
+    padded when it is not a multiple of 16 bytes)."""
+    ev = 16 // A.element_size()
+    if nb * M * N * K < PACK_MIN_MACS[A.element_size()] or M == 0 or N == 0 or K == 0:
+        return a, ta, lda, sa, b, tb, ldb, sb, K
+    a_ok = _dma_ready(a, lda, sa, M if ta else K, ev)
+    b_ok = _dma_ready(b, ldb, sb, K if tb else N, ev)
+    kp = -(-K // ev) * ev
+    if a_ok and b_ok:
+        return a, ta, lda, sa, b, tb, ldb, sb, K
+    if kp != K or not a_ok:
+        pa = _pack_k(A, kp)
+        a, ta, lda, sa = pa, False, kp, (M * kp if pa.dim() == 3 and pa.shape[0] > 1 else 0)
+    if kp != K or not b_ok:
+        pb = _pack_k(B.transpose(-1, -2), kp)
+        b, tb, ldb, sb = pb, True, kp, (N * kp if pb.dim() == 3 and pb.shape[0] > 1 else 0)
+    return a, ta, lda, sa, b, tb, ldb, sb, kp
+
+
+def _packed_syrk_operand(A, trans, a, t, lda, n, k):
+    """SYRK's (a, t, lda, k) for op(A) (n, k): as laid out, or packed
+    K-contiguous with k padded to a multiple of 16 bytes (see _packed_operands)."""
+    ev = 16 // A.element_size()
+    if n * n * k < PACK_MIN_MACS[A.element_size()] or n == 0 or k == 0 or _dma_ready(a, lda, 0, n if t else k, ev):
+        return a, t, lda, k
+    kp = -(-k // ev) * ev
+    return _pack_k(A.t() if trans else A, kp), False, kp, kp
+
+
 def gemm(
     A: torch.Tensor,
     B: torch.Tensor,
@@ -119,6 +183,9 @@ def gemm(
             raise ValueError(f"gemm: inner dimensions differ: {tuple(A.shape)} @ {tuple(B.shape)}")
         a, ta, lda = _mat_layout(A)
         b, tb, ldb = _mat_layout(B)
+        a, ta, lda, _, b, tb, ldb, _, K = _packed_operands(
+            A, B, a, ta, lda, 0, b, tb, ldb, 0, M, N, K, 1
+        )
         if out is None:
             D, ldd = torch.empty((M, N), dtype=A.dtype, device=dev), N
         else:
@@ -153,6 +220,9 @@ def gemm(
         raise ValueError(f"gemm: batch sizes {bA} and {bB} do not broadcast")
     a, ta, lda, sa = _batched_layout(A)
     b, tb, ldb, sb = _batched_layout(B)
+    a, ta, lda, sa, b, tb, ldb, sb, K = _packed_operands(
+        A, B, a, ta, lda, sa, b, tb, ldb, sb, M, N, K, nb
+    )
     D = torch.empty((nb, M, N), dtype=A.dtype, device=dev)
     ws = gemm_workspace(dev)
     c, ldc, sc = None, N, 0
@@ -188,6 +258,7 @@ def syrk(
     t = t != bool(trans)  # a transposed view flips the layout flag
     n = A.shape[1] if trans else A.shape[0]
     k = A.shape[0] if trans else A.shape[1]
+    a, t, lda, k = _packed_syrk_operand(A, trans, a, t, lda, n, k)
     D = torch.empty((n, n), dtype=A.dtype, device=dev)
     ws = gemm_workspace(dev)
     c, ldc = None, n
@@ -240,6 +311,7 @@ def syrk_checked(
     t = t != bool(trans)
     n = A.shape[1] if trans else A.shape[0]
     k = A.shape[0] if trans else A.shape[1]
+    a, t, lda, k = _packed_syrk_operand(A, trans, a, t, lda, n, k)
     if tuple(C.shape) != (n, n):
         raise ValueError(f"syrk: C must be {n} x {n}, got {tuple(C.shape)}")
     c = C if (C.stride(1) == 1 and C.stride(0) >= n) else C.contiguous()
