@@ -84,6 +84,25 @@ int trnblas_hip_gemm(int dtype, int transA, int transB, int64_t M, int64_t N, in
 size_t trnblas_hip_gemm_workspace(void);
 
 /*
+ * Operand packing:  P[b] (R x kp, row-major) = X[b] (R x K) with zero
+ * columns K .. kp - 1.
+ *
+ * Replaces the zero padding of GEMM operands to the kernel's tile multiples,
+ * `_pad_gemm_operands` (trnblas/nki/dispatch.py:2344-2368). Here it serves
+ * operands that trnblas_hip_gemm / trnblas_hip_syrk cannot read by LDS DMA
+ * in place: packed K-contiguous with kp a multiple of 16 bytes, they take the
+ * DMA kernel (zero products add nothing to any sum).
+ * Element (r, k) of X[b] is at X + b * sxb + r * sr + k * sk (strides in
+ * elements, >= 0; sk == 1 is copied along k, any other layout through an LDS
+ * transpose). P[b] starts at P + b * spb (spb >= R * kp when batch > 1).
+ * dtype: TRNBLAS_F32, TRNBLAS_BF16 or TRNBLAS_F16 (bits are copied as they are).
+ * P must not overlap X. Asynchronous on `stream`.
+ */
+int trnblas_hip_pack_k(int dtype, int64_t R, int64_t K, const void* X, int64_t sr, int64_t sk,
+                       int64_t sxb, void* P, int64_t kp, int64_t spb, int64_t batch,
+                       void* stream);
+
+/*
  * SYRK:  D = alpha * op(A) * op(A)^T + beta * sym_uplo(C), returned full.
  *
  * Replaces torch.ops.trnblas.syrk (trnblas/nki/_native.py:124-132; kernel

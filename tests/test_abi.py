@@ -45,6 +45,11 @@ def test_argument_errors_are_reported_without_a_gpu():
     rc = lib.trnblas_hip_gemm(7, 0, 0, 4, 4, 4, 1.0, None, 4, 0, None, 4, 0, 0.0, None, 4, 0,
                               None, 4, 0, 1, None, 0, None)
     assert rc == _lib.E_ARG and b"dtype" in lib.trnblas_hip_last_error()
+    rc = lib.trnblas_hip_pack_k(0, 4, 5, None, 5, 1, 0, None, 4, 20, 1, None)
+    assert rc == _lib.E_ARG and b"bad sizes" in lib.trnblas_hip_last_error()  # kp < K
+    rc = lib.trnblas_hip_pack_k(1, 4, 5, None, 5, 1, 0, None, 8, 20, 2, None)
+    assert rc == _lib.E_ARG and b"batch stride" in lib.trnblas_hip_last_error()
+    assert lib.trnblas_hip_pack_k(0, 0, 5, None, 5, 1, 0, None, 8, 0, 1, None) == 0  # R == 0: nothing to do
     rc = lib.trnblas_hip_ozaki_gemm(0, 13, 4, 4, 128, 128, None, 128, 0, None, 128, 0, None,
                                     None, None, 4, 1, None)
     assert rc == _lib.E_ARG and b"slices" in lib.trnblas_hip_last_error()

@@ -409,6 +409,13 @@ def test_packed_operands_are_dma_ready_and_exact(monkeypatch, dtype, M, N, K, sh
     from trnblas_amd.hip import kernels as k
 
     monkeypatch.setattr(k, "PACK_MIN_MACS", {4: 0, 2: 0})
+
+    def pack_on_host(X, kp):  # trnblas_hip_pack_k's result, for CPU tensors
+        P = torch.zeros((*X.shape[:-1], kp), dtype=X.dtype)
+        P[..., : X.shape[-1]] = X
+        return P
+
+    monkeypatch.setattr(k, "_pack_k", pack_on_host)
     g = torch.Generator().manual_seed(M + N + K + 2 * ta + tb)
     A = torch.randn(K, M, generator=g).T if ta else torch.randn(M, K, generator=g)
     B = torch.randn(N, K, generator=g).T if tb else torch.randn(K, N, generator=g)

@@ -517,3 +517,32 @@ def test_syrk_packed_operand(dev, monkeypatch, dtype, tol, n, k, trans):
     ref = opA @ opA.T + 0.5 * Cs
     den = opA.abs() @ opA.abs().T + 0.5 * Cs.abs()
     assert ((D.double() - ref).abs() / den).max().item() <= tol
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("R,K,kp", [(1, 1, 4), (64, 64, 64), (65, 63, 72), (130, 257, 264), (3, 1000, 1008)])
+@pytest.mark.parametrize("layout", ["row", "trans", "strided", "batched", "broadcast"])
+def test_pack_k_kernel(dev, dtype, R, K, kp, layout):
+    # trnblas_hip_pack_k copies bits exactly and zero-fills columns K .. kp - 1
+    # for a row-major source, a transposed view, a general strided view
+    # (every other row and column), a batch, and a stride-0 batch
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(R * 3 + K + kp)
+    if layout == "row":
+        X = torch.randn(R, K, generator=g).to(dtype).to(dev)
+    elif layout == "trans":
+        X = torch.randn(K, R, generator=g).to(dtype).to(dev).T
+    elif layout == "strided":
+        X = torch.randn(2 * R, 2 * K, generator=g).to(dtype).to(dev)[::2, ::2]
+    elif layout == "batched":
+        X = torch.randn(3, K, R, generator=g).to(dtype).to(dev).transpose(1, 2)
+    else:
+        X = torch.randn(1, R, K, generator=g).to(dtype).to(dev).expand(2, R, K)
+    P = kernels._pack_k(X, kp)
+    ref = torch.zeros((*X.shape[:-1], kp), dtype=dtype, device=dev)
+    ref[..., :K] = X
+    torch.cuda.synchronize()
+    assert P.shape == ref.shape and P.is_contiguous()
+    assert torch.equal(P.view(torch.int16 if dtype != torch.float32 else torch.int32),
+                       ref.view(torch.int16 if dtype != torch.float32 else torch.int32))

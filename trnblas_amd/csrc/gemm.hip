@@ -1024,6 +1024,51 @@ static int dispatch(int dtype, const GemmArgs& g, bool akc, bool bkc, size_t ws_
   return TRNBLAS_E_ARG;
 }
 
+// Operand packing (trnblas_hip_pack_k): X (R x K, element (r, k) at
+// X + r sr + k sk) copied into row-major P (R x kp) with zero columns
+// K .. kp - 1, one 64 x 64 block per workgroup, moved as raw bits (U: the
+// element's size). A K-contiguous source (sk == 1) is copied along k; any
+// other is read along r (coalesced for a transposed view, sr == 1) into an
+// LDS block and written along k.
+struct PackArgs {
+  const void* X;
+  void* P;
+  int64_t R, K, kp, sr, sk, sxb, spb, tiles_r, tiles_k;
+};
+
+template <typename U>
+__global__ __launch_bounds__(256) void pack_k_kernel(PackArgs p) {
+  __shared__ U blk[64][65];
+  int64_t b = blockIdx.x;
+  const int64_t ik = b % p.tiles_k;
+  b /= p.tiles_k;
+  const int64_t ir = b % p.tiles_r;
+  b /= p.tiles_r;
+  const int64_t r0 = ir * 64, k0 = ik * 64;
+  const U* X = static_cast<const U*>(p.X) + b * p.sxb;
+  U* P = static_cast<U*>(p.P) + b * p.spb;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  if (p.sk == 1) {
+#pragma unroll 4
+    for (int i = 0; i < 16; ++i) {
+      const int64_t r = r0 + ty + 4 * i, k = k0 + tx;
+      if (r < p.R && k < p.kp) P[r * p.kp + k] = k < p.K ? X[r * p.sr + k] : U(0);
+    }
+    return;
+  }
+#pragma unroll 4
+  for (int i = 0; i < 16; ++i) {
+    const int64_t r = r0 + tx, k = k0 + ty + 4 * i;
+    blk[ty + 4 * i][tx] = (r < p.R && k < p.K) ? X[r * p.sr + k * p.sk] : U(0);
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int i = 0; i < 16; ++i) {
+    const int64_t r = r0 + ty + 4 * i, k = k0 + tx;
+    if (r < p.R && k < p.kp) P[r * p.kp + k] = blk[tx][ty + 4 * i];
+  }
+}
+
 }  // namespace trnblas
 
 using namespace trnblas;
@@ -1031,6 +1076,28 @@ using namespace trnblas;
 extern "C" size_t trnblas_hip_gemm_workspace(void) {
   // two fp32 partial tiles per resident workgroup slot (at most 2 per CU)
   return (size_t)device_cus() * 2 * 2 * kSkSlotBytes;
+}
+
+extern "C" int trnblas_hip_pack_k(int dtype, int64_t R, int64_t K, const void* X, int64_t sr,
+                                  int64_t sk, int64_t sxb, void* P, int64_t kp, int64_t spb,
+                                  int64_t batch, void* stream) {
+  clear_error();
+  TRNBLAS_CHECK_ARG(dtype == TRNBLAS_F32 || dtype == TRNBLAS_BF16 || dtype == TRNBLAS_F16,
+                    "pack_k: dtype %d not supported", dtype);
+  TRNBLAS_CHECK_ARG(R >= 0 && K >= 0 && batch >= 0 && kp >= K, "pack_k: bad sizes");
+  TRNBLAS_CHECK_ARG(sr >= 0 && sk >= 0 && sxb >= 0 && spb >= 0, "pack_k: negative stride");
+  if (R == 0 || kp == 0 || batch == 0) return TRNBLAS_OK;
+  TRNBLAS_CHECK_ARG(batch == 1 || spb >= R * kp, "pack_k: batch stride of P below R * kp");
+  TRNBLAS_CHECK_ARG(P != nullptr && (K == 0 || X != nullptr), "pack_k: NULL operand");
+  PackArgs a{X, P, R, K, kp, sr, sk, sxb, spb, (R + 63) / 64, (kp + 63) / 64};
+  const int64_t blocks = a.tiles_r * a.tiles_k * batch;
+  TRNBLAS_CHECK_ARG(blocks < (1ll << 31), "pack_k: too many 64 x 64 blocks");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TRNBLAS_F32)
+    hipLaunchKernelGGL(pack_k_kernel<uint32_t>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(pack_k_kernel<uint16_t>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  return check_launch("trnblas_hip_pack_k");
 }
 
 extern "C" int trnblas_hip_gemm(int dtype, int transA, int transB, int64_t M, int64_t N,

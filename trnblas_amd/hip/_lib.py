@@ -19,7 +19,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 _PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("TRNBLAS_HIP_LIB", _PKG / "lib" / "libtrnblas_hip.so"))
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 F32, BF16, F16, F64 = 0, 1, 2, 3
 DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
@@ -47,6 +47,11 @@ SIGNATURES = {
         + [_c_ptr],
     ),
     "trnblas_hip_gemm_workspace": (_c_size, []),
+    "trnblas_hip_pack_k": (
+        _c_int,
+        [_c_int, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64]
+        + [_c_ptr],
+    ),
     "trnblas_hip_syrk": (
         _c_int,
         [_c_int, _c_int, _c_int, _c_i64, _c_i64, _c_dbl, _c_ptr, _c_i64, _c_dbl, _c_ptr]

@@ -96,16 +96,16 @@ def _batched_layout(X: torch.Tensor):
 # 16-byte aligned base, and a leading dimension, batch stride and contiguous
 # extent that are multiples of 16 bytes. Other operands run on the
 # register-staged kernel: on the MI355X 74 TFLOP/s fp32 at 4095^3 and 8191^3
-# (DMA kernel: 119 and 132 after packing) and 81 TFLOP/s bf16 at 4095^3
-# (566 after packing). From PACK_MIN_MACS multiply-adds per launch on (by
-# element size), such operands are first copied into fresh K-contiguous
-# buffers whose rows are padded with zeros to a multiple of 16 bytes (zero
-# products add nothing to any sum; the reference pads its kernel operands
-# the same way, nki/dispatch.py:2344-2368) and the product takes the DMA
-# kernel. Below it the copies' launches cost more than they save (fp32
-# 1023^3: 54 us in place, 67 us packed; 1535^3: 132 and 120 us; bf16 767^3:
-# 38 and 47 us, 1535^3: 120 and 67 us).
-PACK_MIN_MACS = {4: 1 << 31, 2: 1 << 30}
+# (the DMA kernel after packing: 126 and 132) and 81 TFLOP/s bf16 at 4095^3
+# (737 after packing). From PACK_MIN_MACS multiply-adds per launch on (by
+# element size), such operands are first copied by trnblas_hip_pack_k into
+# fresh K-contiguous buffers whose rows are padded with zeros to a multiple
+# of 16 bytes (zero products add nothing to any sum; the reference pads its
+# kernel operands the same way, nki/dispatch.py:2344-2368) and the product
+# takes the DMA kernel. Below it the two pack launches cost more than they
+# save (fp32 767^3: 40 us in place, 45 us packed; 1023^3: 52 and 52;
+# 1535^3: 126 and 99; bf16 511^3: 29 and 32; 767^3: 38 and 34).
+PACK_MIN_MACS = {4: 1 << 30, 2: 1 << 28}
 
 
 def _dma_ready(t: torch.Tensor, ld: int, stride: int, ext: int, ev: int) -> bool:
@@ -113,13 +113,16 @@ def _dma_ready(t: torch.Tensor, ld: int, stride: int, ext: int, ev: int) -> bool
 
 
 def _pack_k(X: torch.Tensor, kp: int) -> torch.Tensor:
-    """X (..., R, K) copied into a fresh row-major (..., R, kp) buffer whose
-    columns K .. kp - 1 are zero."""
-    k = X.shape[-1]
+    """X (R, K) or (batch, R, K), any strides, copied into a fresh row-major
+    (..., R, kp) buffer whose columns K .. kp - 1 are zero (one launch of
+    trnblas_hip_pack_k)."""
+    R, k = X.shape[-2], X.shape[-1]
+    nb, sxb = (X.shape[0], X.stride(0)) if X.dim() == 3 else (1, 0)
     P = torch.empty((*X.shape[:-1], kp), dtype=X.dtype, device=X.device)
-    P[..., :k].copy_(X)
-    if kp > k:
-        P[..., k:].zero_()
+    call(
+        "trnblas_hip_pack_k", _lib.DTYPE_CODES[X.dtype], R, k, ptr(X), X.stride(-2),
+        X.stride(-1), sxb, ptr(P), kp, R * kp, nb, stream_of(X.device),
+    )  # fmt: skip
     return P
 
 
