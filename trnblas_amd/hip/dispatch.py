@@ -82,9 +82,16 @@ _BACKENDS = ("auto", "pytorch", "hip", "nki")
 _backend = "auto"
 
 
+_hip_seen = False
+
+
 def has_hip() -> bool:
-    """A ROCm GPU is visible to torch (does not load the op library)."""
-    return bool(getattr(torch.version, "hip", None)) and torch.cuda.is_available()
+    """A ROCm GPU is visible to torch (does not load the op library). A
+    positive answer is kept: it is asked on every call of the public API."""
+    global _hip_seen
+    if not _hip_seen:
+        _hip_seen = bool(getattr(torch.version, "hip", None)) and torch.cuda.is_available()
+    return _hip_seen
 
 
 def set_backend(backend: str) -> None:
@@ -471,7 +478,7 @@ def _gpu_device(*ts) -> torch.device:
 
 
 def _to(t, dev):
-    return None if t is None else t.to(dev, non_blocking=False)
+    return t if t is None or t.device == dev else t.to(dev, non_blocking=False)
 
 
 def _to_host(t: torch.Tensor, orig: torch.device) -> torch.Tensor:
@@ -495,6 +502,8 @@ def _fused_epilogue_ok(C, beta, shape, dtype, device) -> bool:
     """True when beta * C can be fused into the kernel's store: C absent /
     beta 0, or C of the result dtype and device broadcasting to `shape`."""
     if C is None or beta == 0.0:
+        return True
+    if C.dtype == dtype and C.device == device and tuple(C.shape) == tuple(shape):
         return True
     return (
         C.dtype == dtype
@@ -597,8 +606,9 @@ def gemm_scaled(alpha, a, b, beta, C):
     the route is a kernel route (level3.gemm / batched_gemm)."""
     if a.dim() < 2 or b.dim() < 2:
         return _torch_scale_add(torch.matmul(a, b), alpha, beta, C)
-    batch = _lib.broadcast_shapes(a.shape[:-2], b.shape[:-2])
-    route = _gemm_route(a, b, op="gemm" if a.dim() == 2 and b.dim() == 2 else "batched_gemm")
+    flat = a.dim() == 2 and b.dim() == 2
+    batch = () if flat else _lib.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    route = _gemm_route(a, b, op="gemm" if flat else "batched_gemm")
     if route not in ("hip", "upload") or math.prod(batch) == 0 or len(batch) > 1:
         if route in ("hip", "upload") and len(batch) > 1:
             return _torch_scale_add(nki_batched_gemm(a, b), alpha, beta, C)

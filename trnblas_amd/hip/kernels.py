@@ -200,7 +200,7 @@ def gemm(
         ws = gemm_workspace(dev)
         c, ldc = None, N
         if beta != 0.0 and C is not None:
-            c = C.expand(M, N)
+            c = C if tuple(C.shape) == (M, N) else C.expand(M, N)
             if c.stride(1) != 1 or c.stride(0) < N:
                 c = c.contiguous()
             ldc = c.stride(0)
