@@ -443,3 +443,22 @@ def test_packed_operands_below_threshold_untouched():
     A, B = torch.randn(37, 71), torch.randn(71, 53)
     out = k._packed_operands(A, B, A, False, 71, 0, B, False, 53, 0, 37, 53, 71, 1)
     assert out[0] is A and out[4] is B and out[8] == 71
+
+
+def test_unready_16bit_route_rule():
+    # 16-bit 2-D operands the DMA kernel cannot read in place go to hipBLASLt
+    # from 2^26 multiply-adds (stride logic only, on CPU tensors)
+    bf = torch.bfloat16
+    A, B = torch.zeros(512, 512, dtype=bf), torch.zeros(512, 512, dtype=bf)
+    assert not d._unready_16bit_to_aten(A, B, "gemm")  # ready
+    A3, B3 = torch.zeros(511, 511, dtype=bf), torch.zeros(511, 511, dtype=bf)
+    assert d._unready_16bit_to_aten(A3, B3, "gemm")  # ragged K / N
+    assert d._unready_16bit_to_aten(A3.T, B3.T, "gemm")  # transposed views, ragged M / K
+    assert not d._unready_16bit_to_aten(A3, B3, "syrk")
+    assert not d._unready_16bit_to_aten(A3.float(), B3.float(), "gemm")  # fp32 stays
+    small = torch.zeros(255, 255, dtype=bf)
+    assert not d._unready_16bit_to_aten(small, small, "gemm")  # below 2^26
+    buf = torch.zeros(512 * 512 + 1, dtype=bf)
+    off = buf[1:].view(512, 512)  # one element off a 16-byte boundary
+    assert d._unready_16bit_to_aten(off, B, "gemm")
+    assert d._dma_ready_2d(torch.zeros(64, 64, dtype=bf).T, 64, 64)

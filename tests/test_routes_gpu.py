@@ -154,3 +154,19 @@ def test_autotune_measures_once_per_bucket(dev, monkeypatch, tmp_path):
     assert d._gemm_route(A, B) == route and d._autotune_measured == 1
     # fp32 stays on the kernel without a measurement
     assert d._gemm_route(A.float(), B.float()) == "hip" and d._autotune_measured == 1
+
+
+def test_unready_16bit_routes_to_hipblaslt(dev):
+    # bf16 operands the DMA kernel cannot read in place (K = 1023), below the
+    # hipBLASLt shape bucket: hipBLASLt from 2^26 multiply-adds, the kernel
+    # below; both within the 16-bit gate
+    g = torch.Generator(device=dev).manual_seed(31)
+    for n, launches in ((1023, []), (255, ["gemm"])):
+        A = torch.randn(n, n, device=dev, generator=g).bfloat16()
+        B = torch.randn(n, n, device=dev, generator=g).bfloat16()
+        with _Launches() as seen:
+            D = tb.gemm(1.0, A, B)
+        assert seen.names == launches
+        ref = A.double() @ B.double()
+        den = A.double().abs() @ B.double().abs()
+        assert _cw(D.double(), ref, den) <= 2.0**-8

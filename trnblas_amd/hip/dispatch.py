@@ -322,6 +322,38 @@ def _aten_gemm_wins(a_shape, b_shape, dtype: torch.dtype, contiguous: bool, op: 
     return nb * M * N >= _ATEN_16BIT_MIN_MN and K >= _ATEN_16BIT_MIN_K
 
 
+def _dma_ready_2d(X: torch.Tensor, rows_ext: int, cols_ext: int) -> bool:
+    """A 2-D 16-bit operand the GEMM kernel reads by LDS DMA in place: a
+    16-byte aligned base, and a row stride and contiguous extent that are
+    multiples of 8 elements (a layout the launcher copies counts by its
+    copy's extent). Strides only: no copy is made."""
+    s0, s1 = X.stride()
+    if s1 == 1 and s0 >= cols_ext:
+        return X.data_ptr() % 16 == 0 and s0 % 8 == 0 and cols_ext % 8 == 0
+    if s0 == 1 and s1 >= rows_ext:
+        return X.data_ptr() % 16 == 0 and s1 % 8 == 0 and rows_ext % 8 == 0
+    return cols_ext % 8 == 0
+
+
+# 16-bit 2-D products whose operands the DMA kernel cannot read in place,
+# below the hipBLASLt bucket above: the register-staged kernel, or packing
+# plus the DMA kernel, against hipBLASLt (bf16, square, measured on the
+# MI355X): 255^3 38 / 30 / 50 us, 511^3 29 / 32 / 23, 767^3 38 / 34 / 28,
+# 1023^3 51 / 40 / 27, 1535^3 111 / 52 / 45. From 2^26 multiply-adds on they
+# go to hipBLASLt.
+_ATEN_16BIT_UNREADY_MIN_MACS = 1 << 26
+
+
+def _unready_16bit_to_aten(a: torch.Tensor, b: torch.Tensor, op: str) -> bool:
+    if op == "syrk" or a.dtype not in (torch.bfloat16, torch.float16) or a.dim() != 2 or b.dim() != 2:
+        return False
+    M, K = a.shape
+    N = b.shape[1]
+    if M * N * K < _ATEN_16BIT_UNREADY_MIN_MACS:
+        return False
+    return not (_dma_ready_2d(a, M, K) and _dma_ready_2d(b, K, N))
+
+
 # ── autotune: measured kernel-vs-hipBLASLt choice per shape bucket ───────────
 #
 # The reference times each of its tile configurations on the first call of a
@@ -452,6 +484,8 @@ def _gemm_route(*tensors, op: str = "gemm", macs: float | None = None, nbytes: i
             if tuned is not None:
                 return tuned
             if _aten_gemm_wins(a.shape, b.shape, a.dtype, a.is_contiguous() and b.is_contiguous(), op):
+                return "aten"
+            if _unready_16bit_to_aten(a, b, op):
                 return "aten"
         return "hip"
     if not _on_host(*tensors):
