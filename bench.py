@@ -322,8 +322,8 @@ def run_extras(dev, tb, only=None) -> dict:
         # slice counts 8..12 (fast mode): time and max |C - DGEMM| / (|A||B|);
         # the difference to DGEMM settles at DGEMM's own error once the
         # truncation is below it (tests/test_config5_slices_gpu.py judges each
-        # k against a near-exact product: k = 10 meets the reference's host gate on
-        # this data)
+        # k against a near-exact product over the whole output: k = 11 is the
+        # smallest that meets the reference's host gate on this data)
         sweep = []
         for k in range(8, 13):
             tk = gpu_time_ms(lambda: tb.gemm_fp64(Ao, Bo, slices=k, mode="fast"), reps=3, warm=1)

@@ -22,25 +22,44 @@ import math
 import numpy as np
 
 
-def ref_exact(A: np.ndarray, B: np.ndarray) -> np.ndarray:
-    A = np.asarray(A, dtype=np.float64)
-    B = np.asarray(B, dtype=np.float64)
+def ref_exact(A, B, xp=np):
+    """The near-correctly-rounded product of A (M, K) and B (K, N).
+
+    xp=np: numpy arrays on the host. xp=torch: fp64 tensors on any device,
+    the same operations in the same order. Every slice product is exact in
+    any fp64 GEMM, whatever its summation order or blocking: a piece is
+    q 2^(e - c) with |q| <= 2^(b-1), so each term of a slice product's row i,
+    column j is an integer multiple of 2^(eA_i + eB_j - c_s - c_t) below
+    2^(2b-2) of that unit, and the K terms and every partial sum stay below
+    K 2^(2b-2) <= 2^53 units. The elementwise Neumaier steps are the same
+    IEEE operations on both, so the two give the same bits (checked by the
+    GPU test that uses the device form)."""
+    if xp is np:
+        A = np.asarray(A, dtype=np.float64)
+        B = np.asarray(B, dtype=np.float64)
     K = A.shape[1]
     b = math.floor((55 - math.log2(max(K, 2))) / 2)
     k = math.ceil(80 / b)
 
     def pieces(X, axis):
-        amax = np.abs(X).max(axis=axis, keepdims=True)
-        nz = amax > 0
-        e = np.where(nz, np.ceil(np.log2(np.where(nz, amax, 1.0))), 0.0)
-        rem = X * np.exp2(-e)
+        if xp is np:
+            amax = np.abs(X).max(axis=axis, keepdims=True)
+            nz = amax > 0
+            e = np.where(nz, np.ceil(np.log2(np.where(nz, amax, 1.0))), 0.0)
+            rem = X * np.exp2(-e)
+        else:
+            amax = X.abs().amax(dim=axis, keepdim=True)
+            nz = amax > 0
+            e = xp.where(nz, xp.ceil(xp.log2(xp.where(nz, amax, xp.ones_like(amax)))),
+                         xp.zeros_like(amax))
+            rem = X * xp.exp2(-e)
         out = []
         for s in range(k):
             width = (b - 1) if s == 0 else b
             scaled = rem * 2.0**width
-            q = np.rint(scaled)
+            q = xp.round(scaled) if xp is not np else np.rint(scaled)
             rem = scaled - q
-            out.append(q * np.exp2(e - ((b - 1) + b * s)))
+            out.append(q * xp.exp2(e - ((b - 1) + b * s)))
         return out
 
     Ap, Bp = pieces(A, 1), pieces(B, 0)
@@ -51,12 +70,13 @@ def ref_exact(A: np.ndarray, B: np.ndarray) -> np.ndarray:
     for s, t in order:
         P = Ap[s] @ Bp[t]
         if total is None:
-            total, comp = P, np.zeros_like(P)
+            total, comp = P, xp.zeros_like(P)
             continue
         nxt = total + P
-        big = np.abs(total) >= np.abs(P)
-        comp += np.where(big, (total - nxt) + P, (P - nxt) + total)
+        big = xp.abs(total) >= xp.abs(P)
+        comp += xp.where(big, (total - nxt) + P, (P - nxt) + total)
         total = nxt
+        del P, nxt, big
     return total + comp
 
 

@@ -28,3 +28,14 @@ def test_max_cw_zero_for_exact_and_positive_for_perturbed():
     ex = ref_exact(A, B)
     assert max_cw(ex, A, B, exact=ex) == 0.0
     assert max_cw(ex * (1 + 1e-12), A, B, exact=ex) > 0.0
+
+
+def test_torch_form_bit_equal_to_numpy():
+    """The device form (xp=torch) runs the same operations: same bits."""
+    import torch
+
+    for dist, shape, seed in (("logu4", (37, 500, 29), 3), ("normal", (16, 8192, 9), 4)):
+        A, B = inputs(*shape, dist=dist, seed=seed)
+        a = ref_exact(A, B)
+        b = ref_exact(torch.from_numpy(A), torch.from_numpy(B), xp=torch).numpy()
+        assert np.array_equal(a.view(np.int64), b.view(np.int64)), (dist, shape)

@@ -738,8 +738,7 @@ __device__ __forceinline__ void oz_dma16_asm(const void* base, const void* lds, 
 // q / (2 KS + 1); pad slots and rows outside the matrix read zeros without a
 // memory access.
 //
-// KS = 10 (the slice count at which C5's wide-range data reaches host-fp64
-// accuracy) is laid out to keep two workgroups per CU ("LZ"): rows of 2 KS =
+// KS = 10 is laid out to keep two workgroups per CU ("LZ"): rows of 2 KS =
 // 20 groups with no pad, group j of row r in slot j ^ ((r >> 2) & 3) (the
 // 16 rows of a fragment read: 4 (r % 4) + the XOR term covers 16 distinct
 // bank groups), so a stage is 40 KiB and two workgroups fit the 160 KiB of

@@ -252,14 +252,16 @@ def config3_inputs(device, seed: int = 3):
 
 def config5_inputs(device, n: int = 8192, seed: int = 5):
     """C5 rules: A, B (n x n) fp64, each entry U(-1, 1) 2^round(N(0, 4^2)),
-    drawn on the device from a seeded device generator (A's two draws, then
-    B's)."""
-    g = torch.Generator(device=device).manual_seed(seed)
+    drawn on the host CPU from torch.Generator().manual_seed(seed) in the
+    order A's uniforms, A's exponents, B's uniforms, B's exponents, then
+    copied to `device` (the same values on every machine with this torch's
+    CPU generator)."""
+    g = torch.Generator().manual_seed(seed)
 
     def draw():
-        u = torch.rand(n, n, generator=g, device=device, dtype=torch.float64) * 2 - 1
-        e = torch.round(4.0 * torch.randn(n, n, generator=g, device=device, dtype=torch.float64))
-        return u * torch.exp2(e)
+        u = torch.rand(n, n, generator=g, dtype=torch.float64) * 2 - 1
+        e = torch.round(4.0 * torch.randn(n, n, generator=g, dtype=torch.float64))
+        return (u * torch.exp2(e)).to(device)
 
     A = draw()
     return A, draw()
