@@ -6,8 +6,19 @@
  * hipStream_t passed as void*; NULL = the null stream), allocates nothing and
  * returns 0 on success or a negative TRNBLAS_E_* code. The message of the
  * last failure on the calling thread is returned by trnblas_hip_last_error().
- * Outputs are caller-allocated; inputs are never written. Functions are
- * reentrant and keep no mutable global state.
+ * Outputs are caller-allocated; inputs are never written.
+ *
+ * Global state. The library keeps an immutable kernel table, a thread-local
+ * error message, and two pieces of mutable per-device state:
+ *  - trnblas_hip_metric_inv_half creates, on its first call on a device,
+ *    two side streams and their events for that device and keeps them until
+ *    the process ends; calls on one device share them and are serialised on
+ *    the host by a mutex (two threads calling it on one device do not
+ *    overlap);
+ *  - trnblas_hip_pair_energy_noalloc keeps its partial sums in one static
+ *    device array per GPU: calls that overlap on one GPU (two streams, or
+ *    two threads) race on it and must be serialised by the caller.
+ * Every other function is reentrant: it touches only its arguments.
  *
  * The reference (trnsci/trnblas 0.13.0) has no native code: its device path is
  * the NKI kernels behind the `torch.ops.trnblas.*` custom ops registered in

@@ -35,3 +35,19 @@ def test_make_inputs_and_flops():
     assert np.all(np.diff(ev.numpy()) >= 0) and ev.min() > 0.1
     # flops of (8, 2, 4): 2a 2*64*2*4 + 2b 2*2*6*8*4 + 3 2*2*6*16 + 4 2*4*36*4
     assert df_mp2.flops(8, 2, 4) == 1024 + 768 + 384 + 1152
+
+
+def test_bench_harness_shapes_and_cli(capsys):
+    # the example's bench shapes and harness (examples/df_mp2.py:269-333)
+    assert df_mp2.BENCH_SHAPES == {"small": (128, 16, 384), "medium": (512, 64, 1536),
+                                   "large": (768, 96, 2304)}
+    assert df_mp2.BENCH_SHAPES["large"][0] - df_mp2.BENCH_SHAPES["large"][1] == 672  # C3's nvir
+    rows = df_mp2.bench("small", passes="both", use_batched_pair=True, verbose=False)
+    assert [r["pass_"] for r in rows] == ["cold", "warm"]
+    inp = df_mp2.make_inputs(*df_mp2.BENCH_SHAPES["small"])
+    want = od.df_mp2_energy_ref(*(t.double().numpy() for t in inp))
+    for r in rows:
+        assert abs(r["E"] - want) <= 1e-6 * abs(want)
+        assert r["tflops"] > 0 and {"chol", "half", "metric", "energy"} <= set(r)
+    df_mp2.main(["--demo", "--fused-energy"])
+    assert "E_MP2" in capsys.readouterr().out

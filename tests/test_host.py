@@ -462,3 +462,121 @@ def test_unready_16bit_route_rule():
     off = buf[1:].view(512, 512)  # one element off a 16-byte boundary
     assert d._unready_16bit_to_aten(off, B, "gemm")
     assert d._dma_ready_2d(torch.zeros(64, 64, dtype=bf).T, 64, 64)
+
+
+# ── drop-in switches read from the environment ──────────────────────────────
+
+
+@pytest.mark.parametrize("value,on", [(None, True), ("1", True), ("yes", True), ("0", False),
+                                      ("false", False), (" Off ", False), ("no", False)])
+def test_pinned_output_switch(monkeypatch, value, on):
+    # TRNBLAS_PINNED_OUTPUT (nki/dispatch.py:2052-2060), read at every call
+    if value is None:
+        monkeypatch.delenv("TRNBLAS_PINNED_OUTPUT", raising=False)
+    else:
+        monkeypatch.setenv("TRNBLAS_PINNED_OUTPUT", value)
+    assert d._pinned_output_enabled() is on
+    t = torch.arange(6.0)
+    assert d._to_host(t, torch.device("cpu")) is t  # host tensors are never copied
+
+
+def test_metric_solve_switch(monkeypatch):
+    # TRNBLAS_METRIC_SOLVE=auto|host|device (nki/dispatch.py:1833-1849)
+    J = torch.eye(4, dtype=torch.float64) * 4.0
+    for v in ("auto", "host", "device", " HOST "):
+        monkeypatch.setenv("TRNBLAS_METRIC_SOLVE", v)
+        assert d._metric_solve_route(J) == "device"  # a host J: host LAPACK through torch
+        assert torch.allclose(d.nki_metric_inv_half(J), torch.eye(4, dtype=torch.float64) * 0.5)
+    monkeypatch.setenv("TRNBLAS_METRIC_SOLVE", "gpu")
+    with pytest.raises(ValueError, match="TRNBLAS_METRIC_SOLVE"):
+        d.nki_metric_inv_half(J)
+
+
+def test_ozaki_device_split_switch_warns_once(monkeypatch):
+    # TRNBLAS_OZAKI_DEVICE_SPLIT=0 (nki/dispatch.py:853-862) cannot change the
+    # digits here (the split is native fp64 on the device): one warning says so
+    monkeypatch.setattr(d, "_oz_split_noted", False)
+    monkeypatch.setenv("TRNBLAS_OZAKI_DEVICE_SPLIT", "0")
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        d._note_ozaki_device_split()
+        d._note_ozaki_device_split()
+    assert len([x for x in w if "TRNBLAS_OZAKI_DEVICE_SPLIT" in str(x.message)]) == 1
+    monkeypatch.setattr(d, "_oz_split_noted", False)
+    monkeypatch.setenv("TRNBLAS_OZAKI_DEVICE_SPLIT", "1")
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        d._note_ozaki_device_split()
+    assert not w
+
+
+def test_gemm_ragged_switch(monkeypatch):
+    # TRNBLAS_GEMM_RAGGED=0 (nki/dispatch.py:144-151): operands the DMA kernel
+    # cannot read are packed and zero-padded at every size
+    from trnblas_amd.hip import kernels as k
+
+    monkeypatch.setattr(k, "_pack_k", lambda X, kp: torch.nn.functional.pad(X, (0, kp - X.shape[-1])))
+    A, B = torch.randn(37, 71), torch.randn(71, 53)
+    args = (A, B, A, False, 71, 0, B, False, 53, 0, 37, 53, 71, 1)
+    assert k._packed_operands(*args)[8] == 71  # on: small products stay in place
+    monkeypatch.setattr(k, "_RAGGED_ENABLED", False)
+    out = k._packed_operands(*args)
+    assert out[8] == 72 and out[0] is not A and torch.equal(out[0][:, :71], A)
+    code = "import trnblas_amd.hip.kernels as k; print(k._RAGGED_ENABLED)"
+    for v, want in (("0", "False"), ("off", "False"), ("1", "True")):
+        env = dict(__import__("os").environ, TRNBLAS_GEMM_RAGGED=v)
+        r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env)
+        assert r.stdout.strip() == want, (v, r.stderr)
+
+
+def test_autotune_skips_capture_and_survives_hipblaslt_failure(monkeypatch, tmp_path):
+    # no timing inside a graph capture; a hipBLASLt failure keeps the kernel
+    from trnblas_amd.hip import dispatch as d
+    from trnblas_amd.hip import kernels as k
+
+    monkeypatch.setattr(d, "_autotune_mem", {})
+    monkeypatch.setattr(d, "_autotune_loaded", True, raising=False)
+    monkeypatch.setattr(d, "_save_autotune_cache", lambda: None)
+    h = torch.empty(64, 64, dtype=torch.bfloat16)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    monkeypatch.setattr(d, "_time_device_call", lambda f: pytest.fail("timed during capture"))
+    assert d._autotune_gemm_route(h, h, "gemm") is None
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    calls = []
+
+    def timed(f):
+        calls.append(f)
+        if len(calls) == 2:
+            raise RuntimeError("hipBLASLt failed")
+        return 1.0
+
+    monkeypatch.setattr(d, "_time_device_call", timed)
+    monkeypatch.setattr(k, "gemm", lambda a, b: None)
+    assert d._autotune_gemm_route(h, h, "gemm") == "hip"
+    assert len(calls) == 2 and not d._autotune_mem  # not cached
+
+
+@pytest.mark.parametrize("Mp,Kp,N,k,limit", [
+    (4096, 4096, 4096, 8, ozaki.BLOCK_BYTES), (16384, 16384, 241, 8, ozaki.BLOCK_BYTES),
+    (3328, 8448, 241, 8, ozaki.BLOCK_BYTES), (1024, 2048, 3000, 8, 1 << 22), (256, 1 << 20, 64, 10, 1 << 26),
+])  # fmt: skip
+def test_ozaki_plan_interface(Mp, Kp, N, k, limit):
+    # the reference's launch-plan contract (tests/test_ozaki.py:145-166)
+    mbs, kbs, nbs = ozaki.plan(Mp, Kp, N, k, limit)
+    for blocks, D in ((mbs, Mp), (kbs, Kp), (nbs, N)):
+        assert blocks[0][0] == 0 and sum(sz for _, sz in blocks) == D
+        assert all(a + sa == b for (a, sa), (b, _) in zip(blocks, blocks[1:]))
+    assert all(sz % 128 == 0 for _, sz in mbs + kbs)
+    Mb, Kb, Nb = mbs[0][1], kbs[0][1], nbs[0][1]
+    assert 2 * k * Kb * Mb <= limit and 2 * k * Kb * Nb <= limit and 8 * Mb * Nb <= limit
+    assert Mb <= ozaki.LAUNCH_M and Nb <= ozaki.LAUNCH_N
+    assert Kb == ozaki.k_block(Kp, k, limit)
+    if limit == ozaki.BLOCK_BYTES and Mp * Kp * 2 * k <= limit:
+        assert len(kbs) == 1
+
+
+def test_ozaki_plan_known_answers():
+    assert len(ozaki.plan(768, 1024, 600, 4, max_m=256, max_n=200)[0]) == 3
+    mbs, kbs, nbs = ozaki.plan(2304, 512, 1500, 3, 2 * 3 * 512 * 1024)
+    assert len(mbs) > 1 and len(nbs) > 1 and len(kbs) == 1
+    assert len(ozaki.plan(128, 3072, 20, 8, 2 * 8 * 128 * 1024)[1]) > 1

@@ -222,3 +222,27 @@ def test_pair_energy_wide_dynamic_range(dev, math):
     got = float(kernels.pair_energy_sym(B.to(dev), eo.float().to(dev), ev.float().to(dev), math=math))
     want = pe.pair_energy_f64(B, eo.float(), ev.float())
     assert abs(got - want) <= 1e-6 * abs(want), (got, want)
+
+
+@pytest.mark.parametrize("math,tol", [("fp32", 1e-6), ("bf16x6", 1e-6), ("fp16x3", 1e-6)])
+def test_pair_energy_wide_range_rows(dev, math, tol):
+    # rows whose entries spread over 2^-16 .. 2^16 of each other: fp16x3 scales
+    # each row so its largest entry sits at 2^14, so entries 2^-28 below it
+    # are fp16 subnormals and keep an absolute error (<= 2^-39 of the row
+    # maximum) instead of a relative one. The energy is a sum of products
+    # dominated by the large entries; the gate is the same rel 1e-6 against
+    # fp64, and the measured error of each arithmetic is printed.
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(17)
+    nocc, nvir, naux = 6, 130, 200
+    B = torch.randn(nocc, nvir, naux, generator=g, dtype=torch.float64)
+    B = B * torch.exp2(torch.randint(-16, 17, (nocc, nvir, naux), generator=g).double()) * 0.05
+    B = B.float()
+    eo = -1.5 + 1.2 * torch.rand(nocc, generator=g)
+    ev = 0.1 + 2.9 * torch.rand(nvir, generator=g)
+    got = float(kernels.pair_energy_sym(B.to(dev), eo.to(dev), ev.to(dev), math=math))
+    want = pe.pair_energy_f64(B, eo, ev)
+    rel = abs(got - want) / abs(want)
+    print(f"wide-range rows, {math}: rel {rel:.2e}", flush=True)
+    assert rel <= tol, rel

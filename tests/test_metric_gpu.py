@@ -151,3 +151,78 @@ def test_metric_inv_half_device_error_later_block(dev):
     J[261, 261] = -2.0
     with pytest.raises(torch.linalg.LinAlgError, match="order 262"):
         tb.metric_inv_half(J)
+
+
+def _trsm_case(n, m, side, seed):
+    g = torch.Generator().manual_seed(seed)
+    A = torch.randn(n, n, generator=g, dtype=torch.float64) / n + 2 * torch.eye(n, dtype=torch.float64)
+    B = torch.randn((n, m) if side == "left" else (m, n), generator=g, dtype=torch.float64)
+    return A, B
+
+
+@pytest.mark.parametrize("n,m", [(300, 70), (1000, 700)])
+@pytest.mark.parametrize("side,uplo,trans,diag", FLAGS)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_trsm_device_flags_multiblock(dev, n, m, side, uplo, trans, diag, dtype):
+    """3 and 8 diagonal blocks of 128 (uneven halving, nested updates), ragged
+    n, nrhs above one GEMM tile, right solves through strided views."""
+    A, B = _trsm_case(n, m, side, 100 + n)
+    X = tb.trsm(0.75, A.to(dev, dtype), B.to(dev, dtype), side=side, uplo=uplo, trans=trans, diag=diag)
+    assert X.device.type == "cuda" and X.dtype == dtype and X.shape == B.shape
+    want = om.trsm_ref(0.75, A.numpy(), B.numpy(), side, uplo, trans, diag)
+    tol = 1e-12 if dtype == torch.float64 else 1e-4
+    assert np.abs(X.double().cpu().numpy() - want).max() <= tol * np.abs(want).max()
+
+
+@pytest.mark.parametrize("side,uplo,trans,diag", [("left", "lower", False, "nonunit"),
+                                                  ("right", "upper", True, "unit"),
+                                                  ("left", "upper", True, "nonunit"),
+                                                  ("right", "lower", False, "nonunit")])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_trsm_device_large(dev, side, uplo, trans, diag, dtype):
+    n, m = 2500, 600  # 20 blocks, the last ragged
+    A, B = _trsm_case(n, m, side, 7)
+    X = tb.trsm(1.0, A.to(dev, dtype), B.to(dev, dtype), side=side, uplo=uplo, trans=trans, diag=diag)
+    want = om.trsm_ref(1.0, A.numpy(), B.numpy(), side, uplo, trans, diag)
+    tol = 1e-12 if dtype == torch.float64 else 1e-4
+    assert np.abs(X.double().cpu().numpy() - want).max() <= tol * np.abs(want).max()
+
+
+@pytest.mark.parametrize("side", ["left", "right"])
+def test_trsm_device_ill_conditioned(dev, side):
+    """A Cholesky factor with cond ~1e4 (an SPD matrix of eigenvalues 1 .. 1e-8):
+    the block inverses of the diagonal are where such a triangle loses
+    accuracy. fp64 against torch's solve_triangular on the same device, with
+    a backward-error (residual) gate and a forward gate scaled by cond."""
+    n, m = 1000, 300
+    rng = np.random.default_rng(5)
+    Q, _ = np.linalg.qr(rng.standard_normal((n, n)))
+    J = (Q * np.logspace(0, -8, n)) @ Q.T
+    L = np.linalg.cholesky((J + J.T) / 2)
+    B = rng.standard_normal((n, m) if side == "left" else (m, n))
+    Ld, Bd = torch.from_numpy(L).to(dev), torch.from_numpy(B).to(dev)
+    X = tb.trsm(1.0, Ld, Bd, side=side, uplo="lower")
+    if side == "left":
+        ref = torch.linalg.solve_triangular(Ld, Bd, upper=False)
+        res = Ld @ X - Bd
+    else:
+        ref = torch.linalg.solve_triangular(Ld, Bd, upper=False, left=False)
+        res = X @ Ld - Bd
+    scale = float(Ld.abs().max()) * float(X.abs().max()) * n
+    assert float(res.abs().max()) <= 1e-13 * scale
+    cond = np.linalg.cond(L)
+    assert float((X - ref).abs().max()) <= 1e-14 * cond * float(ref.abs().max())
+
+
+def test_metric_solve_host_route(dev, monkeypatch):
+    # TRNBLAS_METRIC_SOLVE=host (nki/dispatch.py:1833-1870): host LAPACK in
+    # fp64, the factor back on J's device in J's dtype
+    J = torch.from_numpy(om.spd(300, seed=9))
+    monkeypatch.setenv("TRNBLAS_METRIC_SOLVE", "host")
+    X = tb.metric_inv_half(J.to(dev, torch.float32))
+    assert X.device.type == "cuda" and X.dtype == torch.float32
+    want = om.metric_inv_half_ref(J.numpy())
+    assert np.abs(X.double().cpu().numpy() - want).max() <= 1e-6 * np.abs(want).max()
+    monkeypatch.setenv("TRNBLAS_METRIC_SOLVE", "device")
+    Xd = tb.metric_inv_half(J.to(dev))
+    assert np.abs(Xd.cpu().numpy() - want).max() <= 1e-12 * np.abs(want).max()

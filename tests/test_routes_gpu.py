@@ -66,6 +66,16 @@ def test_upload_route_gemm_batched_syrk(dev):
     ref3 = A3.double() @ B3.double()
     assert _cw(D3, ref3, A3.double().abs() @ B3.double().abs()) <= 1e-6
 
+    # TRNBLAS_PINNED_OUTPUT=0 (nki/dispatch.py:2052-2060): pageable results
+    import os
+
+    os.environ["TRNBLAS_PINNED_OUTPUT"] = "0"
+    try:
+        D0 = tb.gemm(1.0, A, B, beta=0.5, C=C)
+    finally:
+        del os.environ["TRNBLAS_PINNED_OUTPUT"]
+    assert D0.device.type == "cpu" and not D0.is_pinned() and torch.equal(D0, D)
+
     As = torch.randn(1536, 2048, generator=g)
     X = torch.randn(1536, 1536, generator=g)
     Cs = torch.tril(X) + torch.tril(X, -1).T

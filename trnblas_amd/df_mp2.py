@@ -197,6 +197,95 @@ def make_inputs(nbasis: int, nocc: int, naux: int, seed: int = 42, device: str =
     return tuple(t.to(device) for t in (C_occ, C_vir, eri_3c, J_metric, eps_occ, eps_vir))
 
 
+# The example's benchmark shapes (examples/df_mp2.py:269-273), as
+# (nbasis, nocc, naux); "large" has nvir 672, the C3 pair-energy shape.
+BENCH_SHAPES = {
+    "small": (128, 16, 384),
+    "medium": (512, 64, 1536),
+    "large": (768, 96, 2304),
+}
+
+
+def bench(shape_name: str, device: str = "cpu", use_fused: bool = False, use_fused_gemm: bool = False,
+          use_batched_pair: bool = False, passes: str = "both", verbose: bool = True) -> list:
+    """Cold and / or warm timing of one `df_mp2_energy` at a bench shape (the
+    example's `bench`, examples/df_mp2.py:276-333): per-step seconds, total,
+    approximate TFLOP/s and the energy E, one dict per pass (also printed).
+    On the GPU the cold pass includes loading the kernels; there is no
+    per-shape compile, so the two passes differ by little."""
+    import time
+
+    nbasis, nocc, naux = BENCH_SHAPES[shape_name]
+    nvir = nbasis - nocc
+    fl = flops(nbasis, nocc, naux)
+    inputs = make_inputs(nbasis, nocc, naux, device=device)
+    mode = ("batched-pair" if use_batched_pair else "fused-gemm" if use_fused_gemm
+            else "fused" if use_fused else "torch")  # fmt: skip
+    if verbose:
+        print(f"[shape={shape_name} nbasis={nbasis} nocc={nocc} nvir={nvir} naux={naux}]")
+        print(f"  approx flops: {fl / 1e9:.1f} G  backend: {_d.get_backend()}  device: {device}  "
+              f"energy_mode: {mode}")  # fmt: skip
+    out = []
+    for label in {"cold": ["cold"], "warm": ["warm"], "both": ["cold", "warm"]}[passes]:
+        t: dict = {}
+        t0 = time.perf_counter()
+        e = df_mp2_energy(*inputs, timings=t, use_fused=use_fused, use_fused_gemm=use_fused_gemm,
+                          use_batched_pair=use_batched_pair)  # fmt: skip
+        if torch.device(device).type == "cuda":
+            torch.cuda.synchronize()
+        total = time.perf_counter() - t0
+        row = dict(pass_=label, shape=shape_name, mode=mode, total=total, tflops=fl / total / 1e12,
+                   E=e, **t)  # fmt: skip
+        out.append(row)
+        if verbose:
+            print(f"  {label}: chol {t['chol']:.3f}s  half {t['half']:.3f}s  metric {t['metric']:.3f}s  "
+                  f"energy {t['energy']:.3f}s  total {total:.3f}s  ~{row['tflops']:.2f} TFLOPS  E={e:.6e}")
+    return out
+
+
+def main(argv=None) -> None:
+    """The example's command line (examples/df_mp2.py:336-428):
+    python -m trnblas_amd.df_mp2 [--bench [--shape S]] [--demo] [--nbasis N
+    --nocc O --naux P] [--device cuda] [--fused-energy | --fused-gemm-energy
+    | --batched-pair-energy] [--passes cold|warm|both]."""
+    import argparse
+    import time
+
+    ap = argparse.ArgumentParser(description="DF-MP2 using trnblas_amd")
+    ap.add_argument("--demo", action="store_true", help="small demo (water-like)")
+    ap.add_argument("--bench", action="store_true", help="cold / warm timing of the bench shapes")
+    ap.add_argument("--shape", choices=list(BENCH_SHAPES), help="restrict --bench to one shape")
+    ap.add_argument("--nbasis", type=int, default=24)
+    ap.add_argument("--nocc", type=int, default=5)
+    ap.add_argument("--naux", type=int, default=None)
+    ap.add_argument("--device", default="cpu", help="torch device of the inputs (cpu, cuda, cuda:0 ...)")
+    ap.add_argument("--fused-energy", action="store_true", help="chunked GEMM + the HIP mp2_energy reduction")
+    ap.add_argument("--fused-gemm-energy", action="store_true", help="one fused launch per ordered pair")
+    ap.add_argument("--batched-pair-energy", action="store_true", help="the fused pair energy, one launch")
+    ap.add_argument("--passes", choices=["cold", "warm", "both"], default="both")
+    a = ap.parse_args(argv)
+    kw = dict(use_fused=a.fused_energy, use_fused_gemm=a.fused_gemm_energy,
+              use_batched_pair=a.batched_pair_energy)  # fmt: skip
+    if a.bench:
+        for shape in [a.shape] if a.shape else list(BENCH_SHAPES):
+            bench(shape, device=a.device, passes=a.passes, **kw)
+        return
+    if a.demo:
+        a.nbasis, a.nocc = 24, 5
+    nbasis, nocc = a.nbasis, a.nocc
+    naux = a.naux or 3 * nbasis
+    inputs = make_inputs(nbasis, nocc, naux, device=a.device)
+    print(f"DF-MP2: nbasis {nbasis}, nocc {nocc}, nvir {nbasis - nocc}, naux {naux}, "
+          f"backend {_d.get_backend()}")  # fmt: skip
+    t: dict = {}
+    t0 = time.perf_counter()
+    e = df_mp2_energy(*inputs, timings=t, **kw)
+    total = time.perf_counter() - t0
+    for k, v in t.items():
+        print(f"  {k:15s}: {v:.3f}s")
+    print(f"\n  E_MP2 = {e:.10f} (synthetic data)\n  Total: {total:.3f}s")
+
+
 def chain_flops(nao: int, nocc: int, nvir: int, naux: int) -> dict:
     """Algorithmic flops of the config-4 chain (symmetric pair count)."""
     return dict(
@@ -293,3 +382,7 @@ def chain_inputs(nao: int, nocc: int, nvir: int, naux: int, device, seed: int = 
         eo.float().to(device),
         ev.float().to(device),
     )
+
+
+if __name__ == "__main__":
+    main()

@@ -44,6 +44,13 @@ def _env_flag(*names: str) -> bool:
 
 
 _REQUIRE_HIP = _env_flag("TRNBLAS_REQUIRE_HIP", "TRNBLAS_REQUIRE_NKI")
+_OFF = ("0", "false", "no", "off")
+
+
+def _env_on(name: str, default: str = "1") -> bool:
+    """A switch that is on unless set to 0 / false / no / off (the
+    reference's convention for its default-on switches)."""
+    return os.environ.get(name, default).strip().lower() not in _OFF
 
 
 class HipFallbackWarning(UserWarning):
@@ -448,6 +455,10 @@ def _autotune_gemm_route(a: torch.Tensor, b: torch.Tensor, op: str) -> str | Non
     hit = _autotune_mem.get(key)
     if hit is not None:
         return hit
+    if torch.cuda.is_current_stream_capturing():
+        # no timing inside a graph capture (event syncs would break it): the
+        # static rule decides, and the bucket is measured on a later eager call
+        return None
     from . import kernels
 
     try:
@@ -459,7 +470,10 @@ def _autotune_gemm_route(a: torch.Tensor, b: torch.Tensor, op: str) -> str | Non
     except Exception as exc:  # noqa: BLE001
         _kernel_failed(exc)  # raises under TRNBLAS_REQUIRE_HIP
         return "aten"  # not cached: the kernel is retried in the next process
-    t_aten = _time_device_call(lambda: torch.matmul(a, b))
+    try:
+        t_aten = _time_device_call(lambda: torch.matmul(a, b))
+    except Exception:  # noqa: BLE001  hipBLASLt failed: keep the kernel, uncached
+        return "hip"
     choice = "aten" if t_aten < t_hip else "hip"
     _autotune_mem[key] = choice
     _autotune_measured += 1
@@ -515,14 +529,24 @@ def _to(t, dev):
     return t if t is None or t.device == dev else t.to(dev, non_blocking=False)
 
 
+_PINNED_OUTPUT_MIN_BYTES = 1 << 20
+
+
+def _pinned_output_enabled() -> bool:
+    """TRNBLAS_PINNED_OUTPUT=0 (or false / no / off) turns pinned results off
+    (nki/dispatch.py:2052-2060); read at every call, as the reference does."""
+    return _env_on("TRNBLAS_PINNED_OUTPUT")
+
+
 def _to_host(t: torch.Tensor, orig: torch.device) -> torch.Tensor:
-    """A device result back on the host device `orig`: into fresh pinned
-    memory (device-to-host copies from pageable memory run ~4 GB/s on the
-    MI355X host, from pinned ~10x faster; the reference's `_host_empty` /
-    `_to_host`, nki/dispatch.py:2055-2101, makes the same choice)."""
+    """A device result back on the host device `orig`: results of 1 MiB and
+    more into fresh pinned memory (device-to-host copies from pageable memory
+    run ~4 GB/s on the MI355X host, from pinned ~10x faster; the reference's
+    `_host_empty` / `_to_host`, nki/dispatch.py:2055-2101, makes the same
+    choice), unless TRNBLAS_PINNED_OUTPUT turns that off."""
     if orig.type != "cpu" or t.device.type == "cpu":
         return t.to(orig)
-    if t.numel() * t.element_size() < (1 << 20):
+    if t.numel() * t.element_size() < _PINNED_OUTPUT_MIN_BYTES or not _pinned_output_enabled():
         return t.cpu()
     out = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
     out.copy_(t)
@@ -769,6 +793,28 @@ def _metric_inv_half_blocked(J: torch.Tensor) -> torch.Tensor:
     return X
 
 
+_METRIC_SOLVE_CHOICES = ("auto", "host", "device")
+
+
+def _metric_solve_route(J: torch.Tensor) -> str:
+    """'host' or 'device' for `nki_metric_inv_half` (the reference's
+    `_metric_solve_route`, nki/dispatch.py:1833-1849, and its
+    TRNBLAS_METRIC_SOLVE=auto|host|device override). "auto" keeps a device J
+    on the device at every size: on the MI355X the fp64 HIP driver beats the
+    host's LAPACK from the smallest metrics up (naux 4096: 2.8 ms against
+    139-217 ms), where the reference's Trainium route sends naux <= 1024 to
+    the host. "host" computes the factor with host LAPACK in fp64 and copies
+    it back. A host J takes host LAPACK whatever the setting."""
+    choice = os.environ.get("TRNBLAS_METRIC_SOLVE", "auto").strip().lower()
+    if choice not in _METRIC_SOLVE_CHOICES:
+        raise ValueError(
+            f"TRNBLAS_METRIC_SOLVE must be one of {_METRIC_SOLVE_CHOICES}; got {choice!r}"
+        )
+    if not J.is_cuda:
+        return "device"  # plain torch on the host (host LAPACK), as the reference
+    return "host" if choice == "host" else "device"
+
+
 def nki_metric_inv_half(J: torch.Tensor) -> torch.Tensor:
     """Cholesky inverse factor X = L^-T of an SPD metric J = L L^T, so
     X X^T = J^-1 and `A @ X` is the density-fitting metric contraction
@@ -787,7 +833,20 @@ def nki_metric_inv_half(J: torch.Tensor) -> torch.Tensor:
         )
     if J.dim() != 2 or J.shape[0] != J.shape[1]:
         raise ValueError(f"metric_inv_half: J must be square; got {tuple(J.shape)}")
-    if J.is_cuda and J.is_floating_point():
+    route = _metric_solve_route(J)
+    if route == "host":
+        # the reference's host route (nki/dispatch.py:1854-1870): fp64 LAPACK
+        # on the host, the factor copied back in J's dtype
+        Jd = J.detach().to("cpu", torch.float64)
+        L, info = torch.linalg.cholesky_ex(Jd)
+        if int(info) != 0:
+            raise torch.linalg.LinAlgError(
+                f"metric Cholesky failed: leading minor of order {int(info)} is not positive-definite"
+            )
+        eye = torch.eye(Jd.shape[0], dtype=torch.float64)
+        X = torch.linalg.solve_triangular(L.mT, eye, upper=True).contiguous()
+        return X.to(dtype=J.dtype).to(J.device)
+    if route == "device" and J.is_cuda and J.is_floating_point():
         return _metric_inv_half_blocked(J).to(J.dtype)
     cdt = _solve_dtype(J)
     L, info = torch.linalg.cholesky_ex(J.to(cdt))
@@ -1072,6 +1131,25 @@ def _ozaki_route() -> str:
     return "kernel" if _use_hip() else "torch"
 
 
+_oz_split_noted = False
+
+
+def _note_ozaki_device_split() -> None:
+    """TRNBLAS_OZAKI_DEVICE_SPLIT=0 keeps the reference's split on the host
+    (nki/dispatch.py:853-862), a Trainium workaround for its missing fp64.
+    Here the split is native fp64 on the device with the same digits, so
+    the switch has no effect; say so once instead of ignoring it silently."""
+    global _oz_split_noted
+    if not _oz_split_noted and not _env_on("TRNBLAS_OZAKI_DEVICE_SPLIT"):
+        _oz_split_noted = True
+        warnings.warn(
+            "TRNBLAS_OZAKI_DEVICE_SPLIT=0 has no effect on ROCm: gemm_fp64 always splits on "
+            "the device in native fp64, into the same digits as the host split",
+            UserWarning,
+            stacklevel=3,
+        )
+
+
 def nki_gemm_fp64(a: torch.Tensor, b: torch.Tensor, slices: int, mode: str | None = None) -> torch.Tensor:
     """fp64 a @ b by the Ozaki split on the device (dispatch.py:958-980).
     a (M, K), b (K, N) real tensors (any float dtype; computed as fp64).
@@ -1081,6 +1159,7 @@ def nki_gemm_fp64(a: torch.Tensor, b: torch.Tensor, slices: int, mode: str | Non
 
     k = ozaki.check_slices(slices)
     mode = ozaki.check_mode(mode)
+    _note_ozaki_device_split()
     if _ozaki_route() == "torch":
         return torch.matmul(a.double(), b.double())
     dev = _gpu_device(a, b)

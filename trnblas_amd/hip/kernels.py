@@ -107,6 +107,18 @@ def _batched_layout(X: torch.Tensor):
 # 1535^3: 126 and 99; bf16 511^3: 29 and 32; 767^3: 38 and 34).
 PACK_MIN_MACS = {4: 1 << 30, 2: 1 << 28}
 
+# TRNBLAS_GEMM_RAGGED=0 restores the reference's pad-first path
+# (nki/dispatch.py:144-151, read at import as there): every operand the DMA
+# kernel cannot read in place is packed and zero-padded first, whatever the
+# size; ragged M / N edges stay in the kernel either way.
+_RAGGED_ENABLED: bool = os.environ.get("TRNBLAS_GEMM_RAGGED", "1").strip().lower() not in (
+    "0", "false", "no", "off",
+)  # fmt: skip
+
+
+def _pack_min_macs(elem_size: int) -> int:
+    return PACK_MIN_MACS[elem_size] if _RAGGED_ENABLED else 0
+
 
 def _dma_ready(t: torch.Tensor, ld: int, stride: int, ext: int, ev: int) -> bool:
     return t.data_ptr() % 16 == 0 and ld % ev == 0 and stride % ev == 0 and ext % ev == 0
@@ -132,7 +144,7 @@ def _packed_operands(A, B, a, ta, lda, sa, b, tb, ldb, sb, M, N, K, nb):
     with the operands the DMA kernel cannot read packed K-contiguous (and K
     padded when it is not a multiple of 16 bytes)."""
     ev = 16 // A.element_size()
-    if nb * M * N * K < PACK_MIN_MACS[A.element_size()] or M == 0 or N == 0 or K == 0:
+    if nb * M * N * K < _pack_min_macs(A.element_size()) or M == 0 or N == 0 or K == 0:
         return a, ta, lda, sa, b, tb, ldb, sb, K
     a_ok = _dma_ready(a, lda, sa, M if ta else K, ev)
     b_ok = _dma_ready(b, ldb, sb, K if tb else N, ev)
@@ -152,7 +164,7 @@ def _packed_syrk_operand(A, trans, a, t, lda, n, k):
     """SYRK's (a, t, lda, k) for op(A) (n, k): as laid out, or packed
     K-contiguous with k padded to a multiple of 16 bytes (see _packed_operands)."""
     ev = 16 // A.element_size()
-    if n * n * k < PACK_MIN_MACS[A.element_size()] or n == 0 or k == 0 or _dma_ready(a, lda, 0, n if t else k, ev):
+    if n * n * k < _pack_min_macs(A.element_size()) or n == 0 or k == 0 or _dma_ready(a, lda, 0, n if t else k, ev):
         return a, t, lda, k
     kp = -(-k // ev) * ev
     return _pack_k(A.t() if trans else A, kp), False, kp, kp
@@ -369,10 +381,19 @@ _PE_ENTRY = {
 
 def pair_energy_math() -> str:
     """Arithmetic of the fused pair-energy kernel: TRNBLAS_PAIR_ENERGY_MATH =
-    "fp16x3" (default: f16 MFMA on two-piece splits of row-scaled operands,
-    three products, fp32 slice sums; the fastest, with fp32 MFMA's accuracy
-    against fp64), "bf16x6" (bf16 MFMA on three-piece splits, six products;
-    the most accurate) or "fp32" (fp32 MFMA)."""
+    "fp16x3" (default, the fastest: f16 MFMA on two-piece splits of
+    row-scaled operands, three products, fp32 slice sums), "bf16x6" (bf16
+    MFMA on three-piece splits, six products; the most accurate) or "fp32"
+    (fp32 MFMA).
+
+    Accuracy per product x y: fp32 MFMA and bf16x6 are within about 2^-22 of
+    x y; fp16x3 keeps 22 significand bits per operand and drops lo_x lo_y, so
+    within 3 2^-22 (about 4x fp32's), and an entry more than 2^28 below its
+    row's largest entry becomes an fp16 subnormal with an absolute error of
+    at most 2^-39 of that maximum rather than a relative one. On energies
+    (sums dominated by the large entries) all three meet rel 1e-6 against
+    fp64 (C3: fp16x3 2.3e-9, fp32 2.3e-9, bf16x6 1.3e-10); callers that need
+    fp32-class accuracy product by product choose "bf16x6" or "fp32"."""
     return _check_math(os.environ.get("TRNBLAS_PAIR_ENERGY_MATH", "fp16x3").strip().lower())
 
 

@@ -103,6 +103,36 @@ def k_block(Kp: int, slices: int, limit: int = BLOCK_BYTES) -> int:
     return max(TILE_K, (cap // 1024) // TILE_K * TILE_K)
 
 
+# The reference's launch caps (ozaki.py:470-481): Trainium compile time grows
+# with a launch's whole problem, so its launches are capped at 1024 x 1024
+# outputs. The int8 kernels here need no cap; the names stay for callers.
+LAUNCH_M = 1024
+LAUNCH_N = 1024
+
+
+def _cuts(total: int, step: int) -> list:
+    return [(i, min(step, total - i)) for i in range(0, total, step)]
+
+
+def plan(Mp: int, Kp: int, N: int, slices: int, limit: int = BLOCK_BYTES,
+         max_m: int = LAUNCH_M, max_n: int = LAUNCH_N):
+    """The reference's launch blocks (m_blocks, k_blocks, n_blocks), each
+    [(start, size)] (ozaki.py:484-511), for callers of that interface: every
+    launch at most max_m x max_n outputs with its operands (2 k Kb Mb,
+    2 k Kb Nb bytes) and result (8 Mb Nb bytes) within `limit`. Here only
+    the K block changes the arithmetic (`k_block`, which `run_device` uses):
+    the M / N blocks of one launch compute the same (hi, lo) chains, so the
+    kernels cover all of M and N in one launch."""
+    k = check_slices(slices)
+    cap = limit // (2 * k)
+    kb = k_block(Kp, k, limit)
+    mb = max(TILE_K, min(Mp, max_m // TILE_K * TILE_K, (cap // kb) // TILE_K * TILE_K))
+    nb = max(1, min(N, max_n, cap // kb))
+    if 8 * mb * nb > limit:
+        nb = max(1, min(nb, limit // (8 * mb)))
+    return _cuts(Mp, mb), _cuts(Kp, kb), _cuts(N, nb)
+
+
 def split_device(X: torch.Tensor, slices: int, per: str, interleaved: bool = False,
                  check: bool = True):
     """Device digits of `ozaki.split(X, slices, per, pad=(128, 128))`:
