@@ -65,6 +65,59 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def host_info() -> dict:
+    """The host the CPU legs run on: CPU model (lscpu's "Model name", from
+    /proc/cpuinfo), the CPUs in this process's affinity mask, P = the
+    physical cores among them (distinct (package, core) ids), and
+    OMP_WAIT_POLICY."""
+    cpus = sorted(os.sched_getaffinity(0))
+    model, cores, cur = None, set(), {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if ":" not in line:
+                if cur.get("processor") is not None and int(cur["processor"]) in cpus:
+                    cores.add((cur.get("physical id"), cur.get("core id")))
+                cur = {}
+                continue
+            k, v = (x.strip() for x in line.split(":", 1))
+            cur[k] = v
+            if k == "model name" and model is None:
+                model = v
+        if cur.get("processor") is not None and int(cur["processor"]) in cpus:
+            cores.add((cur.get("physical id"), cur.get("core id")))
+    except OSError:
+        pass
+    phys = len(cores) if cores and None not in {c for pair in cores for c in pair} else len(cpus)
+    return {"cpu_model": model, "affinity_cpus": len(cpus), "physical_cores_P": phys,
+            "omp_wait_policy": os.environ.get("OMP_WAIT_POLICY"),
+            "torch_default_threads": torch.get_num_threads()}  # fmt: skip
+
+
+class threads:
+    """torch.set_num_threads(n) for the duration of a block."""
+
+    def __init__(self, n: int):
+        self.n = n
+
+    def __enter__(self):
+        self.prev = torch.get_num_threads()
+        torch.set_num_threads(self.n)
+
+    def __exit__(self, *exc):
+        torch.set_num_threads(self.prev)
+
+
+def cpu_ms(fn, reps: int) -> float:
+    """Median wall time of fn() in ms after one untimed call."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return median(ts)
+
+
 def median(xs):
     xs = sorted(xs)
     return xs[len(xs) // 2]
@@ -106,30 +159,26 @@ def gpu_time_ms(fn, reps: int, warm: int = 1) -> float:
     return median(ts)
 
 
-def cpu_baseline_level3(A, C, Ab, Bb, threads: int) -> dict:
+def cpu_baseline_level3(A, C, Ab, Bb, n_threads: int) -> dict:
     """The reference's CPU path on one full step (oracle/blas.py), median of 3."""
     from oracle import blas
 
-    prev = torch.get_num_threads()
-    torch.set_num_threads(threads)
-    try:
-        Ah, Ch, Abh, Bbh = (x.cpu() for x in (A, C, Ab, Bb))
-        ts = []
-        for r in range(4):
-            t0 = time.perf_counter()
-            blas.syrk_cpu(1.0, Ah, 0.5, Ch, uplo="lower")
-            blas.batched_gemm_cpu(1.0, Abh, Bbh)
-            if r:
-                ts.append(time.perf_counter() - t0)
-        t = median(ts)
-    finally:
-        torch.set_num_threads(prev)
-    return {"value": STEP_FLOP / t / 1e12, "unit": "TFLOP/s", "cores": threads, "ms": t * 1e3}
+    Ah, Ch, Abh, Bbh = (x.cpu() for x in (A, C, Ab, Bb))
+
+    def one():
+        blas.syrk_cpu(1.0, Ah, 0.5, Ch, uplo="lower")
+        blas.batched_gemm_cpu(1.0, Abh, Bbh)
+
+    with threads(n_threads):
+        t = cpu_ms(one, 3) * 1e-3
+    return {"value": STEP_FLOP / t / 1e12, "unit": "TFLOP/s", "cores": n_threads, "ms": t * 1e3}
 
 
-def run_extras(dev, tb, only=None) -> dict:
+def run_extras(dev, tb, only=None, P: int = 1, do_cpu: bool = True) -> dict:
     """The other BASELINE workloads (C1, fp32 8192^3, C3, C5) and the metric
-    stage; `only` selects a subset by name."""
+    stage; `only` selects a subset by name. CPU legs run at P threads (the
+    physical cores of the affinity mask) and at 2 threads (the reference's
+    publishing convention, docs/benchmarks.md:169-173)."""
     from trnblas_amd import df_mp2
     from trnblas_amd.hip import dispatch, kernels
 
@@ -140,10 +189,13 @@ def run_extras(dev, tb, only=None) -> dict:
         t = gpu_time_ms(lambda: tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True), reps=20, warm=20)
         D = tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True)
         Ah, Bh, Ch = A.cpu(), B.cpu(), C.cpu()
-        t0 = time.perf_counter()
-        cpu = Ah.T @ Bh
-        cpu.mul_(1.0).add_(Ch, alpha=0.5)
-        cpu_ms = (time.perf_counter() - t0) * 1e3
+        from oracle import blas
+
+        with threads(P):
+            cpu = blas.gemm_cpu(1.0, Ah, Bh, 0.5, Ch, transA=True)  # the reference's CPU path
+            c1_cpu_ms = cpu_ms(lambda: blas.gemm_cpu(1.0, Ah, Bh, 0.5, Ch, transA=True), 5) if do_cpu else None
+        with threads(2):
+            c1_cpu2_ms = cpu_ms(lambda: blas.gemm_cpu(1.0, Ah, Bh, 0.5, Ch, transA=True), 3) if do_cpu else None
         den = Ah.double().abs().T @ Bh.double().abs() + 0.5 * Ch.double().abs()
         err = float(((D.cpu().double() - cpu.double()) / den).abs().max())
         # hipBLASLt through torch on the same operands (A^T as a view)
@@ -171,7 +223,8 @@ def run_extras(dev, tb, only=None) -> dict:
             "ms": t, "tflops": fl / t / 1e9, "frac_fp32_peak": fl / t / 1e9 / PEAK_FP32_MFMA,
             "ms_back_to_back": t_b2b, "tflops_back_to_back": fl / t_b2b / 1e9,
             "kernel_ms": tk, "kernel_tflops": fl / tk / 1e9, "kernel_frac_fp32_peak": fl / tk / 1e9 / PEAK_FP32_MFMA,
-            "cw_err_vs_cpu_path": err, "gate": 1e-6, "cpu_ms": cpu_ms, "cpu_threads": torch.get_num_threads(),
+            "cw_err_vs_cpu_path": err, "gate": 1e-6, "cpu_ms": c1_cpu_ms, "cpu_threads": P,
+            "cpu_ms_at_2_threads": c1_cpu2_ms,
             "route": dispatch._gemm_route(A.mT, B), "torch_hipblaslt_ms": tl,
             "torch_hipblaslt_tflops": fl / tl / 1e9, "torch_hipblaslt_ms_back_to_back": tl_b2b,
             "torch_hipblaslt_cw_err_vs_cpu_path": err_l,
@@ -179,9 +232,9 @@ def run_extras(dev, tb, only=None) -> dict:
         log("c1", out["c1_gemm_2048_transA"])
     if only is None or "gemm8192" in only:
         # fp32 GEMM 8192^3 (north-star target: >= 70 % of fp32 MFMA peak)
-        g = torch.Generator(device=dev).manual_seed(0)
-        X = torch.randn(8192, 8192, device=dev, generator=g)
-        Y = torch.randn(8192, 8192, device=dev, generator=g)
+        g = torch.Generator().manual_seed(0)
+        X = torch.randn(8192, 8192, generator=g).to(dev)
+        Y = torch.randn(8192, 8192, generator=g).to(dev)
         t = gpu_time_ms(lambda: tb.gemm(1.0, X, Y), reps=10, warm=2)
         tl = gpu_time_ms(lambda: torch.matmul(X, Y), reps=10, warm=2)
         fl = 2 * 8192**3
@@ -200,12 +253,18 @@ def run_extras(dev, tb, only=None) -> dict:
         tk_nn = gpu_time_ms(lambda: kernels.gemm(Xb, Yb, 1.0, 0.0, None), reps=10, warm=2)
         tk_nt = gpu_time_ms(lambda: kernels.gemm(Xb, Yb.mT, 1.0, 0.0, None), reps=10, warm=2)
         out["gemm_bf16_8192"] = {
-            "route_nn": dispatch._gemm_route(Xb, Yb), "route_nt": dispatch._gemm_route(Xb, Yb.mT),
-            "nn_ms": tb_nn, "nn_tflops": fl / tb_nn / 1e9, "nt_ms": tb_nt, "nt_tflops": fl / tb_nt / 1e9,
-            "frac_bf16_peak_nt": fl / tb_nt / 1e9 / PEAK_BF16_MFMA,
+            # the public call (whichever route it takes) ...
+            "public_route_nn": dispatch._gemm_route(Xb, Yb), "public_route_nt": dispatch._gemm_route(Xb, Yb.mT),
+            "public_nn_ms": tb_nn, "public_nn_tflops": fl / tb_nn / 1e9,
+            "public_nt_ms": tb_nt, "public_nt_tflops": fl / tb_nt / 1e9,
+            # ... the hand-written HIP kernel on its own ...
             "kernel_nn_ms": tk_nn, "kernel_nn_tflops": fl / tk_nn / 1e9,
+            "kernel_nn_frac_bf16_peak": fl / tk_nn / 1e9 / PEAK_BF16_MFMA,
             "kernel_nt_ms": tk_nt, "kernel_nt_tflops": fl / tk_nt / 1e9,
-            "torch_hipblaslt_nn_ms": tlb, "torch_tflops": fl / tlb / 1e9,
+            "kernel_nt_frac_bf16_peak": fl / tk_nt / 1e9 / PEAK_BF16_MFMA,
+            # ... and hipBLASLt (torch.matmul) on its own
+            "hipblaslt_nn_ms": tlb, "hipblaslt_nn_tflops": fl / tlb / 1e9,
+            "hipblaslt_nn_frac_bf16_peak": fl / tlb / 1e9 / PEAK_BF16_MFMA,
         }  # fmt: skip
         log("gemm8192bf16", out["gemm_bf16_8192"])
         del Xb, Yb
@@ -249,8 +308,7 @@ def run_extras(dev, tb, only=None) -> dict:
             "achieved": 3 * fl / t_launch / 1e9, "peak": PEAK_BF16_MFMA, "unit": "TFLOP/s (f16 MFMA)",
             "frac": 3 * fl / t_launch / 1e9 / PEAK_BF16_MFMA,
             "achieved_fp32_equiv": fl / t_launch / 1e9, "ceiling_fp32_equiv": PEAK_BF16_MFMA / 3,
-            "frac_fp32_peak": fl / t_launch / 1e9 / PEAK_FP32_MFMA,
-            "algorithmic_flop_per_launch": fl, "traffic": None,
+            "algorithmic_flop_per_launch": fl, "traffic": committed_traffic("pair_energy_x3c"),
         }  # fmt: skip
         # The reference's CPU path (the fp32 torch pair loop of
         # dispatch.py:2514-2533, restated in oracle/pair_energy.py) over all
@@ -258,9 +316,18 @@ def run_extras(dev, tb, only=None) -> dict:
         from oracle import pair_energy as pe
 
         Bh, eoh, evh = Bp.cpu(), eo.cpu(), ev.cpu()
-        t0 = time.perf_counter()
-        e_cpu = float(pe.batched_pair_cpu(Bh, eoh, evh))
-        cpu_loop_ms = (time.perf_counter() - t0) * 1e3
+        e_cpu, cpu_loop_ms, cpu2_sample_ms = float("nan"), None, None
+        if do_cpu:
+            with threads(P):
+                t0 = time.perf_counter()
+                e_cpu = float(pe.batched_pair_cpu(Bh, eoh, evh))
+                cpu_loop_ms = (time.perf_counter() - t0) * 1e3
+            # at 2 threads a bounded sample: rows i = 0..11 (1152 of the 9216
+            # ordered pairs, 1/8 of the loop), scaled by 8
+            with threads(2):
+                t0 = time.perf_counter()
+                pe.batched_pair_cpu(Bh, eoh, evh, rows=range(12))
+                cpu2_sample_ms = (time.perf_counter() - t0) * 1e3
         del Bh
         out["pair_energy_c3_96_672_2304"] = {
             "fused_ms": tf, "fused_math": "fp16x3", "unfused_gpu_ms": tu,
@@ -276,8 +343,11 @@ def run_extras(dev, tb, only=None) -> dict:
             "rel_err_fused_fp32_mfma_vs_fp64": abs(e_f32 - e64) / abs(e64),
             "rel_err_unfused_fp32_vs_fp64": abs(e_unf - e64) / abs(e64), "gate": 1e-6,
             "cpu_fp32_loop_ms": cpu_loop_ms, "rel_err_cpu_fp32_loop_vs_fp64": abs(e_cpu - e64) / abs(e64),
-            "cpu_sample": "the whole fp32 torch pair loop (9216 ordered pairs), once",
-            "cpu_threads": torch.get_num_threads(), "roofline": roof,
+            "cpu_sample": "the whole fp32 torch pair loop (9216 ordered pairs), once, at P threads",
+            "cpu_threads": P,
+            "cpu_fp32_loop_ms_at_2_threads": None if cpu2_sample_ms is None else 8 * cpu2_sample_ms,
+            "cpu_sample_at_2_threads": "rows i = 0..11 of the loop (1152 ordered pairs), once, x8",
+            "roofline": roof,
         }  # fmt: skip
         log("c3", out["pair_energy_c3_96_672_2304"])
         del Bp
@@ -300,7 +370,7 @@ def run_extras(dev, tb, only=None) -> dict:
             "flop": tot, "tflops": tot / t_all / 1e9,
             "half_transform_tflops": (fl["half1"] + fl["half2"]) / th / 1e9,
             "energy_tflops_sym": fl["energy"] / te / 1e9, "energy_math": "fp16x3",
-            "frac_fp32_peak": tot / t_all / 1e9 / PEAK_FP32_MFMA,
+            "half_transform_frac_fp32_peak": (fl["half1"] + fl["half2"]) / th / 1e9 / PEAK_FP32_MFMA,
             "energy_frac_f16_peak": 3 * fl["energy"] / te / 1e9 / PEAK_BF16_MFMA,
             "parity": "tests/test_config4_gpu.py: rel <= 1e-6 against the fp64 chain on the device",
         }  # fmt: skip
@@ -333,6 +403,24 @@ def run_extras(dev, tb, only=None) -> dict:
                 "k": k, "ms": tk, "int8_tops": opk / tk / 1e9, "frac_int8_peak": opk / tk / 1e9 / PEAK_INT8,
                 "fp64_equiv_tflops": 2 * n**3 / tk / 1e9, "max_cw_diff_vs_dgemm": ek,
             })  # fmt: skip
+        # the reference's gemm_fp64 off the device: host fp64 A @ B
+        # (nki/dispatch.py:965-966), the whole product at P threads, and at 2
+        # threads a bounded sample (rows 0..1023, 1/8 of the work) x8
+        c5_cpu = {}
+        if do_cpu:
+            Ah, Bh = Ao.cpu(), Bo.cpu()
+            with threads(P):
+                t0 = time.perf_counter()
+                Ah @ Bh
+                c5_cpu["host_fp64_ms"] = (time.perf_counter() - t0) * 1e3
+            with threads(2):
+                t0 = time.perf_counter()
+                Ah[:1024] @ Bh
+                c5_cpu["host_fp64_ms_at_2_threads"] = 8 * (time.perf_counter() - t0) * 1e3
+            c5_cpu.update(host_threads=P, host_sample_at_2_threads="rows 0..1023 of A @ B, once, x8")
+            del Ah, Bh
+        k_host = 11  # tests/test_config5_slices_gpu.py: the smallest k at host-fp64 accuracy here
+        t_host = next(x["ms"] for x in sweep if x["k"] == k_host)
         out["ozaki_gemm_fp64_c5_8192_k8"] = {
             "ms": to, "mode": "fast (default: int32 diagonals, fp64 recombination)",
             "int8_tops": ops / to / 1e9, "frac_int8_peak": ops / to / 1e9 / PEAK_INT8,
@@ -340,6 +428,13 @@ def run_extras(dev, tb, only=None) -> dict:
             "native_dgemm_tflops": 2 * n**3 / td / 1e9, "max_cw_err_vs_dgemm": err,
             "exact_mode_ms": tx, "exact_mode_frac_int8_peak": ops / tx / 1e9 / PEAK_INT8,
             "exact_mode_max_cw_err_vs_dgemm": errx, "slice_sweep_fast": sweep,
+            "host_accurate": {
+                "slices": k_host, "mode": "fast", "ms": t_host, "fp64_equiv_tflops": 2 * n**3 / t_host / 1e9,
+                "native_dgemm_ms": td, "speedup_vs_dgemm": td / t_host,
+                "gate": "max(4 host, 4e-15) over the whole output, asserted: "
+                        "tests/test_config5_slices_gpu.py (k = 10 misses it)",
+            },
+            **c5_cpu,
             "accuracy_gate": "every element within the 8-slice error bound (C5 wide-range data): "
             "tests/test_api_gpu.py::test_config5_gemm_fp64_accuracy_full_size, both modes",
         }  # fmt: skip
@@ -364,13 +459,13 @@ def run_extras(dev, tb, only=None) -> dict:
         t0 = time.perf_counter()
         Lh = torch.linalg.cholesky(Jh)
         torch.linalg.solve_triangular(Lh.mT, torch.eye(n, dtype=torch.float64), upper=True)
-        cpu_ms = (time.perf_counter() - t0) * 1e3
+        lapack_ms = (time.perf_counter() - t0) * 1e3
         fl = 2 * n**3 / 3  # algorithmic: Cholesky n^3 / 3 + triangular inverse n^3 / 3
         out["metric_inv_half_fp64_4096"] = {
             "ms": tm, "tflops": fl / tm / 1e9, "frac_fp64_peak": fl / tm / 1e9 / PEAK_FP64_MFMA,
             "max_abs_XtJX_minus_I": resid, "trsm_4096x4096_ms": tt,
             "trsm_tflops": n**3 / tt / 1e9, "trsm_rel_residual": tres,
-            "cpu_lapack_ms": cpu_ms, "cpu_threads": torch.get_num_threads(),
+            "cpu_lapack_ms": lapack_ms, "cpu_threads": torch.get_num_threads(),
         }  # fmt: skip
         log("metric", out["metric_inv_half_fp64_4096"])
         del J, L, R, X, Y
@@ -476,19 +571,20 @@ def main():
     del ref, den, refb, denb, Ad
     t_b = gpu_time_ms(lambda: tb.batched_gemm(1.0, Ab, Bb), reps=20, warm=20)  # past the clock ramp
     cpu = None
+    host = host_info()
+    P = host["physical_cores_P"]
     if not args.no_cpu:
-        threads = torch.get_num_threads()
-        cpu = cpu_baseline_level3(A, C, Ab, Bb, threads)
+        cpu = cpu_baseline_level3(A, C, Ab, Bb, P)
         cpu2 = cpu_baseline_level3(A, C, Ab, Bb, 2)
         cpu.update(kind="port", sample="one full step (C2a SYRK + C2b batched), median of 3",
-                   at_2_threads=cpu2["value"], ms_at_2_threads=cpu2["ms"])  # fmt: skip
+                   at_2_threads=cpu2["value"], ms_at_2_threads=cpu2["ms"], host=host)  # fmt: skip
     extra = {
         "syrk_c2a": {"ms": syrk_ms, "tflops_triangle": achieved, "cw_err_vs_fp64": syrk_err},
         "batched_c2b": {"ms": t_b, "tflops": BATCHED_FLOP / t_b / 1e9, "cw_err_vs_fp64": bat_err},
     }
     if not args.no_extras:
         only = None if args.only is None else set(args.only.split(","))
-        extra.update(run_extras(dev, tb, only))
+        extra.update(run_extras(dev, tb, only, P=P, do_cpu=not args.no_cpu))
     line = {
         "metric": "GEMM TFLOP/s & %MFMA peak; DF-MP2 pair-energy ms at 96/672/2304",
         "value": value,

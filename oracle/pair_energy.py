@@ -79,11 +79,12 @@ def pair_energies_f64(Bi, Bj, eps_i, eps_j, eps_vir, pairs) -> torch.Tensor:
     return out
 
 
-def batched_pair_cpu(B, eps_occ, eps_vir) -> torch.Tensor:
-    """dispatch.py:2514-2533: the nocc^2 loop, summed in B's dtype."""
+def batched_pair_cpu(B, eps_occ, eps_vir, rows=None) -> torch.Tensor:
+    """dispatch.py:2514-2533: the nocc^2 loop, summed in B's dtype. rows: the
+    rows i to loop over (default all; a subset gives a timing sample)."""
     e = torch.zeros((), dtype=B.dtype, device=B.device)
     nocc = B.shape[0]
-    for i in range(nocc):
+    for i in range(nocc) if rows is None else rows:
         for j in range(nocc):
             T = B[i] @ B[j].T
             D = float(eps_occ[i]) + float(eps_occ[j]) - eps_vir.unsqueeze(1) - eps_vir.unsqueeze(0)

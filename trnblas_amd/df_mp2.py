@@ -360,7 +360,14 @@ def chain_inputs(nao: int, nocc: int, nvir: int, naux: int, device, seed: int = 
     """C4 rules: eri (naux, nao, nao) = 0.02 N(0,1) symmetrised in its last two
     indices as (X + X^T) / sqrt(2) (so entries stay N(0, 0.02^2) off the
     diagonal); C_occ, C_vir the first nocc / next nvir columns of the Q of a
-    QR of an N(0,1) (nao x nao) matrix; eps as config 3."""
+    QR of an N(0,1) (nao x nao) matrix; eps as config 3.
+
+    Everything is drawn on the host CPU from torch.Generator().manual_seed(
+    seed), in that order: the QR matrix and eps in fp64, then X in fp32 in
+    fixed chunks of 2^26 values (whole P-slices), each chunk copied to
+    `device` and symmetrised there. X is drawn in fp32 rather than fp64
+    because 4.3e9 fp64 normals take about a minute on the GPU box's host
+    (fp32: ~12 s)."""
     g = torch.Generator().manual_seed(seed)
     Mq = torch.randn(nao, nao, generator=g, dtype=torch.float64)
     Q, _ = torch.linalg.qr(Mq)
@@ -368,13 +375,14 @@ def chain_inputs(nao: int, nocc: int, nvir: int, naux: int, device, seed: int = 
     C_vir = Q[:, nocc : nocc + nvir].contiguous()
     eo = -1.5 + 1.2 * torch.rand(nocc, generator=g, dtype=torch.float64)
     ev = 0.1 + 2.9 * torch.rand(nvir, generator=g, dtype=torch.float64)
-    gd = torch.Generator(device=device).manual_seed(seed)
     eri = torch.empty((naux, nao, nao), dtype=torch.float32, device=device)
-    step = max(1, (1 << 28) // (nao * nao))
+    step = max(1, (1 << 26) // (nao * nao))
+    scale = 0.02 / math.sqrt(2.0)
     for p0 in range(0, naux, step):
         p1 = min(naux, p0 + step)
-        X = 0.02 * torch.randn((p1 - p0, nao, nao), generator=gd, device=device)
-        eri[p0:p1] = (X + X.transpose(1, 2)) / math.sqrt(2.0)
+        X = torch.randn((p1 - p0, nao, nao), generator=g, dtype=torch.float32).to(device)
+        eri[p0:p1] = (X + X.transpose(1, 2)) * scale
+        del X
     return (
         eri,
         C_occ.float().to(device),
