@@ -364,6 +364,55 @@ int trnblas_hip_ozaki_hilo(int slices, int64_t M, int64_t N, int64_t Kp, const i
                            int64_t ldb_slice, float* hilo, int64_t ldh, void* stream);
 
 /*
+ * gemm_fp64 by Ozaki scheme II (the "crt" mode of trnblas_amd.gemm_fp64):
+ * the same precision knob as the digit split of `nki_gemm_fp64`
+ * (trnblas/nki/dispatch.py:958-980, trnblas/ozaki.py:123-455), which these
+ * four calls replace in that mode. Each operand is represented as one
+ * integer per element, A'_il = rint(a_il 2^(p - eA_i)) and B'_lj =
+ * rint(b_lj 2^(p - eB_j)) with p = 7 slices - 1 (the precision of `slices`
+ * 7-bit digits) and eA_i / eB_j the frexp exponents of the row / column
+ * maxima; A'B' is computed exactly from int8 GEMMs modulo pairwise coprime
+ * moduli m_t <= 256 (256, 255, 253, 251, 247, 241, ...; 32 at most) and the
+ * Chinese remainder theorem; C = A'B' 2^(eA_i + eB_j - 2p). The error is
+ * the operand rounding alone, within the `slices`-digit truncation bound.
+ *
+ * trnblas_hip_crt_moduli: the number of moduli for `slices` and inner
+ * dimension K (the fewest whose product M >= 2 K 2^(2p) + 2), or a negative
+ * code.
+ *
+ * trnblas_hip_crt_split: exponents and balanced int8 residues (r in
+ * [-m/2, m/2)) of X (R x C fp64, row-major, ldx) for the first nmod moduli.
+ * per_row = 1 (A): one exponent per row, residue (t, r, k) of X[r][k] at
+ * res[t * ld_plane + r * ld_res + k]; per_row = 0 (B): one exponent per
+ * column, residue (t, c, k) of X[k][c] at res[t * ld_plane + c * ld_res + k]
+ * (written transposed). K runs to kp (a multiple of 64, >= the K extent),
+ * padded with zero residues. exps: int32 per row / column; flags: int32[2],
+ * flags[1] = 1 when X holds inf / nan (the residues are then undefined).
+ *
+ * trnblas_hip_crt_gemm: for t < nmod, P_t = RA_t RB_t^T mod m_t as balanced
+ * int8 residues, RA (t, M rows, Kp) and RB (t, N rows, Kp) from
+ * trnblas_hip_crt_split (16-byte aligned, ld >= Kp multiples of 16). P is
+ * 32 x 32 blocked: plane t at P + t * p_plane (p_plane >= ceil(M / 32)
+ * ceil(N / 32) 1024 bytes), block (bm, bn) at 1024 (bm ceil(N / 32) + bn),
+ * where byte 16 l + e is element (32 bm + 8 (e / 4) + 4 (l / 32) + e % 4,
+ * 32 bn + l % 32) (the layout of the MFMA accumulators).
+ *
+ * trnblas_hip_crt_combine: C[m * ldc_m + n * ldc_n] (fp64) from the residue
+ * planes and exponents: Garner's mixed-radix digits, the value by fp64 fma
+ * Horner over digit pairs, times 2^(eA_m + eB_n - 2p).
+ */
+int trnblas_hip_crt_moduli(int slices, int64_t K);
+int trnblas_hip_crt_split(int per_row, int64_t R, int64_t C, const double* X, int64_t ldx,
+                          int slices, int nmod, int64_t kp, int8_t* res, int64_t ld_res,
+                          int64_t ld_plane, int32_t* exps, int32_t* flags, void* stream);
+int trnblas_hip_crt_gemm(int nmod, int64_t M, int64_t N, int64_t Kp, const int8_t* RA,
+                         int64_t lda, int64_t lda_plane, const int8_t* RB, int64_t ldb,
+                         int64_t ldb_plane, int8_t* P, int64_t p_plane, void* stream);
+int trnblas_hip_crt_combine(int slices, int nmod, int64_t M, int64_t N, const int8_t* P,
+                            int64_t p_plane, const int32_t* eA, const int32_t* eB, double* C,
+                            int64_t ldc_m, int64_t ldc_n, void* stream);
+
+/*
  * One diagonal block of the blocked Cholesky of metric_inv_half, fp64:
  * A (nb x nb, 0 <= nb <= 128, row-major, leading dimension lda; only its lower
  * triangle is read) is overwritten in its lower triangle by the Cholesky

@@ -27,6 +27,6 @@ int check_launch(const char* what) {
 
 }  // namespace trnblas
 
-extern "C" int trnblas_hip_abi_version(void) { return 10; }
+extern "C" int trnblas_hip_abi_version(void) { return 11; }
 
 extern "C" const char* trnblas_hip_last_error(void) { return trnblas::g_last_error; }

@@ -1217,6 +1217,472 @@ static int oz_check_operands(int slices, int64_t M, int64_t N, int64_t Kp, int64
   return TRNBLAS_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Ozaki scheme II (Ozaki, Uchino and Imamura, 2025): the exact product of
+// the integer operands A' = rint(A 2^(p - eA)), B' = rint(B 2^(p - eB))
+// (p = 7 slices - 1: the precision of `slices` 7-bit digits) by the Chinese
+// remainder theorem over pairwise coprime int8 moduli. Each modulus costs
+// one int8 GEMM of balanced residues (|r| <= 128, int32 sums exact), where
+// the digit split costs slices (slices + 1) / 2 of them for all moduli
+// together being fewer: at C5, 22 GEMMs against 66 for 11 slices.
+//
+//  * crt_residues_row / _col: A' (by rows) and B' (by columns, written
+//    transposed) as int8 residues, K contiguous, one plane per modulus;
+//  * crt_gemm_kernel: per modulus t the int8 GEMM A'_t B'_t^T on
+//    v_mfma_i32_32x32x32_i8, its int32 sums reduced to balanced residues mod
+//    m_t in the epilogue and stored in a 32 x 32 blocked layout (lane l's 16
+//    accumulator bytes of block (bm, bn) are 16 contiguous bytes);
+//  * crt_combine_kernel: per element, Garner's mixed-radix digits from the
+//    residues (exact small-integer fp32 arithmetic), the value by Horner in
+//    fp64 fma over digit pairs (radices m_2g m_2g+1), scaled by
+//    2^(eA + eB - 2p).
+
+constexpr int kCrtMax = 32;
+// pairwise coprime, <= 256, largest first (256 first: the balanced
+// mixed-radix range is exactly [-M/2, M/2 - 1])
+constexpr int kCrtMod[kCrtMax] = {256, 255, 253, 251, 247, 241, 239, 233, 229, 227, 223,
+                                  217, 211, 199, 197, 193, 191, 181, 179, 173, 167, 163,
+                                  157, 151, 149, 139, 137, 131, 127, 113, 109, 107};
+
+struct CrtTab {
+  int m[kCrtMax];           // the moduli
+  int q[kCrtMax][kCrtMax];  // q[s][t] = (m_0 ... m_{s-1}) mod m_t, s < t
+  int inv[kCrtMax];         // (m_0 ... m_{t-1})^-1 mod m_t
+  int w28[kCrtMax];         // 2^28 mod m_t
+  int w56[kCrtMax];         // 2^56 mod m_t
+  double rcp[kCrtMax];      // 1 / m_t
+};
+
+constexpr int crt_modinv(int a, int m) {  // a^-1 mod m, gcd(a, m) = 1
+  int t = 0, nt = 1, r = m, nr = a % m;
+  while (nr != 0) {
+    const int q = r / nr;
+    int x = t - q * nt;
+    t = nt;
+    nt = x;
+    x = r - q * nr;
+    r = nr;
+    nr = x;
+  }
+  return t < 0 ? t + m : t;
+}
+
+constexpr CrtTab crt_tab() {
+  CrtTab c{};
+  for (int t = 0; t < kCrtMax; ++t) {
+    const int m = kCrtMod[t];
+    c.m[t] = m;
+    long long P = 1 % m;
+    for (int s = 0; s < t; ++s) {
+      c.q[s][t] = (int)P;
+      P = P * kCrtMod[s] % m;
+    }
+    c.inv[t] = t ? crt_modinv((int)P, m) : 1;
+    long long w = 1;
+    for (int i = 0; i < 28; ++i) w = w * 2 % m;
+    c.w28[t] = (int)w;
+    for (int i = 0; i < 28; ++i) w = w * 2 % m;
+    c.w56[t] = (int)w;
+    c.rcp[t] = 1.0 / m;
+  }
+  return c;
+}
+
+constexpr CrtTab kCrtTab = crt_tab();
+__constant__ CrtTab c_crt_tab = crt_tab();  // for per-launch (runtime) modulus indices
+
+// y = rint(x 2^sh) (|y| <= 2^p, p <= 90) as sign and 28-bit limbs:
+// |y| = y2 2^56 + y1 2^28 + y0, 0 <= yk < 2^28, every step exact (|y| is an
+// integer of at most 53 significant bits).
+struct CrtLimbs {
+  double y0, y1, y2;
+  bool neg;
+};
+
+__device__ __forceinline__ CrtLimbs crt_limbs(double x, int sh) {
+  double y = rint(ldexp(x, sh));
+  CrtLimbs l;
+  l.neg = y < 0.0;
+  y = fabs(y);
+  l.y2 = floor(y * 0x1p-56);
+  y = fma(-l.y2, 0x1p56, y);
+  l.y1 = floor(y * 0x1p-28);
+  l.y0 = fma(-l.y1, 0x1p28, y);
+  return l;
+}
+
+// The balanced residue of sign * |y| modulo m_T: [-m/2, m/2) for even m,
+// [-(m-1)/2, (m-1)/2] for odd m. s = y2 w56 + y1 w28 + y0 < 2^37 is exact in
+// fp64; floor(s / m) from the reciprocal is off by at most one, fixed below.
+template <int T>
+__device__ __forceinline__ int crt_residue(const CrtLimbs& l) {
+  constexpr int m = kCrtMod[T];
+  const double s = fma(l.y2, (double)kCrtTab.w56[T], fma(l.y1, (double)kCrtTab.w28[T], l.y0));
+  const double q = floor(s * kCrtTab.rcp[T]);
+  double r = fma(-q, (double)m, s);
+  r = r < 0.0 ? r + m : r;
+  r = r >= (double)m ? r - m : r;
+  int ri = (int)r;
+  ri = l.neg ? -ri : ri;
+  ri = ri >= m - m / 2 ? ri - m : ri;
+  ri = ri < -(m / 2) ? ri + m : ri;
+  return ri;
+}
+
+// Residues of one element for every modulus t < nmod, byte b of word u[t].
+template <int T>
+__device__ __forceinline__ void crt_residues_of(const CrtLimbs& l, int nmod, uint32_t* u, int b) {
+  if constexpr (T < kCrtMax) {
+    if (T < nmod) {
+      u[T] |= (uint32_t)(uint8_t)(int8_t)crt_residue<T>(l) << (8 * b);
+      crt_residues_of<T + 1>(l, nmod, u, b);
+    }
+  }
+}
+
+// Row residues: X (R, C) row-major with exponent e_r per row, residues
+// out[t * ld_plane + r * ld + c] for c < kp (columns C .. kp - 1 zero).
+// A workgroup covers 1024 columns of one row, 4 per thread.
+__global__ __launch_bounds__(256) void crt_residues_row_kernel(const double* X, int64_t ldx,
+                                                               int R, int C, int kp, int p,
+                                                               int nmod, const int32_t* exps,
+                                                               int8_t* out, int64_t ld,
+                                                               int64_t ld_plane) {
+  const int cgs = (kp + 1023) / 1024;
+  const int64_t r = blockIdx.x / cgs;
+  const int c0 = (int)(blockIdx.x - r * cgs) * 1024 + 4 * (int)threadIdx.x;
+  if (c0 >= kp) return;
+  const int e = exps[r];
+  if (e == kNonFinite) return;
+  uint32_t u[kCrtMax];
+#pragma unroll
+  for (int t = 0; t < kCrtMax; ++t) u[t] = 0;
+  const double* src = X + r * ldx;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const double x = c0 + i < C ? src[c0 + i] : 0.0;
+    crt_residues_of<0>(crt_limbs(x, p - e), nmod, u, i);
+  }
+#pragma unroll
+  for (int t = 0; t < kCrtMax; ++t)
+    if (t < nmod) *reinterpret_cast<uint32_t*>(out + t * ld_plane + r * ld + c0) = u[t];
+}
+
+// Column residues, written transposed: X (R, C) row-major with exponent e_c
+// per column, residues out[t * ld_plane + c * ld + r] for r < kp (rows R ..
+// kp - 1 zero). 64 columns x 64 rows per workgroup; thread: column c0 +
+// t / 4, rows r0 + 16 (t % 4) .. +15, one 16-byte store per modulus.
+__global__ __launch_bounds__(256) void crt_residues_col_kernel(const double* X, int64_t ldx,
+                                                               int R, int C, int kp, int p,
+                                                               int nmod, const int32_t* exps,
+                                                               int8_t* out, int64_t ld,
+                                                               int64_t ld_plane) {
+  const int c = blockIdx.x * 64 + (threadIdx.x >> 2);
+  const int rr = blockIdx.y * 64 + (threadIdx.x & 3) * 16;
+  if (c >= C || rr >= kp) return;
+  const int e = exps[c];
+  if (e == kNonFinite) return;
+  uint32_t u[4][kCrtMax];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int t = 0; t < kCrtMax; ++t) u[q][t] = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = rr + i;
+    const double x = r < R ? X[(int64_t)r * ldx + c] : 0.0;
+    crt_residues_of<0>(crt_limbs(x, p - e), nmod, u[i >> 2], i & 3);
+  }
+#pragma unroll
+  for (int t = 0; t < kCrtMax; ++t)
+    if (t < nmod)
+      *reinterpret_cast<i32x4*>(out + t * ld_plane + (int64_t)c * ld + rr) =
+          i32x4{(int)u[0][t], (int)u[1][t], (int)u[2][t], (int)u[3][t]};
+}
+
+struct CrtGemmArgs {
+  int M, N, Kp;          // Kp a multiple of 64
+  const int8_t* A;       // residue plane t at A + t lda_plane, row m at + m lda
+  int64_t lda, lda_plane;
+  const int8_t* B;       // B^T residues: row n (K contiguous)
+  int64_t ldb, ldb_plane;
+  int8_t* P;             // product residues, 32 x 32 blocked, plane t at P + t p_plane
+  int64_t p_plane;
+  int nbm, nbn;          // 32-row / 32-column blocks of the output
+  int tiles_m, tiles_n;  // 256 x 256 tiles
+};
+
+constexpr int kCrtT = 256, kCrtBK = 64, kCrtStages = 3;
+constexpr int kCrtPanel = kCrtT * kCrtBK;  // bytes of one operand panel per stage (16 KiB)
+constexpr int kCrtStage = 2 * kCrtPanel;
+
+// Balanced residue of an int32 modulo m (|a| < 2^31, exact in fp64).
+__device__ __forceinline__ int crt_smod32(int a, int m, double rcp) {
+  const double x = (double)a;
+  const double q = floor(x * rcp);
+  int r = (int)fma(-q, (double)m, x);
+  r += r < 0 ? m : 0;
+  r -= r >= m ? m : 0;
+  return r >= m - (m >> 1) ? r - m : r;
+}
+
+// The int8 GEMM of one modulus (blockIdx.y) on a 256 x 256 output tile:
+// 4 waves (2 x 2) of 128 x 128, each 4 x 4 blocks of v_mfma_i32_32x32x32_i8
+// (256 int32 accumulators per lane), so a k-step's 16 fragment reads (8 of
+// A, 8 of B, 16 bytes per lane each) feed 32 MFMAs: half the LDS bytes per
+// MFMA of a 64 x 64 wave tile, whose fragment reads would keep the LDS as
+// busy as the matrix cores. K steps of 64 bytes through three LDS stages of
+// 32 KiB (prefetch distance two). A stage holds 256 rows of 64 bytes per
+// operand; group j of row r sits in slot j ^ ((r >> 2) & 3), so the 16
+// rows of a fragment read fall on distinct bank groups and a 1 KiB DMA
+// block is 16 whole rows. The DMA (buffer_load_dwordx4 ... lds) is issued
+// by inline asm, out of sight of the compiler's wait tracking (which would
+// otherwise make the next step's fragment reads wait for it), and waited
+// for explicitly: vmcnt(8) leaves the 8 DMAs of the step after next in
+// flight. Rows past M / N load zeros without a memory access. ACCUM: add
+// the residues already in P (a K block after the first).
+template <bool ACCUM>
+__global__ __launch_bounds__(256, 1) void crt_gemm_kernel(CrtGemmArgs g) {
+  __shared__ __attribute__((aligned(16))) int8_t lds[kCrtStages * kCrtStage];
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int lane = tid & 63;
+  const int mod = blockIdx.y;
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  int tm, tn;
+  grouped_tile(t, g.tiles_m, g.tiles_n, 4, tm, tn);
+  const int m0 = tm * kCrtT, n0 = tn * kCrtT;
+  const int8_t* baseA = g.A + mod * g.lda_plane + (int64_t)m0 * g.lda;
+  const int8_t* baseB = g.B + mod * g.ldb_plane + (int64_t)n0 * g.ldb;
+  const int nsteps = g.Kp / kCrtBK;
+
+  // DMA: wave w moves blocks b = w + 4u (u < 4) of each panel; lane l of a
+  // block fills row 16 b + l / 4, slot l % 4, i.e. source group
+  // (l % 4) ^ ((l >> 4) & 3) of that row
+  uint32_t vA[4], vB[4];
+  {
+    const int gsrc = (lane & 3) ^ ((lane >> 4) & 3);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int row = 16 * (w + 4 * u) + (lane >> 2);
+      vA[u] = m0 + row < g.M ? (uint32_t)(row * g.lda + 16 * gsrc) : kOzOob;
+      vB[u] = n0 + row < g.N ? (uint32_t)(row * g.ldb + 16 * gsrc) : kOzOob;
+    }
+  }
+  auto dma = [&](int step, int st) __attribute__((always_inline)) {
+    int8_t* dst = lds + st * kCrtStage;
+    const int soff = step * kCrtBK;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      oz_dma16_asm(baseA, dst + (w + 4 * u) * 1024, vA[u], soff);
+      oz_dma16_asm(baseB, dst + kCrtPanel + (w + 4 * u) * 1024, vB[u], soff);
+    }
+  };
+
+  i32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+
+  // fragment of chunk c (32 bytes of K): row (l % 32) of the block, group
+  // 2 c + l / 32 in slot (2 c + l / 32) ^ ((l % 32 >> 2) & 3)
+  const int wm = w & 1, wn = w >> 1;
+  const int sw = ((lane & 31) >> 2) & 3;
+  const int o0 = (lane & 31) * kCrtBK + 16 * ((lane >> 5) ^ sw);
+  const int o1 = (lane & 31) * kCrtBK + 16 * ((2 + (lane >> 5)) ^ sw);
+  const int rowA = 128 * wm * kCrtBK, rowB = kCrtPanel + 128 * wn * kCrtBK;
+
+  dma(0, 0);
+  if (nsteps > 1) dma(1, 1);
+  int st = 0;
+  for (int s = 0; s < nsteps; ++s) {
+    if (s + 1 < nsteps)
+      asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    if (s + 2 < nsteps) dma(s + 2, st == 0 ? 2 : st - 1);
+    const int8_t* cur = lds + st * kCrtStage;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int o = c ? o1 : o0;
+      i32x4 fa[4], fb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        fa[i] = *reinterpret_cast<const i32x4*>(cur + rowA + 32 * i * kCrtBK + o);
+        fb[i] = *reinterpret_cast<const i32x4*>(cur + rowB + 32 * i * kCrtBK + o);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    st = st == 2 ? 0 : st + 1;
+  }
+
+  // epilogue: balanced residues mod m, 16 bytes per lane per 32 x 32 block
+  asm volatile("" : "+v"(lane));
+  const int m = c_crt_tab.m[mod];
+  const double rcp = c_crt_tab.rcp[mod];
+  int8_t* P = g.P + mod * g.p_plane;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int bm = (m0 + 128 * wm + 32 * i) >> 5, bn = (n0 + 128 * wn + 32 * j) >> 5;
+      if (bm >= g.nbm || bn >= g.nbn) continue;
+      i32x4* dst = reinterpret_cast<i32x4*>(P + (((int64_t)bm * g.nbn + bn) * 64 + lane) * 16);
+      i32x4 old = {0, 0, 0, 0};
+      if constexpr (ACCUM) old = *dst;
+      uint32_t wd[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int prev = (int8_t)(uint8_t)((uint32_t)old[e >> 2] >> (8 * (e & 3)));
+        wd[e >> 2] |= (uint32_t)(uint8_t)(int8_t)crt_smod32(acc[i][j][e] + prev, m, rcp) << (8 * (e & 3));
+      }
+      *dst = i32x4{(int)wd[0], (int)wd[1], (int)wd[2], (int)wd[3]};
+    }
+}
+
+// Garner digit t of an element from its residue r_t and the digits v_s,
+// s < t (floats holding small integers; every step exact in fp32:
+// |sum| < 32 * 128 * 256 = 2^20, products < 2^16).
+template <int T>
+__device__ __forceinline__ float crt_digit(const float* v, float r) {
+  constexpr int m = kCrtMod[T];
+  float acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < T; ++s) acc = fmaf(v[s], (float)kCrtTab.q[s][T], acc);
+  const float x = r - acc;
+  float q = floorf(x * (1.0f / m));
+  float y = fmaf(-q, (float)m, x);
+  y = y < 0.0f ? y + m : y;
+  y = y >= (float)m ? y - m : y;
+  y *= (float)kCrtTab.inv[T];
+  q = floorf(y * (1.0f / m));
+  float z = fmaf(-q, (float)m, y);
+  z = z < 0.0f ? z + m : z;
+  z = z >= (float)m ? z - m : z;
+  return z >= (float)(m - m / 2) ? z - m : z;
+}
+
+// The digits of one element: byte b of residue word wd[t] for t < nmod.
+__device__ __forceinline__ void crt_digits(float* v, const uint32_t* wd, int b, int nmod) {
+#pragma unroll
+  for (int t = 0; t < kCrtMax; ++t) {
+    if (t < nmod) {
+      const float r = (float)(int8_t)(uint8_t)(wd[t] >> (8 * b));
+      v[t] = r;
+      if (t == 1) v[1] = crt_digit<1>(v, r);
+#define CRT_DIGIT(T) if (t == T) v[T] = crt_digit<T>(v, r);
+      CRT_DIGIT(2) CRT_DIGIT(3) CRT_DIGIT(4) CRT_DIGIT(5) CRT_DIGIT(6) CRT_DIGIT(7) CRT_DIGIT(8)
+      CRT_DIGIT(9) CRT_DIGIT(10) CRT_DIGIT(11) CRT_DIGIT(12) CRT_DIGIT(13) CRT_DIGIT(14)
+      CRT_DIGIT(15) CRT_DIGIT(16) CRT_DIGIT(17) CRT_DIGIT(18) CRT_DIGIT(19) CRT_DIGIT(20)
+      CRT_DIGIT(21) CRT_DIGIT(22) CRT_DIGIT(23) CRT_DIGIT(24) CRT_DIGIT(25) CRT_DIGIT(26)
+      CRT_DIGIT(27) CRT_DIGIT(28) CRT_DIGIT(29) CRT_DIGIT(30) CRT_DIGIT(31)
+#undef CRT_DIGIT
+    }
+  }
+}
+
+// The value sum_t v_t prod_{s<t} m_s by Horner over digit pairs
+// V_g = v_2g + m_2g v_2g+1 (exact) with radices m_2g m_2g+1, from the top:
+// one fp64 fma per pair.
+__device__ __forceinline__ double crt_horner(const float* v, int nmod) {
+  const int top = (nmod - 1) >> 1;
+  double H = 0.0;
+#pragma unroll
+  for (int g = kCrtMax / 2 - 1; g >= 0; --g) {
+    if (g <= top) {
+      const double V = 2 * g + 1 < nmod ? fma((double)kCrtMod[2 * g], (double)v[2 * g + 1], (double)v[2 * g])
+                                        : (double)v[2 * g];
+      H = g == top ? V : fma(H, (double)(kCrtMod[2 * g] * kCrtMod[2 * g + 1]), V);
+    }
+  }
+  return H;
+}
+
+struct CrtCombineArgs {
+  int M, N, nmod, p;
+  const int8_t* P;
+  int64_t p_plane;
+  int nbm, nbn;
+  const int32_t* eA;
+  const int32_t* eB;
+  double* C;
+  int64_t ldc_m, ldc_n;
+};
+
+// One wave per 32 x 32 block of the product residues (4 blocks per
+// workgroup): lane l holds 16 bytes per modulus, the elements of column
+// l % 32, rows 8 (e / 4) + 4 (l / 32) + e % 4 (the MFMA accumulator layout).
+__global__ __launch_bounds__(256) void crt_combine_kernel(CrtCombineArgs g) {
+  const int lane = threadIdx.x & 63;
+  const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= (int64_t)g.nbm * g.nbn) return;
+  const int bm = (int)(blk / g.nbn), bn = (int)(blk - (int64_t)bm * g.nbn);
+  const int n = bn * 32 + (lane & 31);
+  if (n >= g.N) return;
+  const int eb = g.eB[n];
+  const int8_t* src = g.P + blk * 1024 + lane * 16;
+  uint32_t wd[4][kCrtMax];
+#pragma unroll
+  for (int t = 0; t < kCrtMax; ++t)
+    if (t < g.nmod) {
+      const i32x4 x = *reinterpret_cast<const i32x4*>(src + t * g.p_plane);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wd[q][t] = (uint32_t)x[q];
+    }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    for (int b = 0; b < 4; ++b) {
+      const int m = bm * 32 + 8 * q + 4 * (lane >> 5) + b;
+      if (m >= g.M) continue;
+      float v[kCrtMax];
+      crt_digits(v, wd[q], b, g.nmod);
+      const double H = crt_horner(v, g.nmod);
+      const int ea = g.eA[m];
+      g.C[(int64_t)m * g.ldc_m + (int64_t)n * g.ldc_n] = ldexp(H, ea + eb - 2 * g.p);
+    }
+  }
+}
+
+// Moduli count for `slices` and K: the fewest leading moduli whose product M
+// satisfies M >= 2 K 2^(2p) + 2 (multi-word integers, 32-bit limbs).
+static int crt_count(int slices, int64_t K) {
+  const int p = 7 * slices - 1;
+  constexpr int L = 12;  // 384 bits
+  uint32_t need[L] = {0}, M[L] = {0};
+  // need = 2 K 2^(2p) + 2 = (K << (2p + 1)) + 2
+  const int sh = 2 * p + 1;
+  const unsigned __int128 v = (unsigned __int128)(uint64_t)(K > 0 ? K : 1) << (sh % 32);
+  for (int i = 0; i < 4 && sh / 32 + i < L; ++i) need[sh / 32 + i] = (uint32_t)(v >> (32 * i));
+  // + 2
+  uint64_t carry = 2;
+  for (int i = 0; i < L && carry; ++i) {
+    const uint64_t s = (uint64_t)need[i] + carry;
+    need[i] = (uint32_t)s;
+    carry = s >> 32;
+  }
+  M[0] = 1;
+  for (int n = 1; n <= kCrtMax; ++n) {
+    uint64_t c = 0;
+    for (int i = 0; i < L; ++i) {
+      const uint64_t s = (uint64_t)M[i] * (uint64_t)kCrtMod[n - 1] + c;
+      M[i] = (uint32_t)s;
+      c = s >> 32;
+    }
+    // M >= need ?
+    int cmp = 0;
+    for (int i = L - 1; i >= 0 && cmp == 0; --i) cmp = M[i] > need[i] ? 1 : (M[i] < need[i] ? -1 : 0);
+    if (cmp >= 0) return n;
+  }
+  return -1;
+}
+
 }  // namespace trnblas
 
 using namespace trnblas;
@@ -1350,4 +1816,160 @@ extern "C" int trnblas_hip_ozaki_hilo(int slices, int64_t M, int64_t N, int64_t 
   g.hilo = hilo;
   g.ldh = ldh;
   return oz_launch(g, 1, (hipStream_t)stream);
+}
+
+extern "C" int trnblas_hip_crt_moduli(int slices, int64_t K) {
+  clear_error();
+  TRNBLAS_CHECK_ARG(slices >= 1 && slices <= 12, "crt: slices %d not in [1, 12]", slices);
+  TRNBLAS_CHECK_ARG(K >= 0 && K < (1ll << 40), "crt: bad K %lld", (long long)K);
+  const int n = crt_count(slices, K);
+  TRNBLAS_CHECK_ARG(n > 0, "crt: K %lld needs more than %d moduli at %d slices", (long long)K,
+                    kCrtMax, slices);
+  return n;
+}
+
+extern "C" int trnblas_hip_crt_split(int per_row, int64_t R, int64_t C, const double* X,
+                                     int64_t ldx, int slices, int nmod, int64_t kp, int8_t* res,
+                                     int64_t ld_res, int64_t ld_plane, int32_t* exps,
+                                     int32_t* flags, void* stream) {
+  clear_error();
+  hipStream_t s = (hipStream_t)stream;
+  TRNBLAS_CHECK_ARG(per_row == 0 || per_row == 1, "crt_split: per_row %d", per_row);
+  TRNBLAS_CHECK_ARG(slices >= 1 && slices <= 12, "crt_split: slices %d not in [1, 12]", slices);
+  TRNBLAS_CHECK_ARG(nmod >= 1 && nmod <= kCrtMax, "crt_split: nmod %d not in [1, %d]", nmod,
+                    kCrtMax);
+  TRNBLAS_CHECK_ARG(R > 0 && C > 0 && R < (1 << 30) && C < (1 << 30), "crt_split: bad size");
+  TRNBLAS_CHECK_ARG(X && res && exps && flags && ldx >= C, "crt_split: bad X / residues / exps");
+  const int64_t kd = per_row ? C : R;  // the K extent
+  const int64_t rows = per_row ? R : C;
+  TRNBLAS_CHECK_ARG(kp >= kd && kp % 64 == 0 && kp < (1ll << 30),
+                    "crt_split: kp %lld must be a multiple of 64 >= K", (long long)kp);
+  TRNBLAS_CHECK_ARG(ld_res >= kp && ld_res % 16 == 0 && ld_plane >= rows * ld_res &&
+                        ld_plane % 16 == 0 && ((uintptr_t)res & 15) == 0,
+                    "crt_split: bad residue layout");
+  if (per_row) {
+    hipLaunchKernelGGL(oz_emax_row_kernel, dim3((unsigned)R), dim3(256), 0, s, X, ldx, (int)R,
+                       (int)C, exps);
+  } else {
+    TRNBLAS_CHECK_ARG((R + kEmaxRows - 1) / kEmaxRows < 65536, "crt_split: too many rows");
+    hipLaunchKernelGGL(oz_fill_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, s, exps,
+                       (int)C, (int32_t)0x80000000);
+    hipLaunchKernelGGL(oz_emax_col_kernel,
+                       dim3((unsigned)((C + 63) / 64), (unsigned)((R + kEmaxRows - 1) / kEmaxRows)),
+                       dim3(256), 0, s, X, ldx, (int)R, (int)C, exps);
+  }
+  int rc = check_launch("crt_split(emax)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(oz_flags_kernel, dim3(1), dim3(1024), 0, s, exps, (int)rows, flags);
+  rc = check_launch("crt_split(flags)");
+  if (rc) return rc;
+  const int p = 7 * slices - 1;
+  if (per_row) {
+    const int64_t blocks = R * ((kp + 1023) / 1024);
+    TRNBLAS_CHECK_ARG(blocks < (1ll << 31), "crt_split: too large");
+    hipLaunchKernelGGL(crt_residues_row_kernel, dim3((unsigned)blocks), dim3(256), 0, s, X, ldx,
+                       (int)R, (int)C, (int)kp, p, nmod, (const int32_t*)exps, res, ld_res,
+                       ld_plane);
+  } else {
+    TRNBLAS_CHECK_ARG(kp / 64 < 65536, "crt_split: too many rows");
+    hipLaunchKernelGGL(crt_residues_col_kernel, dim3((unsigned)((C + 63) / 64), (unsigned)(kp / 64)),
+                       dim3(256), 0, s, X, ldx, (int)R, (int)C, (int)kp, p, nmod,
+                       (const int32_t*)exps, res, ld_res, ld_plane);
+  }
+  return check_launch("crt_split(residues)");
+}
+
+extern "C" int trnblas_hip_crt_gemm(int nmod, int64_t M, int64_t N, int64_t Kp, const int8_t* RA,
+                                    int64_t lda, int64_t lda_plane, const int8_t* RB,
+                                    int64_t ldb, int64_t ldb_plane, int8_t* P, int64_t p_plane,
+                                    void* stream) {
+  clear_error();
+  TRNBLAS_CHECK_ARG(nmod >= 1 && nmod <= kCrtMax, "crt_gemm: nmod %d not in [1, %d]", nmod,
+                    kCrtMax);
+  TRNBLAS_CHECK_ARG(M > 0 && N > 0 && M < (1 << 30) && N < (1 << 30), "crt_gemm: bad size");
+  TRNBLAS_CHECK_ARG(Kp > 0 && Kp % kCrtBK == 0, "crt_gemm: Kp %lld not a positive multiple of 64",
+                    (long long)Kp);
+  TRNBLAS_CHECK_ARG(RA && RB && P, "crt_gemm: NULL operand");
+  TRNBLAS_CHECK_ARG(lda >= Kp && ldb >= Kp && lda % 16 == 0 && ldb % 16 == 0 &&
+                        lda_plane % 16 == 0 && ldb_plane % 16 == 0 &&
+                        ((uintptr_t)RA & 15) == 0 && ((uintptr_t)RB & 15) == 0,
+                    "crt_gemm: residue operands must be 16-byte aligned with ld >= Kp");
+  // every DMA offset (row < 256, K offset < Kp) inside the 31-bit buffer range
+  TRNBLAS_CHECK_ARG(255 * lda + Kp < 0x7ffffff0ll && 255 * ldb + Kp < 0x7ffffff0ll,
+                    "crt_gemm: leading dimension too large for 32-bit tile offsets");
+  const int nbm = (int)((M + 31) / 32), nbn = (int)((N + 31) / 32);
+  TRNBLAS_CHECK_ARG(p_plane >= (int64_t)nbm * nbn * 1024 && p_plane % 16 == 0 &&
+                        ((uintptr_t)P & 15) == 0,
+                    "crt_gemm: product planes need %lld bytes each, 16-byte aligned",
+                    (long long)nbm * nbn * 1024);
+  CrtGemmArgs g{};
+  g.M = (int)M;
+  g.N = (int)N;
+  g.Kp = (int)Kp;
+  g.A = RA;
+  g.lda = lda;
+  g.lda_plane = lda_plane;
+  g.B = RB;
+  g.ldb = ldb;
+  g.ldb_plane = ldb_plane;
+  g.P = P;
+  g.p_plane = p_plane;
+  g.nbm = nbm;
+  g.nbn = nbn;
+  g.tiles_m = (int)((M + kCrtT - 1) / kCrtT);
+  g.tiles_n = (int)((N + kCrtT - 1) / kCrtT);
+  const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
+  TRNBLAS_CHECK_ARG(nt < (1ll << 31), "crt_gemm: too many tiles");
+  // |residue| <= 128: a K block of 2^16 sums below 2^30 in int32; longer K
+  // runs one launch per block, each adding its residues to the last (mod m)
+  constexpr int64_t kKb = 1 << 16;
+  for (int64_t k0 = 0; k0 < Kp; k0 += kKb) {
+    g.A = RA + k0;
+    g.B = RB + k0;
+    g.Kp = (int)std::min<int64_t>(kKb, Kp - k0);
+    if (k0 == 0)
+      hipLaunchKernelGGL(crt_gemm_kernel<false>, dim3((unsigned)nt, (unsigned)nmod), dim3(256), 0,
+                         (hipStream_t)stream, g);
+    else
+      hipLaunchKernelGGL(crt_gemm_kernel<true>, dim3((unsigned)nt, (unsigned)nmod), dim3(256), 0,
+                         (hipStream_t)stream, g);
+    const int rc = check_launch("crt_gemm");
+    if (rc) return rc;
+  }
+  return TRNBLAS_OK;
+}
+
+extern "C" int trnblas_hip_crt_combine(int slices, int nmod, int64_t M, int64_t N,
+                                       const int8_t* P, int64_t p_plane, const int32_t* eA,
+                                       const int32_t* eB, double* C, int64_t ldc_m,
+                                       int64_t ldc_n, void* stream) {
+  clear_error();
+  TRNBLAS_CHECK_ARG(slices >= 1 && slices <= 12, "crt_combine: slices %d not in [1, 12]", slices);
+  TRNBLAS_CHECK_ARG(nmod >= 1 && nmod <= kCrtMax, "crt_combine: nmod %d not in [1, %d]", nmod,
+                    kCrtMax);
+  TRNBLAS_CHECK_ARG(M > 0 && N > 0 && M < (1 << 30) && N < (1 << 30), "crt_combine: bad size");
+  TRNBLAS_CHECK_ARG(P && eA && eB && C, "crt_combine: NULL argument");
+  const int nbm = (int)((M + 31) / 32), nbn = (int)((N + 31) / 32);
+  TRNBLAS_CHECK_ARG(p_plane >= (int64_t)nbm * nbn * 1024 && p_plane % 16 == 0 &&
+                        ((uintptr_t)P & 15) == 0,
+                    "crt_combine: bad product planes");
+  CrtCombineArgs g{};
+  g.M = (int)M;
+  g.N = (int)N;
+  g.nmod = nmod;
+  g.p = 7 * slices - 1;
+  g.P = P;
+  g.p_plane = p_plane;
+  g.nbm = nbm;
+  g.nbn = nbn;
+  g.eA = eA;
+  g.eB = eB;
+  g.C = C;
+  g.ldc_m = ldc_m;
+  g.ldc_n = ldc_n;
+  const int64_t blocks = ((int64_t)nbm * nbn + 3) / 4;
+  TRNBLAS_CHECK_ARG(blocks < (1ll << 31), "crt_combine: too large");
+  hipLaunchKernelGGL(crt_combine_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     g);
+  return check_launch("crt_combine");
 }

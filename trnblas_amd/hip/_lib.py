@@ -19,7 +19,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 _PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("TRNBLAS_HIP_LIB", _PKG / "lib" / "libtrnblas_hip.so"))
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 F32, BF16, F16, F64 = 0, 1, 2, 3
 DTYPE_CODES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
@@ -107,6 +107,22 @@ SIGNATURES = {
         _c_int,
         [_c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64]
         + [_c_ptr, _c_i64, _c_ptr],
+    ),
+    "trnblas_hip_crt_moduli": (_c_int, [_c_int, _c_i64]),
+    "trnblas_hip_crt_split": (
+        _c_int,
+        [_c_int, _c_i64, _c_i64, _c_ptr, _c_i64, _c_int, _c_int, _c_i64, _c_ptr, _c_i64, _c_i64]
+        + [_c_ptr, _c_ptr, _c_ptr],
+    ),
+    "trnblas_hip_crt_gemm": (
+        _c_int,
+        [_c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr]
+        + [_c_i64, _c_ptr],
+    ),
+    "trnblas_hip_crt_combine": (
+        _c_int,
+        [_c_int, _c_int, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64]
+        + [_c_ptr],
     ),
     "trnblas_hip_chol_block": (
         _c_int,

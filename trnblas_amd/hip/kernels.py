@@ -780,6 +780,66 @@ def ozaki_gemm(dA, eA, dB, eB, M: int, N: int, slices: int, kb: int | None = Non
     return out
 
 
+CRT_KP = 64  # K padding of the residue operands (the CRT GEMM's k-step)
+
+
+def crt_moduli(slices: int, K: int) -> int:
+    """Moduli the scheme-II product of inner dimension K needs at `slices`
+    (trnblas_hip_crt_moduli; host arithmetic, no device call)."""
+    return call("trnblas_hip_crt_moduli", slices, K)
+
+
+def crt_split(X: torch.Tensor, slices: int, nmod: int, per: str, kp: int):
+    """Exponents and int8 residues of a device fp64 matrix X (R, C) for the
+    first nmod moduli: per="row" -> residues (nmod, R, kp) of the rows (K = C),
+    per="col" -> (nmod, C, kp) of the columns (K = R, written transposed).
+    Returns (residues, exps, nonfinite) with `nonfinite` a 0-d device flag."""
+    dev = _require_device(X)
+    if X.dtype != torch.float64:
+        raise TypeError("crt_split takes float64")
+    if X.stride(-1) != 1:
+        X = X.contiguous()
+    R, C = X.shape
+    rows = R if per == "row" else C
+    res = torch.empty((nmod, rows, kp), dtype=torch.int8, device=dev)
+    exps = torch.empty(rows, dtype=torch.int32, device=dev)
+    flags = torch.zeros(2, dtype=torch.int32, device=dev)
+    _probed_call(
+        "crt_split", "trnblas_hip_crt_split", int(per == "row"), R, C, ptr(X), X.stride(0),
+        slices, nmod, kp, ptr(res), kp, rows * kp, ptr(exps), ptr(flags), stream_of(dev),
+    )  # fmt: skip
+    return res, exps, flags[1]
+
+
+def crt_gemm(RA: torch.Tensor, RB: torch.Tensor, M: int, N: int) -> torch.Tensor:
+    """Product residues P_t = RA_t RB_t^T mod m_t, 32 x 32 blocked (see
+    trnblas_hip_crt_gemm): (nmod, ceil(M/32) ceil(N/32) 1024) int8."""
+    dev = _require_device(RA, RB)
+    nmod, _, kp = RA.shape
+    plane = -(-M // 32) * -(-N // 32) * 1024
+    P = torch.empty((nmod, plane), dtype=torch.int8, device=dev)
+    _probed_call(
+        "crt_gemm", "trnblas_hip_crt_gemm", nmod, M, N, kp, ptr(RA), RA.stride(1), RA.stride(0),
+        ptr(RB), RB.stride(1), RB.stride(0), ptr(P), plane, stream_of(dev),
+    )  # fmt: skip
+    return P
+
+
+def crt_combine(P: torch.Tensor, eA: torch.Tensor, eB: torch.Tensor, M: int, N: int, slices: int,
+                out: torch.Tensor | None = None, transpose_out: bool = False) -> torch.Tensor:
+    """fp64 C (M, N) (or C^T into `out` (N, M) with transpose_out) from the
+    product residue planes and the operand exponents."""
+    dev = _require_device(P, eA, eB)
+    if out is None:
+        out = torch.empty((N, M) if transpose_out else (M, N), dtype=torch.float64, device=dev)
+    ldc_m, ldc_n = (out.stride(1), out.stride(0)) if transpose_out else (out.stride(0), out.stride(1))
+    _probed_call(
+        "crt_combine", "trnblas_hip_crt_combine", slices, P.shape[0], M, N, ptr(P), P.stride(0),
+        ptr(eA), ptr(eB), ptr(out), ldc_m, ldc_n, stream_of(dev),
+    )  # fmt: skip
+    return out
+
+
 def ozaki_hilo(dA, dB, M: int, N: int, slices: int) -> torch.Tensor:
     """Raw (2, M, N) fp32 (hi, lo) of the slice GEMM (one K block)."""
     dev = _require_device(dA, dB)

@@ -118,10 +118,17 @@ def gemm_fp64(
     reference's `ozaki.reference_gemm` bit for bit. mode "fast" (the default,
     TRNBLAS_OZAKI_MODE) sums each diagonal of slice pairs exactly in int32 and
     recombines all diagonals in fp64: same digits, same products, an error
-    within the same truncation bound, not bitwise. Accuracy (max |C - C_exact|
-    / (|A| |B|), normal data): about 1e-12 at k = 6, 1e-14 at k = 7, 2e-16 to
-    3e-16 at k = 8 (the default, host-fp64 level); scaling is per row of A and
-    column of B, so data spread over 10^+-4 needs k = 10. 1 <= slices <= 12.
+    within the same truncation bound, not bitwise. mode "crt" (Ozaki scheme
+    II) rounds each operand to the precision of k digits as one integer
+    (p = 7k - 1 bits below its row / column maximum) and forms the integer
+    product exactly from one int8 GEMM per modulus of a Chinese-remainder
+    basis: within the same bound (no digit products are dropped), in
+    n_moduli(k, K) GEMMs (16 at k = 8, 22 at k = 11 for K = 8192) instead of
+    k (k + 1) / 2 (36, 66). Accuracy (max |C - C_exact| / (|A| |B|), normal
+    data): about 1e-12 at k = 6, 1e-14 at k = 7, 2e-16 to 3e-16 at k = 8
+    (the default, host-fp64 level); scaling is per row of A and column of B,
+    so data spread over 10^+-4 needs k = 10, and the wider spread of
+    BASELINE config 5 (exponents 2^round(N(0, 16))) k = 11. 1 <= slices <= 12.
 
     A (M, K) and B (K, N) are 2-D real tensors of any float dtype (computed as
     fp64). Returns float64 (M, N) on A's device. Without a ROCm GPU, under

@@ -167,15 +167,19 @@ def _digits_of(X: torch.Tensor, k: int, want: str, interleaved: bool = False):
     return split_device(X.contiguous(), k, "col", interleaved, False)
 
 
-MODES = ("fast", "exact")
+MODES = ("fast", "exact", "crt")
 
 
 def default_mode() -> str:
-    """Recombination of the slice products: TRNBLAS_OZAKI_MODE = "fast"
-    (default: each diagonal of slice pairs summed exactly in int32, all
-    diagonals recombined in fp64; within the reference's truncation bound) or
-    "exact" (the reference's groups and fp32 TwoSum order: bit-equal to
-    `ozaki.reference_gemm`)."""
+    """How gemm_fp64 multiplies: TRNBLAS_OZAKI_MODE = "fast" (default: the
+    reference's digits and slice products, each diagonal of slice pairs
+    summed exactly in int32, all diagonals recombined in fp64; within the
+    reference's truncation bound), "exact" (the reference's groups and fp32
+    TwoSum order: bit-equal to `ozaki.reference_gemm`) or "crt" (Ozaki scheme
+    II: each operand rounded to the precision of `slices` digits as one
+    integer, the integer product exact by the Chinese remainder theorem over
+    int8 moduli; within the same bound, with no dropped digit products, in
+    n_moduli GEMMs instead of slices (slices + 1) / 2)."""
     return check_mode(os.environ.get("TRNBLAS_OZAKI_MODE", "fast").strip().lower())
 
 
@@ -185,6 +189,39 @@ def check_mode(mode: str | None) -> str:
     if mode not in MODES:
         raise ValueError(f"Ozaki mode must be one of {MODES}; got {mode!r}")
     return mode
+
+
+def _residues_of(X: torch.Tensor, k: int, nmod: int, kp: int, want: str):
+    """Residues (nmod, rows, kp) of the operand role `want` ("A": rows of A,
+    "B": columns of B); a transposed view is split in its own layout."""
+    from .hip import kernels
+
+    if want == "A":
+        if X.mT.is_contiguous() and not X.is_contiguous():
+            return kernels.crt_split(X.mT, k, nmod, "col", kp)
+        return kernels.crt_split(X.contiguous(), k, nmod, "row", kp)
+    if X.mT.is_contiguous() and not X.is_contiguous():
+        return kernels.crt_split(X.mT, k, nmod, "row", kp)
+    return kernels.crt_split(X.contiguous(), k, nmod, "col", kp)
+
+
+def _run_crt(A: torch.Tensor, B: torch.Tensor, k: int, C: torch.Tensor) -> torch.Tensor:
+    """Scheme II on the device: residues of both operands, one int8 GEMM per
+    modulus (one launch), the CRT recombination into C."""
+    from .hip import kernels
+
+    M, K = A.shape
+    N = B.shape[1]
+    nmod = kernels.crt_moduli(k, K)
+    kp = _round_up(K, kernels.CRT_KP)
+    RA, eA, bad_a = _residues_of(A, k, nmod, kp, "A")
+    RB, eB, bad_b = _residues_of(B, k, nmod, kp, "B")
+    P = kernels.crt_gemm(RA, RB, M, N)
+    del RA, RB
+    kernels.crt_combine(P, eA, eB, M, N, k, out=C)
+    if int(bad_a | bad_b):  # one small device-to-host read
+        raise OzakiNonFinite()
+    return C
 
 
 def run_device(
@@ -205,6 +242,8 @@ def run_device(
         return C
     if K == 0:
         return C.zero_()
+    if mode == "crt":
+        return _run_crt(A, B, k, C)
     fast = mode == "fast"
     # the fast schedule reads the digits interleaved (a row's k slices of a
     # 32-wide K chunk side by side)
