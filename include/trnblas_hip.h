@@ -382,16 +382,18 @@ int trnblas_hip_ozaki_hilo(int slices, int64_t M, int64_t N, int64_t Kp, const i
  *
  * trnblas_hip_crt_split: exponents and balanced int8 residues (r in
  * [-m/2, m/2)) of X (R x C fp64, row-major, ldx) for the first nmod moduli.
- * per_row = 1 (A): one exponent per row, residue (t, r, k) of X[r][k] at
- * res[t * ld_plane + r * ld_res + k]; per_row = 0 (B): one exponent per
- * column, residue (t, c, k) of X[k][c] at res[t * ld_plane + c * ld_res + k]
- * (written transposed). K runs to kp (a multiple of 64, >= the K extent),
- * padded with zero residues. exps: int32 per row / column; flags: int32[2],
- * flags[1] = 1 when X holds inf / nan (the residues are then undefined).
+ * per_row = 1 (A): one exponent per row, operand row r = row r of X (K = C);
+ * per_row = 0 (B): one exponent per column, operand row c = column c of X
+ * (K = R). The residues are blocked: residue (t, row r, k) at
+ * res[t * ld_plane + ((r / 16) (kp / 64) + k / 64) 1024 + (r % 16) 64 + k % 64]
+ * (16 rows x 64 bytes per contiguous KiB; ld_plane >= ceil(rows / 16) 16 kp),
+ * K runs to kp (a multiple of 64, >= the K extent), padded with zero
+ * residues. exps: int32 per row / column; flags: int32[2], flags[1] = 1
+ * when X holds inf / nan (the residues are then undefined).
  *
  * trnblas_hip_crt_gemm: for t < nmod, P_t = RA_t RB_t^T mod m_t as balanced
- * int8 residues, RA (t, M rows, Kp) and RB (t, N rows, Kp) from
- * trnblas_hip_crt_split (16-byte aligned, ld >= Kp multiples of 16). P is
+ * int8 residues, RA (M operand rows) and RB (N operand rows) in the blocked
+ * layout of trnblas_hip_crt_split with K extent Kp (16-byte aligned). P is
  * 32 x 32 blocked: plane t at P + t * p_plane (p_plane >= ceil(M / 32)
  * ceil(N / 32) 1024 bytes), block (bm, bn) at 1024 (bm ceil(N / 32) + bn),
  * where byte 16 l + e is element (32 bm + 8 (e / 4) + 4 (l / 32) + e % 4,
@@ -403,11 +405,11 @@ int trnblas_hip_ozaki_hilo(int slices, int64_t M, int64_t N, int64_t Kp, const i
  */
 int trnblas_hip_crt_moduli(int slices, int64_t K);
 int trnblas_hip_crt_split(int per_row, int64_t R, int64_t C, const double* X, int64_t ldx,
-                          int slices, int nmod, int64_t kp, int8_t* res, int64_t ld_res,
-                          int64_t ld_plane, int32_t* exps, int32_t* flags, void* stream);
+                          int slices, int nmod, int64_t kp, int8_t* res, int64_t ld_plane,
+                          int32_t* exps, int32_t* flags, void* stream);
 int trnblas_hip_crt_gemm(int nmod, int64_t M, int64_t N, int64_t Kp, const int8_t* RA,
-                         int64_t lda, int64_t lda_plane, const int8_t* RB, int64_t ldb,
-                         int64_t ldb_plane, int8_t* P, int64_t p_plane, void* stream);
+                         int64_t lda_plane, const int8_t* RB, int64_t ldb_plane, int8_t* P,
+                         int64_t p_plane, void* stream);
 int trnblas_hip_crt_combine(int slices, int nmod, int64_t M, int64_t N, const int8_t* P,
                             int64_t p_plane, const int32_t* eA, const int32_t* eB, double* C,
                             int64_t ldc_m, int64_t ldc_n, void* stream);

@@ -88,3 +88,23 @@ def test_config5_exact_mode_host_accurate_slices(c5):
     bound = oz.error_bound(A, B, HOST_ACCURATE_SLICES, absA_absB=den, xp=torch)
     assert bool(((C - ex).abs() <= bound + A.shape[1] * 2.0**-53 * den).all())
     assert err <= gate, (err, gate)
+
+
+def test_config5_crt_mode_host_accuracy(c5):
+    """Scheme II (mode "crt") on the same data and gate: no digit products are
+    dropped, so at equal k it is at least as accurate as the digit split."""
+    A, B, ex, den, host_C = c5
+    n = A.shape[1]
+    gate = max(4 * _cw(host_C, ex, den), 4e-15)
+    errs = {}
+    for k in (9, 10, 11, 12):
+        C = tb.gemm_fp64(A, B, slices=k, mode="crt")
+        errs[k] = _cw(C, ex, den)
+        bound = oz.error_bound(A, B, k, absA_absB=den, xp=torch) + n * 2.0**-53 * den
+        assert bool(((C - ex).abs() <= bound).all()), k
+        del C, bound
+    meets = [k for k, e in errs.items() if e <= gate]
+    print(f"config5 crt mode: gate {gate:.3e}, " + ", ".join(f"k={k}: {e:.3e}" for k, e in errs.items())
+          + f"; smallest k at host accuracy: {meets[0] if meets else None}", flush=True)
+    assert meets and meets[0] <= HOST_ACCURATE_SLICES, errs
+    assert all(errs[k] <= gate for k in range(meets[0], 13)), errs

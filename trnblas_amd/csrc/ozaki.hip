@@ -24,6 +24,7 @@
 //    store (no (hi, lo) round trip through HBM), including the fp64 sum of K
 //    blocks for very long K (`plan`'s K blocking).
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -1289,6 +1290,51 @@ constexpr CrtTab crt_tab() {
 }
 
 constexpr CrtTab kCrtTab = crt_tab();
+
+// Paired moduli mu_g = m_2g m_2g+1 (< 2^16) for the recombination: the
+// balanced mixed-radix digits in these radices are exactly
+// v_2g + m_2g v_2g+1 of the single-modulus digits.
+constexpr int kCrtPairs = kCrtMax / 2;
+struct CrtPairTab {
+  long long mu[kCrtPairs];              // m_2g m_2g+1
+  int pinv[kCrtPairs];                  // m_2g^-1 mod m_2g+1
+  long long q[kCrtPairs][kCrtPairs];    // q[h][g] = (mu_0 ... mu_h-1) mod mu_g, h < g
+  long long inv[kCrtPairs];             // (mu_0 ... mu_g-1)^-1 mod mu_g
+  double rcp[kCrtPairs];                // 1 / mu_g
+};
+
+constexpr long long crt_modinv64(long long a, long long m) {
+  long long t = 0, nt = 1, r = m, nr = a % m;
+  while (nr != 0) {
+    const long long q = r / nr;
+    long long x = t - q * nt;
+    t = nt;
+    nt = x;
+    x = r - q * nr;
+    r = nr;
+    nr = x;
+  }
+  return t < 0 ? t + m : t;
+}
+
+constexpr CrtPairTab crt_pair_tab() {
+  CrtPairTab c{};
+  for (int g = 0; g < kCrtPairs; ++g) {
+    const long long mu = (long long)kCrtMod[2 * g] * kCrtMod[2 * g + 1];
+    c.mu[g] = mu;
+    c.pinv[g] = crt_modinv(kCrtMod[2 * g] % kCrtMod[2 * g + 1], kCrtMod[2 * g + 1]);
+    long long P = 1 % mu;
+    for (int h = 0; h < g; ++h) {
+      c.q[h][g] = P;
+      P = P * c.mu[h] % mu;
+    }
+    c.inv[g] = g ? crt_modinv64(P, mu) : 1;
+    c.rcp[g] = 1.0 / (double)mu;
+  }
+  return c;
+}
+
+constexpr CrtPairTab kCrtPair = crt_pair_tab();
 __constant__ CrtTab c_crt_tab = crt_tab();  // for per-launch (runtime) modulus indices
 
 // y = rint(x 2^sh) (|y| <= 2^p, p <= 90) as sign and 28-bit limbs:
@@ -1340,71 +1386,95 @@ __device__ __forceinline__ void crt_residues_of(const CrtLimbs& l, int nmod, uin
   }
 }
 
-// Row residues: X (R, C) row-major with exponent e_r per row, residues
-// out[t * ld_plane + r * ld + c] for c < kp (columns C .. kp - 1 zero).
-// A workgroup covers 1024 columns of one row, 4 per thread.
+// Residue planes are blocked: element (row r, k) of modulus t's plane at
+// t * ld_plane + ((r / 16) * (kp / 64) + k / 64) * 1024 + (r % 16) * 64 + k % 64,
+// so the 16 rows x 64 bytes that one LDS DMA instruction of the GEMM moves
+// are one contiguous KiB (eight whole cache lines).
+__device__ __forceinline__ int64_t crt_blk(int64_t r, int k, int nkc) {
+  return ((r >> 4) * nkc + (k >> 6)) * 1024 + (r & 15) * 64 + (k & 63);
+}
+
+// Row residues: X (R, C) row-major with exponent e_r per row, residues of
+// row r, k < kp (columns C .. kp - 1 zero). A workgroup covers 16 rows x
+// 64 columns (one KiB block per modulus); thread t: row 16 blockIdx.y +
+// t / 16, columns 64 blockIdx.x + 4 (t % 16) .. +3. A wave's 4-byte stores
+// of a modulus fill 256 contiguous bytes.
 __global__ __launch_bounds__(256) void crt_residues_row_kernel(const double* X, int64_t ldx,
                                                                int R, int C, int kp, int p,
                                                                int nmod, const int32_t* exps,
-                                                               int8_t* out, int64_t ld,
-                                                               int64_t ld_plane) {
-  const int cgs = (kp + 1023) / 1024;
-  const int64_t r = blockIdx.x / cgs;
-  const int c0 = (int)(blockIdx.x - r * cgs) * 1024 + 4 * (int)threadIdx.x;
-  if (c0 >= kp) return;
+                                                               int8_t* out, int64_t ld_plane) {
+  const int64_t r = (int64_t)blockIdx.y * 16 + (threadIdx.x >> 4);
+  const int k0 = blockIdx.x * 64 + 4 * (threadIdx.x & 15);
+  if (r >= R) return;
   const int e = exps[r];
   if (e == kNonFinite) return;
   uint32_t u[kCrtMax];
 #pragma unroll
   for (int t = 0; t < kCrtMax; ++t) u[t] = 0;
-  const double* src = X + r * ldx;
+  const double* src = X + r * ldx + k0;
+  double x[4];
+  if (k0 + 4 <= C && ((reinterpret_cast<uintptr_t>(src) & 15) == 0)) {
+    const double2 a = *reinterpret_cast<const double2*>(src);
+    const double2 b = *reinterpret_cast<const double2*>(src + 2);
+    x[0] = a.x;
+    x[1] = a.y;
+    x[2] = b.x;
+    x[3] = b.y;
+  } else {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const double x = c0 + i < C ? src[c0 + i] : 0.0;
-    crt_residues_of<0>(crt_limbs(x, p - e), nmod, u, i);
+    for (int i = 0; i < 4; ++i) x[i] = k0 + i < C ? src[i] : 0.0;
   }
 #pragma unroll
+  for (int i = 0; i < 4; ++i) crt_residues_of<0>(crt_limbs(x[i], p - e), nmod, u, i);
+  int8_t* dst = out + crt_blk(r, k0, kp >> 6);
+#pragma unroll
   for (int t = 0; t < kCrtMax; ++t)
-    if (t < nmod) *reinterpret_cast<uint32_t*>(out + t * ld_plane + r * ld + c0) = u[t];
+    if (t < nmod) *reinterpret_cast<uint32_t*>(dst + t * ld_plane) = u[t];
 }
 
-// Column residues, written transposed: X (R, C) row-major with exponent e_c
-// per column, residues out[t * ld_plane + c * ld + r] for r < kp (rows R ..
-// kp - 1 zero). 64 columns x 64 rows per workgroup; thread: column c0 +
-// t / 4, rows r0 + 16 (t % 4) .. +15, one 16-byte store per modulus.
+// Column residues: X (R, C) row-major with exponent e_c per column, the
+// residues of column c as operand row c, k = r < kp (rows R .. kp - 1
+// zero). A workgroup covers 64 rows (k) x 64 columns: the tile is read row
+// by row (coalesced) into LDS, then thread t takes column 16 q + t / 16 of
+// pass q (q < 4) and rows 4 (t % 16) .. +3 of it, so a wave's 4-byte
+// stores of a modulus fill 256 contiguous bytes of the blocked layout.
 __global__ __launch_bounds__(256) void crt_residues_col_kernel(const double* X, int64_t ldx,
                                                                int R, int C, int kp, int p,
                                                                int nmod, const int32_t* exps,
-                                                               int8_t* out, int64_t ld,
-                                                               int64_t ld_plane) {
-  const int c = blockIdx.x * 64 + (threadIdx.x >> 2);
-  const int rr = blockIdx.y * 64 + (threadIdx.x & 3) * 16;
-  if (c >= C || rr >= kp) return;
-  const int e = exps[c];
-  if (e == kNonFinite) return;
-  uint32_t u[4][kCrtMax];
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-#pragma unroll
-    for (int t = 0; t < kCrtMax; ++t) u[q][t] = 0;
+                                                               int8_t* out, int64_t ld_plane) {
+  __shared__ double tile[64][65];  // [column][row], padded: column reads spread over banks
+  const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int r = rr + i;
-    const double x = r < R ? X[(int64_t)r * ldx + c] : 0.0;
-    crt_residues_of<0>(crt_limbs(x, p - e), nmod, u[i >> 2], i & 3);
+    const int r = r0 + 4 * i + ty, c = c0 + tx;
+    tile[tx][4 * i + ty] = (r < R && c < C) ? X[(int64_t)r * ldx + c] : 0.0;
   }
+  __syncthreads();
+  const int kk = 4 * (threadIdx.x & 15);
 #pragma unroll
-  for (int t = 0; t < kCrtMax; ++t)
-    if (t < nmod)
-      *reinterpret_cast<i32x4*>(out + t * ld_plane + (int64_t)c * ld + rr) =
-          i32x4{(int)u[0][t], (int)u[1][t], (int)u[2][t], (int)u[3][t]};
+  for (int q = 0; q < 4; ++q) {
+    const int cl = 16 * q + (threadIdx.x >> 4), c = c0 + cl;
+    if (c >= C) continue;
+    const int e = exps[c];
+    if (e == kNonFinite) continue;
+    uint32_t u[kCrtMax];
+#pragma unroll
+    for (int t = 0; t < kCrtMax; ++t) u[t] = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) crt_residues_of<0>(crt_limbs(tile[cl][kk + i], p - e), nmod, u, i);
+    int8_t* dst = out + crt_blk(c, r0 + kk, kp >> 6);
+#pragma unroll
+    for (int t = 0; t < kCrtMax; ++t)
+      if (t < nmod) *reinterpret_cast<uint32_t*>(dst + t * ld_plane) = u[t];
+  }
 }
 
 struct CrtGemmArgs {
   int M, N, Kp;          // Kp a multiple of 64
-  const int8_t* A;       // residue plane t at A + t lda_plane, row m at + m lda
-  int64_t lda, lda_plane;
-  const int8_t* B;       // B^T residues: row n (K contiguous)
+  const int8_t* A;       // blocked residues (crt_blk): plane t at A + t lda_plane,
+  int64_t lda, lda_plane;  // lda = bytes from one 16-row block to the next
+  const int8_t* B;       // B^T residues, blocked the same way
   int64_t ldb, ldb_plane;
   int8_t* P;             // product residues, 32 x 32 blocked, plane t at P + t p_plane
   int64_t p_plane;
@@ -1412,9 +1482,9 @@ struct CrtGemmArgs {
   int tiles_m, tiles_n;  // 256 x 256 tiles
 };
 
-constexpr int kCrtT = 256, kCrtBK = 64, kCrtStages = 3;
-constexpr int kCrtPanel = kCrtT * kCrtBK;  // bytes of one operand panel per stage (16 KiB)
-constexpr int kCrtStage = 2 * kCrtPanel;
+constexpr int kCrtTM = 256, kCrtTN = 256, kCrtBK = 64, kCrtStages = 4;
+constexpr int kCrtPanelA = kCrtTM * kCrtBK;              // 16 KiB per stage
+constexpr int kCrtStage = kCrtPanelA + kCrtTN * kCrtBK;  // 32 KiB
 
 // Balanced residue of an int32 modulo m (|a| < 2^31, exact in fp64).
 __device__ __forceinline__ int crt_smod32(int a, int m, double rcp) {
@@ -1428,19 +1498,22 @@ __device__ __forceinline__ int crt_smod32(int a, int m, double rcp) {
 
 // The int8 GEMM of one modulus (blockIdx.y) on a 256 x 256 output tile:
 // 4 waves (2 x 2) of 128 x 128, each 4 x 4 blocks of v_mfma_i32_32x32x32_i8
-// (256 int32 accumulators per lane), so a k-step's 16 fragment reads (8 of
-// A, 8 of B, 16 bytes per lane each) feed 32 MFMAs: half the LDS bytes per
-// MFMA of a 64 x 64 wave tile, whose fragment reads would keep the LDS as
-// busy as the matrix cores. K steps of 64 bytes through three LDS stages of
-// 32 KiB (prefetch distance two). A stage holds 256 rows of 64 bytes per
-// operand; group j of row r sits in slot j ^ ((r >> 2) & 3), so the 16
-// rows of a fragment read fall on distinct bank groups and a 1 KiB DMA
-// block is 16 whole rows. The DMA (buffer_load_dwordx4 ... lds) is issued
-// by inline asm, out of sight of the compiler's wait tracking (which would
-// otherwise make the next step's fragment reads wait for it), and waited
-// for explicitly: vmcnt(8) leaves the 8 DMAs of the step after next in
-// flight. Rows past M / N load zeros without a memory access. ACCUM: add
-// the residues already in P (a K block after the first).
+// (256 int32 accumulators per lane, in AGPRs), so a 32-byte chunk's 8
+// fragment reads (4 of A, 4 of B, 16 bytes per lane each) feed 16 MFMAs:
+// half the LDS bytes per MFMA of a 64 x 64 wave tile. K steps of 64 bytes
+// through four LDS stages of 32 KiB: the DMA of step s + 3 goes out once
+// every wave has passed the barrier of step s (so every wave is done
+// reading step s - 1, whose stage it refills), and each chunk's fragments
+// are read before the MFMAs of the chunk before issue, so their LDS latency
+// hides behind those MFMAs (one wave per SIMD has no other wave to hide
+// it). A stage holds 256 rows of A then 256 of B, 64 bytes each; group j of
+// row r sits in slot j ^ ((r >> 2) & 3), so the 16 rows of a fragment read
+// fall on distinct bank groups and a 1 KiB DMA block is 16 whole rows. The
+// DMA (buffer_load_dwordx4 ... lds) is issued by inline asm, out of sight
+// of the compiler's wait tracking, and waited for explicitly (vmcnt leaves
+// the later steps' DMAs of this wave in flight). Rows past M / N load
+// zeros without a memory access. ACCUM: add the residues already in P (a K
+// block after the first).
 template <bool ACCUM>
 __global__ __launch_bounds__(256, 1) void crt_gemm_kernel(CrtGemmArgs g) {
   __shared__ __attribute__((aligned(16))) int8_t lds[kCrtStages * kCrtStage];
@@ -1451,32 +1524,36 @@ __global__ __launch_bounds__(256, 1) void crt_gemm_kernel(CrtGemmArgs g) {
   const int t = xcd_remap(blockIdx.x, gridDim.x);
   int tm, tn;
   grouped_tile(t, g.tiles_m, g.tiles_n, 4, tm, tn);
-  const int m0 = tm * kCrtT, n0 = tn * kCrtT;
-  const int8_t* baseA = g.A + mod * g.lda_plane + (int64_t)m0 * g.lda;
-  const int8_t* baseB = g.B + mod * g.ldb_plane + (int64_t)n0 * g.ldb;
+  const int m0 = tm * kCrtTM, n0 = tn * kCrtTN;
+  const int8_t* baseA = g.A + mod * g.lda_plane + (int64_t)(m0 >> 4) * g.lda;
+  const int8_t* baseB = g.B + mod * g.ldb_plane + (int64_t)(n0 >> 4) * g.ldb;
   const int nsteps = g.Kp / kCrtBK;
 
-  // DMA: wave w moves blocks b = w + 4u (u < 4) of each panel; lane l of a
-  // block fills row 16 b + l / 4, slot l % 4, i.e. source group
+  // DMA: wave w moves blocks b = w + 4u (u < 4) of each panel (rows 16 b ..
+  // 16 b + 15: one contiguous KiB of the blocked residues per k-step); lane
+  // l of a block fills row 16 b + l / 4, slot l % 4, i.e. source group
   // (l % 4) ^ ((l >> 4) & 3) of that row
   uint32_t vA[4], vB[4];
   {
     const int gsrc = (lane & 3) ^ ((lane >> 4) & 3);
+    const int in_blk = (lane >> 2) * 64 + 16 * gsrc;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int row = 16 * (w + 4 * u) + (lane >> 2);
-      vA[u] = m0 + row < g.M ? (uint32_t)(row * g.lda + 16 * gsrc) : kOzOob;
-      vB[u] = n0 + row < g.N ? (uint32_t)(row * g.ldb + 16 * gsrc) : kOzOob;
+      vA[u] = m0 + row < g.M ? (uint32_t)((w + 4 * u) * g.lda + in_blk) : kOzOob;
+      vB[u] = n0 + row < g.N ? (uint32_t)((w + 4 * u) * g.ldb + in_blk) : kOzOob;
     }
   }
-  auto dma = [&](int step, int st) __attribute__((always_inline)) {
-    int8_t* dst = lds + st * kCrtStage;
-    const int soff = step * kCrtBK;
+  // block u (< 4) of both panels of a step
+  auto dma_u = [&](int step, int u) __attribute__((always_inline)) {
+    int8_t* dst = lds + (step & (kCrtStages - 1)) * kCrtStage;
+    const int soff = step * 1024;
+    oz_dma16_asm(baseA, dst + (w + 4 * u) * 1024, vA[u], soff);
+    oz_dma16_asm(baseB, dst + kCrtPanelA + (w + 4 * u) * 1024, vB[u], soff);
+  };
+  auto dma = [&](int step) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      oz_dma16_asm(baseA, dst + (w + 4 * u) * 1024, vA[u], soff);
-      oz_dma16_asm(baseB, dst + kCrtPanel + (w + 4 * u) * 1024, vB[u], soff);
-    }
+    for (int u = 0; u < 4; ++u) dma_u(step, u);
   };
 
   i32x16 acc[4][4];
@@ -1493,35 +1570,80 @@ __global__ __launch_bounds__(256, 1) void crt_gemm_kernel(CrtGemmArgs g) {
   const int sw = ((lane & 31) >> 2) & 3;
   const int o0 = (lane & 31) * kCrtBK + 16 * ((lane >> 5) ^ sw);
   const int o1 = (lane & 31) * kCrtBK + 16 * ((2 + (lane >> 5)) ^ sw);
-  const int rowA = 128 * wm * kCrtBK, rowB = kCrtPanel + 128 * wn * kCrtBK;
-
-  dma(0, 0);
-  if (nsteps > 1) dma(1, 1);
-  int st = 0;
-  for (int s = 0; s < nsteps; ++s) {
-    if (s + 1 < nsteps)
-      asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if (s + 2 < nsteps) dma(s + 2, st == 0 ? 2 : st - 1);
-    const int8_t* cur = lds + st * kCrtStage;
+  const int rowA = 128 * wm * kCrtBK, rowB = kCrtPanelA + 128 * wn * kCrtBK;
+  // the fragments of chunk c of a step: f[i] = A block i, f[4 + j] = B block j
+  auto rd = [&](int step, int c, i32x4 (&f)[8]) __attribute__((always_inline)) {
+    const int8_t* cur = lds + (step & (kCrtStages - 1)) * kCrtStage;
+    const int o = c ? o1 : o0;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int o = c ? o1 : o0;
-      i32x4 fa[4], fb[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        fa[i] = *reinterpret_cast<const i32x4*>(cur + rowA + 32 * i * kCrtBK + o);
-        fb[i] = *reinterpret_cast<const i32x4*>(cur + rowB + 32 * i * kCrtBK + o);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    for (int i = 0; i < 4; ++i) {
+      f[i] = *reinterpret_cast<const i32x4*>(cur + rowA + 32 * i * kCrtBK + o);
+      f[4 + i] = *reinterpret_cast<const i32x4*>(cur + rowB + 32 * i * kCrtBK + o);
     }
-    st = st == 2 ? 0 : st + 1;
-  }
+  };
+  auto mm_row = [&](const i32x4 (&f)[8], int i) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[i], f[4 + j], acc[i][j], 0, 0, 0);
+  };
+  auto mm = [&](const i32x4 (&f)[8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mm_row(f, i);
+  };
+
+  // prefetch distance 3: the DMA of step s + 3 refills the stage of s - 1
+  dma(0);
+  if (nsteps > 1) dma(1);
+  if (nsteps > 2) dma(2);
+  // this wave's DMA of step 0 has landed (8 DMAs per step and wave)
+  if (nsteps > 2)
+    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+  else if (nsteps > 1)
+    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  i32x4 f0[8], f1[8];
+  rd(0, 0, f0);
+  // step s: chunk 1's reads behind chunk 0's MFMAs; then the barrier that
+  // publishes step s + 1 (this wave's DMA of s + 1 has landed; vmcnt(8)
+  // leaves the 8 of s + 2 in flight), the DMA of s + 3 and the reads of
+  // chunk 0 of s + 1, behind chunk 1's MFMAs. The steady-state loop has no
+  // branches (the last steps are peeled), so the compiler's LDS wait counts
+  // before chunk 1's MFMAs leave the next step's reads in flight;
+  // sched_barrier keeps the compiler from sinking the reads below the
+  // MFMAs, which it prefers for register pressure.
+  // The 8 DMA issues of s + 3 go out between chunk 1's MFMA rows (2 per
+  // row of 4 MFMAs), where the matrix cores have queued work, instead of as
+  // one block at the phase boundary (timed: the block cost ~a quarter of
+  // the GEMM's time).
+  auto body = [&](int s, auto next, auto refill, auto wait8) __attribute__((always_inline)) {
+    rd(s, 1, f1);
+    __builtin_amdgcn_sched_barrier(0);
+    mm(f0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (decltype(next)::value) {
+      if constexpr (decltype(wait8)::value)
+        asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      rd(s + 1, 0, f0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mm_row(f1, i);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (decltype(next)::value && decltype(refill)::value) dma_u(s + 3, i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  using Y = std::true_type;
+  using N = std::false_type;
+  int s = 0;
+  for (; s + 3 < nsteps; ++s) body(s, Y{}, Y{}, Y{});
+  if (s + 2 < nsteps) body(s++, Y{}, N{}, Y{});
+  if (s + 1 < nsteps) body(s++, Y{}, N{}, N{});
+  body(s, N{}, N{}, N{});
 
   // epilogue: balanced residues mod m, 16 bytes per lane per 32 x 32 block
   asm volatile("" : "+v"(lane));
@@ -1547,61 +1669,60 @@ __global__ __launch_bounds__(256, 1) void crt_gemm_kernel(CrtGemmArgs g) {
     }
 }
 
-// Garner digit t of an element from its residue r_t and the digits v_s,
-// s < t (floats holding small integers; every step exact in fp32:
-// |sum| < 32 * 128 * 256 = 2^20, products < 2^16).
-template <int T>
-__device__ __forceinline__ float crt_digit(const float* v, float r) {
-  constexpr int m = kCrtMod[T];
-  float acc = 0.0f;
-#pragma unroll
-  for (int s = 0; s < T; ++s) acc = fmaf(v[s], (float)kCrtTab.q[s][T], acc);
-  const float x = r - acc;
-  float q = floorf(x * (1.0f / m));
-  float y = fmaf(-q, (float)m, x);
-  y = y < 0.0f ? y + m : y;
-  y = y >= (float)m ? y - m : y;
-  y *= (float)kCrtTab.inv[T];
-  q = floorf(y * (1.0f / m));
-  float z = fmaf(-q, (float)m, y);
-  z = z < 0.0f ? z + m : z;
-  z = z >= (float)m ? z - m : z;
-  return z >= (float)(m - m / 2) ? z - m : z;
+// x mod m for an integer-valued double |x| < 2^52 (exact: floor(x / m)
+// from the reciprocal is off by at most one, fixed after the exact fma).
+__device__ __forceinline__ double crt_mod(double x, double m, double rcp) {
+  const double q = floor(x * rcp);
+  double r = fma(-q, m, x);
+  r = r < 0.0 ? r + m : r;
+  return r >= m ? r - m : r;
 }
 
-// The digits of one element: byte b of residue word wd[t] for t < nmod.
-__device__ __forceinline__ void crt_digits(float* v, const uint32_t* wd, int b, int nmod) {
+// Garner's digits of one element in the paired radices and its value by
+// Horner. r[t]: the residue mod m_t (t < nmod). Pair g (moduli 2g, 2g + 1)
+// first becomes one residue R mod mu_g = m_2g m_2g+1 (two-modulus CRT);
+// the last group is a single modulus when nmod is odd. Digit g:
+// V_g = ((R_g - sum_{h<g} V_h (mu_0..mu_h-1 mod mu_g)) (mu_0..mu_g-1)^-1)
+// mods mu_g; every sum stays below 2^36, exact in fp64. Then
+// H = V_top, H = fma(H, mu_g, V_g) down to g = 0 (one rounding per step).
+template <int NMOD>
+__device__ __forceinline__ double crt_value(const float* r) {
+  constexpr int nmod = NMOD;
+  double V[kCrtPairs];
+  constexpr int top = (nmod - 1) >> 1;
 #pragma unroll
-  for (int t = 0; t < kCrtMax; ++t) {
-    if (t < nmod) {
-      const float r = (float)(int8_t)(uint8_t)(wd[t] >> (8 * b));
-      v[t] = r;
-      if (t == 1) v[1] = crt_digit<1>(v, r);
-#define CRT_DIGIT(T) if (t == T) v[T] = crt_digit<T>(v, r);
-      CRT_DIGIT(2) CRT_DIGIT(3) CRT_DIGIT(4) CRT_DIGIT(5) CRT_DIGIT(6) CRT_DIGIT(7) CRT_DIGIT(8)
-      CRT_DIGIT(9) CRT_DIGIT(10) CRT_DIGIT(11) CRT_DIGIT(12) CRT_DIGIT(13) CRT_DIGIT(14)
-      CRT_DIGIT(15) CRT_DIGIT(16) CRT_DIGIT(17) CRT_DIGIT(18) CRT_DIGIT(19) CRT_DIGIT(20)
-      CRT_DIGIT(21) CRT_DIGIT(22) CRT_DIGIT(23) CRT_DIGIT(24) CRT_DIGIT(25) CRT_DIGIT(26)
-      CRT_DIGIT(27) CRT_DIGIT(28) CRT_DIGIT(29) CRT_DIGIT(30) CRT_DIGIT(31)
-#undef CRT_DIGIT
+  for (int g = 0; g < kCrtPairs; ++g) {
+    if (g <= top) {
+      const bool pair = 2 * g + 1 < nmod;  // a compile-time constant once unrolled
+      const double ma = kCrtMod[2 * g];
+      double R, mu, rcp, inv;
+      double acc = 0.0;
+      if (pair) {
+        const double mb = kCrtMod[2 * g + 1], rcpb = 1.0 / kCrtMod[2 * g + 1];
+        const double d = crt_mod(crt_mod((double)(r[2 * g + 1] - r[2 * g]), mb, rcpb) * kCrtPair.pinv[g], mb, rcpb);
+        R = fma(ma, d, (double)r[2 * g]);
+        mu = (double)kCrtPair.mu[g];
+        rcp = kCrtPair.rcp[g];
+        inv = (double)kCrtPair.inv[g];
+#pragma unroll
+        for (int h = 0; h < g; ++h) acc = fma(V[h], (double)kCrtPair.q[h][g], acc);
+      } else {
+        R = r[2 * g];
+        mu = ma;
+        rcp = kCrtTab.rcp[2 * g];
+        inv = (double)kCrtTab.inv[2 * g];
+#pragma unroll
+        for (int h = 0; h < g; ++h) acc = fma(V[h], (double)kCrtTab.q[2 * h][2 * g], acc);
+      }
+      const double z = crt_mod(crt_mod(R - acc, mu, rcp) * inv, mu, rcp);
+      // balanced: [-mu/2, mu/2) (mu even only for g = 0) or +-(mu - 1)/2
+      V[g] = z >= mu - floor(mu * 0.5) ? z - mu : z;
     }
   }
-}
-
-// The value sum_t v_t prod_{s<t} m_s by Horner over digit pairs
-// V_g = v_2g + m_2g v_2g+1 (exact) with radices m_2g m_2g+1, from the top:
-// one fp64 fma per pair.
-__device__ __forceinline__ double crt_horner(const float* v, int nmod) {
-  const int top = (nmod - 1) >> 1;
   double H = 0.0;
 #pragma unroll
-  for (int g = kCrtMax / 2 - 1; g >= 0; --g) {
-    if (g <= top) {
-      const double V = 2 * g + 1 < nmod ? fma((double)kCrtMod[2 * g], (double)v[2 * g + 1], (double)v[2 * g])
-                                        : (double)v[2 * g];
-      H = g == top ? V : fma(H, (double)(kCrtMod[2 * g] * kCrtMod[2 * g + 1]), V);
-    }
-  }
+  for (int g = kCrtPairs - 1; g >= 0; --g)
+    if (g <= top) H = g == top ? V[g] : fma(H, (double)kCrtPair.mu[g], V[g]);
   return H;
 }
 
@@ -1619,6 +1740,9 @@ struct CrtCombineArgs {
 // One wave per 32 x 32 block of the product residues (4 blocks per
 // workgroup): lane l holds 16 bytes per modulus, the elements of column
 // l % 32, rows 8 (e / 4) + 4 (l / 32) + e % 4 (the MFMA accumulator layout).
+// NMOD, the modulus count, is a template parameter: the digit loops then
+// have no runtime branches.
+template <int NMOD>
 __global__ __launch_bounds__(256) void crt_combine_kernel(CrtCombineArgs g) {
   const int lane = threadIdx.x & 63;
   const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -1628,24 +1752,21 @@ __global__ __launch_bounds__(256) void crt_combine_kernel(CrtCombineArgs g) {
   if (n >= g.N) return;
   const int eb = g.eB[n];
   const int8_t* src = g.P + blk * 1024 + lane * 16;
-  uint32_t wd[4][kCrtMax];
-#pragma unroll
-  for (int t = 0; t < kCrtMax; ++t)
-    if (t < g.nmod) {
-      const i32x4 x = *reinterpret_cast<const i32x4*>(src + t * g.p_plane);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) wd[q][t] = (uint32_t)x[q];
-    }
-#pragma unroll
+  // word q of the lane's 16 bytes holds elements 4 q .. 4 q + 3
+#pragma unroll 1
   for (int q = 0; q < 4; ++q) {
+    uint32_t wd[NMOD];
+#pragma unroll
+    for (int t = 0; t < NMOD; ++t) wd[t] = *reinterpret_cast<const uint32_t*>(src + t * g.p_plane + 4 * q);
+#pragma unroll 1
     for (int b = 0; b < 4; ++b) {
       const int m = bm * 32 + 8 * q + 4 * (lane >> 5) + b;
       if (m >= g.M) continue;
-      float v[kCrtMax];
-      crt_digits(v, wd[q], b, g.nmod);
-      const double H = crt_horner(v, g.nmod);
-      const int ea = g.eA[m];
-      g.C[(int64_t)m * g.ldc_m + (int64_t)n * g.ldc_n] = ldexp(H, ea + eb - 2 * g.p);
+      float r[NMOD];
+#pragma unroll
+      for (int t = 0; t < NMOD; ++t) r[t] = (float)(int8_t)(uint8_t)(wd[t] >> (8 * b));
+      const double H = crt_value<NMOD>(r);
+      g.C[(int64_t)m * g.ldc_m + (int64_t)n * g.ldc_n] = ldexp(H, g.eA[m] + eb - 2 * g.p);
     }
   }
 }
@@ -1830,8 +1951,8 @@ extern "C" int trnblas_hip_crt_moduli(int slices, int64_t K) {
 
 extern "C" int trnblas_hip_crt_split(int per_row, int64_t R, int64_t C, const double* X,
                                      int64_t ldx, int slices, int nmod, int64_t kp, int8_t* res,
-                                     int64_t ld_res, int64_t ld_plane, int32_t* exps,
-                                     int32_t* flags, void* stream) {
+                                     int64_t ld_plane, int32_t* exps, int32_t* flags,
+                                     void* stream) {
   clear_error();
   hipStream_t s = (hipStream_t)stream;
   TRNBLAS_CHECK_ARG(per_row == 0 || per_row == 1, "crt_split: per_row %d", per_row);
@@ -1844,9 +1965,9 @@ extern "C" int trnblas_hip_crt_split(int per_row, int64_t R, int64_t C, const do
   const int64_t rows = per_row ? R : C;
   TRNBLAS_CHECK_ARG(kp >= kd && kp % 64 == 0 && kp < (1ll << 30),
                     "crt_split: kp %lld must be a multiple of 64 >= K", (long long)kp);
-  TRNBLAS_CHECK_ARG(ld_res >= kp && ld_res % 16 == 0 && ld_plane >= rows * ld_res &&
-                        ld_plane % 16 == 0 && ((uintptr_t)res & 15) == 0,
-                    "crt_split: bad residue layout");
+  TRNBLAS_CHECK_ARG(ld_plane >= (rows + 15) / 16 * 16 * kp && ld_plane % 16 == 0 &&
+                        ((uintptr_t)res & 15) == 0,
+                    "crt_split: residue planes need ceil(rows / 16) 16 kp bytes, 16-byte aligned");
   if (per_row) {
     hipLaunchKernelGGL(oz_emax_row_kernel, dim3((unsigned)R), dim3(256), 0, s, X, ldx, (int)R,
                        (int)C, exps);
@@ -1865,24 +1986,22 @@ extern "C" int trnblas_hip_crt_split(int per_row, int64_t R, int64_t C, const do
   if (rc) return rc;
   const int p = 7 * slices - 1;
   if (per_row) {
-    const int64_t blocks = R * ((kp + 1023) / 1024);
-    TRNBLAS_CHECK_ARG(blocks < (1ll << 31), "crt_split: too large");
-    hipLaunchKernelGGL(crt_residues_row_kernel, dim3((unsigned)blocks), dim3(256), 0, s, X, ldx,
-                       (int)R, (int)C, (int)kp, p, nmod, (const int32_t*)exps, res, ld_res,
-                       ld_plane);
+    TRNBLAS_CHECK_ARG((R + 15) / 16 < 65536, "crt_split: too many rows");
+    hipLaunchKernelGGL(crt_residues_row_kernel, dim3((unsigned)(kp / 64), (unsigned)((R + 15) / 16)),
+                       dim3(256), 0, s, X, ldx, (int)R, (int)C, (int)kp, p, nmod,
+                       (const int32_t*)exps, res, ld_plane);
   } else {
     TRNBLAS_CHECK_ARG(kp / 64 < 65536, "crt_split: too many rows");
     hipLaunchKernelGGL(crt_residues_col_kernel, dim3((unsigned)((C + 63) / 64), (unsigned)(kp / 64)),
                        dim3(256), 0, s, X, ldx, (int)R, (int)C, (int)kp, p, nmod,
-                       (const int32_t*)exps, res, ld_res, ld_plane);
+                       (const int32_t*)exps, res, ld_plane);
   }
   return check_launch("crt_split(residues)");
 }
 
 extern "C" int trnblas_hip_crt_gemm(int nmod, int64_t M, int64_t N, int64_t Kp, const int8_t* RA,
-                                    int64_t lda, int64_t lda_plane, const int8_t* RB,
-                                    int64_t ldb, int64_t ldb_plane, int8_t* P, int64_t p_plane,
-                                    void* stream) {
+                                    int64_t lda_plane, const int8_t* RB, int64_t ldb_plane,
+                                    int8_t* P, int64_t p_plane, void* stream) {
   clear_error();
   TRNBLAS_CHECK_ARG(nmod >= 1 && nmod <= kCrtMax, "crt_gemm: nmod %d not in [1, %d]", nmod,
                     kCrtMax);
@@ -1890,13 +2009,14 @@ extern "C" int trnblas_hip_crt_gemm(int nmod, int64_t M, int64_t N, int64_t Kp, 
   TRNBLAS_CHECK_ARG(Kp > 0 && Kp % kCrtBK == 0, "crt_gemm: Kp %lld not a positive multiple of 64",
                     (long long)Kp);
   TRNBLAS_CHECK_ARG(RA && RB && P, "crt_gemm: NULL operand");
-  TRNBLAS_CHECK_ARG(lda >= Kp && ldb >= Kp && lda % 16 == 0 && ldb % 16 == 0 &&
+  TRNBLAS_CHECK_ARG(lda_plane >= (M + 15) / 16 * 16 * Kp && ldb_plane >= (N + 15) / 16 * 16 * Kp &&
                         lda_plane % 16 == 0 && ldb_plane % 16 == 0 &&
                         ((uintptr_t)RA & 15) == 0 && ((uintptr_t)RB & 15) == 0,
-                    "crt_gemm: residue operands must be 16-byte aligned with ld >= Kp");
-  // every DMA offset (row < 256, K offset < Kp) inside the 31-bit buffer range
-  TRNBLAS_CHECK_ARG(255 * lda + Kp < 0x7ffffff0ll && 255 * ldb + Kp < 0x7ffffff0ll,
-                    "crt_gemm: leading dimension too large for 32-bit tile offsets");
+                    "crt_gemm: residue planes (trnblas_hip_crt_split's blocked layout) too small or "
+                    "not 16-byte aligned");
+  // every DMA offset (16 blocks of 16 rows, the K offset) inside the 31-bit buffer range
+  TRNBLAS_CHECK_ARG(16 * 16 * Kp + 1024 < 0x7ffffff0ll,
+                    "crt_gemm: K too long for 32-bit tile offsets");
   const int nbm = (int)((M + 31) / 32), nbn = (int)((N + 31) / 32);
   TRNBLAS_CHECK_ARG(p_plane >= (int64_t)nbm * nbn * 1024 && p_plane % 16 == 0 &&
                         ((uintptr_t)P & 15) == 0,
@@ -1907,25 +2027,25 @@ extern "C" int trnblas_hip_crt_gemm(int nmod, int64_t M, int64_t N, int64_t Kp, 
   g.N = (int)N;
   g.Kp = (int)Kp;
   g.A = RA;
-  g.lda = lda;
+  g.lda = 16 * Kp;  // one 16-row block: Kp / 64 KiB blocks
   g.lda_plane = lda_plane;
   g.B = RB;
-  g.ldb = ldb;
+  g.ldb = 16 * Kp;
   g.ldb_plane = ldb_plane;
   g.P = P;
   g.p_plane = p_plane;
   g.nbm = nbm;
   g.nbn = nbn;
-  g.tiles_m = (int)((M + kCrtT - 1) / kCrtT);
-  g.tiles_n = (int)((N + kCrtT - 1) / kCrtT);
+  g.tiles_m = (int)((M + kCrtTM - 1) / kCrtTM);
+  g.tiles_n = (int)((N + kCrtTN - 1) / kCrtTN);
   const int64_t nt = (int64_t)g.tiles_m * g.tiles_n;
   TRNBLAS_CHECK_ARG(nt < (1ll << 31), "crt_gemm: too many tiles");
   // |residue| <= 128: a K block of 2^16 sums below 2^30 in int32; longer K
   // runs one launch per block, each adding its residues to the last (mod m)
   constexpr int64_t kKb = 1 << 16;
   for (int64_t k0 = 0; k0 < Kp; k0 += kKb) {
-    g.A = RA + k0;
-    g.B = RB + k0;
+    g.A = RA + k0 * 16;  // K block k0: KiB block k0 / 64 of every 16-row block
+    g.B = RB + k0 * 16;
     g.Kp = (int)std::min<int64_t>(kKb, Kp - k0);
     if (k0 == 0)
       hipLaunchKernelGGL(crt_gemm_kernel<false>, dim3((unsigned)nt, (unsigned)nmod), dim3(256), 0,
@@ -1969,7 +2089,19 @@ extern "C" int trnblas_hip_crt_combine(int slices, int nmod, int64_t M, int64_t 
   g.ldc_n = ldc_n;
   const int64_t blocks = ((int64_t)nbm * nbn + 3) / 4;
   TRNBLAS_CHECK_ARG(blocks < (1ll << 31), "crt_combine: too large");
-  hipLaunchKernelGGL(crt_combine_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
-                     g);
+  const dim3 grid((unsigned)blocks), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  switch (nmod) {
+#define CRT_COMB(N) \
+  case N:           \
+    hipLaunchKernelGGL(crt_combine_kernel<N>, grid, block, 0, s, g); \
+    break;
+    CRT_COMB(1) CRT_COMB(2) CRT_COMB(3) CRT_COMB(4) CRT_COMB(5) CRT_COMB(6) CRT_COMB(7)
+    CRT_COMB(8) CRT_COMB(9) CRT_COMB(10) CRT_COMB(11) CRT_COMB(12) CRT_COMB(13) CRT_COMB(14)
+    CRT_COMB(15) CRT_COMB(16) CRT_COMB(17) CRT_COMB(18) CRT_COMB(19) CRT_COMB(20) CRT_COMB(21)
+    CRT_COMB(22) CRT_COMB(23) CRT_COMB(24) CRT_COMB(25) CRT_COMB(26) CRT_COMB(27) CRT_COMB(28)
+    CRT_COMB(29) CRT_COMB(30) CRT_COMB(31) CRT_COMB(32)
+#undef CRT_COMB
+  }
   return check_launch("crt_combine");
 }

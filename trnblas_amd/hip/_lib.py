@@ -111,13 +111,12 @@ SIGNATURES = {
     "trnblas_hip_crt_moduli": (_c_int, [_c_int, _c_i64]),
     "trnblas_hip_crt_split": (
         _c_int,
-        [_c_int, _c_i64, _c_i64, _c_ptr, _c_i64, _c_int, _c_int, _c_i64, _c_ptr, _c_i64, _c_i64]
+        [_c_int, _c_i64, _c_i64, _c_ptr, _c_i64, _c_int, _c_int, _c_i64, _c_ptr, _c_i64]
         + [_c_ptr, _c_ptr, _c_ptr],
     ),
     "trnblas_hip_crt_gemm": (
         _c_int,
-        [_c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr]
-        + [_c_i64, _c_ptr],
+        [_c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
     ),
     "trnblas_hip_crt_combine": (
         _c_int,

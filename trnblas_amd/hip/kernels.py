@@ -791,8 +791,10 @@ def crt_moduli(slices: int, K: int) -> int:
 
 def crt_split(X: torch.Tensor, slices: int, nmod: int, per: str, kp: int):
     """Exponents and int8 residues of a device fp64 matrix X (R, C) for the
-    first nmod moduli: per="row" -> residues (nmod, R, kp) of the rows (K = C),
-    per="col" -> (nmod, C, kp) of the columns (K = R, written transposed).
+    first nmod moduli: per="row" -> residues of the rows (K = C), per="col"
+    -> of the columns (K = R). The residues are blocked, 16 operand rows x
+    64 K values per contiguous KiB: a (nmod, ceil(rows / 16), kp / 64, 16, 64)
+    tensor, element (t, r, k) at [t, r // 16, k // 64, r % 16, k % 64].
     Returns (residues, exps, nonfinite) with `nonfinite` a 0-d device flag."""
     dev = _require_device(X)
     if X.dtype != torch.float64:
@@ -801,26 +803,34 @@ def crt_split(X: torch.Tensor, slices: int, nmod: int, per: str, kp: int):
         X = X.contiguous()
     R, C = X.shape
     rows = R if per == "row" else C
-    res = torch.empty((nmod, rows, kp), dtype=torch.int8, device=dev)
+    rb = -(-rows // 16)
+    res = torch.empty((nmod, rb, kp // 64, 16, 64), dtype=torch.int8, device=dev)
     exps = torch.empty(rows, dtype=torch.int32, device=dev)
     flags = torch.zeros(2, dtype=torch.int32, device=dev)
     _probed_call(
         "crt_split", "trnblas_hip_crt_split", int(per == "row"), R, C, ptr(X), X.stride(0),
-        slices, nmod, kp, ptr(res), kp, rows * kp, ptr(exps), ptr(flags), stream_of(dev),
+        slices, nmod, kp, ptr(res), res.stride(0), ptr(exps), ptr(flags), stream_of(dev),
     )  # fmt: skip
     return res, exps, flags[1]
 
 
+def crt_unblock(res: torch.Tensor) -> torch.Tensor:
+    """(nmod, rows16, kp) view-order copy of blocked residues (tests)."""
+    n, rb, kc, _, _ = res.shape
+    return res.permute(0, 1, 3, 2, 4).reshape(n, rb * 16, kc * 64)
+
+
 def crt_gemm(RA: torch.Tensor, RB: torch.Tensor, M: int, N: int) -> torch.Tensor:
-    """Product residues P_t = RA_t RB_t^T mod m_t, 32 x 32 blocked (see
-    trnblas_hip_crt_gemm): (nmod, ceil(M/32) ceil(N/32) 1024) int8."""
+    """Product residues P_t = RA_t RB_t^T mod m_t from blocked residues
+    (crt_split), 32 x 32 blocked (see trnblas_hip_crt_gemm):
+    (nmod, ceil(M/32) ceil(N/32) 1024) int8."""
     dev = _require_device(RA, RB)
-    nmod, _, kp = RA.shape
+    nmod, kp = RA.shape[0], RA.shape[2] * 64
     plane = -(-M // 32) * -(-N // 32) * 1024
     P = torch.empty((nmod, plane), dtype=torch.int8, device=dev)
     _probed_call(
-        "crt_gemm", "trnblas_hip_crt_gemm", nmod, M, N, kp, ptr(RA), RA.stride(1), RA.stride(0),
-        ptr(RB), RB.stride(1), RB.stride(0), ptr(P), plane, stream_of(dev),
+        "crt_gemm", "trnblas_hip_crt_gemm", nmod, M, N, kp, ptr(RA), RA.stride(0), ptr(RB),
+        RB.stride(0), ptr(P), plane, stream_of(dev),
     )  # fmt: skip
     return P
 
