@@ -1,7 +1,7 @@
 """A seeded random sweep of the public Level-3 API on the GPU: shapes from 1
 to a few thousand (ragged edges, tiny and long K, both layouts of every
 operand, alpha / beta, broadcast batches), N(0, 1) and same-sign U(0, 1)
-data, fp32 / bf16 / fp16, and gemm_fp64 in both modes at 1..12 slices.
+data, fp32 / bf16 / fp16, and gemm_fp64 in its three modes at 1..12 slices.
 
 The sweep runs the HIP kernels (backend 'hip': no hipBLASLt route). Gates:
 fp32 within 1e-6 |A||B| (+ |beta||C|) of fp64 (the north-star gate); 16-bit
@@ -111,7 +111,7 @@ def test_gemm_fp64_random_sweep(dev, seed):
     rng = random.Random(100 + seed)
     for c in range(12):
         M, N, K = rng.randint(1, 300), rng.randint(1, 300), rng.randint(1, 2500)
-        k, mode = rng.randint(1, 12), rng.choice(["fast", "exact"])
+        k, mode = rng.randint(1, 12), rng.choice(["fast", "exact", "crt"])
         r = np.random.default_rng(1000 * seed + c)
         A = r.uniform(-1, 1, (M, K)) * 2.0 ** np.round(r.normal(0, 4, (M, K)))
         B = r.uniform(-1, 1, (K, N))
@@ -121,3 +121,7 @@ def test_gemm_fp64_random_sweep(dev, seed):
         assert (np.abs(C - A @ B) <= bound).all(), (M, N, K, k, mode)
         if mode == "exact" and M * N * K <= 2_000_000:
             assert np.array_equal(C.view(np.int64), oz.reference_gemm(A, B, k).view(np.int64)), (M, N, K, k)
+        if mode == "crt" and M * N <= 20_000:
+            from oracle import ozaki_crt as oc
+
+            assert np.array_equal(C.view(np.int64), oc.gemm_crt(A, B, k).view(np.int64)), (M, N, K, k)
