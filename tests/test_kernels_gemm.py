@@ -409,6 +409,32 @@ def test_gemm_narrow_tiles(dev, batch, M, N, K, ta, tb):
     assert err <= 1e-6, err
 
 
+@pytest.mark.parametrize("batch,M,N,K", [(1, 2048, 2048, 2048), (2, 1024, 2048, 1024), (1, 1900, 2100, 1037), (1, 2040, 2044, 3000)])
+def test_gemm_pipe_kernel_transposed_a(dev, batch, M, N, K):
+    # A^T B with one round of 128 x 128 tiles over the CUs and K >= 1024 runs
+    # the one-workgroup-per-CU kernel (compute waves + operand movers): a
+    # batch, ragged M / N / K, C broadcast over the batch with an odd row
+    # stride (scalar epilogue), alpha / beta, deterministic, at the 1e-6 gate
+    from trnblas_amd.hip import kernels
+
+    g = torch.Generator().manual_seed(M + N + K + batch)
+    A = torch.randn(batch, K, M, generator=g).transpose(1, 2)
+    B = torch.randn(batch, K, N, generator=g)
+    Cw = torch.randn(M, N + 1, generator=g)
+    C = Cw[:, :N]
+    Ad, Bd, Cd = A.to(dev), B.to(dev), Cw.to(dev)[:, :N]
+    if batch == 1:
+        D = kernels.gemm(Ad[0], Bd[0], 0.75, 0.5, Cd).unsqueeze(0)
+        D2 = kernels.gemm(Ad[0], Bd[0], 0.75, 0.5, Cd).unsqueeze(0)
+    else:
+        D = kernels.gemm(Ad, Bd, 0.75, 0.5, Cd)
+        D2 = kernels.gemm(Ad, Bd, 0.75, 0.5, Cd)
+    torch.cuda.synchronize()
+    assert torch.equal(D, D2)
+    err = max(_cw_err(D[b].cpu(), A[b], B[b], 0.75, 0.5, C) for b in range(batch))
+    assert err <= 1e-6, err
+
+
 @pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2.0**-8), (torch.float16, 2.0**-10)])
 @pytest.mark.parametrize("M,N,K", [(1024, 1024, 4096), (1280, 1272, 1280), (512, 520, 8192), (2048, 2048, 2048)])
 @pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])

@@ -64,4 +64,30 @@ __device__ __forceinline__ void grouped_tile(int t, int ntm, int ntn, int group,
   tn = r / gs;
 }
 
+// One 16-byte-per-lane LDS DMA (buffer_load_dwordx4 ... lds) issued by
+// inline asm, so the compiler does not see it: it then places no wait for it
+// before LDS reads of the other stage, and the kernel waits for it itself
+// (`s_waitcnt vmcnt` before the barrier that publishes the stage). Lane l's
+// 16 bytes at voff + soff of the resource land at lds + 16 l.
+__device__ __forceinline__ void lds_dma16_asm(const void* base, const void* lds, uint32_t voff,
+                                              int soff) {
+  const uint64_t b = (uint64_t)base;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(b >> 32) & 0xffffu));
+  r[2] = 0x7ffffff0;
+  r[3] = 0x00020000;
+  const int m = __builtin_amdgcn_readfirstlane(
+      (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds);
+  // m0 (the LDS address of the DMA) is saved and restored around the load,
+  // so the statement leaves every register the compiler may use as it was
+  int saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(m), "v"(voff), "s"(r), "s"(soff)
+      : "memory");
+}
+
 }  // namespace trnblas

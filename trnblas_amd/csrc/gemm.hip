@@ -28,6 +28,7 @@
 //  * the tile walk is XCD-aware: each of the 8 XCDs (own L2) walks a
 //    contiguous range of tiles in grouped order.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -51,6 +52,7 @@ struct GemmArgs {
   int uplo;              // SYRK: 0 = lower triangle of C referenced, 1 = upper
   const int32_t* tri;    // SYRK: triangle flags of C (device), or null; see syrk_upper
   int vec4;              // SYRK: C and D take 4-element vector accesses (aligned, ld % 4 == 0)
+  int vec2;              // sgemm_pipe_kernel: C and D take 2-element accesses (aligned, ld even)
   int sk_groups;         // stream-K workgroups (0 = data-parallel)
   int dp_tiles;          // under stream-K: leading tiles computed whole
   float* ws;             // stream-K partial tiles [sk_groups][2][BM * BN]
@@ -842,6 +844,316 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs g) {
   for (int u = 0; u < 4; ++u) store_out<T, SYRK>(g, C, D, m0 + r, n0 + c + u, v[u], up);
 }
 
+// fp32 GEMM with one workgroup per CU (sgemm_pipe_kernel). A 128 x 128 tile
+// per workgroup: four compute waves of 64 x 64 (2 x 2 blocks of
+// v_mfma_f32_32x32x2_f32, one wave per SIMD) and four movers, waves that only
+// move operands: k-tiles of 32 are loaded into the movers' registers two
+// k-tiles ahead and stored into four LDS stages of 32 KiB (A panel, then B
+// panel). (LDS DMA was measured slower here: a wave's LDS DMAs complete one
+// at a time, so compute waves that issued their share stalled at the issue,
+// 124 TFLOP/s at 8192^3 against 140 with the DMAs left out; two and four
+// DMA-only waves gave 118 and 130.) With one compute wave per SIMD no other wave
+// hides a wave's LDS reads, so they hide behind its own MFMAs: the fragments
+// of each 8-wide k slice (k-oct) are read before the MFMAs of the k-oct
+// before issue, and the barrier that publishes k-tile s + 1 comes before the
+// last k-oct's MFMAs of k-tile s.
+//
+// k order: MFMA j (0..3) of k-oct o gives lane l the k = 8 o + 4 h + j
+// (h = l / 32) in both operands. A K-contiguous panel (128 rows of 32 values,
+// 16-byte group c of row r in slot c ^ ((r >> 1) & 7)) then gives a lane its
+// four values of row 32 p + l % 32 in one 16-byte read. An M/N-contiguous
+// panel (32 k rows of 128 values) gives, in one 8-byte read of k row
+// 8 o + 4 h + j, the values of columns 2 (l % 32) and 2 (l % 32) + 1: the two
+// 32-row blocks p of a wave are then its even and its odd rows (columns),
+// which the store follows. Rows and columns past M / N and k past K read as
+// zeros (offsets past the buffer's records). The accumulation follows
+// gemm_dma_kernel: MFMA chains of span k-tiles folded into a separate sum.
+constexpr int kPipeBK = 32;
+constexpr int kPipeStages = 4;
+constexpr int kPipePanel = 128 * kPipeBK;   // floats per panel (16 KiB)
+constexpr int kPipeStage = 2 * kPipePanel;  // floats per stage (32 KiB)
+constexpr int kPipeThreads = 512;           // 4 compute waves + 4 movers
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+template <bool AKC, bool BKC>
+__global__ __launch_bounds__(kPipeThreads, 1) void sgemm_pipe_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) float lds[kPipeStages * kPipeStage];
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int lane = tid & 63;
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  int bat, tm, tn;
+  decode_tile<false>(g, t, bat, tm, tn);
+  const int m0 = tm * 128, n0 = tn * 128;
+  const int K = g.K, nk = g.nk;
+
+  if (w >= 4) {
+    // The movers: wave 4 + m (m < 4) moves blocks 8 (m & 1) .. + 7 of the A
+    // panel (m < 2) or the B panel (m >= 2) of each stage, 1 KiB per block:
+    // a 16-byte buffer load per lane into registers two k-tiles ahead, then
+    // one 16-byte LDS store per lane (lane l of block b: bytes 16 l of the
+    // block's KiB). K-contiguous panel, block b: rows 8 b .. 8 b + 7; lane l
+    // holds row 8 b + l / 8, slot l % 8 = source group (l % 8) ^ ((row >> 1)
+    // & 7). M/N-contiguous panel, block b: k rows 2 b, 2 b + 1; lane l holds
+    // k row 2 b + l / 32, group l % 32. A lane's load is valid while its row /
+    // column is inside the matrix and kq <= K - k0 (kq: one past the lane's
+    // last k); others read zeros.
+    const int m = w - 4;
+    const bool onB = m >= 2;
+    const bool kc = onB ? BKC : AKC;
+    const float* X = static_cast<const float*>(onB ? g.B : g.A) + bat * (onB ? g.sB : g.sA);
+    const int64_t ld = onB ? g.ldb : g.lda;
+    const int r0 = onB ? n0 : m0, left = (onB ? g.N : g.M) - r0;
+    uint32_t v[8];
+    int kq[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int b = 8 * (m & 1) + u;
+      if (kc) {
+        const int row = 8 * b + (lane >> 3);
+        const int grp = (lane & 7) ^ ((row >> 1) & 7);
+        v[u] = (uint32_t)((int64_t)row * ld * 4 + 16 * grp);
+        kq[u] = row < left ? 4 * grp + 4 : 1 << 30;
+      } else {
+        const int krow = 2 * b + (lane >> 5);
+        const int col = 4 * (lane & 31);
+        v[u] = (uint32_t)((int64_t)krow * ld * 4 + 4 * col);
+        kq[u] = col < left ? krow + 1 : 1 << 30;
+      }
+    }
+    auto gload = [&](int kt, i32x4(&r)[8]) __attribute__((always_inline)) {
+      const int k0 = kt * kPipeBK, kl = K - k0;
+      const float* base = kc ? X + (int64_t)r0 * ld + k0 : X + (int64_t)k0 * ld + r0;
+      const __amdgpu_buffer_rsrc_t rs = make_rsrc(base);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        r[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, kq[u] <= kl ? v[u] : kOob, 0, 0);
+    };
+    auto lwrite = [&](int kt, const i32x4(&r)[8]) __attribute__((always_inline)) {
+      float* dst = lds + (kt & (kPipeStages - 1)) * kPipeStage + (onB ? kPipePanel : 0) +
+                   8 * (m & 1) * 256 + 4 * lane;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) *reinterpret_cast<i32x4*>(dst + u * 256) = r[u];
+    };
+    if (nk == 0) return;
+    // Barrier s publishes k-tile s: the movers' stores of it are done
+    // (lgkmcnt(0)). Between barriers s and s + 1 a mover stores k-tile s + 1
+    // (loaded two steps before) into the stage of k-tile s - 3 and loads
+    // k-tile s + 3 into the registers it freed. Register set s & 1 holds
+    // k-tiles s and s + 2.
+    i32x4 ra[8], rb[8];
+    gload(0, ra);
+    if (nk > 1) gload(1, rb);
+    lwrite(0, ra);
+    if (nk > 2) gload(2, ra);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    auto step = [&](int s, i32x4(&r)[8]) __attribute__((always_inline)) {
+      lwrite(s + 1, r);
+      if (s + 3 < nk) gload(s + 3, r);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    int s = 0;
+    for (; s + 2 < nk; s += 2) {
+      step(s, rb);
+      step(s + 1, ra);
+    }
+    if (s + 1 < nk) step(s, rb);
+    return;
+  }
+
+  const int wm0 = 64 * (w & 1), wn0 = 64 * (w >> 1);
+  const int h = lane >> 5, li = lane & 31;
+  const int sw = (li >> 1) & 7;
+  struct Frag {
+    float a[2][4], b[2][4];
+  };
+  // fragments of k-oct o of the stage at st
+  auto rd = [&](const float* st, int o, Frag& f) __attribute__((always_inline)) {
+    if constexpr (AKC) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(st + (wm0 + 32 * p + li) * kPipeBK +
+                                                        4 * ((2 * o + h) ^ sw));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f.a[p][j] = v[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x2 v =
+            *reinterpret_cast<const f32x2*>(st + (8 * o + 4 * h + j) * 128 + wm0 + 2 * li);
+        f.a[0][j] = v[0];
+        f.a[1][j] = v[1];
+      }
+    }
+    const float* sb = st + kPipePanel;
+    if constexpr (BKC) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(sb + (wn0 + 32 * q + li) * kPipeBK +
+                                                        4 * ((2 * o + h) ^ sw));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f.b[q][j] = v[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x2 v =
+            *reinterpret_cast<const f32x2*>(sb + (8 * o + 4 * h + j) * 128 + wn0 + 2 * li);
+        f.b[0][j] = v[0];
+        f.b[1][j] = v[1];
+      }
+    }
+  };
+  f32x16 acc[2][2], sum[2][2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[p][q][r] = sum[p][q][r] = 0.0f;
+  // the four MFMAs of sub-step j of a k-oct
+  auto mm_j = [&](const Frag& f, int j) __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        acc[p][q] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[p][j], f.b[q][j], acc[p][q], 0, 0, 0);
+  };
+  auto mm = [&](const Frag& f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mm_j(f, j);
+  };
+
+  // C for the lane's outputs (beta != 0), loaded during the last k-tile.
+  // Lane l of block (p, q) holds block column l % 32 and block rows
+  // 8 (e / 4) + 4 h + e % 4 of its registers e.
+  const float* C = static_cast<const float*>(g.C) + (g.C ? bat * g.sC : 0);
+  const int M = g.M, Nn = g.N;
+  const float beta = g.beta;
+  auto row_of = [&](int p, int e) __attribute__((always_inline)) {
+    const int br = 8 * (e >> 2) + 4 * h + (e & 3);
+    return m0 + wm0 + (AKC ? 32 * p + br : 2 * br + p);
+  };
+  auto col_of = [&](int q) __attribute__((always_inline)) {
+    return n0 + wn0 + (BKC ? 32 * q + li : 2 * li + q);
+  };
+  float cv[2][2][16];
+  auto load_c = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = row_of(p, e);
+        const bool mok = m < M && beta != 0.0f;
+        if constexpr (BKC) {
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const int n = col_of(q);
+            cv[p][q][e] = mok && n < Nn ? C[(int64_t)m * g.ldc + n] : 0.0f;
+          }
+        } else {
+          const int n = col_of(0);  // n + 1 < N whenever n < N (N % 4 == 0)
+          if (mok && n < Nn && g.vec2) {
+            const f32x2 c = *reinterpret_cast<const f32x2*>(C + (int64_t)m * g.ldc + n);
+            cv[p][0][e] = c[0];
+            cv[p][1][e] = c[1];
+          } else {
+            cv[p][0][e] = mok && n < Nn ? C[(int64_t)m * g.ldc + n] : 0.0f;
+            cv[p][1][e] = mok && n < Nn ? C[(int64_t)m * g.ldc + n + 1] : 0.0f;
+          }
+        }
+      }
+  };
+
+  Frag f0, f1;
+  // k-tile s: the reads of k-octs 1..3 go out before the MFMAs of the k-oct
+  // before; then the barrier that publishes s + 1, the reads of k-oct 0 of
+  // s + 1, and the last k-oct's MFMAs. The loop has no branch but the fold,
+  // and the last k-tile is peeled, so the compiler's LDS wait counts stay
+  // exact; sched_barrier keeps the reads ahead of the MFMAs. The last
+  // k-tile loads C first.
+  auto body = [&](int s, auto next) __attribute__((always_inline)) {
+    constexpr bool NEXT = decltype(next)::value;
+    if constexpr (!NEXT) load_c();
+    const float* cur = lds + (s & (kPipeStages - 1)) * kPipeStage;
+    rd(cur, 1, f1);
+    __builtin_amdgcn_sched_barrier(0);
+    mm(f0);
+    __builtin_amdgcn_sched_barrier(0);
+    rd(cur, 2, f0);
+    __builtin_amdgcn_sched_barrier(0);
+    mm(f1);
+    __builtin_amdgcn_sched_barrier(0);
+    rd(cur, 3, f1);
+    __builtin_amdgcn_sched_barrier(0);
+    mm(f0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NEXT) {
+      asm volatile("s_barrier" ::: "memory");
+      rd(lds + ((s + 1) & (kPipeStages - 1)) * kPipeStage, 0, f0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mm(f1);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto fold = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) fold_span(sum[p][q], acc[p][q]);
+  };
+  using Y = std::true_type;
+  using N = std::false_type;
+  if (nk > 0) {
+    asm volatile("s_barrier" ::: "memory");  // k-tile 0 is in LDS
+    rd(lds, 0, f0);
+    int chain = g.span, s = 0;
+    for (; s + 1 < nk; ++s) {
+      body(s, Y{});
+      if (--chain == 0) {
+        fold();
+        chain = g.span;
+      }
+    }
+    body(s, N{});
+    fold();
+  } else {
+    load_c();
+  }
+
+  // D = alpha sum + beta C
+  asm volatile("" : "+v"(lane));
+  float* D = static_cast<float*>(g.D) + bat * g.sD;
+  const float alpha = g.alpha;
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = row_of(p, e);
+      if (m >= M) continue;
+      float v[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) v[q] = __builtin_fmaf(beta, cv[p][q][e], alpha * sum[p][q][e]);
+      if constexpr (BKC) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          if (col_of(q) < Nn) D[(int64_t)m * g.ldd + col_of(q)] = v[q];
+      } else {
+        const int n = col_of(0);
+        if (n < Nn) {
+          if (g.vec2) {
+            *reinterpret_cast<f32x2*>(D + (int64_t)m * g.ldd + n) = f32x2{v[0], v[1]};
+          } else {
+            D[(int64_t)m * g.ldd + n] = v[0];
+            D[(int64_t)m * g.ldd + n + 1] = v[1];
+          }
+        }
+      }
+    }
+}
+
 template <typename T>
 struct Cfg {
   static constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
@@ -937,6 +1249,35 @@ static int launch_narrow(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   return check_launch("trnblas_hip_gemm(fixup)");
 }
 
+// fp32 GEMM on sgemm_pipe_kernel (whole 128 x 128 tiles, one workgroup per
+// CU); C and D take 2-element accesses when 8-byte aligned with even ld.
+template <bool AKC, bool BKC>
+static int launch_pipe(GemmArgs g, hipStream_t s) {
+  g.nk = (g.K + kPipeBK - 1) / kPipeBK;
+  g.span = chain_length(g.K, 4) / kPipeBK;
+  g.vec2 = g.ldd % 2 == 0 && (reinterpret_cast<uintptr_t>(g.D) & 7) == 0 &&
+           (g.C == nullptr || (g.ldc % 2 == 0 && (reinterpret_cast<uintptr_t>(g.C) & 7) == 0));
+  hipLaunchKernelGGL((sgemm_pipe_kernel<AKC, BKC>), dim3(g.ntiles), dim3(kPipeThreads), 0, s, g);
+  return check_launch("trnblas_hip_gemm");
+}
+
+// sgemm_pipe_kernel where it was measured faster than gemm_dma_kernel: both
+// operands M/N-contiguous (A^T B, C1's layout) and one round of 128 x 128
+// tiles that fills 90 % of the CUs or more, with 32 k-tiles or more. C1
+// (2048^3 A^T B + 0.5 C) 0.140 against 0.149 ms. Not where a K-contiguous
+// B's fragments come from 16-byte reads in both kernels (A B^T, A^T B^T at
+// 2048^3: 0.159 / 0.161 against 0.135 / 0.141 ms), nor for fewer tiles than
+// CUs (gemm_dma_kernel splits them by stream-K), nor at 8192^3 (133.7
+// against 138 TFLOP/s: the steady state of one compute wave per SIMD stays
+// at ~0.85 of the MFMA issue rate, 4800 cycles per 4096-cycle k-tile, timed
+// in-kernel).
+template <bool AKC, bool BKC>
+static bool pipe_pays(const GemmArgs& g) {
+  const int cus = device_cus();
+  return !AKC && !BKC && g.ntiles <= cus && 10 * g.ntiles >= 9 * cus &&
+         (g.K + kPipeBK - 1) / kPipeBK >= 32;
+}
+
 template <typename T, bool AKC, bool BKC, bool VEC, bool SYRK>
 static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   using C = Cfg<T>;
@@ -944,6 +1285,9 @@ static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   constexpr int BK = DMA ? 128 / (int)sizeof(T) : C::template bk<VEC>();
   g.nk = (g.K + BK - 1) / BK;
   g.span = chain_length(g.K, (int)sizeof(T)) / BK;  // even for the DMA kernel's k-tiles
+  if constexpr (DMA && !SYRK && sizeof(T) == 4) {
+    if (pipe_pays<AKC, BKC>(g)) return launch_pipe<AKC, BKC>(g, s);
+  }
   if constexpr (DMA && !SYRK) {
     if (narrow_tiles_pay(g, (int)sizeof(T))) return launch_narrow<T, AKC, BKC>(g, ws_bytes, s);
   }

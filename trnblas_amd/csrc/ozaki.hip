@@ -690,32 +690,6 @@ __global__ __launch_bounds__(256, NB == 1 ? 2 : 1) void oz_fast_kernel(OzArgs g)
   if (nsteps == 0) flush(true);
 }
 
-// One 16-byte-per-lane LDS DMA (buffer_load_dwordx4 ... lds) issued by
-// inline asm, so the compiler does not see it: it then places no wait for it
-// before LDS reads of the other stage, and the kernel waits for it itself
-// (`s_waitcnt vmcnt` before the barrier that publishes the stage). Lane l's
-// 16 bytes at voff + soff of the resource land at lds + 16 l.
-__device__ __forceinline__ void oz_dma16_asm(const void* base, const void* lds, uint32_t voff,
-                                             int soff) {
-  const uint64_t b = (uint64_t)base;
-  i32x4 r;
-  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
-  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(b >> 32) & 0xffffu));
-  r[2] = 0x7ffffff0;
-  r[3] = 0x00020000;
-  const int m = __builtin_amdgcn_readfirstlane(
-      (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds);
-  // m0 (the LDS address of the DMA) is saved and restored around the load,
-  // so the statement leaves every register the compiler may use as it was
-  int saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(m), "v"(voff), "s"(r), "s"(soff)
-      : "memory");
-}
-
 // Fast mode on interleaved digits of any slice count KS (1..12): row r's
 // 32-wide K chunk kc holds the KS slices' 32 bytes side by side at
 // r * ld + kc * 32 KS + s * 32 (trnblas_hip_ozaki_split, per_row bit 1), so
@@ -746,7 +720,7 @@ __device__ __forceinline__ void oz_dma16_asm(const void* base, const void* lds, 
 // LDS; and B's fragments are read one slice ahead of their MFMAs instead of
 // all at once (accumulators 160 + A fragments 40 + B 8 VGPRs fit the 256 of
 // two waves per SIMD). Those reads follow the next step's DMA, so that DMA
-// is issued by inline asm (oz_dma16_asm) and waited for explicitly.
+// is issued by inline asm (lds_dma16_asm) and waited for explicitly.
 template <int KS>
 __global__ __launch_bounds__(256, KS <= 10 ? 2 : 1) void oz_fast_ilk_kernel(OzArgs g) {
   constexpr int T = 64, W = 4;
@@ -787,8 +761,8 @@ __global__ __launch_bounds__(256, KS <= 10 ? 2 : 1) void oz_fast_ilk_kernel(OzAr
       int8_t* dst = lds + buf * STAGE + (w + u * W) * 1024;
       const uint32_t va = voffA[u], vb = voffB[u];
       if constexpr (LZ) {
-        oz_dma16_asm(baseA, dst, va, soff);
-        oz_dma16_asm(baseB, dst + OPA, vb, soff);
+        lds_dma16_asm(baseA, dst, va, soff);
+        lds_dma16_asm(baseB, dst + OPA, vb, soff);
       } else {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(oz_rsrc(baseA),
                                                  (__attribute__((address_space(3))) void*)dst, 16,
@@ -1548,8 +1522,8 @@ __global__ __launch_bounds__(256, 1) void crt_gemm_kernel(CrtGemmArgs g) {
   auto dma_u = [&](int step, int u) __attribute__((always_inline)) {
     int8_t* dst = lds + (step & (kCrtStages - 1)) * kCrtStage;
     const int soff = step * 1024;
-    oz_dma16_asm(baseA, dst + (w + 4 * u) * 1024, vA[u], soff);
-    oz_dma16_asm(baseB, dst + kCrtPanelA + (w + 4 * u) * 1024, vB[u], soff);
+    lds_dma16_asm(baseA, dst + (w + 4 * u) * 1024, vA[u], soff);
+    lds_dma16_asm(baseB, dst + kCrtPanelA + (w + 4 * u) * 1024, vB[u], soff);
   };
   auto dma = [&](int step) __attribute__((always_inline)) {
 #pragma unroll

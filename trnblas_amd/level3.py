@@ -127,8 +127,9 @@ def gemm_fp64(
     k (k + 1) / 2 (36, 66). Accuracy (max |C - C_exact| / (|A| |B|), normal
     data): about 1e-12 at k = 6, 1e-14 at k = 7, 2e-16 to 3e-16 at k = 8
     (the default, host-fp64 level); scaling is per row of A and column of B,
-    so data spread over 10^+-4 needs k = 10, and the wider spread of
-    BASELINE config 5 (exponents 2^round(N(0, 16))) k = 11. 1 <= slices <= 12.
+    so data spread over 10^+-4 needs k = 10, and entries 2^round(N(0, 16))
+    times N(0, 1) at 8192^3 need k = 11 in mode "fast" and k = 10 in mode
+    "crt" to match a host fp64 product. 1 <= slices <= 12.
 
     A (M, K) and B (K, N) are 2-D real tensors of any float dtype (computed as
     fp64). Returns float64 (M, N) on A's device. Without a ROCm GPU, under
