@@ -794,9 +794,10 @@ __global__ __launch_bounds__(256, KS <= 10 ? 2 : 1) void oz_fast_ilk_kernel(OzAr
   // Lane l of a 32x32 block: column l % 32, rows 8 (e/4) + 4 (l/32) + e % 4.
   constexpr int k = KS;
   const int off = -2 * (kSliceBits - 1) - kSliceBits * (k - 1);
-  const int n = n0 + 32 * wn + (lane & 31);
-  const int eb = n < g.N ? g.eB[n] : 0;
   auto flush = [&](bool first) {
+    // (n and B's exponent are formed here, not kept live across the steps)
+    const int n = n0 + 32 * wn + (lane & 31);
+    const int eb = n < g.N ? g.eB[n] : 0;
     double v[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
