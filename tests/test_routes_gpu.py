@@ -180,3 +180,67 @@ def test_unready_16bit_routes_to_hipblaslt(dev):
         ref = A.double() @ B.double()
         den = A.double().abs() @ B.double().abs()
         assert _cw(D.double(), ref, den) <= 2.0**-8
+
+
+@pytest.mark.parametrize(
+    "M,N,K,tra,trb", [(2048, 2048, 2048, True, False), (300, 260, 128, False, True), (64, 64, 64, True, True),
+                    (130, 68, 4100, False, False)],
+)
+def test_gemm_fast_path_equals_general_path(dev, monkeypatch, M, N, K, tra, trb):
+    # the public 2-D fp32 gemm on device operands skips the general routing;
+    # its result is the library call's, bit for bit, and it never reaches
+    # gemm_scaled
+    g = torch.Generator().manual_seed(M + N + K)
+    A = torch.randn((K, M) if tra else (M, K), generator=g).to(dev)
+    B = torch.randn((N, K) if trb else (K, N), generator=g).to(dev)
+    C = torch.randn(M, N, generator=g).to(dev)
+    want = kernels.gemm(A.mT if tra else A, B.mT if trb else B, 0.75, 0.5, C)
+
+    def refuse(*a, **k):
+        raise AssertionError("general path taken")
+
+    monkeypatch.setattr(d, "gemm_scaled", refuse)
+    D = tb.gemm(0.75, A, B, beta=0.5, C=C, transA=tra, transB=trb)
+    torch.cuda.synchronize()
+    assert torch.equal(D, want)
+    D0 = tb.gemm(1.0, A, B, transA=tra, transB=trb)  # no C
+    assert torch.equal(D0, kernels.gemm(A.mT if tra else A, B.mT if trb else B))
+
+
+def test_gemm_fast_path_declines(dev, monkeypatch):
+    # every case the fast path does not take reaches the general path, with
+    # the general path's result
+    g = torch.Generator().manual_seed(5)
+    A = torch.randn(96, 80, generator=g).to(dev)
+    B = torch.randn(80, 72, generator=g).to(dev)
+    C = torch.randn(96, 72, generator=g).to(dev)
+    taken = []
+    general = d.gemm_scaled
+
+    def spy(*a, **k):
+        taken.append(1)
+        return general(*a, **k)
+
+    monkeypatch.setattr(d, "gemm_scaled", spy)
+    ref = A.double() @ B.double()
+    den = A.double().abs() @ B.double().abs()
+    cases = [
+        lambda: tb.gemm(1.0, A, B, beta=0.5, C=C[:1].expand(96, 72)),  # broadcast C view
+        lambda: tb.gemm(1.0, A[:, 1:], B[1:]),  # 4-byte aligned base, K = 79
+        lambda: tb.gemm(1.0, A.half(), B.half()),  # not fp32
+        lambda: tb.gemm(1.0, A, B, transA="N"),  # a string flag
+    ]
+    for i, fn in enumerate(cases):
+        n0 = len(taken)
+        D = fn()
+        assert len(taken) == n0 + 1, i
+        assert D.shape[0] == 96
+    Ag = A.clone().requires_grad_(True)
+    n0 = len(taken)
+    D = tb.gemm(1.0, Ag, B)
+    assert len(taken) == n0 + 1 and D.requires_grad
+    monkeypatch.setenv("TRNBLAS_NATIVE_GEMM", "aten")
+    n0 = len(taken)
+    D = tb.gemm(1.0, A, B)
+    assert len(taken) == n0 + 1
+    assert (((D.double() - ref).abs() / den).max()) <= 1e-6

@@ -659,6 +659,98 @@ def nki_batched_gemm(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
         return torch.matmul(A, B)
 
 
+_F32 = torch.float32
+_gemm_fn = None  # the library's trnblas_hip_gemm, once loaded
+_kernels = None  # the kernels module, once imported
+
+
+def gemm_fast(alpha, A, B, beta, C, transA, transB):
+    """level3.gemm's common case without the general routing: 2-D fp32
+    operands on one GPU, no gradient, the native GEMM policy auto or hip,
+    each operand row-major or a transposed row-major view that the kernel
+    reads in place (16-byte aligned, leading dimension and contiguous extent
+    multiples of 4), C absent or of the result's shape with unit column
+    stride. Returns alpha op(A) op(B) + beta C, or None (the general path
+    then decides, as for every other call; also on a library error, which
+    the general path reports). The route is the one `_gemm_route` gives
+    these operands ("hip"); the host time per call is about half of the
+    general path's."""
+    global _gemm_fn, _kernels
+    kern = _kernels
+    if kern is None:
+        from . import kernels as kern
+
+        _kernels = kern
+    if (
+        type(transA) is not bool
+        or type(transB) is not bool
+        or A.dtype is not _F32
+        or B.dtype is not _F32
+        or not A.is_cuda
+        or A.dim() != 2
+        or B.dim() != 2
+        or _backend == "pytorch"
+        or kern._launch_probe is not None
+    ):
+        return None
+    dev = A.get_device()
+    if B.get_device() != dev or (torch.is_grad_enabled() and (A.requires_grad or B.requires_grad)):
+        return None
+    policy = os.environ.get("TRNBLAS_NATIVE_GEMM")
+    if policy is not None and policy.strip().lower() not in ("auto", "hip", "nki"):
+        return None
+    if _backend == "auto" and not has_hip():
+        return None
+    # op(A) (M, K) and op(B) (K, N) from the stored strides: trans flag of
+    # the C ABI (the operand is stored transposed) and leading dimension
+    ar, ac = A.shape
+    br, bc = B.shape
+    M, K = (ac, ar) if transA else (ar, ac)
+    K2, N = (bc, br) if transB else (br, bc)
+    if K != K2 or M == 0 or N == 0 or K == 0:
+        return None
+    a0, a1 = A.stride()
+    b0, b1 = B.stride()
+    if a1 == 1 and a0 >= ac:  # stored row-major (ar, ac)
+        ta, lda, aext = transA, a0, ac
+    elif a0 == 1 and a1 >= ar:  # stored column-major: a transposed view
+        ta, lda, aext = not transA, a1, ar
+    else:
+        return None
+    if b1 == 1 and b0 >= bc:
+        tb, ldb, bext = transB, b0, bc
+    elif b0 == 1 and b1 >= br:
+        tb, ldb, bext = not transB, b1, br
+    else:
+        return None
+    pa, pb = A.data_ptr(), B.data_ptr()
+    if (pa | pb) & 15 or (lda | ldb | aext | bext) & 3:
+        return None
+    c, ldc, cb = 0, N, 0.0
+    if C is not None and beta != 0.0:
+        if (
+            C.dtype is not _F32
+            or not C.is_cuda
+            or C.get_device() != dev
+            or C.dim() != 2
+            or C.shape[0] != M
+            or C.shape[1] != N
+            or C.stride(1) != 1
+            or C.stride(0) < N
+            or (torch.is_grad_enabled() and C.requires_grad)
+        ):
+            return None
+        c, ldc, cb = C.data_ptr(), C.stride(0), float(beta)
+    fn = _gemm_fn
+    if fn is None:
+        fn = _gemm_fn = _lib.load().trnblas_hip_gemm
+    ws = kern.gemm_workspace(A.device)
+    D = torch.empty((M, N), dtype=_F32, device=A.device)
+    rc = fn(0, int(ta), int(tb), M, N, K, float(alpha), pa, lda, 0, pb, ldb, 0, cb, c or None, ldc, 0,
+            D.data_ptr(), N, 0, 1, ws.data_ptr(), ws.numel(), torch._C._cuda_getCurrentRawStream(dev))  # fmt: skip
+    return D if rc >= 0 else None
+
+
 def gemm_scaled(alpha, a, b, beta, C):
     """alpha * a @ b + beta * C with the epilogue fused into the kernel when
     the route is a kernel route (level3.gemm / batched_gemm)."""

@@ -72,6 +72,9 @@ def gemm(
     op(X) = X, or X with its last two dims transposed when trans. A
     transposed operand is read in place by the kernel (no copy).
     """
+    D = _d.gemm_fast(alpha, A, B, beta, C, transA, transB)
+    if D is not None:
+        return D
     transA, transB = trans_flag(transA, "transA"), trans_flag(transB, "transB")
     a = A.mT if transA and A.dim() >= 2 else A
     b = B.mT if transB and B.dim() >= 2 else B
