@@ -249,6 +249,7 @@ def run_extras(dev, tb, only=None, P: int = 1, do_cpu: bool = True) -> dict:
         tb_nn = gpu_time_ms(lambda: tb.gemm(1.0, Xb, Yb), reps=10, warm=2)
         tb_nt = gpu_time_ms(lambda: tb.gemm(1.0, Xb, Yb, transB=True), reps=10, warm=2)
         tlb = gpu_time_ms(lambda: torch.matmul(Xb, Yb), reps=10, warm=2)
+        tlb_nt = gpu_time_ms(lambda: torch.matmul(Xb, Yb.mT), reps=10, warm=2)
         # the HIP kernel itself (the public call above takes the measured route)
         tk_nn = gpu_time_ms(lambda: kernels.gemm(Xb, Yb, 1.0, 0.0, None), reps=10, warm=2)
         tk_nt = gpu_time_ms(lambda: kernels.gemm(Xb, Yb.mT, 1.0, 0.0, None), reps=10, warm=2)
@@ -265,6 +266,8 @@ def run_extras(dev, tb, only=None, P: int = 1, do_cpu: bool = True) -> dict:
             # ... and hipBLASLt (torch.matmul) on its own
             "hipblaslt_nn_ms": tlb, "hipblaslt_nn_tflops": fl / tlb / 1e9,
             "hipblaslt_nn_frac_bf16_peak": fl / tlb / 1e9 / PEAK_BF16_MFMA,
+            "hipblaslt_nt_ms": tlb_nt, "hipblaslt_nt_tflops": fl / tlb_nt / 1e9,
+            "hipblaslt_nt_frac_bf16_peak": fl / tlb_nt / 1e9 / PEAK_BF16_MFMA,
         }  # fmt: skip
         log("gemm8192bf16", out["gemm_bf16_8192"])
         del Xb, Yb

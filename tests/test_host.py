@@ -82,7 +82,11 @@ def test_route_table(monkeypatch):
     [
         ((8192, 8192), (8192, 8192), torch.float32, True, "gemm", False),  # fp32: accuracy gate
         ((8192, 8192), (8192, 8192), torch.bfloat16, True, "gemm", True),
-        ((2048, 2048), (2048, 2048), torch.bfloat16, True, "gemm", True),
+        ((2048, 2048), (2048, 2048), torch.bfloat16, True, "gemm", False),  # 2^22 outputs, K 2048
+        ((2048, 1024), (1024, 4096), torch.bfloat16, True, "gemm", False),  # 2^23 outputs, K 1024
+        ((2048, 4096), (4096, 4096), torch.bfloat16, True, "gemm", True),  # 2^23 outputs, K 4096
+        ((2048, 8192), (8192, 2048), torch.float16, True, "gemm", True),  # 2^22 outputs, K 8192
+        ((4096, 1024), (1024, 4096), torch.bfloat16, True, "gemm", True),  # 2^24 outputs
         ((2048, 128), (128, 2048), torch.bfloat16, True, "gemm", False),  # short K: the kernel
         ((1024, 8192), (8192, 1024), torch.bfloat16, True, "gemm", False),  # long K: the kernel
         ((256, 8192), (8192, 8192), torch.float16, True, "gemm", False),

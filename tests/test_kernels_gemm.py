@@ -300,6 +300,31 @@ def test_gemm_16bit_large(dev, dtype, tol, batch, M, N, K):
     assert ((D - ref).abs() / den).max().item() <= tol
 
 
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2.0**-8), (torch.float16, 2.0**-11)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_gemm_16bit_wide_tiles(dev, dtype, tol, ta, tb):
+    # 16-bit GEMM on aligned operands whose 256 x 256 tiles fill every CU
+    # (4000 x 4104: 16 x 17 tiles) with K of 8 k-tiles or more runs
+    # hgemm256_kernel: every layout (K- or M/N-contiguous panels), ragged M,
+    # N and K (520 = 8 k-tiles + 8), alpha and beta; a second call gives the
+    # same bits
+    from trnblas_amd.hip import kernels
+
+    M, N, K = 4000, 4104, 520
+    g = torch.Generator(device=dev).manual_seed(M + 7 * ta + 3 * tb)
+    A = torch.randn(K, M, device=dev, generator=g).to(dtype).T if ta else torch.randn(M, K, device=dev, generator=g).to(dtype)
+    B = torch.randn(N, K, device=dev, generator=g).to(dtype).T if tb else torch.randn(K, N, device=dev, generator=g).to(dtype)
+    C = torch.randn(M, N, device=dev, generator=g).to(dtype)
+    D = kernels.gemm(A, B, 0.75, 0.5, C)
+    D2 = kernels.gemm(A, B, 0.75, 0.5, C)
+    torch.cuda.synchronize()
+    assert torch.equal(D, D2)
+    Af, Bf, Cf = A.float(), B.float(), C.float()
+    ref = 0.75 * (Af @ Bf) + 0.5 * Cf
+    den = 0.75 * (Af.abs() @ Bf.abs()) + 0.5 * Cf.abs()
+    assert ((D.float() - ref).abs() / den).max().item() <= tol
+
+
 def test_stream_k_two_streams(dev):
     # split-k GEMMs launched on two streams may run at the same time: each
     # stream has its own partial-tile workspace, so both match the results

@@ -96,7 +96,7 @@ def test_device_gemm_route_by_dtype_and_shape(dev):
     with _Launches() as seen:
         D = tb.gemm(1.0, A, A)
     assert seen.names == ["gemm"]
-    # bf16 at 4096^3: hipBLASLt (measured 0.72-0.80 of the kernel's time)
+    # bf16 at 4096^3: hipBLASLt (measured 0.77-0.87 of the kernel's time)
     Ab = A.bfloat16()
     with _Launches() as seen:
         Db = tb.gemm(1.0, Ab, Ab)

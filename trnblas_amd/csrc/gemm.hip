@@ -787,6 +787,161 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
   }
 }
 
+// 16-bit GEMM on 256 x 256 tiles (aligned operands, whole tiles, one
+// workgroup per CU). A 128 x 128 tile stages 32 KiB per 64-wide k-tile for
+// 512 cycles of MFMA issue per SIMD, less than its LDS DMA takes at ~40
+// bytes per clock per CU; a 256 x 256 tile stages twice the bytes for four
+// times the MFMAs. 512 threads: wave w owns rows 128 (w & 1) .. + 127 and
+// columns 64 (w >> 1) .. + 63 (4 x 2 MFMA 32x32x16 blocks). The panels, DMA
+// blocks, swizzles and fragment reads are those of gemm_dma_kernel with
+// 256-row panels (M/N-contiguous rows of 256 values: a DMA block is two
+// rows), in two LDS stages of 64 KiB; each wave moves 4 blocks of each panel
+// per k-tile. The DMA is issued by inline asm (invisible to the compiler's
+// wait tracking), so fragment reads of the current stage may follow it; the
+// kernel waits for its own DMAs (vmcnt(0)) before the barrier that
+// publishes the next stage. Fragments are read one 16-wide k chunk ahead of
+// the MFMAs (two sets of six). One MFMA chain over all of K (no folded
+// partial sums: 16-bit results are held to 2^-8 |A||B|, far above an fp32
+// chain's rounding).
+template <typename T, bool AKC, bool BKC>
+__global__ __launch_bounds__(512, 1) void hgemm256_kernel(GemmArgs g) {
+  static_assert(sizeof(T) == 2, "16-bit operands");
+  constexpr int EV = 8, BM = 256, BN = 256, BK = 64, WM = 128, WN = 64, FM = 4, FN = 2;
+  constexpr int NB = 4;                // DMA blocks per panel per wave
+  constexpr int CH = 2 * EV;           // k per fragment chunk
+  constexpr int PANEL = BM * BK;       // values of one panel (32 KiB)
+  constexpr int MG = 256 / EV;         // 16-byte groups in an M/N-contiguous row
+  constexpr int MSW = 2 * sizeof(T);   // M/N swizzle (groups)
+  __shared__ __attribute__((aligned(16))) T lds[2][2 * PANEL];
+
+  const int tid = threadIdx.x;
+  int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm0 = (wave & 1) * WM, wn0 = (wave >> 1) * WN;
+  const int M = g.M, N = g.N, K = g.K, nk = g.nk;
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  int bat, tm, tn;
+  decode_tile<false>(g, t, bat, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const T* A = static_cast<const T*>(g.A) + bat * g.sA;
+  const T* B = static_cast<const T*>(g.B) + bat * g.sB;
+
+  // DMA block b = 4 wave + u of a panel. KC: row 8 b + l / 8, global group
+  // (l % 8) ^ swizzle; MN: row 2 b + l / 32, global group (l % 32) ^ swizzle.
+  auto geo = [&](bool kc, int u, int& row, int& grp) __attribute__((always_inline)) {
+    const int b = NB * wave + u;
+    if (kc) {
+      row = 8 * b + (lane >> 3);
+      grp = (lane & 7) ^ ((row >> 1) & 7);
+    } else {
+      row = 2 * b + lane / MG;
+      grp = (lane % MG) ^ (MSW * ((row / EV) & 1));
+    }
+  };
+  auto dma = [&](T* st, int kt) __attribute__((always_inline)) {
+    const int k0 = kt * BK;
+    const T* pa = AKC ? A + (int64_t)m0 * g.lda + k0 : A + (int64_t)k0 * g.lda + m0;
+    const T* pb = BKC ? B + (int64_t)n0 * g.ldb + k0 : B + (int64_t)k0 * g.ldb + n0;
+    const int ra = AKC ? M - m0 : K - k0, ca = AKC ? K - k0 : M - m0;
+    const int rb = BKC ? N - n0 : K - k0, cb = BKC ? K - k0 : N - n0;
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      int rw, gp;
+      geo(AKC, u, rw, gp);
+      const uint32_t va = rw < ra && EV * gp < ca
+                              ? (uint32_t)((int64_t)rw * g.lda * (int64_t)sizeof(T) + 16 * gp)
+                              : kOob;
+      lds_dma16_asm(pa, st + (NB * wave + u) * (1024 / sizeof(T)), va, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      int rw, gp;
+      geo(BKC, u, rw, gp);
+      const uint32_t vb = rw < rb && EV * gp < cb
+                              ? (uint32_t)((int64_t)rw * g.ldb * (int64_t)sizeof(T) + 16 * gp)
+                              : kOob;
+      lds_dma16_asm(pb, st + PANEL + (NB * wave + u) * (1024 / sizeof(T)), vb, 0);
+    }
+  };
+
+  // Fragment of the lane's row r at k offset kk (a multiple of EV): one
+  // 16-byte read from a K-contiguous panel, two transposing 8-byte reads
+  // from an M/N-contiguous one (rows of 256 values).
+  auto frag = [&](const T* p, bool kc, int r, int kk) __attribute__((always_inline)) {
+    if (kc)
+      return *reinterpret_cast<const i32x4*>(p + r * BK + EV * ((kk / EV) ^ ((r >> 1) & 7)));
+    const int i = lane & 15;
+    const int c0 = r - i + 4 * (i & 3);
+    const int k1 = kk + (i >> 2);
+    const T* s0 = p + k1 * BM + EV * ((c0 / EV) ^ (MSW * ((kk / EV) & 1))) + (c0 & 4);
+    union {
+      s16x4 h[2];
+      i32x4 v;
+    } u;
+    u.h[0] = lds_tr16(s0);
+    u.h[1] = lds_tr16(s0 + 4 * BM);
+    return u.v;
+  };
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  i32x4 fa[2][FM], fb[2][FN];
+  auto rd = [&](const T* cur, int c, int set) __attribute__((always_inline)) {
+    const int kk = c * CH + (lane >> 5) * EV;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) fa[set][i] = frag(cur, AKC, wm0 + i * 32 + (lane & 31), kk);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) fb[set][j] = frag(cur + PANEL, BKC, wn0 + j * 32 + (lane & 31), kk);
+  };
+  auto mm = [&](int set) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) mma_frag(acc[i][j], fa[set][i], fb[set][j], (T*)nullptr);
+  };
+  auto publish = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // One k-tile per iteration with the stage chosen at run time (unrolled
+  // copies per stage give the accumulators different registers in each copy
+  // and spill at the joins): chunk 0's fragments, the DMA of k-tile kt + 1
+  // into the other stage, then chunk c's MFMAs behind chunk c + 1's reads,
+  // with scheduling barriers that keep each chunk's reads behind the MFMAs
+  // two chunks back (else all four chunks' fragments are live at once).
+  if (nk > 0) dma(lds[0], 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    publish();  // k-tile kt has landed; every read of the other stage is done
+    // the lane index is opaque per k-tile, so its LDS and DMA addresses are
+    // recomputed here instead of hoisted out of the loop and kept live
+    asm volatile("" : "+v"(lane));
+    const T* cur = lds[kt & 1];
+    rd(cur, 0, 0);
+    if (kt + 1 < nk) dma(lds[(kt & 1) ^ 1], kt + 1);
+    rd(cur, 1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mm(0);
+    __builtin_amdgcn_sched_barrier(0);
+    rd(cur, 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    mm(1);
+    __builtin_amdgcn_sched_barrier(0);
+    rd(cur, 3, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mm(0);
+    __builtin_amdgcn_sched_barrier(0);
+    mm(1);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  store_tile<T, false, FM, FN, BM, BN>(g, acc, bat, m0, n0, wm0, wn0, lane, -1, 0);
+}
+
 // Sums the stream-K partials of each split tile in workgroup order
 // (deterministic) and applies the epilogue. Grid: (split tiles, BM / 8):
 // each workgroup finishes 8 rows of one tile, one float4 of partials per
@@ -1278,6 +1433,31 @@ static bool pipe_pays(const GemmArgs& g) {
          (g.K + kPipeBK - 1) / kPipeBK >= 32;
 }
 
+// hgemm256_kernel where its 256 x 256 tiles fill every CU at least once, in
+// rounds that keep 90 % of the CUs busy, and K spans 8 k-tiles or more
+// (16-bit GEMM on aligned operands, 32-bit panel offsets for 256-row
+// panels). Measured against gemm_dma_kernel (bf16, ms, NN / NT): 4096^2 x
+// 1024 0.053 / 0.051 against 0.063 / 0.061, 4096^3 0.146 / 0.142 against
+// 0.166 / 0.157, 8192^3 1.030 / 0.956 against 1.213 / 1.093, 16384 x 4096 x
+// 2048 0.301 / 0.279 against 0.343 / 0.324; with a partial last round it
+// loses (5120^3: 400 tiles, 0.328 / 0.299 against 0.317 / 0.301; 6144^3:
+// 576 tiles, 0.541 / 0.530 against 0.531 / 0.485; 7168^3: 784 tiles).
+static bool wide_tiles_pay(const GemmArgs& g) {
+  const int64_t tiles = (int64_t)((g.M + 255) / 256) * ((g.N + 255) / 256) * g.batch;
+  const int64_t cus = device_cus(), rounds = (tiles + cus - 1) / cus;
+  return tiles >= cus && 10 * tiles >= 9 * rounds * cus && g.K >= 512;
+}
+
+template <typename T, bool AKC, bool BKC>
+static int launch_wide(GemmArgs g, hipStream_t s) {
+  g.tiles_m = (g.M + 255) / 256;
+  g.tiles_n = (g.N + 255) / 256;
+  g.ntiles = g.tiles_m * g.tiles_n * g.batch;
+  g.nk = (g.K + 63) / 64;
+  hipLaunchKernelGGL((hgemm256_kernel<T, AKC, BKC>), dim3(g.ntiles), dim3(512), 0, s, g);
+  return check_launch("trnblas_hip_gemm");
+}
+
 template <typename T, bool AKC, bool BKC, bool VEC, bool SYRK>
 static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   using C = Cfg<T>;
@@ -1287,6 +1467,11 @@ static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   g.span = chain_length(g.K, (int)sizeof(T)) / BK;  // even for the DMA kernel's k-tiles
   if constexpr (DMA && !SYRK && sizeof(T) == 4) {
     if (pipe_pays<AKC, BKC>(g)) return launch_pipe<AKC, BKC>(g, s);
+  }
+  if constexpr (DMA && !SYRK && sizeof(T) == 2) {
+    const int64_t span_a = (AKC ? 256 : 64) * g.lda * 2, span_b = (BKC ? 256 : 64) * g.ldb * 2;
+    if (wide_tiles_pay(g) && span_a < (int64_t)kRecords - 64 && span_b < (int64_t)kRecords - 64)
+      return launch_wide<T, AKC, BKC>(g, s);
   }
   if constexpr (DMA && !SYRK) {
     if (narrow_tiles_pay(g, (int)sizeof(T))) return launch_narrow<T, AKC, BKC>(g, ws_bytes, s);

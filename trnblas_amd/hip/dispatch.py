@@ -307,14 +307,21 @@ def _host_gemm_wins(macs: float, nbytes: int, dtype: torch.dtype) -> bool:
 #    the 1e-6 componentwise gate the fp32 path is held to.
 #  * SYRK stays on the kernel (the triangle: 1.2-1.7x faster than the full
 #    product on hipBLASLt, C2a).
-#  * bf16 / fp16 go to hipBLASLt when batch * M * N >= 2^22 and K >= 512
-#    (0.66-0.88 of the kernel's time at 2048^3 .. 8192^3 and 8192^2 x 256;
-#    C2b batched 0.74); the kernel keeps the small, short-K and long-K shapes
-#    (2048^2 x 128: 0.8x, 1024^2 x 8192 and 256 x 8192^2: 0.65-0.75x of
-#    hipBLASLt's time). Batched products go to hipBLASLt only with contiguous
-#    operands (a transposed right operand of a 16-bit bmm is avoided).
+#  * bf16 / fp16 go to hipBLASLt when batch * M * N >= 2^22 and K >= 512,
+#    except up to 2^23 outputs with K <= 2048, where the kernel is 3-20 %
+#    faster (2048^2 x 512, 2048^3, 1024 x 4096 x 2048, 2048 x 4096 x 1024,
+#    NN / NT / TN). hipBLASLt's time against the kernel's elsewhere: 0.83-0.98
+#    at 2^22-2^23 outputs with K 4096-8192, 0.70-0.81 at 2896^3, 0.72-0.87
+#    at 8192^3 (where the kernel runs 256 x 256 tiles: NN 1067, NT 1150 TF/s
+#    against 1358 / 1524), C2b batched 0.74. The kernel also keeps the short-K
+#    and long-K shapes (2048^2 x 128: 0.8x, 1024^2 x 8192 and 256 x 8192^2:
+#    0.65-0.75x of hipBLASLt's time). Batched products go to hipBLASLt only
+#    with contiguous operands (a transposed right operand of a 16-bit bmm is
+#    avoided).
 _ATEN_16BIT_MIN_MN = 1 << 22
 _ATEN_16BIT_MIN_K = 512
+_ATEN_16BIT_MID_MN = 1 << 23
+_ATEN_16BIT_SHORT_K = 2048
 
 
 def _aten_gemm_wins(a_shape, b_shape, dtype: torch.dtype, contiguous: bool, op: str = "gemm") -> bool:
@@ -326,7 +333,10 @@ def _aten_gemm_wins(a_shape, b_shape, dtype: torch.dtype, contiguous: bool, op: 
     nb = math.prod(_lib.broadcast_shapes(tuple(a_shape[:-2]), tuple(b_shape[:-2])))
     if nb > 1 and not contiguous:
         return False
-    return nb * M * N >= _ATEN_16BIT_MIN_MN and K >= _ATEN_16BIT_MIN_K
+    mn = nb * M * N
+    if mn < _ATEN_16BIT_MIN_MN or K < _ATEN_16BIT_MIN_K:
+        return False
+    return not (mn <= _ATEN_16BIT_MID_MN and K <= _ATEN_16BIT_SHORT_K)
 
 
 def _dma_ready_2d(X: torch.Tensor, rows_ext: int, cols_ext: int) -> bool:
