@@ -557,10 +557,13 @@ __device__ __forceinline__ s16x4 lds_tr16(const void* p) {
 // whole rows and the fragment reads are bank-conflict free:
 //  * K-contiguous panel, 128 rows of 128 bytes: group q of row r sits in
 //    slot q ^ ((r >> 1) & 7); a DMA block is 8 rows;
-//  * M/N-contiguous panel, rows k of 128 values (512 or 256 bytes): group q
-//    of row k sits in slot q ^ (2 sizeof(T) ((k / EV) & 1)), which moves the
-//    second lane half's column reads (k + EV) onto the other half of the
-//    banks; a DMA block is 2 (fp32) or 4 rows.
+//  * M/N-contiguous panel, rows k of 128 values (512 or 256 bytes): fp32,
+//    group q of row k sits in slot q ^ (8 ((k / 4) & 1)), which moves the
+//    second lane half's column reads (k + 4) onto the other half of the
+//    banks; 16-bit, in slot q ^ (4 (k & 3)): the transposing reads of a
+//    16-lane group take rows k .. k + 3 at the same columns, and the 64-byte
+//    shift per row puts them on distinct banks (the 64-value rows of BN = 64
+//    keep q ^ (4 ((k / 8) & 1))); a DMA block is 2 (fp32) or 4 rows.
 // Lane l of a DMA block loads the global group that belongs in its slot
 // (the swizzles are their own inverses), so each row's lanes still read the
 // row's bytes exactly once. Ragged edges: a group outside the matrix gets
@@ -582,6 +585,10 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
   constexpr int MGA = 128 / EV, MGB = BN / EV;  // 16-byte groups in an M/N-contiguous row
   constexpr int NBW = BPANEL * (int)sizeof(T) / 4096;  // B DMA blocks per wave (4 or 2)
   constexpr int MSW = 2 * sizeof(T);  // M/N swizzle (groups)
+  // slot XOR of row k of an M/N-contiguous panel with mg 16-byte groups per row
+  auto mn_swz = [](int k, int mg) __attribute__((always_inline)) {
+    return (sizeof(T) == 2 && mg == 16) ? 4 * (k & 3) : MSW * ((k / EV) & 1);
+  };
   __shared__ __attribute__((aligned(16))) T st0[PANEL + BPANEL];
   __shared__ __attribute__((aligned(16))) T st1[PANEL + BPANEL];
 
@@ -622,7 +629,7 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
           grp = (lane & 7) ^ ((row >> 1) & 7);
         } else {
           row = (64 / mg) * b + lane / mg;
-          grp = (lane % mg) ^ (MSW * ((row / EV) & 1));
+          grp = (lane % mg) ^ mn_swz(row, mg);
         }
       };
 #pragma unroll
@@ -674,7 +681,7 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
         const int i = lane & 15;
         const int c0 = r - i + 4 * (i & 3);
         const int k1 = kk + (i >> 2);
-        const T* s0 = p + k1 * W + EV * ((c0 / EV) ^ (MSW * ((kk / EV) & 1))) + (c0 & 4);
+        const T* s0 = p + k1 * W + EV * ((c0 / EV) ^ mn_swz(k1, W / EV)) + (c0 & 4);
         union {
           s16x4 h[2];
           i32x4 v;
@@ -792,11 +799,15 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmArgs g) {
 // 512 cycles of MFMA issue per SIMD, less than its LDS DMA takes at ~40
 // bytes per clock per CU; a 256 x 256 tile stages twice the bytes for four
 // times the MFMAs. 512 threads: wave w owns rows 128 (w & 1) .. + 127 and
-// columns 64 (w >> 1) .. + 63 (4 x 2 MFMA 32x32x16 blocks). The panels, DMA
-// blocks, swizzles and fragment reads are those of gemm_dma_kernel with
-// 256-row panels (M/N-contiguous rows of 256 values: a DMA block is two
-// rows), in two LDS stages of 64 KiB; each wave moves 4 blocks of each panel
-// per k-tile. The DMA is issued by inline asm (invisible to the compiler's
+// columns 64 (w >> 1) .. + 63 (4 x 2 MFMA 32x32x16 blocks). The K-contiguous
+// panels, DMA blocks and fragment reads are those of gemm_dma_kernel with
+// 256-row panels; an M/N-contiguous panel has rows k of 256 values (a DMA
+// block is two rows) with group q of row k in slot q ^ (4 (k & 3)): the
+// transposing reads of a 16-lane group take rows k .. k + 3 at the same
+// columns, and the 64-byte shift per row puts them on distinct banks (with
+// gemm_dma_kernel's swizzle, half of the kernel's LDS cycles were bank
+// conflicts). Two LDS stages of 64 KiB; each wave moves 4 blocks of each
+// panel per k-tile. The DMA is issued by inline asm (invisible to the compiler's
 // wait tracking), so fragment reads of the current stage may follow it; the
 // kernel waits for its own DMAs (vmcnt(0)) before the barrier that
 // publishes the next stage. Fragments are read one 16-wide k chunk ahead of
@@ -811,7 +822,6 @@ __global__ __launch_bounds__(512, 1) void hgemm256_kernel(GemmArgs g) {
   constexpr int CH = 2 * EV;           // k per fragment chunk
   constexpr int PANEL = BM * BK;       // values of one panel (32 KiB)
   constexpr int MG = 256 / EV;         // 16-byte groups in an M/N-contiguous row
-  constexpr int MSW = 2 * sizeof(T);   // M/N swizzle (groups)
   __shared__ __attribute__((aligned(16))) T lds[2][2 * PANEL];
 
   const int tid = threadIdx.x;
@@ -835,7 +845,7 @@ __global__ __launch_bounds__(512, 1) void hgemm256_kernel(GemmArgs g) {
       grp = (lane & 7) ^ ((row >> 1) & 7);
     } else {
       row = 2 * b + lane / MG;
-      grp = (lane % MG) ^ (MSW * ((row / EV) & 1));
+      grp = (lane % MG) ^ (4 * (row & 3));
     }
   };
   auto dma = [&](T* st, int kt) __attribute__((always_inline)) {
@@ -873,7 +883,7 @@ __global__ __launch_bounds__(512, 1) void hgemm256_kernel(GemmArgs g) {
     const int i = lane & 15;
     const int c0 = r - i + 4 * (i & 3);
     const int k1 = kk + (i >> 2);
-    const T* s0 = p + k1 * BM + EV * ((c0 / EV) ^ (MSW * ((kk / EV) & 1))) + (c0 & 4);
+    const T* s0 = p + k1 * BM + EV * ((c0 / EV) ^ (4 * (k1 & 3))) + (c0 & 4);
     union {
       s16x4 h[2];
       i32x4 v;

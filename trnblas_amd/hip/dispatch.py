@@ -308,12 +308,13 @@ def _host_gemm_wins(macs: float, nbytes: int, dtype: torch.dtype) -> bool:
 #  * SYRK stays on the kernel (the triangle: 1.2-1.7x faster than the full
 #    product on hipBLASLt, C2a).
 #  * bf16 / fp16 go to hipBLASLt when batch * M * N >= 2^22 and K >= 512,
-#    except up to 2^23 outputs with K <= 2048, where the kernel is 3-20 %
+#    except up to 2^23 outputs with K <= 2048, where the kernel is 7-34 %
 #    faster (2048^2 x 512, 2048^3, 1024 x 4096 x 2048, 2048 x 4096 x 1024,
-#    NN / NT / TN). hipBLASLt's time against the kernel's elsewhere: 0.83-0.98
-#    at 2^22-2^23 outputs with K 4096-8192, 0.70-0.81 at 2896^3, 0.72-0.87
-#    at 8192^3 (where the kernel runs 256 x 256 tiles: NN 1067, NT 1150 TF/s
-#    against 1358 / 1524), C2b batched 0.74. The kernel also keeps the short-K
+#    NN / NT / TN / TT). hipBLASLt's time against the kernel's elsewhere:
+#    0.87-0.99 at 2^22-2^23 outputs with K 4096-8192 (TN 0.96-1.05),
+#    0.70-0.97 at 2896^3, 0.77-0.87 at 4096^3 (TN 1.0) and 0.73-0.87 at
+#    8192^3 (the kernel on 256 x 256 tiles: NN 1043, NT 1092, TN 1010, TT
+#    1022 TF/s against 1369 / 1520 / 1157 / 1371), C2b batched 0.74. The kernel also keeps the short-K
 #    and long-K shapes (2048^2 x 128: 0.8x, 1024^2 x 8192 and 256 x 8192^2:
 #    0.65-0.75x of hipBLASLt's time). Batched products go to hipBLASLt only
 #    with contiguous operands (a transposed right operand of a 16-bit bmm is
