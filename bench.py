@@ -246,6 +246,9 @@ def run_extras(dev, tb, only=None, P: int = 1, do_cpu: bool = True) -> dict:
         # the same product in bf16 (fp32 accumulate), NN and NT (B^T read in place)
         Xb, Yb = X.bfloat16(), Y.bfloat16()
         del X, Y
+        # untimed settle: the first bf16 timing after the fp32 block read
+        # ~15 % slow whichever call came first
+        gpu_time_ms(lambda: torch.matmul(Xb, Yb), reps=10, warm=5)
         tb_nn = gpu_time_ms(lambda: tb.gemm(1.0, Xb, Yb), reps=10, warm=2)
         tb_nt = gpu_time_ms(lambda: tb.gemm(1.0, Xb, Yb, transB=True), reps=10, warm=2)
         tlb = gpu_time_ms(lambda: torch.matmul(Xb, Yb), reps=10, warm=2)
