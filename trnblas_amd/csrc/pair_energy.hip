@@ -808,18 +808,17 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
   // Load instruction qq = slot * 6 NPC + piece * 6 + blk (rows 16 blk ..
   // 16 blk + 15 of that slot's panel) fills stage offset qq KiB; wave w
   // issues qq = w + 8 u. The lane offsets are those of pair_energy_x3_kernel
-  // (row-pair layout, one 128-byte line per 8 lanes) and do not depend on
-  // the panel; a panel's resource spans its valid row pairs only (the
-  // padding row of an odd nvir is zero), so rows past nvir read as zeros.
+  // (row-pair layout, one 128-byte line per 8 lanes): row r = 16 blk + l / 4
+  // and x3_slot(r, .) depends on r mod 8 only, so the lane's part (row l / 4
+  // of the block) is one offset for every load, and the wave-uniform part
+  // (16 blk rows and the piece) moves the resource's base and shortens its
+  // range by as much. A panel's resource spans its valid row pairs only (the
+  // padding row of an odd nvir is zero), so rows past nvir read as zeros:
+  // the range check sees the lane offset (not the soffset, which carries
+  // the k slice).
   const int lr = lane >> 2;
-  uint32_t voff[NL];
-#pragma unroll
-  for (int u = 0; u < NL; ++u) {
-    const int qq = w + 8 * u < NQ ? w + 8 * u : w + 8 * u - 8;
-    const int e = qq % BPS, pc = e / 6, r = 16 * (e - 6 * pc) + lr;
-    voff[u] = (uint32_t)(((r >> 1) * nk * (NPC * 64) + pc * 64 + (r & 1) * 32 +
-                          8 * x3_slot(r, lane & 3)) * 2);
-  }
+  const uint32_t voff =
+      (uint32_t)(((lr >> 1) * nk * (NPC * 64) + (lr & 1) * 32 + 8 * x3_slot(lr, lane & 3)) * 2);
   // Panel (slot sl, pass ps): operand rows from rbase; its resource spans the
   // valid row pairs only. Wave-uniform scalars, computed per load.
   const int pairsA = min((nvir - a0 + 1) >> 1, S / 2), pairsB = min((nvir - b0 + 1) >> 1, S / 2);
@@ -832,19 +831,21 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
 #pragma unroll
     for (int u = 0; u < NL; ++u) {
       const int qq = w + 8 * u < NQ ? w + 8 * u : w + 8 * u - 8;
-      const int sl = qq / BPS;
+      const int sl = qq / BPS, e = qq - sl * BPS, pc = e / 6;
+      const int uo = ((8 * (e - 6 * pc)) * nk * (NPC * 64) + pc * 64) * 2;  // bytes
       const bool onA = (sl == 0) == (ps == 0);  // the panel's rows are the A tile's
       // operand row i, j0 or j1 by arithmetic (a select chain becomes a table in memory)
       const int o = i + (sl > 0) * (j0 - i) + (sl > 1) * (j1 - j0);
-      const uint16_t* base = g.Pi + o * ostride + (onA ? rowA : rowB);
-      const uint32_t v = voff[u];
+      const int nrec = (onA ? pairsA : pairsB) * nk * NPC * 128 - uo;
+      const char* base =
+          reinterpret_cast<const char*>(g.Pi + o * ostride + (onA ? rowA : rowB)) + uo;
       // (readfirstlane: an offset the compiler keeps in a VGPR after a select
       // wraps the load in a loop over the lanes' distinct values)
       const int soff = __builtin_amdgcn_readfirstlane(sl0 * NPC * 128);
       set[u] = __builtin_amdgcn_raw_buffer_load_b128(
-          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0,
-                                            (onA ? pairsA : pairsB) * nk * NPC * 128, 0x00020000),
-          v, soff, 0);
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, nrec > 0 ? nrec : 0,
+                                            0x00020000),
+          voff, soff, 0);
     }
   };
   auto store = [&](const i32x4(&set)[NL], int buf) __attribute__((always_inline)) {
