@@ -308,13 +308,13 @@ def run_extras(dev, tb, only=None, P: int = 1, do_cpu: bool = True) -> dict:
         torch.cuda.synchronize()
         t_launch = probe.mean_ms()
         roof = {
-            "kernel": "row_exp_kernel + split_planes_kernel<2> + pair_energy_x3c_kernel<2> "
+            "kernel": "row_exp_kernel + split_planes_kernel<2> + pair_energy_quad_kernel "
                       "(trnblas_hip_pair_energy_fp16x3)",
             "bound": "mfma", "launch_ms": t_launch,
             "achieved": 3 * fl / t_launch / 1e9, "peak": PEAK_BF16_MFMA, "unit": "TFLOP/s (f16 MFMA)",
             "frac": 3 * fl / t_launch / 1e9 / PEAK_BF16_MFMA,
             "achieved_fp32_equiv": fl / t_launch / 1e9, "ceiling_fp32_equiv": PEAK_BF16_MFMA / 3,
-            "algorithmic_flop_per_launch": fl, "traffic": committed_traffic("pair_energy_x3c"),
+            "algorithmic_flop_per_launch": fl, "traffic": committed_traffic("pair_energy_quad"),
         }  # fmt: skip
         # The reference's CPU path (the fp32 torch pair loop of
         # dispatch.py:2514-2533, restated in oracle/pair_energy.py) over all

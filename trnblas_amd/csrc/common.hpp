@@ -69,13 +69,15 @@ __device__ __forceinline__ void grouped_tile(int t, int ntm, int ntn, int group,
 // before LDS reads of the other stage, and the kernel waits for it itself
 // (`s_waitcnt vmcnt` before the barrier that publishes the stage). Lane l's
 // 16 bytes at voff + soff of the resource land at lds + 16 l.
+// The resource spans nrec bytes from base: a lane whose voff (the range
+// check does not include soff) is at or past nrec reads zeros.
 __device__ __forceinline__ void lds_dma16_asm(const void* base, const void* lds, uint32_t voff,
-                                              int soff) {
+                                              int soff, int nrec = 0x7ffffff0) {
   const uint64_t b = (uint64_t)base;
   i32x4 r;
   r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
   r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(b >> 32) & 0xffffu));
-  r[2] = 0x7ffffff0;
+  r[2] = __builtin_amdgcn_readfirstlane(nrec);
   r[3] = 0x00020000;
   const int m = __builtin_amdgcn_readfirstlane(
       (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds);

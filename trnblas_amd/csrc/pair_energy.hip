@@ -639,9 +639,12 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
   // buffer P (the barrier publishes it and retires every read of buffer
   // 1 - P), set P is free (its slice t went to LDS in step t - 1) and takes
   // slice t + 2, slice t is multiplied (the NPROD products of each block,
-  // smallest first, into its partial, started at zero when FIRST), then set
-  // 1 - P (slice t + 1) goes to buffer 1 - P.
-  auto step = [&](auto P_, auto FIRST_, int t) {
+  // smallest first, into its partial: bf16x6 started at zero when FIRST, the
+  // two-slice partial added to the pass's sum below; fp16x3 started at zero
+  // every slice and added to the pass's sum at once, the order of
+  // pair_energy_quad_kernel), then set 1 - P (slice t + 1) goes to buffer
+  // 1 - P.
+  auto step = [&](auto P_, auto FIRST_, int t, f32x4(&acc)[3][3]) {
     constexpr int P = decltype(P_)::value;
     constexpr bool FIRST = decltype(FIRST_)::value;
     __syncthreads();
@@ -660,15 +663,26 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
       i32x4 fb[NPC];
 #pragma unroll
       for (int pc = 0; pc < NPC; ++pc) fb[pc] = frag(pc, 1, br0 + 16 * cb + (lane & 15));
+      if constexpr (NPC == 2) {
 #pragma unroll
-      for (int rb = 0; rb < 3; ++rb)
-        part[rb][cb] = M::mma(fa[rb][M::ka[0]], fb[M::kb[0]],
-                              FIRST ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb]);
+        for (int e = 0; e < M::NPROD; ++e)
 #pragma unroll
-      for (int e = 1; e < M::NPROD; ++e) {
+          for (int rb = 0; rb < 3; ++rb)
+            part[rb][cb] = M::mma(fa[rb][M::ka[e]], fb[M::kb[e]],
+                                  e == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb]);
+#pragma unroll
+        for (int rb = 0; rb < 3; ++rb) acc[rb][cb] += part[rb][cb];
+      } else {
 #pragma unroll
         for (int rb = 0; rb < 3; ++rb)
-          part[rb][cb] = M::mma(fa[rb][M::ka[e]], fb[M::kb[e]], part[rb][cb]);
+          part[rb][cb] = M::mma(fa[rb][M::ka[0]], fb[M::kb[0]],
+                                FIRST ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb]);
+#pragma unroll
+        for (int e = 1; e < M::NPROD; ++e) {
+#pragma unroll
+          for (int rb = 0; rb < 3; ++rb)
+            part[rb][cb] = M::mma(fa[rb][M::ka[e]], fb[M::kb[e]], part[rb][cb]);
+        }
       }
     }
     if (t + 1 < nsteps) store(stg[1 - P], 1 - P);
@@ -677,16 +691,18 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
   using I1 = std::integral_constant<int, 1>;
   using T = std::true_type;
   using F = std::false_type;
-  // One pass: slice pairs (t even, t + 1), each partial added to the pass's
-  // sum in fp32.
+  // One pass: slice pairs (t even, t + 1); bf16x6 adds each partial to the
+  // pass's sum in fp32.
   auto run_pass = [&](f32x4(&acc)[3][3], int t0) {
     for (int u = 0; u < nk; u += 2) {
-      step(I0(), T(), t0 + u);
-      step(I1(), F(), t0 + u + 1);
+      step(I0(), T(), t0 + u, acc);
+      step(I1(), F(), t0 + u + 1, acc);
+      if constexpr (NPC != 2) {
 #pragma unroll
-      for (int rb = 0; rb < 3; ++rb)
+        for (int rb = 0; rb < 3; ++rb)
 #pragma unroll
-        for (int cb = 0; cb < 3; ++cb) acc[rb][cb] += part[rb][cb];
+          for (int cb = 0; cb < 3; ++cb) acc[rb][cb] += part[rb][cb];
+      }
     }
   };
 
@@ -763,11 +779,11 @@ __device__ __forceinline__ void couple_of(int c, int n, int& i, int& j0) {
   j0 = r + 2 * (c - (int)before(r));
 }
 
-// The implicit walk two pairs at a time: work item = (couple (i, j0, j1),
-// tile pair A <= B). Both pairs share B_i, so a k-step stages three 96-row
-// panels (54 KiB bf16x6, 36 KiB fp16x3) for two 96 x 96 outputs where two single-pair workgroups
-// stage four: a quarter fewer operand bytes per product, which is what bounds
-// pair_energy_x3_kernel. 8 waves, one workgroup per CU: waves 4 g .. 4 g + 3
+// The implicit walk two pairs at a time (bf16x6): work item = (couple (i,
+// j0, j1), tile pair A <= B). Both pairs share B_i, so a k-step stages three
+// 96-row panels (54 KiB) for two 96 x 96 outputs where two single-pair
+// workgroups stage four: a quarter fewer operand bytes per product, which is
+// what bounds pair_energy_x3_kernel. 8 waves, one workgroup per CU: waves 4 g .. 4 g + 3
 // compute pair g of the couple, each the 48 x 48 quadrant (w & 1, w >> 1) as
 // in pair_energy_x3_kernel, with the same pieces, MFMA order, two-slice
 // partials and two-deep register pipeline. Stage slots: 0 = the shared panel
@@ -775,6 +791,7 @@ __device__ __forceinline__ void couple_of(int c, int n, int& i, int& j0) {
 // B_jg[A]); a single-pair couple runs pair 0 twice and drops the copy.
 template <int NPC>
 __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
+  static_assert(NPC == 3, "bf16x6; fp16x3 runs pair_energy_quad_kernel");
   using M = PeMath<NPC>;
   constexpr int S = kX3S, BK = kX3BK;
   constexpr int SLOT = NPC * S * BK;  // 16-bit elements of one panel slice, NPC pieces
@@ -873,30 +890,6 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
     auto frag = [&](const uint16_t* b, int pc, int r) __attribute__((always_inline)) {
       return *reinterpret_cast<const i32x4*>(b + (pc * S + r) * BK + fslot);
     };
-    if constexpr (NPC == 2) {
-      // fp16x3: three MFMAs per block are too few to hide a block's reads
-      // behind the block before; all twelve fragments are read first, then
-      // the next slices' loads issue, then the 27 MFMAs
-      i32x4 fa[3][2], fb[3][2];
-#pragma unroll
-      for (int u = 0; u < 3; ++u)
-#pragma unroll
-        for (int pc = 0; pc < 2; ++pc) {
-          fa[u][pc] = frag(bufA, pc, ar0 + 16 * u + (lane & 15));
-          fb[u][pc] = frag(bufB, pc, br0 + 16 * u + (lane & 15));
-        }
-      load(t + 2, stg[P]);
-#pragma unroll
-      for (int e = 0; e < M::NPROD; ++e)
-#pragma unroll
-        for (int cb = 0; cb < 3; ++cb)
-#pragma unroll
-          for (int rb = 0; rb < 3; ++rb)
-            part[rb][cb] = M::mma(fa[rb][M::ka[e]], fb[cb][M::kb[e]],
-                                  FIRST && e == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb]);
-      if (t + 1 < nsteps) store(stg[1 - P], 1 - P);
-      return;
-    }
     load(t + 2, stg[P]);
     i32x4 fa[3][NPC];
     // Blocks (rb, cb) in the order cb-major; before a block's NPROD MFMAs
@@ -1010,6 +1003,233 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
   if ((tid & 255) == 0 && (gp == 0 || two)) {
     const int p = i * g.nocc - i * (i - 1) / 2 + (jg - i);
     g.partial[(int64_t)p * g.nq + q] = (red[4 * gp] + red[4 * gp + 1]) + (red[4 * gp + 2] + red[4 * gp + 3]);
+  }
+}
+
+// The implicit walk four pairs at a time (fp16x3): work item = (square of
+// pairs (i0, i1) x (j0, j1), i0 = 2 sa, j0 = 2 sb, sa <= sb, tile pair
+// A <= B); a square with sa == sb holds three pairs ((i1, j0) is not one),
+// and an odd nocc leaves i1 or j1 absent. A 32-wide k-slice stages the four
+// operand panels B_i0, B_i1, B_j0, B_j1 (48 KiB) for the four pairs' 96 x 96
+// outputs: one panel per pair, where a couple of pairs sharing B_i stages
+// 1.5 (pair_energy_x3c_kernel), which is what bounds these kernels (the LDS
+// DMA moves ~40 bytes per clock per CU; a couple's step stages as long as
+// its MFMAs take). Waves 4 gi .. 4 gi + 3 take i = i_gi and both j, each the
+// 48 x 48 quadrant (qd & 1, qd >> 1) of both pairs (X and X', 144 VGPRs):
+// a slice's products of one pair (pieces smallest first) chain on the MFMA
+// from zero and are added to the pair's sum in fp32, one pair after the
+// other (36 VGPRs of partials), as pair_energy_x3_kernel<2> sums them; a
+// chain over all slices on the MFMA accumulator came out 1.6e-7 low on
+// same-sign sums. Three LDS stages filled by DMA two slices ahead (6 DMAs per wave per
+// slice, slices past the walk clamped to the last so the waits stay exact).
+// Stage slots: 0 B_i0, 1 B_i1, 2 B_j0, 3 B_j1; the i panels hold tile A's
+// rows in pass 0 (X = B_i[A] B_j[B]^T) and tile B's in pass 1 (X' = B_j[A]
+// B_i[B]^T). An absent index repeats the one before it; its pairs are
+// computed and dropped.
+__global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
+  constexpr int NPC = 2;
+  using M = PeMath<NPC>;
+  constexpr int S = kX3S, BK = kX3BK;
+  constexpr int SLOT = NPC * S * BK;
+  constexpr int STAGE = 4 * SLOT;
+  constexpr int NQ = STAGE * 2 / 1024;  // 48 DMAs of 1 KiB per stage
+  constexpr int NL = NQ / 8;            // 6 per wave
+  constexpr int BPS = NPC * 6;
+  static_assert(NQ == 48 && S == 96 && BK == 32, "stage split");
+  constexpr int EPI = 4 * S * (S + 1) * 2;  // four 96 x 97 float blocks, in 16-bit elements
+  constexpr int LDS_ELEMS = 3 * STAGE > EPI ? 3 * STAGE : EPI;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];
+  __shared__ double red[2][2][4];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int gi = w >> 2, qd = w & 3;
+  const int item = xcd_remap(blockIdx.x, gridDim.x);
+  const int c = item / g.nq, q = item - c * g.nq;
+  int sa, sb;
+  tri_tiles(c, (g.nocc + 1) >> 1, sa, sb);
+  const bool hi = 2 * sa + 1 < g.nocc, hj = 2 * sb + 1 < g.nocc;
+  const int i0 = 2 * sa, i1 = hi ? i0 + 1 : i0, j0 = 2 * sb, j1 = hj ? j0 + 1 : j0;
+  const int ig = gi ? i1 : i0;
+  int TA, TB;
+  tri_tiles(q, g.nb, TA, TB);
+  const bool diag = TA == TB;
+  const int a0 = TA * S, b0 = TB * S;
+  const int nvir = g.nvir, ldv = g.ldv;
+  const int nk = ldv / BK;
+  const int nsteps = diag ? nk : 2 * nk;
+  const int64_t ostride = (int64_t)((nvir + 1) >> 1) * 2 * NPC * ldv;
+
+  const int lr = lane >> 2;
+  const uint32_t voff =
+      (uint32_t)(((lr >> 1) * nk * (NPC * 64) + (lr & 1) * 32 + 8 * x3_slot(lr, lane & 3)) * 2);
+  const int pairsA = min((nvir - a0 + 1) >> 1, S / 2), pairsB = min((nvir - b0 + 1) >> 1, S / 2);
+  const int64_t rowA = (int64_t)(a0 >> 1) * nk * (NPC * 64),
+                rowB = (int64_t)(b0 >> 1) * nk * (NPC * 64);
+  // slice t (clamped to the last) into stage buf: slot 0 B_i0, 1 B_i1, 2 B_j0,
+  // 3 B_j1; the i panels hold tile A's rows in pass 0, tile B's in pass 1
+  auto dma = [&](int t, int buf) __attribute__((always_inline)) {
+    if (t >= nsteps) t = nsteps - 1;
+    const int ps = t >= nk ? 1 : 0, sl0 = ps ? t - nk : t;
+    const int soff = __builtin_amdgcn_readfirstlane(sl0 * NPC * 128);
+#pragma unroll
+    for (int u = 0; u < NL; ++u) {
+      const int qq = w + 8 * u;
+      const int sl = qq / BPS, e = qq - sl * BPS, pc = e / 6;
+      const int uo = ((8 * (e - 6 * pc)) * nk * (NPC * 64) + pc * 64) * 2;
+      const bool onA = (sl < 2) == (ps == 0);
+      const int o = i0 + (sl == 1) * (i1 - i0) + (sl == 2) * (j0 - i0) + (sl == 3) * (j1 - i0);
+      const int nrec = (onA ? pairsA : pairsB) * nk * NPC * 128 - uo;
+      lds_dma16_asm(reinterpret_cast<const char*>(g.Pi + o * ostride + (onA ? rowA : rowB)) + uo,
+                lds + buf * STAGE + qq * 512, voff, soff, nrec > 0 ? nrec : 0);
+    }
+  };
+
+  const int ar0 = 48 * (qd & 1), br0 = 48 * (qd >> 1);
+  const int fslot = 8 * x3_slot(lane & 15, lane >> 4);
+  auto frag = [&](const uint16_t* b, int pc, int r) __attribute__((always_inline)) {
+    return *reinterpret_cast<const i32x4*>(b + (pc * S + r) * BK + fslot);
+  };
+  f32x4 accX[2][3][3], accP[2][3][3];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+    for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < 3; ++cb) accX[jj][rb][cb] = accP[jj][rb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto step = [&](auto PS_, int t, int bt, int b2) __attribute__((always_inline)) {
+    constexpr int PS = decltype(PS_)::value;
+    asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");  // slice t landed
+    const uint16_t* st = lds + bt * STAGE;
+    const uint16_t* ip = st + gi * SLOT;
+    i32x4 fi[3][2], fj[2][3][2];
+    const int ri = PS == 0 ? ar0 : br0, rj = PS == 0 ? br0 : ar0;
+#pragma unroll
+    for (int u = 0; u < 3; ++u)
+#pragma unroll
+      for (int pc = 0; pc < 2; ++pc) {
+        fi[u][pc] = frag(ip, pc, ri + 16 * u + (lane & 15));
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) fj[jj][u][pc] = frag(st + (2 + jj) * SLOT, pc, rj + 16 * u + (lane & 15));
+      }
+    dma(t + 2, b2);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      f32x4 part[3][3];  // pair jj's products of the slice
+#pragma unroll
+      for (int e = 0; e < M::NPROD; ++e)
+#pragma unroll
+        for (int cb = 0; cb < 3; ++cb)
+#pragma unroll
+          for (int rb = 0; rb < 3; ++rb) {
+            const f32x4 c0 = e == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb];
+            if constexpr (PS == 0)
+              part[rb][cb] = M::mma(fi[rb][M::ka[e]], fj[jj][cb][M::kb[e]], c0);
+            else
+              part[rb][cb] = M::mma(fj[jj][rb][M::ka[e]], fi[cb][M::kb[e]], c0);
+          }
+#pragma unroll
+      for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 3; ++cb) {
+          if constexpr (PS == 0)
+            accX[jj][rb][cb] += part[rb][cb];
+          else
+            accP[jj][rb][cb] += part[rb][cb];
+        }
+    }
+  };
+  if (nsteps > 0) {
+    dma(0, 0);
+    dma(1, 1);
+    int bt = 0;
+    for (int t = 0; t < nk; ++t) {
+      const int b2 = bt == 0 ? 2 : bt - 1;
+      step(std::integral_constant<int, 0>(), t, bt, b2);
+      bt = bt == 2 ? 0 : bt + 1;
+    }
+    if (!diag) {
+      for (int t = nk; t < nsteps; ++t) {
+        const int b2 = bt == 0 ? 2 : bt - 1;
+        step(std::integral_constant<int, 1>(), t, bt, b2);
+        bt = bt == 2 ? 0 : bt + 1;
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA may land after the workgroup ends
+
+  double sum[2] = {0.0, 0.0};
+  const double ei = (double)g.eps_i[ig];
+  if (!diag) {
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int jg = jj ? j1 : j0;
+      const double eo = ei + (double)g.eps_j[jg];
+#pragma unroll
+      for (int cb = 0; cb < 3; ++cb) {
+        const int b = b0 + br0 + 16 * cb + (lane & 15);
+        const double eb = b < nvir ? (double)g.eps_vir[b] : 0.0;
+#pragma unroll
+        for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int a = a0 + ar0 + 16 * rb + 4 * (lane >> 4) + r;
+            if (a < nvir && b < nvir) {
+              const double x = accX[jj][rb][cb][r] * pe_scale<NPC>(g, g.Ei, ig, a, g.Ei, jg, b);
+              const double xp = accP[jj][rb][cb][r] * pe_scale<NPC>(g, g.Ei, jg, a, g.Ei, ig, b);
+              sum[jj] += 2.0 * (x * x + xp * xp - x * xp) / (eo - (double)g.eps_vir[a] - eb);
+            }
+          }
+      }
+    }
+  } else {
+    __syncthreads();
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      float* xs = reinterpret_cast<float*>(lds) + (2 * gi + jj) * S * (S + 1);
+#pragma unroll
+      for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 3; ++cb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            xs[(ar0 + 16 * rb + 4 * (lane >> 4) + r) * (S + 1) + br0 + 16 * cb + (lane & 15)] =
+                accX[jj][rb][cb][r];
+    }
+    __syncthreads();
+    const int lt = tid & 255;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int jg = jj ? j1 : j0;
+      const double eo = ei + (double)g.eps_j[jg];
+      const float* xs = reinterpret_cast<const float*>(lds) + (2 * gi + jj) * S * (S + 1);
+#pragma unroll 4
+      for (int e = 0; e < S * S / 256; ++e) {
+        const int idx = lt + 256 * e, a = idx / S, b = idx - a * S;
+        if (a0 + a < nvir && a0 + b < nvir) {
+          const double x = xs[a * (S + 1) + b] * pe_scale<NPC>(g, g.Ei, ig, a0 + a, g.Ei, jg, a0 + b);
+          const double xt = xs[b * (S + 1) + a] * pe_scale<NPC>(g, g.Ei, ig, a0 + b, g.Ei, jg, a0 + a);
+          sum[jj] += x * (2.0 * x - xt) / (eo - (double)g.eps_vir[a0 + a] - (double)g.eps_vir[a0 + b]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    const double s = wave_sum(sum[jj]);
+    if (lane == 0) red[gi][jj][qd] = s;
+  }
+  __syncthreads();
+  if (tid < 4) {
+    const int pg = tid >> 1, pj = tid & 1;  // thread t writes pair (i_pg, j_pj)
+    const int pi = pg ? i1 : i0, pjj = pj ? j1 : j0;
+    const bool valid = (pg == 0 || hi) && (pj == 0 || hj) && pi <= pjj;
+    if (valid) {
+      const int p = pi * g.nocc - pi * (pi - 1) / 2 + (pjj - pi);
+      g.partial[(int64_t)p * g.nq + q] =
+          (red[pg][pj][0] + red[pg][pj][1]) + (red[pg][pj][2] + red[pg][pj][3]);
+    }
   }
 }
 
@@ -1133,8 +1353,10 @@ static void x3_split(const float* X, int64_t n, int64_t ld_occ, int64_t ld_vir, 
 template <int NPC>
 static void split_launch(const PairArgs& g, bool implicit, int64_t citems, int64_t items,
                          hipStream_t s) {
-  if (implicit)
-    hipLaunchKernelGGL(pair_energy_x3c_kernel<NPC>, dim3((unsigned)citems), dim3(512), 0, s, g);
+  if (implicit && NPC == 2)
+    hipLaunchKernelGGL(pair_energy_quad_kernel, dim3((unsigned)citems), dim3(512), 0, s, g);
+  else if (implicit)
+    hipLaunchKernelGGL(pair_energy_x3c_kernel<3>, dim3((unsigned)citems), dim3(512), 0, s, g);
   else
     hipLaunchKernelGGL(pair_energy_x3_kernel<NPC>, dim3((unsigned)items), dim3(256), 0, s, g);
 }
@@ -1235,7 +1457,10 @@ static int pair_energy_run(int npc, const char* name, int64_t nvir, int64_t naux
     g.ldv = ldv;
     g.rows_i = (int)ni;
     g.rows_j = (int)(nj ? nj : ni);
-    const int64_t citems = pair_i == nullptr ? pe_couples(nocc) * nq : 0;
+    // implicit walk items: squares of pairs (fp16x3), couples (bf16x6)
+    const int64_t nb2 = (nocc + 1) / 2;
+    const int64_t citems =
+        pair_i == nullptr ? (npc == 2 ? nb2 * (nb2 + 1) / 2 : pe_couples(nocc)) * nq : 0;
     TRNBLAS_CHECK_ARG(citems < (1ll << 31), "%s: too many work items", name);
     if (npc == 3) {
       x3_split<3>(Bi, ni, ldi_occ, ld_vir, (int)nvir, (int)naux, ldv, Pi, nullptr, s);
@@ -1246,7 +1471,7 @@ static int pair_energy_run(int npc, const char* name, int64_t nvir, int64_t naux
     }
     int rc = check_launch(name);
     if (rc) return rc;
-    // the implicit walk: two pairs sharing B_i per workgroup
+    // the implicit walk: four pairs (fp16x3) or two sharing B_i (bf16x6) per workgroup
     if (npc == 3)
       split_launch<3>(g, pair_i == nullptr, citems, items, s);
     else
