@@ -1082,19 +1082,17 @@ def _torch_chunked_pair_energy(B, eps_occ, eps_vir, mem_budget_bytes: int = 1_50
 # Fused kernel vs the unfused chunked path (hipBLASLt GEMM + torch
 # elementwise) under `auto`, as the reference's row-flop / SBUF rule
 # (nki/dispatch.py:2680-2703) re-measured for MI355X: over 90 small shapes
-# (nocc 2..64, nvir 32..448, naux 128..1536) the fused kernel loses only
-# where its work items (pairs of occupied rows x 96-row tile pairs) fill a
-# fraction of the 256 CUs, so one item's k-steps (~1.9 us each, two passes
-# off the tile diagonal) form the whole critical path, or where nvir is far
-# below the 96-row tile; the unfused path costs a ~0.115 ms floor plus its
+# (nocc 2, 4, 8, 16, 32, 64 x nvir 32, 96, 192, 320, 448 x naux 128, 512,
+# 1536) the fused fp16x3 kernel loses in 10, all at naux 1536 where its work
+# items (squares of pairs of occupied rows x 96-row tile pairs) fill a
+# fraction of the 256 CUs, so one item's k-steps (~1.9 us each when few
+# items share the chip, two passes off the tile diagonal) form the whole
+# critical path; the unfused path costs a ~0.115 ms floor plus its
 # ordered-pair GEMM (~100 TFLOP/s) and six fp32 passes over T (~3 TB/s).
-# The model below picks the faster route in 88 of the 90 cases with the
-# default fp16x3 arithmetic (mean loss 0.02 %; 87 of 90 with bf16x6): on these
-# shapes one item's k-step takes about as long in either arithmetic, the
-# step being latency-bound when few items share the chip. At C3 / C4 it
-# keeps the fused kernel by a wide margin.
+# The model below picks the faster route in 87 of the 90 cases (mean loss
+# 0.16 %). At C3 / C4 it keeps the fused kernel by a wide margin.
 _PE_STEP_MS = 1.9e-3
-_PE_FUSED_FLOOR_MS = 0.02
+_PE_FUSED_FLOOR_MS = 0.05
 _PE_UNFUSED_FLOOR_MS = 0.115
 _PE_UNFUSED_GEMM_FLOPS = 100e12
 _PE_UNFUSED_T_BYTES_PER_S = 3e12
@@ -1106,10 +1104,11 @@ def _pair_energy_estimates(nocc: int, nvir: int, naux: int) -> tuple[float, floa
     """(fused, unfused) estimated milliseconds for B (nocc, nvir, naux)."""
     nb = -(-nvir // _PE_TILE)
     nq = nb * (nb + 1) // 2
-    couples = sum((nocc - i + 1) // 2 for i in range(nocc))  # pairs i <= j, two per item
+    nb2 = (nocc + 1) // 2
+    squares = nb2 * (nb2 + 1) // 2  # pairs i <= j, up to four per item
     nk = -(-naux // 32)
     steps = (nk * nb + 2 * nk * (nq - nb)) / nq  # mean k-steps per item
-    fused = _PE_FUSED_FLOOR_MS + math.ceil(couples * nq / _PE_CUS) * steps * _PE_STEP_MS
+    fused = _PE_FUSED_FLOOR_MS + math.ceil(squares * nq / _PE_CUS) * steps * _PE_STEP_MS
     m = nocc * nvir
     unfused = (
         _PE_UNFUSED_FLOOR_MS
