@@ -1020,8 +1020,16 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
 // from zero and are added to the pair's sum in fp32, one pair after the
 // other (36 VGPRs of partials), as pair_energy_x3_kernel<2> sums them; a
 // chain over all slices on the MFMA accumulator came out 1.6e-7 low on
-// same-sign sums. Three LDS stages filled by DMA two slices ahead (6 DMAs per wave per
-// slice, slices past the walk clamped to the last so the waits stay exact).
+// same-sign sums. Three LDS stages, slice s in stage s % 3; each group DMAs
+// its half of a stage (6 DMAs per wave per slice, slices past the walk
+// clamped to the last so the waits stay exact).
+// The two groups share the SIMDs (waves w and w + 4) and run half a step
+// apart, so one group's MFMAs overlap the other's DMA issue and fragment
+// reads: in phase A(t) group 0 multiplies slice t while group 1 DMAs its
+// half of slice t + 2 and reads slice t's fragments; in B(t) group 1
+// multiplies slice t while group 0 DMAs its half of slice t + 3 and reads
+// slice t + 1's fragments. A barrier ends each phase; before it, a wave that
+// just issued DMAs waits for all of its own but the newest slice's.
 // Stage slots: 0 B_i0, 1 B_i1, 2 B_j0, 3 B_j1; the i panels hold tile A's
 // rows in pass 0 (X = B_i[A] B_j[B]^T) and tile B's in pass 1 (X' = B_j[A]
 // B_i[B]^T). An absent index repeats the one before it; its pairs are
@@ -1066,15 +1074,16 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
   const int pairsA = min((nvir - a0 + 1) >> 1, S / 2), pairsB = min((nvir - b0 + 1) >> 1, S / 2);
   const int64_t rowA = (int64_t)(a0 >> 1) * nk * (NPC * 64),
                 rowB = (int64_t)(b0 >> 1) * nk * (NPC * 64);
-  // slice t (clamped to the last) into stage buf: slot 0 B_i0, 1 B_i1, 2 B_j0,
-  // 3 B_j1; the i panels hold tile A's rows in pass 0, tile B's in pass 1
+  // this group's half of slice t (clamped to the last) into stage buf: slot
+  // 0 B_i0, 1 B_i1, 2 B_j0, 3 B_j1; the i panels hold tile A's rows in pass
+  // 0, tile B's in pass 1; group gi moves the 1 KiB pieces 24 gi .. 24 gi + 23
   auto dma = [&](int t, int buf) __attribute__((always_inline)) {
     if (t >= nsteps) t = nsteps - 1;
     const int ps = t >= nk ? 1 : 0, sl0 = ps ? t - nk : t;
     const int soff = __builtin_amdgcn_readfirstlane(sl0 * NPC * 128);
 #pragma unroll
     for (int u = 0; u < NL; ++u) {
-      const int qq = w + 8 * u;
+      const int qq = 24 * gi + qd + 4 * u;
       const int sl = qq / BPS, e = qq - sl * BPS, pc = e / 6;
       const int uo = ((8 * (e - 6 * pc)) * nk * (NPC * 64) + pc * 64) * 2;
       const bool onA = (sl < 2) == (ps == 0);
@@ -1086,10 +1095,6 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
   };
 
   const int ar0 = 48 * (qd & 1), br0 = 48 * (qd >> 1);
-  const int fslot = 8 * x3_slot(lane & 15, lane >> 4);
-  auto frag = [&](const uint16_t* b, int pc, int r) __attribute__((always_inline)) {
-    return *reinterpret_cast<const i32x4*>(b + (pc * S + r) * BK + fslot);
-  };
   f32x4 accX[2][3][3], accP[2][3][3];
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj)
@@ -1097,66 +1102,123 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
     for (int rb = 0; rb < 3; ++rb)
 #pragma unroll
       for (int cb = 0; cb < 3; ++cb) accX[jj][rb][cb] = accP[jj][rb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  auto step = [&](auto PS_, int t, int bt, int b2) __attribute__((always_inline)) {
-    constexpr int PS = decltype(PS_)::value;
-    asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");  // slice t landed
+  i32x4 fi[3][2], fj[2][3][2];  // the wave's fragments of one slice, live from its read phase to its MFMAs
+  // fragments of slice t from stage bt
+  auto rd = [&](int t, int bt) __attribute__((always_inline)) {
+    // the lane index is opaque here, so the fragment addresses are computed
+    // in each read phase instead of hoisted out of the walk and kept live
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int fs = 8 * x3_slot(ln & 15, ln >> 4);
+    const int ps = t >= nk ? 1 : 0;
     const uint16_t* st = lds + bt * STAGE;
     const uint16_t* ip = st + gi * SLOT;
-    i32x4 fi[3][2], fj[2][3][2];
-    const int ri = PS == 0 ? ar0 : br0, rj = PS == 0 ? br0 : ar0;
+    const int ri = ps == 0 ? ar0 : br0, rj = ps == 0 ? br0 : ar0;
 #pragma unroll
     for (int u = 0; u < 3; ++u)
 #pragma unroll
       for (int pc = 0; pc < 2; ++pc) {
-        fi[u][pc] = frag(ip, pc, ri + 16 * u + (lane & 15));
+        fi[u][pc] = *reinterpret_cast<const i32x4*>(ip + (pc * S + ri + 16 * u + (ln & 15)) * BK + fs);
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) fj[jj][u][pc] = frag(st + (2 + jj) * SLOT, pc, rj + 16 * u + (lane & 15));
+        for (int jj = 0; jj < 2; ++jj)
+          fj[jj][u][pc] = *reinterpret_cast<const i32x4*>(st + (2 + jj) * SLOT +
+                                                          (pc * S + rj + 16 * u + (ln & 15)) * BK + fs);
       }
+  };
+  // the slice's products, pair by pair; pair 0's partial of a block is
+  // added to its sum just before pair 1's first product takes its
+  // registers, so one pair's partials are live at a time
+  auto mm = [&](auto PS_) __attribute__((always_inline)) {
+    constexpr int PS = decltype(PS_)::value;
+    auto fold = [&](int jj, int rb, int cb, const f32x4& v) __attribute__((always_inline)) {
+      if constexpr (PS == 0)
+        accX[jj][rb][cb] += v;
+      else
+        accP[jj][rb][cb] += v;
+    };
+    f32x4 part[3][3];
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
-      f32x4 part[3][3];  // pair jj's products of the slice
 #pragma unroll
       for (int e = 0; e < M::NPROD; ++e)
 #pragma unroll
         for (int cb = 0; cb < 3; ++cb)
 #pragma unroll
           for (int rb = 0; rb < 3; ++rb) {
+            if (jj == 1 && e == 0) fold(0, rb, cb, part[rb][cb]);
             const f32x4 c0 = e == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb];
             if constexpr (PS == 0)
               part[rb][cb] = M::mma(fi[rb][M::ka[e]], fj[jj][cb][M::kb[e]], c0);
             else
               part[rb][cb] = M::mma(fj[jj][rb][M::ka[e]], fi[cb][M::kb[e]], c0);
+            if (jj == 1 && e == 0) __builtin_amdgcn_sched_barrier(0);
           }
-#pragma unroll
-      for (int rb = 0; rb < 3; ++rb)
-#pragma unroll
-        for (int cb = 0; cb < 3; ++cb) {
-          if constexpr (PS == 0)
-            accX[jj][rb][cb] += part[rb][cb];
-          else
-            accP[jj][rb][cb] += part[rb][cb];
-        }
-      // slice t + 2's DMA behind pair 0's MFMAs (before them, its issue
-      // delayed the step's first MFMA: C3 28.75 against 28.1 ms)
-      if (jj == 0) dma(t + 2, b2);
     }
+#pragma unroll
+    for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < 3; ++cb) fold(1, rb, cb, part[rb][cb]);
+    __builtin_amdgcn_sched_barrier(0);
   };
+  auto bar = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // this wave's DMAs of all but its newest n slices have landed (6 per slice)
+  auto vwait = [&](int n) __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (n >= 2)
+      asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  };
+  auto m3 = [](int t) { return t - 3 * (t / 3); };
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  // The two passes are separate loops so that the target of the folds (X or
+  // X') is fixed at compile time. Group 0 has its half of slices 0 .. 2 in
+  // flight before the walk and group 1 of slices 0 and 1; both wait for
+  // slice 0, then group 0 reads it.
   if (nsteps > 0) {
-    dma(0, 0);
-    dma(1, 1);
-    int bt = 0;
-    for (int t = 0; t < nk; ++t) {
-      const int b2 = bt == 0 ? 2 : bt - 1;
-      step(std::integral_constant<int, 0>(), t, bt, b2);
-      bt = bt == 2 ? 0 : bt + 1;
-    }
-    if (!diag) {
-      for (int t = nk; t < nsteps; ++t) {
-        const int b2 = bt == 0 ? 2 : bt - 1;
-        step(std::integral_constant<int, 1>(), t, bt, b2);
-        bt = bt == 2 ? 0 : bt + 1;
-      }
+    if (gi == 0) {
+      dma(0, 0);
+      dma(1, 1);
+      dma(2, 2);
+      vwait(2);
+      bar();
+      rd(0, 0);
+      auto walk0 = [&](auto PS_, int t0, int t1) __attribute__((always_inline)) {
+        for (int t = t0; t < t1; ++t) {
+          const int b0s = m3(t), b1s = b0s == 2 ? 0 : b0s + 1;
+          mm(PS_);  // A(t)
+          vwait(1);
+          bar();
+          dma(t + 3, b0s);  // B(t): stage t % 3 was read by both groups in or before A(t)
+          rd(t + 1, b1s);   // past the walk it reads a stage nobody uses
+          bar();
+        }
+      };
+      walk0(P0(), 0, nk);
+      if (!diag) walk0(P1(), nk, nsteps);
+    } else {
+      dma(0, 0);
+      dma(1, 1);
+      vwait(1);
+      bar();
+      auto walk1 = [&](auto PS_, int t0, int t1) __attribute__((always_inline)) {
+        for (int t = t0; t < t1; ++t) {
+          const int b0s = m3(t), b2s = b0s == 0 ? 2 : b0s - 1;
+          dma(t + 2, b2s);  // A(t): stage (t + 2) % 3 held slice t - 1, read before A(t)
+          rd(t, b0s);
+          vwait(1);
+          bar();
+          mm(PS_);  // B(t)
+          bar();
+        }
+      };
+      walk1(P0(), 0, nk);
+      if (!diag) walk1(P1(), nk, nsteps);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA may land after the workgroup ends
