@@ -1009,39 +1009,29 @@ __global__ __launch_bounds__(256) void gemm_fixup_kernel(GemmArgs g) {
   for (int u = 0; u < 4; ++u) store_out<T, SYRK>(g, C, D, m0 + r, n0 + c + u, v[u], up);
 }
 
-// fp32 GEMM with one workgroup per CU (sgemm_pipe_kernel). A 128 x 128 tile
-// per workgroup: four compute waves of 64 x 64 (2 x 2 blocks of
-// v_mfma_f32_32x32x2_f32, one wave per SIMD) and four movers, waves that only
-// move operands: k-tiles of 32 are loaded into the movers' registers two
-// k-tiles ahead and stored into four LDS stages of 32 KiB (A panel, then B
-// panel). (LDS DMA was measured slower here: a wave's LDS DMAs complete one
-// at a time, so compute waves that issued their share stalled at the issue,
-// 124 TFLOP/s at 8192^3 against 140 with the DMAs left out; two and four
-// DMA-only waves gave 118 and 130.) With one compute wave per SIMD no other wave
-// hides a wave's LDS reads, so they hide behind its own MFMAs: the fragments
-// of each 8-wide k slice (k-oct) are read before the MFMAs of the k-oct
-// before issue, and the barrier that publishes k-tile s + 1 comes before the
-// last k-oct's MFMAs of k-tile s.
-//
-// k order: MFMA j (0..3) of k-oct o gives lane l the k = 8 o + 4 h + j
-// (h = l / 32) in both operands. A K-contiguous panel (128 rows of 32 values,
-// 16-byte group c of row r in slot c ^ ((r >> 1) & 7)) then gives a lane its
-// four values of row 32 p + l % 32 in one 16-byte read. An M/N-contiguous
-// panel (32 k rows of 128 values) gives, in one 8-byte read of k row
-// 8 o + 4 h + j, the values of columns 2 (l % 32) and 2 (l % 32) + 1: the two
-// 32-row blocks p of a wave are then its even and its odd rows (columns),
-// which the store follows. Rows and columns past M / N and k past K read as
-// zeros (offsets past the buffer's records). The accumulation follows
-// gemm_dma_kernel: MFMA chains of span k-tiles folded into a separate sum.
+// fp32 GEMM with one workgroup per CU (sgemm_pipe_kernel), both operands
+// M/N-contiguous (A^T B). A 128 x 128 tile per workgroup: eight compute
+// waves of 64 x 32, two per SIMD (4 x 2 blocks of v_mfma_f32_16x16x4_f32),
+// and four movers, waves that only move operands: k-tiles of 32 are loaded
+// into the movers' registers two k-tiles ahead and stored into four LDS
+// stages of 32 KiB (A panel, then B panel, each 32 k rows of 128 values).
+// (LDS DMA was measured slower here: a wave's LDS DMAs complete one at a
+// time, so compute waves that issued their share stalled at the issue, 124
+// TFLOP/s at 8192^3 against 140 with the DMAs left out; two and four
+// DMA-only waves gave 118 and 130.) The fragments of each 8-wide k slice
+// (k-oct) are read before the MFMAs of the k-oct before issue, and the
+// barrier that publishes k-tile s + 1 comes before the last k-oct's MFMAs of
+// k-tile s. Rows and columns past M / N and k past K read as zeros (offsets
+// past the buffer's records). The accumulation follows gemm_dma_kernel: MFMA
+// chains of span k-tiles folded into a separate sum.
 constexpr int kPipeBK = 32;
 constexpr int kPipeStages = 4;
 constexpr int kPipePanel = 128 * kPipeBK;   // floats per panel (16 KiB)
 constexpr int kPipeStage = 2 * kPipePanel;  // floats per stage (32 KiB)
-constexpr int kPipeThreads = 512;           // 4 compute waves + 4 movers
+constexpr int kPipeThreads = 768;           // 8 compute waves + 4 movers
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-template <bool AKC, bool BKC>
 __global__ __launch_bounds__(kPipeThreads, 1) void sgemm_pipe_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) float lds[kPipeStages * kPipeStage];
   const int tid = threadIdx.x;
@@ -1053,20 +1043,17 @@ __global__ __launch_bounds__(kPipeThreads, 1) void sgemm_pipe_kernel(GemmArgs g)
   const int m0 = tm * 128, n0 = tn * 128;
   const int K = g.K, nk = g.nk;
 
-  if (w >= 4) {
-    // The movers: wave 4 + m (m < 4) moves blocks 8 (m & 1) .. + 7 of the A
+  if (w >= 8) {
+    // The movers: wave 8 + m (m < 4) moves blocks 8 (m & 1) .. + 7 of the A
     // panel (m < 2) or the B panel (m >= 2) of each stage, 1 KiB per block:
     // a 16-byte buffer load per lane into registers two k-tiles ahead, then
     // one 16-byte LDS store per lane (lane l of block b: bytes 16 l of the
-    // block's KiB). K-contiguous panel, block b: rows 8 b .. 8 b + 7; lane l
-    // holds row 8 b + l / 8, slot l % 8 = source group (l % 8) ^ ((row >> 1)
-    // & 7). M/N-contiguous panel, block b: k rows 2 b, 2 b + 1; lane l holds
-    // k row 2 b + l / 32, group l % 32. A lane's load is valid while its row /
-    // column is inside the matrix and kq <= K - k0 (kq: one past the lane's
-    // last k); others read zeros.
-    const int m = w - 4;
+    // block's KiB). Block b holds k rows 2 b, 2 b + 1; lane l holds k row
+    // 2 b + l / 32, values 4 (l % 32) .. + 3. A lane's load is valid while
+    // its columns are inside the matrix and kq <= K - k0 (kq: one past the
+    // lane's k); others read zeros.
+    const int m = w - 8;
     const bool onB = m >= 2;
-    const bool kc = onB ? BKC : AKC;
     const float* X = static_cast<const float*>(onB ? g.B : g.A) + bat * (onB ? g.sB : g.sA);
     const int64_t ld = onB ? g.ldb : g.lda;
     const int r0 = onB ? n0 : m0, left = (onB ? g.N : g.M) - r0;
@@ -1075,21 +1062,14 @@ __global__ __launch_bounds__(kPipeThreads, 1) void sgemm_pipe_kernel(GemmArgs g)
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int b = 8 * (m & 1) + u;
-      if (kc) {
-        const int row = 8 * b + (lane >> 3);
-        const int grp = (lane & 7) ^ ((row >> 1) & 7);
-        v[u] = (uint32_t)((int64_t)row * ld * 4 + 16 * grp);
-        kq[u] = row < left ? 4 * grp + 4 : 1 << 30;
-      } else {
-        const int krow = 2 * b + (lane >> 5);
-        const int col = 4 * (lane & 31);
-        v[u] = (uint32_t)((int64_t)krow * ld * 4 + 4 * col);
-        kq[u] = col < left ? krow + 1 : 1 << 30;
-      }
+      const int krow = 2 * b + (lane >> 5);
+      const int col = 4 * (lane & 31);
+      v[u] = (uint32_t)((int64_t)krow * ld * 4 + 4 * col);
+      kq[u] = col < left ? krow + 1 : 1 << 30;
     }
     auto gload = [&](int kt, i32x4(&r)[8]) __attribute__((always_inline)) {
       const int k0 = kt * kPipeBK, kl = K - k0;
-      const float* base = kc ? X + (int64_t)r0 * ld + k0 : X + (int64_t)k0 * ld + r0;
+      const float* base = X + (int64_t)k0 * ld + r0;
       const __amdgpu_buffer_rsrc_t rs = make_rsrc(base);
 #pragma unroll
       for (int u = 0; u < 8; ++u)
@@ -1127,107 +1107,65 @@ __global__ __launch_bounds__(kPipeThreads, 1) void sgemm_pipe_kernel(GemmArgs g)
     return;
   }
 
-  const int wm0 = 64 * (w & 1), wn0 = 64 * (w >> 1);
-  const int h = lane >> 5, li = lane & 31;
-  const int sw = (li >> 1) & 7;
+  const int wm0 = 64 * (w & 1), wn0 = 32 * (w >> 1);
+  const int kg = lane >> 4, li = lane & 15;
+  // v_mfma_f32_16x16x4_f32: lane l holds k = l / 16 of A (row l % 16) and
+  // of B (column l % 16); block p (0..3) of the wave's rows is rows
+  // wm0 + 4 r + p, block q (0..1) of its columns is columns wn0 + 2 c + q,
+  // so one 16-byte read gives a lane its A values of all four row blocks and
+  // one 8-byte read its B values of both column blocks.
   struct Frag {
-    float a[2][4], b[2][4];
+    float a[2][4], b[2][2];  // [k-step of the k-oct][block]
   };
-  // fragments of k-oct o of the stage at st
   auto rd = [&](const float* st, int o, Frag& f) __attribute__((always_inline)) {
-    if constexpr (AKC) {
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(st + (wm0 + 32 * p + li) * kPipeBK +
-                                                        4 * ((2 * o + h) ^ sw));
+    for (int j = 0; j < 2; ++j) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(st + (8 * o + 4 * j + kg) * 128 + wm0 + 4 * li);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) f.a[p][j] = v[j];
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x2 v =
-            *reinterpret_cast<const f32x2*>(st + (8 * o + 4 * h + j) * 128 + wm0 + 2 * li);
-        f.a[0][j] = v[0];
-        f.a[1][j] = v[1];
-      }
-    }
-    const float* sb = st + kPipePanel;
-    if constexpr (BKC) {
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(sb + (wn0 + 32 * q + li) * kPipeBK +
-                                                        4 * ((2 * o + h) ^ sw));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) f.b[q][j] = v[j];
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x2 v =
-            *reinterpret_cast<const f32x2*>(sb + (8 * o + 4 * h + j) * 128 + wn0 + 2 * li);
-        f.b[0][j] = v[0];
-        f.b[1][j] = v[1];
-      }
+      for (int p = 0; p < 4; ++p) f.a[j][p] = v[p];
+      const f32x2 u = *reinterpret_cast<const f32x2*>(st + kPipePanel + (8 * o + 4 * j + kg) * 128 + wn0 + 2 * li);
+      f.b[j][0] = u[0];
+      f.b[j][1] = u[1];
     }
   };
-  f32x16 acc[2][2], sum[2][2];
+  f32x4 acc[4][2], sum[4][2];
 #pragma unroll
-  for (int p = 0; p < 2; ++p)
+  for (int p = 0; p < 4; ++p)
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[p][q][r] = sum[p][q][r] = 0.0f;
-  // the four MFMAs of sub-step j of a k-oct
-  auto mm_j = [&](const Frag& f, int j) __attribute__((always_inline)) {
-#pragma unroll
-    for (int p = 0; p < 2; ++p)
-#pragma unroll
-      for (int q = 0; q < 2; ++q)
-        acc[p][q] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[p][j], f.b[q][j], acc[p][q], 0, 0, 0);
-  };
+    for (int q = 0; q < 2; ++q) acc[p][q] = sum[p][q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   auto mm = [&](const Frag& f) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) mm_j(f, j);
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          acc[p][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[j][p], f.b[j][q], acc[p][q], 0, 0, 0);
   };
 
-  // C for the lane's outputs (beta != 0), loaded during the last k-tile.
-  // Lane l of block (p, q) holds block column l % 32 and block rows
-  // 8 (e / 4) + 4 h + e % 4 of its registers e.
   const float* C = static_cast<const float*>(g.C) + (g.C ? bat * g.sC : 0);
   const int M = g.M, Nn = g.N;
   const float beta = g.beta;
-  auto row_of = [&](int p, int e) __attribute__((always_inline)) {
-    const int br = 8 * (e >> 2) + 4 * h + (e & 3);
-    return m0 + wm0 + (AKC ? 32 * p + br : 2 * br + p);
+  // lane l, register i of block (p, q): row 4 (4 (l / 16) + i) + p, column 2 (l % 16) + q
+  auto row_of = [&](int p, int i) __attribute__((always_inline)) {
+    return m0 + wm0 + 4 * (4 * kg + i) + p;
   };
-  auto col_of = [&](int q) __attribute__((always_inline)) {
-    return n0 + wn0 + (BKC ? 32 * q + li : 2 * li + q);
-  };
-  float cv[2][2][16];
+  const int col = n0 + wn0 + 2 * li;
+  float cv[4][4][2];
   auto load_c = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int p = 0; p < 4; ++p)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = row_of(p, e);
-        const bool mok = m < M && beta != 0.0f;
-        if constexpr (BKC) {
-#pragma unroll
-          for (int q = 0; q < 2; ++q) {
-            const int n = col_of(q);
-            cv[p][q][e] = mok && n < Nn ? C[(int64_t)m * g.ldc + n] : 0.0f;
-          }
+      for (int i = 0; i < 4; ++i) {
+        const int mr = row_of(p, i);
+        const bool ok = mr < M && beta != 0.0f && col < Nn;
+        if (ok && g.vec2) {
+          const f32x2 c = *reinterpret_cast<const f32x2*>(C + (int64_t)mr * g.ldc + col);
+          cv[p][i][0] = c[0];
+          cv[p][i][1] = c[1];
         } else {
-          const int n = col_of(0);  // n + 1 < N whenever n < N (N % 4 == 0)
-          if (mok && n < Nn && g.vec2) {
-            const f32x2 c = *reinterpret_cast<const f32x2*>(C + (int64_t)m * g.ldc + n);
-            cv[p][0][e] = c[0];
-            cv[p][1][e] = c[1];
-          } else {
-            cv[p][0][e] = mok && n < Nn ? C[(int64_t)m * g.ldc + n] : 0.0f;
-            cv[p][1][e] = mok && n < Nn ? C[(int64_t)m * g.ldc + n + 1] : 0.0f;
-          }
+          cv[p][i][0] = ok ? C[(int64_t)mr * g.ldc + col] : 0.0f;
+          cv[p][i][1] = ok ? C[(int64_t)mr * g.ldc + col + 1] : 0.0f;
         }
       }
   };
@@ -1238,7 +1176,7 @@ __global__ __launch_bounds__(kPipeThreads, 1) void sgemm_pipe_kernel(GemmArgs g)
   // s + 1, and the last k-oct's MFMAs. The loop has no branch but the fold,
   // and the last k-tile is peeled, so the compiler's LDS wait counts stay
   // exact; sched_barrier keeps the reads ahead of the MFMAs. The last
-  // k-tile loads C first.
+  // k-tile loads C first (beta != 0).
   auto body = [&](int s, auto next) __attribute__((always_inline)) {
     constexpr bool NEXT = decltype(next)::value;
     if constexpr (!NEXT) load_c();
@@ -1265,9 +1203,12 @@ __global__ __launch_bounds__(kPipeThreads, 1) void sgemm_pipe_kernel(GemmArgs g)
   };
   auto fold = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int p = 0; p < 4; ++p)
 #pragma unroll
-      for (int q = 0; q < 2; ++q) fold_span(sum[p][q], acc[p][q]);
+      for (int q = 0; q < 2; ++q) {
+        sum[p][q] += acc[p][q];
+        acc[p][q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
   };
   using Y = std::true_type;
   using N = std::false_type;
@@ -1287,34 +1228,23 @@ __global__ __launch_bounds__(kPipeThreads, 1) void sgemm_pipe_kernel(GemmArgs g)
   } else {
     load_c();
   }
-
   // D = alpha sum + beta C
   asm volatile("" : "+v"(lane));
   float* D = static_cast<float*>(g.D) + bat * g.sD;
   const float alpha = g.alpha;
 #pragma unroll
-  for (int p = 0; p < 2; ++p)
+  for (int p = 0; p < 4; ++p)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int m = row_of(p, e);
-      if (m >= M) continue;
-      float v[2];
-#pragma unroll
-      for (int q = 0; q < 2; ++q) v[q] = __builtin_fmaf(beta, cv[p][q][e], alpha * sum[p][q][e]);
-      if constexpr (BKC) {
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-          if (col_of(q) < Nn) D[(int64_t)m * g.ldd + col_of(q)] = v[q];
+    for (int i = 0; i < 4; ++i) {
+      const int mr = row_of(p, i);
+      if (mr >= M || col >= Nn) continue;
+      const float v0 = __builtin_fmaf(beta, cv[p][i][0], alpha * sum[p][0][i]);
+      const float v1 = __builtin_fmaf(beta, cv[p][i][1], alpha * sum[p][1][i]);
+      if (g.vec2) {
+        *reinterpret_cast<f32x2*>(D + (int64_t)mr * g.ldd + col) = f32x2{v0, v1};
       } else {
-        const int n = col_of(0);
-        if (n < Nn) {
-          if (g.vec2) {
-            *reinterpret_cast<f32x2*>(D + (int64_t)m * g.ldd + n) = f32x2{v[0], v[1]};
-          } else {
-            D[(int64_t)m * g.ldd + n] = v[0];
-            D[(int64_t)m * g.ldd + n + 1] = v[1];
-          }
-        }
+        D[(int64_t)mr * g.ldd + col] = v0;
+        D[(int64_t)mr * g.ldd + col + 1] = v1;
       }
     }
 }
@@ -1416,30 +1346,29 @@ static int launch_narrow(GemmArgs g, size_t ws_bytes, hipStream_t s) {
 
 // fp32 GEMM on sgemm_pipe_kernel (whole 128 x 128 tiles, one workgroup per
 // CU); C and D take 2-element accesses when 8-byte aligned with even ld.
-template <bool AKC, bool BKC>
 static int launch_pipe(GemmArgs g, hipStream_t s) {
   g.nk = (g.K + kPipeBK - 1) / kPipeBK;
   g.span = chain_length(g.K, 4) / kPipeBK;
   g.vec2 = g.ldd % 2 == 0 && (reinterpret_cast<uintptr_t>(g.D) & 7) == 0 &&
            (g.C == nullptr || (g.ldc % 2 == 0 && (reinterpret_cast<uintptr_t>(g.C) & 7) == 0));
-  hipLaunchKernelGGL((sgemm_pipe_kernel<AKC, BKC>), dim3(g.ntiles), dim3(kPipeThreads), 0, s, g);
+  hipLaunchKernelGGL(sgemm_pipe_kernel, dim3(g.ntiles), dim3(kPipeThreads), 0, s, g);
   return check_launch("trnblas_hip_gemm");
 }
 
 // sgemm_pipe_kernel where it was measured faster than gemm_dma_kernel: both
 // operands M/N-contiguous (A^T B, C1's layout) and one round of 128 x 128
 // tiles that fills 90 % of the CUs or more, with 32 k-tiles or more. C1
-// (2048^3 A^T B + 0.5 C) 0.140 against 0.149 ms. Not where a K-contiguous
-// B's fragments come from 16-byte reads in both kernels (A B^T, A^T B^T at
-// 2048^3: 0.159 / 0.161 against 0.135 / 0.141 ms), nor for fewer tiles than
-// CUs (gemm_dma_kernel splits them by stream-K), nor at 8192^3 (133.7
-// against 138 TFLOP/s: the steady state of one compute wave per SIMD stays
-// at ~0.85 of the MFMA issue rate, 4800 cycles per 4096-cycle k-tile, timed
-// in-kernel).
-template <bool AKC, bool BKC>
+// (2048^3 A^T B + 0.5 C) 0.1375 against 0.149 ms (0.139 with four compute
+// waves of 64 x 64 on v_mfma_f32_32x32x2_f32, one per SIMD; 0.1397 with eight
+// on 32x32x2). With K-contiguous operands gemm_dma_kernel's 16-byte
+// fragment reads win (A B^T, A^T B^T at 2048^3: 0.159 / 0.161 against 0.135
+// / 0.141 ms with the four-wave version), as they do for fewer tiles than
+// CUs (gemm_dma_kernel splits them by stream-K) and at 8192^3 (133.7 against
+// 138 TFLOP/s with the four-wave version: ~4800 cycles per 4096-cycle
+// k-tile, timed in-kernel).
 static bool pipe_pays(const GemmArgs& g) {
   const int cus = device_cus();
-  return !AKC && !BKC && g.ntiles <= cus && 10 * g.ntiles >= 9 * cus &&
+  return g.ntiles <= cus && 10 * g.ntiles >= 9 * cus &&
          (g.K + kPipeBK - 1) / kPipeBK >= 32;
 }
 
@@ -1475,8 +1404,8 @@ static int launch_t(GemmArgs g, size_t ws_bytes, hipStream_t s) {
   constexpr int BK = DMA ? 128 / (int)sizeof(T) : C::template bk<VEC>();
   g.nk = (g.K + BK - 1) / BK;
   g.span = chain_length(g.K, (int)sizeof(T)) / BK;  // even for the DMA kernel's k-tiles
-  if constexpr (DMA && !SYRK && sizeof(T) == 4) {
-    if (pipe_pays<AKC, BKC>(g)) return launch_pipe<AKC, BKC>(g, s);
+  if constexpr (DMA && !SYRK && sizeof(T) == 4 && !AKC && !BKC) {
+    if (pipe_pays(g)) return launch_pipe(g, s);
   }
   if constexpr (DMA && !SYRK && sizeof(T) == 2) {
     const int64_t span_a = (AKC ? 256 : 64) * g.lda * 2, span_b = (BKC ? 256 : 64) * g.ldb * 2;
