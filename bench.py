@@ -186,8 +186,40 @@ def run_extras(dev, tb, only=None, P: int = 1, do_cpu: bool = True) -> dict:
     if only is None or "c1" in only:
         # C1: gemm fp32 A^T B + 0.5 C at 2048^3, against the CPU path
         A, B, C = df_mp2.config1_inputs(dev)
-        t = gpu_time_ms(lambda: tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True), reps=20, warm=20)
-        D = tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True)
+
+        def pub():
+            return tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True)
+
+        def lt():  # hipBLASLt through torch on the same operands (A^T as a view)
+            return torch.addmm(C, A.mT, B, beta=0.5)
+
+        # Single calls include the host's time to issue them, so the two are
+        # timed in alternating blocks under the same host conditions, and
+        # before the CPU legs (whose worker threads compete with the host
+        # side of a call while they wind down).
+        ts, tls = [], []
+        for _ in range(6):
+            ts.append(gpu_time_ms(pub, reps=10, warm=5))
+            tls.append(gpu_time_ms(lt, reps=10, warm=5))
+        t, tl = median(ts), median(tls)
+        D = pub()
+        Dl = lt()
+        # One call between two events includes the host's time to issue it
+        # (the public path's routing and argument handling); 20 calls back
+        # to back show the GPU time per call, and the launch events bracket
+        # the library's kernels alone.
+        def b2b(fn, calls=20):
+            return gpu_time_ms(lambda: [fn() for _ in range(calls)], reps=5, warm=1) / calls
+
+        t_b2b = b2b(pub)
+        tl_b2b = b2b(lt)
+        probe = LaunchEvents("gemm")
+        kernels._launch_probe = probe
+        for _ in range(20):
+            tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True)
+        kernels._launch_probe = None
+        torch.cuda.synchronize()
+        tk = probe.mean_ms()
         Ah, Bh, Ch = A.cpu(), B.cpu(), C.cpu()
         from oracle import blas
 
@@ -198,26 +230,7 @@ def run_extras(dev, tb, only=None, P: int = 1, do_cpu: bool = True) -> dict:
             c1_cpu2_ms = cpu_ms(lambda: blas.gemm_cpu(1.0, Ah, Bh, 0.5, Ch, transA=True), 3) if do_cpu else None
         den = Ah.double().abs().T @ Bh.double().abs() + 0.5 * Ch.double().abs()
         err = float(((D.cpu().double() - cpu.double()) / den).abs().max())
-        # hipBLASLt through torch on the same operands (A^T as a view)
-        tl = gpu_time_ms(lambda: torch.addmm(C, A.mT, B, beta=0.5), reps=20, warm=20)
-        Dl = torch.addmm(C, A.mT, B, beta=0.5)
         err_l = float(((Dl.cpu().double() - cpu.double()) / den).abs().max())
-        # One call between two events includes the host's time to issue it
-        # (the public path's routing and argument handling); 20 calls back
-        # to back show the GPU time per call, and the launch events bracket
-        # the library's kernels alone.
-        def b2b(fn, calls=20):
-            return gpu_time_ms(lambda: [fn() for _ in range(calls)], reps=5, warm=1) / calls
-
-        t_b2b = b2b(lambda: tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True))
-        tl_b2b = b2b(lambda: torch.addmm(C, A.mT, B, beta=0.5))
-        probe = LaunchEvents("gemm")
-        kernels._launch_probe = probe
-        for _ in range(20):
-            tb.gemm(1.0, A, B, beta=0.5, C=C, transA=True)
-        kernels._launch_probe = None
-        torch.cuda.synchronize()
-        tk = probe.mean_ms()
         fl = 2 * 2048**3
         out["c1_gemm_2048_transA"] = {
             "ms": t, "tflops": fl / t / 1e9, "frac_fp32_peak": fl / t / 1e9 / PEAK_FP32_MFMA,
