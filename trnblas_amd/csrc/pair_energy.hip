@@ -1048,6 +1048,8 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
   constexpr int LDS_ELEMS = 3 * STAGE > EPI ? 3 * STAGE : EPI;
   __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_ELEMS];
   __shared__ double red[2][2][4];
+  __shared__ int tileE[4][S];   // diagonal tiles: row exponents of i0, i1, j0, j1
+  __shared__ float tileEv[S];   // and the rows' orbital energies
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1223,31 +1225,66 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA may land after the workgroup ends
 
+  // The energy terms. The exponents and orbital energies of the lane's rows
+  // and columns are loaded once, up front and clamped into the matrix, so
+  // their loads overlap instead of each term waiting for its own; 2^-(e1 +
+  // e2) is the pe_scale factor. Rows and columns past nvir hold X = X' = 0
+  // (their panel rows read as zeros), so their terms are exact zeros with
+  // finite denominators and need no branch.
   double sum[2] = {0.0, 0.0};
   const double ei = (double)g.eps_i[ig];
+  const int32_t* E = g.Ei;
+  const int64_t ldE = g.ldE;
   if (!diag) {
+    int xa_i[12], xa_j[2][12], xb_i[3], xb_j[2][3];
+    float eva[12], evb[3];
+#pragma unroll
+    for (int rb = 0; rb < 3; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int a = min(a0 + ar0 + 16 * rb + 4 * (lane >> 4) + r, nvir - 1);
+        xa_i[4 * rb + r] = E[ig * ldE + a];
+        xa_j[0][4 * rb + r] = E[j0 * ldE + a];
+        xa_j[1][4 * rb + r] = E[j1 * ldE + a];
+        eva[4 * rb + r] = g.eps_vir[a];
+      }
+#pragma unroll
+    for (int cb = 0; cb < 3; ++cb) {
+      const int b = min(b0 + br0 + 16 * cb + (lane & 15), nvir - 1);
+      xb_i[cb] = E[ig * ldE + b];
+      xb_j[0][cb] = E[j0 * ldE + b];
+      xb_j[1][cb] = E[j1 * ldE + b];
+      evb[cb] = g.eps_vir[b];
+    }
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int jg = jj ? j1 : j0;
       const double eo = ei + (double)g.eps_j[jg];
 #pragma unroll
       for (int cb = 0; cb < 3; ++cb) {
-        const int b = b0 + br0 + 16 * cb + (lane & 15);
-        const double eb = b < nvir ? (double)g.eps_vir[b] : 0.0;
+        const double eb = (double)evb[cb];
 #pragma unroll
         for (int rb = 0; rb < 3; ++rb)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int a = a0 + ar0 + 16 * rb + 4 * (lane >> 4) + r;
-            if (a < nvir && b < nvir) {
-              const double x = accX[jj][rb][cb][r] * pe_scale<NPC>(g, g.Ei, ig, a, g.Ei, jg, b);
-              const double xp = accP[jj][rb][cb][r] * pe_scale<NPC>(g, g.Ei, jg, a, g.Ei, ig, b);
-              sum[jj] += 2.0 * (x * x + xp * xp - x * xp) / (eo - (double)g.eps_vir[a] - eb);
-            }
+            const int ka = 4 * rb + r;
+            const double x = accX[jj][rb][cb][r] * ldexp(1.0, -(xa_i[ka] + xb_j[jj][cb]));
+            const double xp = accP[jj][rb][cb][r] * ldexp(1.0, -(xa_j[jj][ka] + xb_i[cb]));
+            sum[jj] += 2.0 * (x * x + xp * xp - x * xp) / (eo - (double)eva[ka] - eb);
           }
       }
     }
   } else {
+    // diagonal tile: X goes through LDS for its transpose; the tile's
+    // exponents (orbitals i0, i1, j0, j1) and orbital energies beside it
+    const int o4[4] = {i0, i1, j0, j1};
+    for (int x = tid; x < 5 * S; x += 512) {
+      const int r = x % S, row = min(a0 + r, nvir - 1), sl = x / S;
+      if (sl < 4)
+        tileE[sl][r] = E[o4[sl] * ldE + row];
+      else
+        tileEv[r] = g.eps_vir[row];
+    }
     __syncthreads();
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
@@ -1263,19 +1300,19 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
     }
     __syncthreads();
     const int lt = tid & 255;
+    const int* ti = tileE[gi];  // exponents of i_gi over the tile's rows
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int jg = jj ? j1 : j0;
+      const int* tj = tileE[2 + jj];
       const double eo = ei + (double)g.eps_j[jg];
       const float* xs = reinterpret_cast<const float*>(lds) + (2 * gi + jj) * S * (S + 1);
 #pragma unroll 4
       for (int e = 0; e < S * S / 256; ++e) {
         const int idx = lt + 256 * e, a = idx / S, b = idx - a * S;
-        if (a0 + a < nvir && a0 + b < nvir) {
-          const double x = xs[a * (S + 1) + b] * pe_scale<NPC>(g, g.Ei, ig, a0 + a, g.Ei, jg, a0 + b);
-          const double xt = xs[b * (S + 1) + a] * pe_scale<NPC>(g, g.Ei, ig, a0 + b, g.Ei, jg, a0 + a);
-          sum[jj] += x * (2.0 * x - xt) / (eo - (double)g.eps_vir[a0 + a] - (double)g.eps_vir[a0 + b]);
-        }
+        const double x = xs[a * (S + 1) + b] * ldexp(1.0, -(ti[a] + tj[b]));
+        const double xt = xs[b * (S + 1) + a] * ldexp(1.0, -(ti[b] + tj[a]));
+        sum[jj] += x * (2.0 * x - xt) / (eo - (double)tileEv[a] - (double)tileEv[b]);
       }
     }
   }
