@@ -1129,7 +1129,10 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
   };
   // the slice's products, pair by pair; pair 0's partial of a block is
   // added to its sum just before pair 1's first product takes its
-  // registers, so one pair's partials are live at a time
+  // registers, so one pair's partials are live at a time, and pair 1's
+  // partial of a block three blocks after its last product issued, so the
+  // adds run beside the remaining MFMAs (only three blocks' adds trail
+  // them)
   auto mm = [&](auto PS_) __attribute__((always_inline)) {
     constexpr int PS = decltype(PS_)::value;
     auto fold = [&](int jj, int rb, int cb, const f32x4& v) __attribute__((always_inline)) {
@@ -1154,12 +1157,15 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
             else
               part[rb][cb] = M::mma(fj[jj][rb][M::ka[e]], fi[cb][M::kb[e]], c0);
             if (jj == 1 && e == 0) __builtin_amdgcn_sched_barrier(0);
+            if (jj == 1 && e == M::NPROD - 1) {
+              const int nb = 3 * cb + rb;  // block order of this loop
+              if (nb >= 3) fold(1, (nb - 3) % 3, (nb - 3) / 3, part[(nb - 3) % 3][(nb - 3) / 3]);
+              __builtin_amdgcn_sched_barrier(0);
+            }
           }
     }
 #pragma unroll
-    for (int rb = 0; rb < 3; ++rb)
-#pragma unroll
-      for (int cb = 0; cb < 3; ++cb) fold(1, rb, cb, part[rb][cb]);
+    for (int ob = 6; ob < 9; ++ob) fold(1, ob % 3, ob / 3, part[ob % 3][ob / 3]);
     __builtin_amdgcn_sched_barrier(0);
   };
   auto bar = [&]() __attribute__((always_inline)) {
