@@ -1127,12 +1127,11 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
                                                           (pc * S + rj + 16 * u + (ln & 15)) * BK + fs);
       }
   };
-  // the slice's products, pair by pair; pair 0's partial of a block is
-  // added to its sum just before pair 1's first product takes its
-  // registers, so one pair's partials are live at a time, and pair 1's
-  // partial of a block three blocks after its last product issued, so the
-  // adds run beside the remaining MFMAs (only three blocks' adds trail
-  // them)
+  // the slice's products, pair by pair, into one pair's partials at a time:
+  // a block's partial is added to the pair's sum three blocks after its
+  // last product issued, so the adds run beside the remaining MFMAs; pair
+  // 0's last three blocks are added just before pair 1's first products
+  // take their registers, and only pair 1's last three trail the MFMAs
   auto mm = [&](auto PS_) __attribute__((always_inline)) {
     constexpr int PS = decltype(PS_)::value;
     auto fold = [&](int jj, int rb, int cb, const f32x4& v) __attribute__((always_inline)) {
@@ -1150,16 +1149,16 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
         for (int cb = 0; cb < 3; ++cb)
 #pragma unroll
           for (int rb = 0; rb < 3; ++rb) {
-            if (jj == 1 && e == 0) fold(0, rb, cb, part[rb][cb]);
+            if (jj == 1 && e == 0 && 3 * cb + rb >= 6) fold(0, rb, cb, part[rb][cb]);
             const f32x4 c0 = e == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb];
             if constexpr (PS == 0)
               part[rb][cb] = M::mma(fi[rb][M::ka[e]], fj[jj][cb][M::kb[e]], c0);
             else
               part[rb][cb] = M::mma(fj[jj][rb][M::ka[e]], fi[cb][M::kb[e]], c0);
-            if (jj == 1 && e == 0) __builtin_amdgcn_sched_barrier(0);
-            if (jj == 1 && e == M::NPROD - 1) {
+            if (jj == 1 && e == 0 && 3 * cb + rb >= 6) __builtin_amdgcn_sched_barrier(0);
+            if (e == M::NPROD - 1) {
               const int nb = 3 * cb + rb;  // block order of this loop
-              if (nb >= 3) fold(1, (nb - 3) % 3, (nb - 3) / 3, part[(nb - 3) % 3][(nb - 3) / 3]);
+              if (nb >= 3) fold(jj, (nb - 3) % 3, (nb - 3) / 3, part[(nb - 3) % 3][(nb - 3) / 3]);
               __builtin_amdgcn_sched_barrier(0);
             }
           }
