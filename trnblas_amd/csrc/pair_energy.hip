@@ -639,14 +639,16 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
   // buffer P (the barrier publishes it and retires every read of buffer
   // 1 - P), set P is free (its slice t went to LDS in step t - 1) and takes
   // slice t + 2, slice t is multiplied (the NPROD products of each block,
-  // smallest first, into its partial: bf16x6 started at zero when FIRST, the
-  // two-slice partial added to the pass's sum below; fp16x3 started at zero
-  // every slice and added to the pass's sum at once, the order of
+  // smallest first, into its partial: with TWO the partial starts at zero
+  // when FIRST and spans two slices, added to the pass's sum below (bf16x6
+  // both passes, fp16x3 pass 0); otherwise it starts at zero every slice and
+  // is added to the pass's sum at once (fp16x3 pass 1), the order of
   // pair_energy_quad_kernel), then set 1 - P (slice t + 1) goes to buffer
   // 1 - P.
-  auto step = [&](auto P_, auto FIRST_, int t, f32x4(&acc)[3][3]) {
+  auto step = [&](auto P_, auto FIRST_, auto TWO_, int t, f32x4(&acc)[3][3]) {
     constexpr int P = decltype(P_)::value;
     constexpr bool FIRST = decltype(FIRST_)::value;
+    constexpr bool TWO = decltype(TWO_)::value;  // two-slice partials
     __syncthreads();
     load(t + 2, stg[P]);
     const uint16_t* buf = lds + P * STAGE;
@@ -663,7 +665,7 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
       i32x4 fb[NPC];
 #pragma unroll
       for (int pc = 0; pc < NPC; ++pc) fb[pc] = frag(pc, 1, br0 + 16 * cb + (lane & 15));
-      if constexpr (NPC == 2) {
+      if constexpr (!TWO) {
 #pragma unroll
         for (int e = 0; e < M::NPROD; ++e)
 #pragma unroll
@@ -693,11 +695,12 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
   using F = std::false_type;
   // One pass: slice pairs (t even, t + 1); bf16x6 adds each partial to the
   // pass's sum in fp32.
-  auto run_pass = [&](f32x4(&acc)[3][3], int t0) {
+  auto run_pass = [&](f32x4(&acc)[3][3], int t0, auto TWO_) {
+    constexpr bool TWO = decltype(TWO_)::value;
     for (int u = 0; u < nk; u += 2) {
-      step(I0(), T(), t0 + u, acc);
-      step(I1(), F(), t0 + u + 1, acc);
-      if constexpr (NPC != 2) {
+      step(I0(), T(), TWO_, t0 + u, acc);
+      step(I1(), F(), TWO_, t0 + u + 1, acc);
+      if constexpr (TWO) {
 #pragma unroll
         for (int rb = 0; rb < 3; ++rb)
 #pragma unroll
@@ -711,8 +714,10 @@ __global__ __launch_bounds__(256, 2) void pair_energy_x3_kernel(PairArgs g) {
     load(1, stg[1]);
     store(stg[0], 0);
   }
-  run_pass(accX, 0);
-  if (!diag) run_pass(accP, nk);
+  // fp16x3 sums X over two-slice partials and X' over one-slice partials,
+  // as pair_energy_quad_kernel does; bf16x6 both over two-slice partials
+  run_pass(accX, 0, T());
+  if (!diag) run_pass(accP, nk, std::integral_constant<bool, NPC != 2>());
   __syncthreads();  // all fragment reads done before the epilogue reuses LDS
 
   // Lane l of a 16 x 16 block holds column l % 16 and rows 4 (l / 16) + r.
@@ -1016,11 +1021,12 @@ __global__ __launch_bounds__(512, 1) void pair_energy_x3c_kernel(PairArgs g) {
 // DMA moves ~40 bytes per clock per CU; a couple's step stages as long as
 // its MFMAs take). Waves 4 gi .. 4 gi + 3 take i = i_gi and both j, each the
 // 48 x 48 quadrant (qd & 1, qd >> 1) of both pairs (X and X', 144 VGPRs):
-// a slice's products of one pair (pieces smallest first) chain on the MFMA
-// from zero and are added to the pair's sum in fp32, one pair after the
-// other (36 VGPRs of partials), as pair_energy_x3_kernel<2> sums them; a
-// chain over all slices on the MFMA accumulator came out 1.6e-7 low on
-// same-sign sums. Three LDS stages, slice s in stage s % 3; each group DMAs
+// the products of one pair (pieces smallest first) chain on the MFMA from
+// zero over two slices in pass 0 (both pairs' partials, 72 VGPRs, live
+// across the step) and over one slice in pass 1 (where X' takes 72 more
+// VGPRs: one pair's partials at a time), and are added to the pair's sum
+// in fp32, as pair_energy_x3_kernel<2> sums them; a chain over all slices
+// on the MFMA accumulator came out 1.6e-7 low on same-sign sums. Three LDS stages, slice s in stage s % 3; each group DMAs
 // its half of a stage (6 DMAs per wave per slice, slices past the walk
 // clamped to the last so the waits stay exact).
 // The two groups share the SIMDs (waves w and w + 4) and run half a step
@@ -1132,15 +1138,16 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
   // last product issued, so the adds run beside the remaining MFMAs; pair
   // 0's last three blocks are added just before pair 1's first products
   // take their registers, and only pair 1's last three trail the MFMAs
-  auto mm = [&](auto PS_) __attribute__((always_inline)) {
+  f32x4 part[2][3][3];  // pass 0: both pairs' two-slice partials live across the step
+  auto mm = [&](auto PS_, auto FIRST_, auto LAST_) __attribute__((always_inline)) {
     constexpr int PS = decltype(PS_)::value;
-    auto fold = [&](int jj, int rb, int cb, const f32x4& v) __attribute__((always_inline)) {
+    constexpr bool FIRST = decltype(FIRST_)::value, LAST = decltype(LAST_)::value;
+    auto fold = [&](int jj, int rb, int cb) __attribute__((always_inline)) {
       if constexpr (PS == 0)
-        accX[jj][rb][cb] += v;
+        accX[jj][rb][cb] += part[jj][rb][cb];
       else
-        accP[jj][rb][cb] += v;
+        accP[jj][rb][cb] += part[jj][rb][cb];
     };
-    f32x4 part[3][3];
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
 #pragma unroll
@@ -1149,22 +1156,24 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
         for (int cb = 0; cb < 3; ++cb)
 #pragma unroll
           for (int rb = 0; rb < 3; ++rb) {
-            if (jj == 1 && e == 0 && 3 * cb + rb >= 6) fold(0, rb, cb, part[rb][cb]);
-            const f32x4 c0 = e == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[rb][cb];
+            if (LAST && jj == 1 && e == 0 && 3 * cb + rb >= 6) fold(0, rb, cb);
+            const f32x4 c0 = FIRST && e == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : part[jj][rb][cb];
             if constexpr (PS == 0)
-              part[rb][cb] = M::mma(fi[rb][M::ka[e]], fj[jj][cb][M::kb[e]], c0);
+              part[jj][rb][cb] = M::mma(fi[rb][M::ka[e]], fj[jj][cb][M::kb[e]], c0);
             else
-              part[rb][cb] = M::mma(fj[jj][rb][M::ka[e]], fi[cb][M::kb[e]], c0);
-            if (jj == 1 && e == 0 && 3 * cb + rb >= 6) __builtin_amdgcn_sched_barrier(0);
-            if (e == M::NPROD - 1) {
+              part[jj][rb][cb] = M::mma(fj[jj][rb][M::ka[e]], fi[cb][M::kb[e]], c0);
+            if (LAST && jj == 1 && e == 0 && 3 * cb + rb >= 6) __builtin_amdgcn_sched_barrier(0);
+            if (LAST && e == M::NPROD - 1) {
               const int nb = 3 * cb + rb;  // block order of this loop
-              if (nb >= 3) fold(jj, (nb - 3) % 3, (nb - 3) / 3, part[(nb - 3) % 3][(nb - 3) / 3]);
+              if (nb >= 3) fold(jj, (nb - 3) % 3, (nb - 3) / 3);
               __builtin_amdgcn_sched_barrier(0);
             }
           }
     }
+    if constexpr (LAST) {
 #pragma unroll
-    for (int ob = 6; ob < 9; ++ob) fold(1, ob % 3, ob / 3, part[ob % 3][ob / 3]);
+      for (int ob = 6; ob < 9; ++ob) fold(1, ob % 3, ob / 3);
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
   auto bar = [&]() __attribute__((always_inline)) {
@@ -1195,15 +1204,25 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
       vwait(2);
       bar();
       rd(0, 0);
+      auto step0 = [&](auto PS_, auto F_, auto L_, int t) __attribute__((always_inline)) {
+        const int b0s = m3(t), b1s = b0s == 2 ? 0 : b0s + 1;
+        mm(PS_, F_, L_);  // A(t)
+        vwait(1);
+        bar();
+        dma(t + 3, b0s);  // B(t): stage t % 3 was read by both groups in or before A(t)
+        rd(t + 1, b1s);   // past the walk it reads a stage nobody uses
+        bar();
+      };
       auto walk0 = [&](auto PS_, int t0, int t1) __attribute__((always_inline)) {
-        for (int t = t0; t < t1; ++t) {
-          const int b0s = m3(t), b1s = b0s == 2 ? 0 : b0s + 1;
-          mm(PS_);  // A(t)
-          vwait(1);
-          bar();
-          dma(t + 3, b0s);  // B(t): stage t % 3 was read by both groups in or before A(t)
-          rd(t + 1, b1s);   // past the walk it reads a stage nobody uses
-          bar();
+        using T = std::true_type;
+        using F = std::false_type;
+        if constexpr (decltype(PS_)::value == 0) {
+          for (int t = t0; t < t1; t += 2) {  // nk is even
+            step0(PS_, T(), F(), t);
+            step0(PS_, F(), T(), t + 1);
+          }
+        } else {
+          for (int t = t0; t < t1; ++t) step0(PS_, T(), T(), t);
         }
       };
       walk0(P0(), 0, nk);
@@ -1213,15 +1232,25 @@ __global__ __launch_bounds__(512, 1) void pair_energy_quad_kernel(PairArgs g) {
       dma(1, 1);
       vwait(1);
       bar();
+      auto step1 = [&](auto PS_, auto F_, auto L_, int t) __attribute__((always_inline)) {
+        const int b0s = m3(t), b2s = b0s == 0 ? 2 : b0s - 1;
+        dma(t + 2, b2s);  // A(t): stage (t + 2) % 3 held slice t - 1, read before A(t)
+        rd(t, b0s);
+        vwait(1);
+        bar();
+        mm(PS_, F_, L_);  // B(t)
+        bar();
+      };
       auto walk1 = [&](auto PS_, int t0, int t1) __attribute__((always_inline)) {
-        for (int t = t0; t < t1; ++t) {
-          const int b0s = m3(t), b2s = b0s == 0 ? 2 : b0s - 1;
-          dma(t + 2, b2s);  // A(t): stage (t + 2) % 3 held slice t - 1, read before A(t)
-          rd(t, b0s);
-          vwait(1);
-          bar();
-          mm(PS_);  // B(t)
-          bar();
+        using T = std::true_type;
+        using F = std::false_type;
+        if constexpr (decltype(PS_)::value == 0) {
+          for (int t = t0; t < t1; t += 2) {
+            step1(PS_, T(), F(), t);
+            step1(PS_, F(), T(), t + 1);
+          }
+        } else {
+          for (int t = t0; t < t1; ++t) step1(PS_, T(), T(), t);
         }
       };
       walk1(P0(), 0, nk);
