@@ -321,7 +321,7 @@ def run_extras(dev, tb, only=None, P: int = 1, do_cpu: bool = True) -> dict:
         torch.cuda.synchronize()
         t_launch = probe.mean_ms()
         roof = {
-            "kernel": "row_exp_kernel + split_planes_kernel<2> + pair_energy_quad_kernel "
+            "kernel": "split_f16x3_kernel + pair_energy_quad_kernel "
                       "(trnblas_hip_pair_energy_fp16x3)",
             "bound": "mfma", "launch_ms": t_launch,
             "achieved": 3 * fl / t_launch / 1e9, "peak": PEAK_BF16_MFMA, "unit": "TFLOP/s (f16 MFMA)",

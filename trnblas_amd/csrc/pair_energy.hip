@@ -425,35 +425,6 @@ __device__ __forceinline__ double pe_scale(const PairArgs& g, const int32_t* Ea,
     return 1.0;
 }
 
-// Row exponents of the fp16x3 split: e(o, a) = 15 - E for the row's largest
-// magnitude m = f 2^E, f in [0.5, 1), so m 2^e lies in [2^14, 2^15); 0 for
-// zero or non-finite rows and for the padding row (a = nvir) of an odd nvir.
-// One wave per row (o, a) of the padded 2 ceil(nvir / 2) rows per occupied
-// index, at E[o * nv2 + a].
-__global__ __launch_bounds__(256) void row_exp_kernel(int nvir, int naux, int nrows,
-                                                      const float* X, int64_t ld_occ,
-                                                      int64_t ld_vir, int32_t* E) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (row >= nrows) return;
-  const int nv2 = (nvir + 1) & ~1, o = row / nv2, a = row - o * nv2;
-  float m = 0.0f;
-  if (a < nvir) {
-    const float* src = X + (int64_t)o * ld_occ + (int64_t)a * ld_vir;
-    for (int k = lane; k < naux; k += 64) m = fmaxf(m, fabsf(src[k]));
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-  if (lane == 0) {
-    int e = 0;
-    if (m > 0.0f && m <= 3.402823466e38f) {
-      int ex;
-      frexpf(m, &ex);
-      e = 15 - ex;
-    }
-    E[row] = e;
-  }
-}
-
 __device__ __forceinline__ void split_f16x2(const f32x4& x, int e, i32x2& hi, i32x2& lo) {
   _Float16 h[4], l[4];
 #pragma unroll
@@ -480,52 +451,104 @@ __device__ __forceinline__ int x3_slot(int r, int grp) { return grp ^ (((r >> 1)
 
 // fp32 operand X (n, nvir, naux), strides (ld_occ, ld_vir, 1), as its NPC
 // pieces p (bf16x6: 0 hi, 1 mid, 2 lo; fp16x3: 0 hi, 1 lo of the row-scaled
-// value, exponents E from row_exp_kernel) in 32-wide k slices s, rows taken
-// in pairs: element (o, a, p, k), a = 2 m + d, k = 32 s + c, at
+// value) in 32-wide k slices s, rows taken in pairs: element (o, a, p, k),
+// a = 2 m + d, k = 32 s + c, at
 //   ((((o * nvp + m) * nk + s) * NPC + p) * 2 + d) * 32 + c,   nvp = ceil(nvir / 2),
 // nk = ldv / 32. The 64 bytes of one row's slice of one piece share a
 // 128-byte line with the other row of its pair, and the pieces of a row
 // pair's slice are NPC x 128 contiguous bytes, so a wave's 16-row load reads
 // 8 whole lines (half lines would cost the address path twice as much).
 // Columns [naux, ldv) are zero, and so is the second row of the last pair
-// of an odd nvir. One thread per 8 consecutive k of a row (rows of the
-// padded 2 ceil(nvir / 2)); `total` = n * 2 ceil(nvir / 2) * ldv / 8 threads.
-template <int NPC, bool VEC>
+// of an odd nvir.
+__device__ __forceinline__ uint16_t* piece_slot(uint16_t* P, int npc, int nvir, int ldv, int o,
+                                                int a, int k0) {
+  const int nvp = (nvir + 1) >> 1, nk = ldv >> 5;
+  return P + ((((int64_t)o * nvp + (a >> 1)) * nk + (k0 >> 5)) * npc * 2 + (a & 1)) * 32 + (k0 & 31);
+}
+
+// 8 consecutive k of row a of X from k0 (zeros past naux and for a >= nvir).
+template <bool VEC>
+__device__ __forceinline__ void load_row8(const float* src, int nvir, int naux, int a, int k0,
+                                          f32x4& x0, f32x4& x1) {
+  if (a >= nvir) {
+    x0 = x1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  } else if (VEC && k0 + 8 <= naux) {
+    x0 = *reinterpret_cast<const f32x4*>(src + k0);
+    x1 = *reinterpret_cast<const f32x4*>(src + k0 + 4);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x0[e] = k0 + e < naux ? src[k0 + e] : 0.0f;
+      x1[e] = k0 + 4 + e < naux ? src[k0 + 4 + e] : 0.0f;
+    }
+  }
+}
+
+// bf16x6 pieces: one thread per 8 consecutive k of a row (rows of the padded
+// 2 ceil(nvir / 2)); `total` = n * 2 ceil(nvir / 2) * ldv / 8 threads.
+template <bool VEC>
 __global__ __launch_bounds__(256) void split_planes_kernel(int nvir, int naux, int ldv, int total,
                                                           const float* X, int64_t ld_occ,
-                                                          int64_t ld_vir, const int32_t* E,
-                                                          uint16_t* P) {
+                                                          int64_t ld_vir, uint16_t* P) {
   const int idx = blockIdx.x * 256 + threadIdx.x;
   if (idx >= total) return;
   const int gpr = ldv >> 3, nv2 = (nvir + 1) & ~1;
   const int row = idx / gpr, k0 = (idx - row * gpr) * 8;
   const int o = row / nv2, a = row - o * nv2;
-  const float* src = X + (int64_t)o * ld_occ + (int64_t)a * ld_vir + k0;
   f32x4 x0, x1;
-  if (a >= nvir) {
-    x0 = x1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  } else if (VEC && k0 + 8 <= naux) {
-    x0 = *reinterpret_cast<const f32x4*>(src);
-    x1 = *reinterpret_cast<const f32x4*>(src + 4);
-  } else {
+  load_row8<VEC>(X + (int64_t)o * ld_occ + (int64_t)a * ld_vir, nvir, naux, a, k0, x0, x1);
+  uint16_t* dst = piece_slot(P, 3, nvir, ldv, o, a, k0);
+  i32x2 h0, m0, l0, h1, m1, l1;
+  split_bf16x3(x0, h0, m0, l0);
+  split_bf16x3(x1, h1, m1, l1);
+  *reinterpret_cast<i32x4*>(dst) = i32x4{h0[0], h0[1], h1[0], h1[1]};
+  *reinterpret_cast<i32x4*>(dst + 64) = i32x4{m0[0], m0[1], m1[0], m1[1]};
+  *reinterpret_cast<i32x4*>(dst + 128) = i32x4{l0[0], l0[1], l1[0], l1[1]};
+}
+
+// fp16x3 pieces and row exponents in one pass over X: one wave per row pair
+// (o, m) of the padded layout. Row a's exponent is e = 15 - E for its
+// largest magnitude f 2^E, f in [0.5, 1), so the row's values times 2^e lie
+// below 2^15; e = 0 for a zero or non-finite row and for the padding row of
+// an odd nvir; it goes to E[o * 2 nvp + a]. The wave's first sweep takes both
+// rows' maxima, the second splits them, re-reading the same lines (from
+// cache, so HBM sees X once). Lane l covers row 2 m + ((l >> 2) & 1), k =
+// 256 j + 32 (l >> 3) + 8 (l & 3) .. + 7 in sweep step j: 8 whole slices of
+// both rows per step. `nrp` = n ceil(nvir / 2) row pairs.
+template <bool VEC>
+__global__ __launch_bounds__(256) void split_f16x3_kernel(int nvir, int naux, int ldv, int nrp,
+                                                         const float* X, int64_t ld_occ,
+                                                         int64_t ld_vir, int32_t* E, uint16_t* P) {
+  const int rp = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (rp >= nrp) return;
+  const int nvp = (nvir + 1) >> 1, o = rp / nvp, m = rp - o * nvp;
+  const int a = 2 * m + ((lane >> 2) & 1);
+  const int kl = 32 * (lane >> 3) + 8 * (lane & 3);
+  const float* src = X + (int64_t)o * ld_occ + (int64_t)(a < nvir ? a : 0) * ld_vir;
+  float mx = 0.0f;
+#pragma unroll 4
+  for (int k0 = kl; k0 < ldv; k0 += 256) {
+    f32x4 x0, x1;
+    load_row8<VEC>(src, nvir, naux, a, k0, x0, x1);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      x0[e] = k0 + e < naux ? src[e] : 0.0f;
-      x1[e] = k0 + 4 + e < naux ? src[4 + e] : 0.0f;
-    }
+    for (int u = 0; u < 4; ++u) mx = fmaxf(mx, fmaxf(fabsf(x0[u]), fabsf(x1[u])));
   }
-  const int nvp = (nvir + 1) >> 1, nk = ldv >> 5;
-  uint16_t* dst = P + ((((int64_t)o * nvp + (a >> 1)) * nk + (k0 >> 5)) * NPC * 2 + (a & 1)) * 32 +
-                  (k0 & 31);
-  if constexpr (NPC == 3) {
-    i32x2 h0, m0, l0, h1, m1, l1;
-    split_bf16x3(x0, h0, m0, l0);
-    split_bf16x3(x1, h1, m1, l1);
-    *reinterpret_cast<i32x4*>(dst) = i32x4{h0[0], h0[1], h1[0], h1[1]};
-    *reinterpret_cast<i32x4*>(dst + 64) = i32x4{m0[0], m0[1], m1[0], m1[1]};
-    *reinterpret_cast<i32x4*>(dst + 128) = i32x4{l0[0], l0[1], l1[0], l1[1]};
-  } else {
-    const int e = E[row];
+  // the maximum over the 32 lanes of the same row (lane bit 2 picks the row)
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1)
+    if (off != 4) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  int e = 0;
+  if (mx > 0.0f && mx <= 3.402823466e38f) {
+    int ex;
+    frexpf(mx, &ex);
+    e = 15 - ex;
+  }
+  if ((lane & ~4) == 0) E[(int64_t)o * 2 * nvp + a] = e;
+#pragma unroll 4
+  for (int k0 = kl; k0 < ldv; k0 += 256) {
+    f32x4 x0, x1;
+    load_row8<VEC>(src, nvir, naux, a, k0, x0, x1);
+    uint16_t* dst = piece_slot(P, 2, nvir, ldv, o, a, k0);
     i32x2 h0, l0, h1, l1;
     split_f16x2(x0, e, h0, l0);
     split_f16x2(x1, e, h1, l1);
@@ -1462,27 +1485,33 @@ extern "C" size_t trnblas_hip_pair_energy_fp16x3_workspace(int64_t nvir, int64_t
   return split_workspace(2, nvir, naux, npairs, ni, nj);
 }
 
-// Split n x nvir rows (o, a) of X into the pieces at P (split_planes_kernel;
-// fp16x3: the row exponents into E first, row_exp_kernel).
+// Split n x nvir rows (o, a) of X into the pieces at P (bf16x6:
+// split_planes_kernel; fp16x3: split_f16x3_kernel, row exponents into E).
 template <int NPC>
 static void x3_split(const float* X, int64_t n, int64_t ld_occ, int64_t ld_vir, int nvir,
                      int naux, int ldv, uint16_t* P, int32_t* E, hipStream_t s) {
   const int64_t threads = n * ((nvir + 1) & ~1) * (ldv / 8);
   if (threads == 0) return;
-  if (NPC == 2) {
-    const int64_t rows = n * ((nvir + 1) & ~1);
-    hipLaunchKernelGGL(row_exp_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, nvir,
-                       naux, (int)rows, X, ld_occ, ld_vir, E);
-  }
-  const unsigned blocks = (unsigned)((threads + 255) / 256);
   const bool vec = (reinterpret_cast<uintptr_t>(X) & 15) == 0 && ld_occ % 4 == 0 &&
                    ld_vir % 4 == 0;
+  if (NPC == 2) {
+    const int64_t nrp = n * ((nvir + 1) >> 1);
+    const unsigned blocks = (unsigned)((nrp + 3) / 4);
+    if (vec)
+      hipLaunchKernelGGL(split_f16x3_kernel<true>, dim3(blocks), dim3(256), 0, s, nvir, naux, ldv,
+                         (int)nrp, X, ld_occ, ld_vir, E, P);
+    else
+      hipLaunchKernelGGL(split_f16x3_kernel<false>, dim3(blocks), dim3(256), 0, s, nvir, naux, ldv,
+                         (int)nrp, X, ld_occ, ld_vir, E, P);
+    return;
+  }
+  const unsigned blocks = (unsigned)((threads + 255) / 256);
   if (vec)
-    hipLaunchKernelGGL((split_planes_kernel<NPC, true>), dim3(blocks), dim3(256), 0, s, nvir, naux,
-                       ldv, (int)threads, X, ld_occ, ld_vir, (const int32_t*)E, P);
+    hipLaunchKernelGGL(split_planes_kernel<true>, dim3(blocks), dim3(256), 0, s, nvir, naux, ldv,
+                       (int)threads, X, ld_occ, ld_vir, P);
   else
-    hipLaunchKernelGGL((split_planes_kernel<NPC, false>), dim3(blocks), dim3(256), 0, s, nvir,
-                       naux, ldv, (int)threads, X, ld_occ, ld_vir, (const int32_t*)E, P);
+    hipLaunchKernelGGL(split_planes_kernel<false>, dim3(blocks), dim3(256), 0, s, nvir, naux, ldv,
+                       (int)threads, X, ld_occ, ld_vir, P);
 }
 
 template <int NPC>
