@@ -15,6 +15,8 @@ invariants (largest scaled magnitude in [2^14, 2^15), hi + lo within 2^-11 of
 an fp16 ulp of hi, lo no larger than half an ulp of hi). The split has no
 counterpart in the reference (its energy runs in fp32 on the NKI engines);
 it is this library's arithmetic, so the format itself is the oracle here.
+The bf16x6 split (three round-to-nearest bf16 pieces, hi + mid + lo == x
+exactly) is checked the same way through trnblas_hip_pair_energy_bf16x6.
 """
 
 import numpy as np
@@ -57,18 +59,19 @@ def _expected(B):
     return P.view(np.uint16), e.reshape(-1), ldv
 
 
-def _run(dev, B):
+def _run(dev, B, math="fp16x3"):
+    npc = 2 if math == "fp16x3" else 3
     lib = _lib.load()
     nocc, nvir, naux = B.shape
     npairs = nocc * (nocc + 1) // 2
     g = torch.Generator().manual_seed(1)
     eo = (-1.5 + 1.2 * torch.rand(nocc, generator=g)).to(dev)
     ev = (0.1 + 2.9 * torch.rand(nvir, generator=g)).to(dev)
-    ws = lib.trnblas_hip_pair_energy_fp16x3_workspace(nvir, naux, npairs, nocc, 0)
+    ws = getattr(lib, f"trnblas_hip_pair_energy_{math}_workspace")(nvir, naux, npairs, nocc, 0)
     work = torch.zeros(ws, dtype=torch.uint8, device=dev)
     total = torch.full((), float("nan"), dtype=torch.float64, device=dev)
     Bd = B.to(dev)
-    _lib.call("trnblas_hip_pair_energy_fp16x3", nvir, naux, Bd.data_ptr(), nocc, Bd.stride(0),
+    _lib.call(f"trnblas_hip_pair_energy_{math}", nvir, naux, Bd.data_ptr(), nocc, Bd.stride(0),
               Bd.data_ptr(), 0, Bd.stride(0), Bd.stride(1), eo.data_ptr(), eo.data_ptr(), ev.data_ptr(),
               nocc, npairs, None, None, None, None, total.data_ptr(), work.data_ptr(), work.numel(),
               _lib.stream_of(dev))  # fmt: skip
@@ -78,8 +81,10 @@ def _run(dev, B):
     base = _al256(lib.trnblas_hip_pair_energy_workspace(nvir, npairs))
     ldv = -(-naux // 64) * 64
     nvp = (nvir + 1) // 2
-    pbytes = 2 * 2 * nocc * nvp * ldv * 2
+    pbytes = 2 * npc * nocc * nvp * ldv * 2
     P = w[base : base + pbytes].view(np.uint16)
+    if npc == 3:
+        return P, None
     eb = base + _al256(pbytes)
     E = w[eb : eb + nocc * 2 * nvp * 4].view(np.int32)
     return P, E
@@ -104,5 +109,36 @@ def test_fp16x3_split_bit_exact(dev, nocc, nvir, naux, kind):
     P, E = _run(dev, B)
     Pe, Ee, _ = _expected(B.numpy())
     np.testing.assert_array_equal(E, Ee)
+    bad = np.flatnonzero(P != Pe)
+    assert bad.size == 0, f"{bad.size} of {P.size} pieces differ, first at {bad[:8]}"
+
+
+def _expected_bf16x6(B):
+    """hi = rn_bf16(x), mid = rn_bf16(x - hi), lo = rn_bf16(x - hi - mid)
+    (fp32 differences, exact), in the same row-pair layout with three pieces."""
+    nocc, nvir, naux = B.shape
+    ldv = -(-naux // 64) * 64
+    nvp, nk = (nvir + 1) // 2, ldv // 32
+    X = torch.zeros(nocc, 2 * nvp, ldv)
+    X[:, :nvir, :naux] = B
+    hi = X.to(torch.bfloat16)
+    r = X - hi.float()
+    mid = r.to(torch.bfloat16)
+    r2 = r - mid.float()
+    lo = r2.to(torch.bfloat16)
+    # every normal x is exactly hi + mid + lo
+    assert torch.equal(hi.double() + mid.double() + lo.double(), X.double())
+    pieces = torch.stack([hi, mid, lo], dim=2).view(torch.int16).numpy()  # (o, a, p, k)
+    pieces = pieces.reshape(nocc, nvp, 2, 3, nk, 32)  # (o, m, d, p, s, c)
+    return pieces.transpose(0, 1, 4, 3, 2, 5).reshape(-1).view(np.uint16)
+
+
+@pytest.mark.parametrize("nocc, nvir, naux", [(3, 7, 33), (4, 10, 128), (2, 1, 300)])
+def test_bf16x6_split_bit_exact(dev, nocc, nvir, naux):
+    print(f"bf16x6 split case nocc {nocc} nvir {nvir} naux {naux}", flush=True)
+    g = torch.Generator().manual_seed(nocc * 100 + nvir + 7)
+    B = 0.05 * torch.randn(nocc, nvir, naux, generator=g)
+    P, _ = _run(dev, B, "bf16x6")
+    Pe = _expected_bf16x6(B)
     bad = np.flatnonzero(P != Pe)
     assert bad.size == 0, f"{bad.size} of {P.size} pieces differ, first at {bad[:8]}"
